@@ -1,0 +1,106 @@
+// engine_internal.hpp -- shared by every translation unit of libengine_hip.so.
+//
+// Errors inside the library are C++ exceptions (eng::Error) carrying an ABI
+// status code; every extern "C" entry point runs its body through
+// eng::guarded(), which turns an exception into that status code plus the
+// thread-local message returned by eng_last_error(). Message layout and the
+// "always-on precondition" semantics follow the reference's check layer
+// (reference include/engine/check.hpp:36-107).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <engine_hip.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace eng {
+
+class Error : public std::runtime_error {
+ public:
+  Error(int code, const std::string& what) : std::runtime_error(what), code_(code) {}
+  int code() const { return code_; }
+
+ private:
+  int code_;
+};
+
+[[noreturn]] void raise(int code, const char* file, int line, const char* expr,
+                        const std::string& msg);
+[[noreturn]] void raise_hip(hipError_t err, const char* file, int line, const char* expr);
+void set_last_error(const std::string& msg);
+void clear_last_error();
+
+// Runs `body`; returns ENG_OK or the status of the exception it threw.
+template <class F>
+int guarded(F&& body) noexcept {
+  try {
+    body();
+    return ENG_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code();
+  } catch (const std::bad_alloc&) {
+    set_last_error("[engine] host allocation failed (std::bad_alloc)");
+    return ENG_DEVICE_ERROR;
+  } catch (const std::exception& e) {
+    set_last_error(std::string("[engine] unexpected exception: ") + e.what());
+    return ENG_DEVICE_ERROR;
+  } catch (...) {
+    set_last_error("[engine] unknown exception");
+    return ENG_DEVICE_ERROR;
+  }
+}
+
+inline hipStream_t as_stream(eng_stream s) { return reinterpret_cast<hipStream_t>(s); }
+inline hipEvent_t as_event(eng_event e) { return reinterpret_cast<hipEvent_t>(e); }
+
+inline bool aligned_to(const void* p, std::uintptr_t bytes) {
+  return (reinterpret_cast<std::uintptr_t>(p) % bytes) == 0;
+}
+
+// Zero-fills `bytes` of device memory with a kernel on `stream` (used for the
+// K == 0 results; a fill kernel rather than hipMemsetAsync so that callers may
+// capture these launches in a HIP graph).
+void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
+
+// Per-(device, stream) reduction workspace of the split-K GEMV. Counters are
+// zero when handed out and every kernel that uses them leaves them at zero.
+struct GemvWorkspace {
+  float* partials = nullptr;      // [capacity_partials] fp32 partial sums
+  float* partial_ss = nullptr;    // [capacity_ss] fp32 partial sums of squares
+  unsigned* counters = nullptr;   // [capacity_counters] arrival counters
+  std::size_t capacity_partials = 0;
+  std::size_t capacity_ss = 0;
+  std::size_t capacity_counters = 0;
+};
+GemvWorkspace& gemv_workspace(hipStream_t stream);
+void release_gemv_workspace(hipStream_t stream);
+
+}  // namespace eng
+
+#define ENG_CHECK(cond, msg)                                                           \
+  do {                                                                                 \
+    if (!(cond)) ::eng::raise(ENG_INVALID_ARGUMENT, __FILE__, __LINE__, #cond, (msg)); \
+  } while (0)
+
+#define ENG_HIP_CHECK(call)                                           \
+  do {                                                                \
+    hipError_t eng_err_ = (call);                                     \
+    if (eng_err_ != hipSuccess) ::eng::raise_hip(eng_err_, __FILE__, __LINE__, #call); \
+  } while (0)
+
+// After a kernel launch: reports launch-configuration errors. With
+// ENGINE_ALWAYS_SYNC_CHECK defined it also synchronises so in-kernel faults are
+// attributed to the launching line (reference include/engine/check.hpp:94-107).
+#ifdef ENGINE_ALWAYS_SYNC_CHECK
+#define ENG_LAUNCH_CHECK()                     \
+  do {                                         \
+    ENG_HIP_CHECK(hipGetLastError());          \
+    ENG_HIP_CHECK(hipDeviceSynchronize());     \
+  } while (0)
+#else
+#define ENG_LAUNCH_CHECK() ENG_HIP_CHECK(hipGetLastError())
+#endif

@@ -1,0 +1,55 @@
+// launch.hpp -- internal launchers shared by the C-ABI entry points.
+// Callers have validated pointers and dimensions and handled the zero-size
+// cases; these only pick a kernel configuration and launch on `stream`.
+#pragma once
+
+#include "../engine_internal.hpp"
+
+#include <cstdint>
+
+namespace eng {
+
+enum class Elem { F32, F16 };
+
+// out[N] = sum_k xs_k * W[k][n]  with  xs_k = x_k * gamma_k (gamma optional);
+// with rms, out is further multiplied by 1/sqrt(sum_k x_k^2 / K + eps).
+struct GemvArgs {
+  const void* W = nullptr;
+  Elem w = Elem::F32;
+  const void* x = nullptr;
+  Elem x_elem = Elem::F32;
+  const float* gamma = nullptr;
+  void* y = nullptr;
+  Elem y_elem = Elem::F32;
+  std::int64_t N = 0;
+  std::int64_t K = 0;
+  bool rms = false;
+  float eps = 0.0f;
+};
+void launch_gemv(const GemvArgs& a, hipStream_t stream);
+
+// C[M x N] = A'[M x K] . B[K x N] on FP32 MFMA, where A' = A with column k
+// scaled by gamma_k when gamma is given; with rms, row r of C is further
+// multiplied by 1/sqrt(sum_k A[r][k]^2 / K + eps).
+struct GemmArgs {
+  const float* A = nullptr;
+  const void* B = nullptr;
+  Elem b = Elem::F32;
+  float* C = nullptr;
+  std::int64_t M = 0;
+  std::int64_t N = 0;
+  std::int64_t K = 0;
+  const float* gamma = nullptr;
+  bool rms = false;
+  float eps = 0.0f;
+};
+void launch_gemm(const GemmArgs& a, hipStream_t stream);
+
+// out[r][c] = in[r][c] * s_r * weight[c] (weight optional).
+void launch_rmsnorm(const float* in, const float* weight, float* out, long long rows,
+                    long long cols, float eps, hipStream_t stream);
+
+// Number of compute units of the current device (cached per device).
+int device_cu_count();
+
+}  // namespace eng

@@ -1,0 +1,82 @@
+// rmsnorm_linear.hip -- fused RMSNorm + linear (reference kernels/rmsnorm_linear.cu:143-201).
+//
+//   out[r][n] = sum_k (in[r][k] * s_r * w_k) * W[k][n],  s_r = 1/sqrt(mean_k in[r][k]^2 + eps)
+//
+// The reference dispatches rmsnorm into pooled scratch and then gemv (M == 1)
+// or the register-tiled GEMM (M > 1). Here both cases are single fused
+// kernels that never materialise the normalised rows: M == 1 runs the split-K
+// GEMV with the sum of squares reduced alongside the dot products, M > 1 runs
+// the MFMA GEMM with gamma applied while A is staged and s_r applied in the
+// epilogue. Preconditions, messages and the "any zero dimension is a no-op"
+// rule are the reference's.
+#include "launch.hpp"
+
+namespace eng {
+namespace {
+
+void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W, Elem w_elem,
+                        float* out, int64_t M, int64_t N, int64_t K, float eps,
+                        eng_stream stream) {
+  ENG_CHECK(M >= 0 && N >= 0 && K >= 0, "rmsnorm_linear: negative dimension");
+  ENG_CHECK(in != nullptr && W != nullptr && out != nullptr,
+            "rmsnorm_linear: null device pointer");
+  ENG_CHECK(eps >= 0.0f, "rmsnorm_linear: eps must be non-negative");
+  if (M == 0 || N == 0 || K == 0) return;
+  hipStream_t s = as_stream(stream);
+  if (M == 1) {
+    GemvArgs g;
+    g.W = W;
+    g.w = w_elem;
+    g.x = in;
+    g.gamma = rms_weight;
+    g.y = out;
+    g.N = N;
+    g.K = K;
+    g.rms = true;
+    g.eps = eps;
+    launch_gemv(g, s);
+    return;
+  }
+  GemmArgs g;
+  g.A = in;
+  g.B = W;
+  g.b = w_elem;
+  g.C = out;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.gamma = rms_weight;
+  g.rms = true;
+  g.eps = eps;
+  launch_gemm(g, s);
+}
+
+}  // namespace
+}  // namespace eng
+
+extern "C" {
+
+int eng_rmsnorm_linear_f32(const float* in, const float* rms_weight, const float* W, float* out,
+                           int64_t M, int64_t N, int64_t K, float eps, eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, out, M, N, K, eps, stream);
+  });
+}
+
+int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_half* W,
+                            float* out, int64_t M, int64_t N, int64_t K, float eps,
+                            eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F16, out, M, N, K, eps, stream);
+  });
+}
+
+int eng_rmsnorm_linear_fused_direct_f32(const float* in, const float* rms_weight,
+                                        const float* W, float* out, int64_t M, int64_t N,
+                                        int64_t K, float eps, eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, out, M, N, K, eps, stream);
+  });
+}
+
+}  // extern "C"

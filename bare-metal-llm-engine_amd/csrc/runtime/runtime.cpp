@@ -1,0 +1,372 @@
+// runtime.cpp -- errors, device queries, memory, streams and events of the C-ABI.
+//
+// HIP-backed replacement of the reference's src/cuda_device.cpp (device
+// queries, 51-301), src/cuda_stream.cpp (RAII stream/event, 11-38) and the
+// raw cudaMalloc/cudaMemcpy/cudaMemset calls of include/engine/device_buffer.hpp
+// (33-92), exposed as plain C functions.
+#include "../engine_internal.hpp"
+
+#include <cstdio>
+#include <cstring>
+#include <sstream>
+#include <string>
+
+namespace eng {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_last_error(const std::string& msg) { g_last_error = msg; }
+void clear_last_error() { g_last_error.clear(); }
+
+void raise(int code, const char* file, int line, const char* expr, const std::string& msg) {
+  std::ostringstream oss;
+  oss << "[engine] " << file << ":" << line << "\n"
+      << "  check failed: " << expr << "\n"
+      << "  " << msg;
+  throw Error(code, oss.str());
+}
+
+void raise_hip(hipError_t err, const char* file, int line, const char* expr) {
+  std::ostringstream oss;
+  oss << hipGetErrorName(err) << ": " << hipGetErrorString(err);
+  raise(ENG_DEVICE_ERROR, file, line, expr, oss.str());
+}
+
+namespace {
+
+int device_count_or_zero() {
+  int n = 0;
+  // Not an error when there is no driver or device: the answer is zero.
+  if (hipGetDeviceCount(&n) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return n;
+}
+
+void current_props(hipDeviceProp_t& prop) {
+  ENG_CHECK(device_count_or_zero() > 0, "no HIP device is visible");
+  int dev = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  ENG_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+}
+
+void copy_out(const std::string& s, char* buf, std::size_t len) {
+  ENG_CHECK(buf != nullptr, "output buffer is null");
+  ENG_CHECK(len > 0, "output buffer length must be positive");
+  std::snprintf(buf, len, "%s", s.c_str());
+}
+
+// Published HBM peak of known parts, in GB/s. hipDeviceProp's memory clock
+// times bus width undercounts HBM3E's data rate, so a known part reports its
+// specification value; anything else falls back to clock x bus bytes x 2.
+double spec_peak_gbs(const hipDeviceProp_t& prop) {
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) return 8000.0;
+  if (std::strncmp(prop.gcnArchName, "gfx942", 6) == 0) return 5300.0;
+  const double clock_hz = static_cast<double>(prop.memoryClockRate) * 1.0e3;
+  const double bus_bytes = static_cast<double>(prop.memoryBusWidth) / 8.0;
+  return clock_hz * bus_bytes * 2.0 / 1.0e9;
+}
+
+}  // namespace
+}  // namespace eng
+
+using eng::guarded;
+
+extern "C" {
+
+const char* eng_last_error(void) { return eng::g_last_error.c_str(); }
+
+const char* eng_build_info(void) {
+  return "engine_hip 0.1 gfx950 -O3 packed-fp32-off"
+#ifdef ENGINE_ALWAYS_SYNC_CHECK
+         " sync-check"
+#endif
+      ;
+}
+
+int eng_device_count(int* count) {
+  return guarded([&] {
+    ENG_CHECK(count != nullptr, "eng_device_count: count is null");
+    *count = eng::device_count_or_zero();
+  });
+}
+
+int eng_device_summary(char* buf, std::size_t len) {
+  return guarded([&] {
+    if (eng::device_count_or_zero() == 0) {
+      eng::copy_out("no HIP device", buf, len);
+      return;
+    }
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    std::ostringstream oss;
+    oss.setf(std::ios::fixed);
+    oss.precision(1);
+    const char* name = prop.name[0] != '\0' ? prop.name : "AMD GPU";
+    oss << name << " | " << prop.gcnArchName << " | "
+        << (static_cast<double>(prop.totalGlobalMem) / (1024.0 * 1024.0 * 1024.0)) << " GiB"
+        << " | " << prop.multiProcessorCount << " CUs"
+        << " | " << (prop.sharedMemPerBlock / 1024) << " KiB LDS/block"
+        << " | " << eng::spec_peak_gbs(prop) << " GB/s";
+    eng::copy_out(oss.str(), buf, len);
+  });
+}
+
+int eng_peak_bandwidth_gbs(double* gbs) {
+  return guarded([&] {
+    ENG_CHECK(gbs != nullptr, "eng_peak_bandwidth_gbs: gbs is null");
+    *gbs = 0.0;
+    if (eng::device_count_or_zero() == 0) return;
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    *gbs = eng::spec_peak_gbs(prop);
+  });
+}
+
+int eng_driver_version(char* buf, std::size_t len) {
+  return guarded([&] {
+    int drv = 0;
+    if (hipDriverGetVersion(&drv) != hipSuccess) {
+      (void)hipGetLastError();
+      eng::copy_out("none", buf, len);
+      return;
+    }
+    eng::copy_out(std::to_string(drv), buf, len);
+  });
+}
+
+int eng_clock_rate_khz(int* khz) {
+  return guarded([&] {
+    ENG_CHECK(khz != nullptr, "eng_clock_rate_khz: khz is null");
+    *khz = 0;
+    if (eng::device_count_or_zero() == 0) return;
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    *khz = prop.clockRate;
+  });
+}
+
+int eng_live_sm_clock_mhz(int* mhz) {
+  return guarded([&] {
+    ENG_CHECK(mhz != nullptr, "eng_live_sm_clock_mhz: mhz is null");
+    *mhz = 0;
+    if (eng::device_count_or_zero() == 0) return;
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    *mhz = prop.clockRate / 1000;
+  });
+}
+
+int eng_live_mem_clock_mhz(int* mhz) {
+  return guarded([&] {
+    ENG_CHECK(mhz != nullptr, "eng_live_mem_clock_mhz: mhz is null");
+    *mhz = 0;
+    if (eng::device_count_or_zero() == 0) return;
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    *mhz = prop.memoryClockRate / 1000;
+  });
+}
+
+int eng_device_arch(char* buf, std::size_t len) {
+  return guarded([&] {
+    if (eng::device_count_or_zero() == 0) {
+      eng::copy_out("none", buf, len);
+      return;
+    }
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    eng::copy_out(prop.gcnArchName, buf, len);
+  });
+}
+
+int eng_device_cu_count(int* cus) {
+  return guarded([&] {
+    ENG_CHECK(cus != nullptr, "eng_device_cu_count: cus is null");
+    *cus = 0;
+    if (eng::device_count_or_zero() == 0) return;
+    hipDeviceProp_t prop{};
+    eng::current_props(prop);
+    *cus = prop.multiProcessorCount;
+  });
+}
+
+// ---------------------------------------------------------------- memory
+
+int eng_malloc(void** ptr, std::size_t bytes) {
+  return guarded([&] {
+    ENG_CHECK(ptr != nullptr, "eng_malloc: ptr is null");
+    *ptr = nullptr;
+    if (bytes == 0) return;
+    ENG_HIP_CHECK(hipMalloc(ptr, bytes));
+  });
+}
+
+int eng_free(void* ptr) {
+  return guarded([&] {
+    if (ptr == nullptr) return;
+    ENG_HIP_CHECK(hipFree(ptr));
+  });
+}
+
+int eng_memcpy_h2d(void* dst, const void* src, std::size_t bytes) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_h2d: null pointer");
+    ENG_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+  });
+}
+
+int eng_memcpy_d2h(void* dst, const void* src, std::size_t bytes) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_d2h: null pointer");
+    ENG_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+  });
+}
+
+int eng_memcpy_d2d(void* dst, const void* src, std::size_t bytes) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_d2d: null pointer");
+    ENG_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+  });
+}
+
+int eng_memcpy_h2d_async(void* dst, const void* src, std::size_t bytes, eng_stream stream) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_h2d_async: null pointer");
+    ENG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, eng::as_stream(stream)));
+  });
+}
+
+int eng_memcpy_d2h_async(void* dst, const void* src, std::size_t bytes, eng_stream stream) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_d2h_async: null pointer");
+    ENG_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, eng::as_stream(stream)));
+  });
+}
+
+int eng_memset(void* ptr, int value, std::size_t bytes) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(ptr != nullptr, "eng_memset: ptr is null");
+    ENG_HIP_CHECK(hipMemset(ptr, value, bytes));
+  });
+}
+
+int eng_memset_async(void* ptr, int value, std::size_t bytes, eng_stream stream) {
+  return guarded([&] {
+    if (bytes == 0) return;
+    ENG_CHECK(ptr != nullptr, "eng_memset_async: ptr is null");
+    ENG_HIP_CHECK(hipMemsetAsync(ptr, value, bytes, eng::as_stream(stream)));
+  });
+}
+
+int eng_device_sync(void) {
+  return guarded([&] { ENG_HIP_CHECK(hipDeviceSynchronize()); });
+}
+
+int eng_check_last_launch(void) {
+  return guarded([&] { ENG_HIP_CHECK(hipGetLastError()); });
+}
+
+// ------------------------------------------------------- streams and events
+
+int eng_stream_create(eng_stream* stream, unsigned int flags) {
+  return guarded([&] {
+    ENG_CHECK(stream != nullptr, "eng_stream_create: stream is null");
+    hipStream_t s = nullptr;
+    // Default priority only: streams of different priorities are not used here.
+    ENG_HIP_CHECK(hipStreamCreateWithFlags(&s, flags));
+    *stream = reinterpret_cast<eng_stream>(s);
+  });
+}
+
+int eng_stream_destroy(eng_stream stream) {
+  return guarded([&] {
+    if (stream == nullptr) return;
+    hipStream_t s = eng::as_stream(stream);
+    // Drain first: the stream's GEMV workspace may still be in use by queued
+    // kernels, and a later stream can be handed the same handle value.
+    ENG_HIP_CHECK(hipStreamSynchronize(s));
+    eng::release_gemv_workspace(s);
+    ENG_HIP_CHECK(hipStreamDestroy(s));
+  });
+}
+
+int eng_stream_sync(eng_stream stream) {
+  return guarded([&] { ENG_HIP_CHECK(hipStreamSynchronize(eng::as_stream(stream))); });
+}
+
+int eng_stream_wait_event(eng_stream stream, eng_event event, unsigned int flags) {
+  return guarded([&] {
+    ENG_CHECK(event != nullptr, "eng_stream_wait_event: event is null");
+    ENG_HIP_CHECK(hipStreamWaitEvent(eng::as_stream(stream), eng::as_event(event), flags));
+  });
+}
+
+int eng_event_create(eng_event* event, unsigned int flags) {
+  return guarded([&] {
+    ENG_CHECK(event != nullptr, "eng_event_create: event is null");
+    hipEvent_t e = nullptr;
+    ENG_HIP_CHECK(hipEventCreateWithFlags(&e, flags));
+    *event = reinterpret_cast<eng_event>(e);
+  });
+}
+
+int eng_event_destroy(eng_event event) {
+  return guarded([&] {
+    if (event == nullptr) return;
+    ENG_HIP_CHECK(hipEventDestroy(eng::as_event(event)));
+  });
+}
+
+int eng_event_record(eng_event event, eng_stream stream) {
+  return guarded([&] {
+    ENG_CHECK(event != nullptr, "eng_event_record: event is null");
+    ENG_HIP_CHECK(hipEventRecord(eng::as_event(event), eng::as_stream(stream)));
+  });
+}
+
+int eng_event_query(eng_event event, int* done) {
+  return guarded([&] {
+    ENG_CHECK(done != nullptr, "eng_event_query: done is null");
+    if (event == nullptr) {
+      *done = 1;
+      return;
+    }
+    const hipError_t q = hipEventQuery(eng::as_event(event));
+    if (q == hipSuccess) {
+      *done = 1;
+    } else if (q == hipErrorNotReady) {
+      (void)hipGetLastError();
+      *done = 0;
+    } else {
+      ENG_HIP_CHECK(q);
+    }
+  });
+}
+
+int eng_event_sync(eng_event event) {
+  return guarded([&] {
+    if (event == nullptr) return;
+    ENG_HIP_CHECK(hipEventSynchronize(eng::as_event(event)));
+  });
+}
+
+int eng_event_elapsed_ms(float* ms, eng_event start, eng_event end) {
+  return guarded([&] {
+    ENG_CHECK(ms != nullptr, "eng_event_elapsed_ms: ms is null");
+    ENG_CHECK(start != nullptr && end != nullptr,
+              "eng_event_elapsed_ms called on uninitialized event");
+    ENG_HIP_CHECK(hipEventElapsedTime(ms, eng::as_event(start), eng::as_event(end)));
+  });
+}
+
+}  // extern "C"

@@ -1,0 +1,98 @@
+#pragma once
+//===----------------------------------------------------------------------===//
+// engine/kernels.hpp -- C++17 launch API of the matrix-multiply path.
+//
+// Restates the reference's raw-pointer launchers (include/engine/kernels.hpp:
+// 34-121; ADR docs/adr/0003) for the functions on this path, with the same
+// names, argument order, defaults and error behaviour:
+//   * every pointer is a DEVICE pointer; dimensions are std::int64_t;
+//   * the last argument is the stream (nullptr = legacy default stream);
+//   * launches are asynchronous; precondition failures throw
+//     engine::EngineError with the reference's message substrings
+//     ("null", "non-negative", "negative", "eps") before anything is launched.
+// Each launcher forwards to the C-ABI in engine_hip.h. `engine::cuda` names
+// the same namespace, so call sites written against the reference compile
+// unchanged.
+//===----------------------------------------------------------------------===//
+
+#include <engine/check.hpp>
+#include <engine/half.hpp>
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace engine {
+namespace hip {
+
+using engine::half;
+
+namespace detail {
+inline const eng_half* bits(const half* p) { return reinterpret_cast<const eng_half*>(p); }
+inline eng_half* bits(half* p) { return reinterpret_cast<eng_half*>(p); }
+}  // namespace detail
+
+/// Row-wise RMSNorm: out = in / sqrt(mean(in^2) + eps) * weight. `weight` may be nullptr.
+/// (reference kernels.hpp:61-63)
+inline void rmsnorm(const float* in, const float* weight, float* out, std::int64_t rows,
+                    std::int64_t cols, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_rmsnorm_f32(in, weight, out, rows, cols, eps, stream));
+}
+
+/// C[M x N] = A[M x K] * B[K x N], row-major, fp32 accumulate; runs on the
+/// FP32 matrix cores (the name is kept from the reference, kernels.hpp:77-81).
+inline void matmul_register_tiled(const float* A, const float* B, float* C, std::int64_t M,
+                                  std::int64_t N, std::int64_t K, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_matmul_f32(A, B, C, M, N, K, stream));
+}
+
+/// out[N] = x[K] * A[K x N], row-major (reference kernels.hpp:83-86).
+inline void gemv(const float* A, const float* x, float* out, std::int64_t N, std::int64_t K,
+                 hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_gemv_f32(A, x, out, N, K, stream));
+}
+
+/// out[M x N] = RMSNorm(in[M x K], rms_weight, eps) * W[K x N]; `rms_weight` may
+/// be nullptr (reference kernels.hpp:92-99). One fused kernel for every M.
+inline void rmsnorm_linear(const float* in, const float* rms_weight, const float* W, float* out,
+                           std::int64_t M, std::int64_t N, std::int64_t K, float eps,
+                           hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_rmsnorm_linear_f32(in, rms_weight, W, out, M, N, K, eps, stream));
+}
+
+/// fp16-weight overload (fp32 activations in and out).
+inline void rmsnorm_linear(const float* in, const float* rms_weight, const half* W, float* out,
+                           std::int64_t M, std::int64_t N, std::int64_t K, float eps,
+                           hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_rmsnorm_linear_f16w(in, rms_weight, detail::bits(W), out, M, N, K, eps, stream));
+}
+
+/// The reference's benchmarking entry that forces its fused kernel
+/// (kernels.hpp:101-104); every M is fused here, so it is rmsnorm_linear.
+inline void rmsnorm_linear_fused_direct(const float* in, const float* rms_weight, const float* W,
+                                        float* out, std::int64_t M, std::int64_t N,
+                                        std::int64_t K, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_rmsnorm_linear_fused_direct_f32(in, rms_weight, W, out, M, N, K, eps, stream));
+}
+
+/// out[N] = x[K] * A[K x N] in FP16 storage with fp32 accumulation; out rounded
+/// to nearest even (reference kernels.hpp:118-121).
+inline void gemv_fp16(const half* A, const half* x, half* out, std::int64_t N, std::int64_t K,
+                      hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_gemv_f16(detail::bits(A), detail::bits(x), detail::bits(out), N, K, stream));
+}
+
+/// fp16-weight overload with fp32 activations in and out (decode with fp16 weights).
+inline void gemv_fp16(const half* A, const float* x, float* out, std::int64_t N, std::int64_t K,
+                      hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_gemv_f16w(detail::bits(A), x, out, N, K, stream));
+}
+
+}  // namespace hip
+
+// Call sites written against the reference use engine::cuda::...
+namespace cuda = hip;
+
+}  // namespace engine

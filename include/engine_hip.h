@@ -1,0 +1,233 @@
+/*
+ * engine_hip.h -- C-ABI of the MI355X (gfx950) matrix-multiply engine.
+ *
+ * This is the drop-in boundary. It is plain C: no HIP, torch or C++ types
+ * cross it. Device pointers are `void*`/typed pointers to device memory,
+ * streams and events are opaque handles (a HIP stream handle may be passed
+ * where an `eng_stream` is expected; NULL is the legacy default stream),
+ * dimensions are signed 64-bit, and every function returns a status code:
+ *
+ *   ENG_OK (0)                 success
+ *   ENG_INVALID_ARGUMENT (1)   a precondition failed; nothing was launched
+ *   ENG_DEVICE_ERROR (2)       the HIP runtime reported an error
+ *
+ * After a non-zero status, eng_last_error() returns the message of the
+ * failure on the calling thread, formatted like the reference's EngineError:
+ *   "[engine] <file>:<line>\n  check failed: <expr>\n  <message>"
+ * and containing the same substrings the reference's contract tests match
+ * ("null", "non-negative", "negative", "eps").
+ *
+ * The C++17 launch API of the reference (namespace engine::cuda, header
+ * include/engine/kernels.hpp) is restated on top of this ABI by the headers
+ * under include/engine/ in this repository.
+ *
+ * Layout convention (reference include/engine/cpu_ref.hpp:14-17): all 2-D
+ * data is row-major and contiguous. GEMV/RMSNorm+linear weights are stored
+ * [K x N] and out = x . W (reference include/engine/kernels.hpp:83-99).
+ */
+#ifndef ENGINE_HIP_H
+#define ENGINE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ENG_OK 0
+#define ENG_INVALID_ARGUMENT 1
+#define ENG_DEVICE_ERROR 2
+
+/* IEEE-754 binary16 bit pattern (the reference's engine::half). */
+typedef uint16_t eng_half;
+/* Opaque stream / event handles (hipStream_t / hipEvent_t underneath). */
+typedef void* eng_stream;
+typedef void* eng_event;
+/* Opaque pooled-allocator handle. */
+typedef struct eng_pool_s* eng_pool;
+
+/* Device kinds, numbered like the reference's engine::Device
+ * (include/engine/tensor.hpp:50-53): 0 = host, 1 = the GPU. */
+#define ENG_DEVICE_CPU 0
+#define ENG_DEVICE_GPU 1
+
+/* Stream / event flags (values of hipStreamNonBlocking / hipEventDisableTiming). */
+#define ENG_STREAM_DEFAULT 0u
+#define ENG_STREAM_NON_BLOCKING 1u
+#define ENG_EVENT_DEFAULT 0u
+#define ENG_EVENT_DISABLE_TIMING 2u
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* eng_last_error(void);
+/* Library build string: "<version> gfx950 <build flags>". */
+const char* eng_build_info(void);
+
+/* ------------------------------------------------------------------------
+ * Device queries. Replace engine::cuda_device_count / cuda_device_summary /
+ * cuda_peak_bandwidth_gbs / cuda_driver_version / cuda_clock_rate_khz /
+ * cuda_live_sm_clock_mhz / cuda_live_mem_clock_mhz
+ * (reference include/engine/cuda_device.hpp:20-48, src/cuda_device.cpp:51-222).
+ * Like the reference, the count answers 0 (not an error) when no device or
+ * driver is present.
+ * ---------------------------------------------------------------------- */
+int eng_device_count(int* count);
+int eng_device_summary(char* buf, size_t len);
+/* Theoretical peak HBM bandwidth from the device's memory clock and bus
+ * width (clock x bus bytes x 2), in GB/s. */
+int eng_peak_bandwidth_gbs(double* gbs);
+int eng_driver_version(char* buf, size_t len);
+int eng_clock_rate_khz(int* khz);
+/* Live clocks are not readable without an SMI library; these report the
+ * nominal clocks (the reference falls back the same way when NVML is
+ * absent, src/cuda_device.cpp:196-222). */
+int eng_live_sm_clock_mhz(int* mhz);
+int eng_live_mem_clock_mhz(int* mhz);
+/* Architecture the device reports (e.g. "gfx950:sramecc+:xnack-"). */
+int eng_device_arch(char* buf, size_t len);
+int eng_device_cu_count(int* cus);
+
+/* ------------------------------------------------------------------------
+ * Memory. Replace the cudaMalloc / cudaFree / cudaMemcpy / cudaMemset calls
+ * behind engine::DeviceBuffer<T> (reference include/engine/device_buffer.hpp:
+ * 33-92) and Storage (src/tensor.cpp:56-95).
+ * ---------------------------------------------------------------------- */
+int eng_malloc(void** ptr, size_t bytes);
+int eng_free(void* ptr);
+int eng_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int eng_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int eng_memcpy_d2d(void* dst, const void* src, size_t bytes);
+int eng_memcpy_h2d_async(void* dst, const void* src, size_t bytes, eng_stream stream);
+int eng_memcpy_d2h_async(void* dst, const void* src, size_t bytes, eng_stream stream);
+int eng_memset(void* ptr, int value, size_t bytes);
+int eng_memset_async(void* ptr, int value, size_t bytes, eng_stream stream);
+int eng_device_sync(void);
+/* hipGetLastError(), cleared; ENG_DEVICE_ERROR with its text if set. */
+int eng_check_last_launch(void);
+
+/* ------------------------------------------------------------------------
+ * Streams and events. Replace engine::CudaStream / CudaEvent
+ * (reference include/engine/cuda_stream.hpp:21-124, src/cuda_stream.cpp:11-38).
+ * Streams are created at the default priority. eng_stream_destroy waits for
+ * the stream's work and releases the per-stream GEMV reduction workspace.
+ * ---------------------------------------------------------------------- */
+int eng_stream_create(eng_stream* stream, unsigned int flags);
+int eng_stream_destroy(eng_stream stream);
+int eng_stream_sync(eng_stream stream);
+int eng_stream_wait_event(eng_stream stream, eng_event event, unsigned int flags);
+int eng_event_create(eng_event* event, unsigned int flags);
+int eng_event_destroy(eng_event event);
+int eng_event_record(eng_event event, eng_stream stream);
+/* *done = 1 when complete, 0 when still pending. */
+int eng_event_query(eng_event event, int* done);
+int eng_event_sync(eng_event event);
+int eng_event_elapsed_ms(float* ms, eng_event start, eng_event end);
+
+/* ------------------------------------------------------------------------
+ * Pooled allocator. Replaces engine::PoolAllocator / pool_allocator(Device) /
+ * AllocStats (reference include/engine/pool_allocator.hpp:27-148,
+ * include/engine/allocator.hpp:34-63, src/pool_allocator.cpp:38-271):
+ * power-of-two buckets of at least 256 B, 256-B alignment, slabs carved
+ * most-recent-first, slab size doubling from the initial size and capped at
+ * 64 MiB, stream-ordered reuse of GPU blocks through a per-block event,
+ * mutex-guarded, exact statistics.
+ * ---------------------------------------------------------------------- */
+typedef struct eng_alloc_stats {
+  uint64_t bytes_in_use;
+  uint64_t bytes_reserved;
+  uint64_t peak_bytes_in_use;
+  uint64_t num_allocs;
+  uint64_t num_driver_allocs;
+} eng_alloc_stats;
+
+int eng_pool_create(eng_pool* pool, int device, size_t initial_slab_bytes);
+int eng_pool_destroy(eng_pool pool);
+/* The process-wide pool of a device kind (created on first use). */
+int eng_pool_default(eng_pool* pool, int device);
+/* bytes == 0 yields *ptr == NULL and ENG_OK, like the reference. */
+int eng_pool_allocate(eng_pool pool, size_t bytes, void** ptr);
+/* Host pools: immediate. GPU pools: reuse deferred until the work queued on
+ * `stream` so far completes (an event is recorded on `stream`). */
+int eng_pool_deallocate(eng_pool pool, void* ptr, eng_stream stream);
+int eng_pool_stats(eng_pool pool, eng_alloc_stats* stats);
+int eng_pool_reset(eng_pool pool);
+/* Passthrough allocator of a device kind (reference src/allocator.cpp:42-118). */
+int eng_passthrough_allocate(int device, size_t bytes, void** ptr);
+int eng_passthrough_deallocate(int device, void* ptr);
+int eng_passthrough_stats(int device, eng_alloc_stats* stats);
+
+/* ------------------------------------------------------------------------
+ * Host fp16 conversions (IEEE-754 round-to-nearest-even; replaces the
+ * host half_to_float / float_to_half of reference include/engine/half.hpp:
+ * 27-105, whose non-CUDA float->half truncates).
+ * ---------------------------------------------------------------------- */
+int eng_f32_to_f16_host(const float* in, eng_half* out, size_t n);
+int eng_f16_to_f32_host(const eng_half* in, float* out, size_t n);
+
+/* ------------------------------------------------------------------------
+ * Kernels. All pointers are DEVICE pointers; launches are asynchronous on
+ * `stream`. Preconditions, messages and zero-size behaviour follow the
+ * reference launchers exactly:
+ *   - null pointer           -> ENG_INVALID_ARGUMENT, "... is null" / "null device pointer"
+ *   - negative dimension     -> ENG_INVALID_ARGUMENT, "... must be non-negative" / "negative dimension"
+ *   - GEMV/GEMM with K == 0  -> output zero-filled on `stream`
+ *   - N == 0 (GEMV), M or N == 0 (GEMM) -> no-op
+ *   - rmsnorm_linear with any dimension 0 -> no-op (nothing written)
+ * ---------------------------------------------------------------------- */
+
+/* C[M x N] = A[M x K] . B[K x N], fp32 accumulate, on FP32 MFMA.
+ * Replaces engine::cuda::matmul_register_tiled
+ * (reference include/engine/kernels.hpp:77-81, kernels/matmul_register_tiled.cu:176-199). */
+int eng_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t N, int64_t K,
+                   eng_stream stream);
+
+/* out[N] = x[K] . A[K x N], fp32. Replaces engine::cuda::gemv
+ * (reference include/engine/kernels.hpp:83-86, kernels/gemv.cu:114-147). */
+int eng_gemv_f32(const float* A, const float* x, float* out, int64_t N, int64_t K,
+                 eng_stream stream);
+
+/* out[N] = x[K] . A[K x N] with half A, x and out, fp32 accumulate, out
+ * rounded to nearest even. Replaces engine::cuda::gemv_fp16
+ * (reference include/engine/kernels.hpp:118-121, kernels/gemv_fp16.cu:117-149). */
+int eng_gemv_f16(const eng_half* A, const eng_half* x, eng_half* out, int64_t N, int64_t K,
+                 eng_stream stream);
+
+/* out[N] = x[K] . A[K x N] with half A and fp32 x / out, fp32 accumulate.
+ * Additive overload of engine::cuda::gemv_fp16 for fp16-weight decode with
+ * fp32 activations (no reference counterpart; same contract as gemv_fp16). */
+int eng_gemv_f16w(const eng_half* A, const float* x, float* out, int64_t N, int64_t K,
+                  eng_stream stream);
+
+/* out[r][c] = in[r][c] / sqrt(mean(in[r][:]^2) + eps) * weight[c]; weight may
+ * be NULL (no gain). Replaces engine::cuda::rmsnorm
+ * (reference include/engine/kernels.hpp:61-63, kernels/rmsnorm.cu:171-192). */
+int eng_rmsnorm_f32(const float* in, const float* weight, float* out, int64_t rows,
+                    int64_t cols, float eps, eng_stream stream);
+
+/* out[M x N] = RMSNorm(in[M x K], rms_weight, eps) . W[K x N]; rms_weight may be
+ * NULL. One fused kernel: the sum of squares is reduced inside the GEMV/GEMM.
+ * Replaces engine::cuda::rmsnorm_linear
+ * (reference include/engine/kernels.hpp:92-99, kernels/rmsnorm_linear.cu:173-201). */
+int eng_rmsnorm_linear_f32(const float* in, const float* rms_weight, const float* W, float* out,
+                           int64_t M, int64_t N, int64_t K, float eps, eng_stream stream);
+
+/* As eng_rmsnorm_linear_f32 with an fp16 weight matrix W[K x N] (fp32 in / out).
+ * Additive overload (no reference counterpart; same contract). */
+int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_half* W,
+                            float* out, int64_t M, int64_t N, int64_t K, float eps,
+                            eng_stream stream);
+
+/* Replaces engine::cuda::rmsnorm_linear_fused_direct
+ * (reference include/engine/kernels.hpp:101-104, kernels/rmsnorm_linear.cu:143-171),
+ * the benchmarking entry that forces the fused kernel for every M. Here every
+ * M is served by fused kernels already, so it runs the same code as
+ * eng_rmsnorm_linear_f32. */
+int eng_rmsnorm_linear_fused_direct_f32(const float* in, const float* rms_weight,
+                                        const float* W, float* out, int64_t M, int64_t N,
+                                        int64_t K, float eps, eng_stream stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* ENGINE_HIP_H */

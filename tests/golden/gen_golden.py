@@ -1,0 +1,147 @@
+"""Writes the golden fixtures under tests/golden/data/ and tests/golden/manifest.json.
+
+Run from the repository root:  python tests/golden/gen_golden.py
+
+Case tables follow the reference's generator (reference
+tools/gen_reference.py:401-440 for shapes, :668-741 for distributions):
+inputs ~ N(0, 1), matrices scaled by 1/sqrt(K), RMSNorm gains ~ 1 + N(0, 0.1^2),
+eps = 1e-5. Added cases: BASELINE config 1 (512^3, U[-1, 1], seed 0) and the
+fp16-weight variants with fp32 activations (gemv_f16w, rmsnorm_linear_f16w).
+
+Inputs are not stored: each is rebuilt from its generator spec by
+tests/golden/detgen.py and checked against the SHA-256 recorded here.
+Expected outputs are computed in float64 with NumPy, independently of the C
+oracle, and stored as float32 ENGREF01 tensors (the reference's convention).
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+sys.path.insert(0, str(HERE))
+
+import detgen  # noqa: E402
+import engref  # noqa: E402
+
+EPS = 1e-5
+
+MATMUL_SHAPES = [(1, 1, 1), (32, 32, 32), (128, 64, 256), (17, 23, 31), (512, 512, 512)]
+RMSNORM_SHAPES = [(1, 4096, True), (128, 4096, True), (32, 127, True), (32, 4096, False)]
+RMSNORM_LINEAR_SHAPES = [
+    (1, 256, 4096, True),
+    (32, 256, 512, True),
+    (1, 768, 256, True),
+    (17, 127, 31, True),
+    (32, 256, 512, False),
+]
+GEMV_SHAPES = [(256, 4096), (768, 256), (127, 31), (64, 128)]
+GEMV_FP16_SHAPES = [(64, 64), (128, 256), (73, 125), (256, 4096)]
+
+
+def f64(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Value of a generated input in float64 (f16 inputs are bit patterns)."""
+    if dtype == "f16":
+        return a.view(np.float16).astype(np.float64)
+    return a.astype(np.float64)
+
+
+def rms_rows(x64: np.ndarray, w64) -> np.ndarray:
+    out = x64 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + EPS)
+    if w64 is not None:
+        out = out * w64
+    return out
+
+
+class Builder:
+    def __init__(self):
+        self.cases = []
+        self.next_seed = 1
+
+    def spec(self, gen, shape, dtype="f32", **kw):
+        s = {"gen": gen, "shape": list(shape), "dtype": dtype, "seed": self.next_seed, **kw}
+        self.next_seed += 1
+        return s
+
+    def add(self, stem, op, params, specs, expected):
+        inputs = {}
+        for name, s in specs.items():
+            arr = detgen.make(s)
+            inputs[name] = dict(s, sha256=detgen.digest(arr))
+        engref.write(HERE / "data" / f"{stem}.bin", {"expected": expected.astype(np.float32)})
+        self.cases.append({"stem": stem, "op": op, "params": params, "inputs": inputs})
+
+    def build(self):
+        for m, n, k in MATMUL_SHAPES:
+            sc = 1.0 / np.sqrt(max(k, 1))
+            specs = {"A": self.spec("normal", (m, k), std=sc), "B": self.spec("normal", (k, n), std=sc)}
+            a, b = (f64(detgen.make(specs[x]), "f32") for x in ("A", "B"))
+            self.add(f"matmul__{m}x{n}x{k}", "matmul", {"M": m, "N": n, "K": k}, specs, a @ b)
+
+        # U[-1, 1], 512^3 (seed field records the config seed).
+        specs = {
+            "A": dict(self.spec("uniform", (512, 512), lo=-1.0, hi=1.0), seed=0),
+            "B": dict(self.spec("uniform", (512, 512), lo=-1.0, hi=1.0), seed=100),
+        }
+        a, b = (f64(detgen.make(specs[x]), "f32") for x in ("A", "B"))
+        self.add("matmul_cfg1__512x512x512", "matmul", {"M": 512, "N": 512, "K": 512}, specs, a @ b)
+
+        for rows, cols, with_w in RMSNORM_SHAPES:
+            specs = {"input": self.spec("normal", (rows, cols))}
+            if with_w:
+                specs["weight"] = self.spec("normal", (cols,), mean=1.0, std=0.1)
+            x = f64(detgen.make(specs["input"]), "f32")
+            w = f64(detgen.make(specs["weight"]), "f32") if with_w else None
+            sfx = "w" if with_w else "now"
+            self.add(f"rmsnorm__{rows}x{cols}_{sfx}", "rmsnorm",
+                     {"rows": rows, "cols": cols, "eps": EPS}, specs, rms_rows(x, w))
+        specs = {"input": self.spec("zeros", (2, 256))}
+        self.add("rmsnorm__zeros", "rmsnorm", {"rows": 2, "cols": 256, "eps": EPS}, specs,
+                 np.zeros((2, 256)))
+
+        for wdt, tag in (("f32", "rmsnorm_linear"), ("f16", "rmsnorm_linear_f16w")):
+            for m, n, k, with_w in RMSNORM_LINEAR_SHAPES:
+                specs = {
+                    "input": self.spec("normal", (m, k)),
+                    "W": self.spec("normal", (k, n), dtype=wdt, std=1.0 / np.sqrt(max(k, 1))),
+                }
+                if with_w:
+                    specs["weight"] = self.spec("normal", (k,), mean=1.0, std=0.1)
+                x = f64(detgen.make(specs["input"]), "f32")
+                W = f64(detgen.make(specs["W"]), wdt)
+                w = f64(detgen.make(specs["weight"]), "f32") if with_w else None
+                sfx = "w" if with_w else "now"
+                self.add(f"{tag}__{m}x{n}x{k}_{sfx}", tag,
+                         {"M": m, "N": n, "K": k, "eps": EPS}, specs, rms_rows(x, w) @ W)
+
+        for n, k in GEMV_SHAPES:
+            specs = {"A": self.spec("normal", (k, n), std=1.0 / np.sqrt(max(k, 1))),
+                     "x": self.spec("normal", (k,))}
+            A = f64(detgen.make(specs["A"]), "f32")
+            x = f64(detgen.make(specs["x"]), "f32")
+            self.add(f"gemv__{n}x{k}", "gemv", {"N": n, "K": k}, specs, x @ A)
+
+        for xdt, tag in (("f16", "gemv_fp16"), ("f32", "gemv_f16w")):
+            for n, k in GEMV_FP16_SHAPES:
+                specs = {"A": self.spec("normal", (k, n), dtype="f16", std=1.0 / np.sqrt(max(k, 1))),
+                         "x": self.spec("normal", (k,), dtype=xdt)}
+                A = f64(detgen.make(specs["A"]), "f16")
+                x = f64(detgen.make(specs["x"]), xdt)
+                self.add(f"{tag}__{n}x{k}", tag, {"N": n, "K": k}, specs, x @ A)
+
+
+def main() -> None:
+    b = Builder()
+    b.build()
+    manifest = {"generator": "tests/golden/detgen.py (SplitMix64, Irwin-Hall normals)",
+                "eps": EPS, "cases": b.cases}
+    (HERE / "manifest.json").write_text(json.dumps(manifest, indent=1) + "\n")
+    print(f"wrote {len(b.cases)} cases to {HERE / 'data'}")
+
+
+if __name__ == "__main__":
+    main()

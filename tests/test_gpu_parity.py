@@ -1,0 +1,356 @@
+"""GPU parity of the HIP kernels, called through the C-ABI.
+
+Tier 1: against the float64 golden fixtures (reference case tables).
+Tier 2: against the C oracle at the BASELINE configs' full sizes (sampled
+        rows for the 4096^3 GEMM) and on odd / misaligned shapes that take the
+        fallback paths.
+Properties: determinism, K == 0 / zero-size contracts, M = 1 equivalences,
+fused == separate, null gain == unit gain, linearity.
+Every comparison uses the derived bound and the tighter statistical bound of
+tests/helpers.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-5
+
+
+# ------------------------------------------------------------------ runners
+def gpu_matmul(eng, A, B):
+    M, K = A.shape
+    N = B.shape[1]
+    dA, dB, dC = eng.upload(A), eng.upload(B), eng.empty((M, N), np.float32)
+    eng.call("eng_matmul_f32", dA.ptr, dB.ptr, dC.ptr, M, N, K, None)
+    eng.sync()
+    return dC.download()
+
+
+def gpu_gemv(eng, A, x):
+    K, N = A.shape
+    half_w = A.dtype == np.uint16
+    half_x = x.dtype == np.uint16
+    dA, dx = eng.upload(A), eng.upload(x)
+    dy = eng.empty(N, np.uint16 if half_x else np.float32)
+    fn = "eng_gemv_f16" if half_x else ("eng_gemv_f16w" if half_w else "eng_gemv_f32")
+    eng.call(fn, dA.ptr, dx.ptr, dy.ptr, N, K, None)
+    eng.sync()
+    return dy.download()
+
+
+def gpu_rmsnorm(eng, x, w):
+    rows, cols = x.shape
+    dx, dy = eng.upload(x), eng.empty(x.shape, np.float32)
+    dw = eng.upload(w) if w is not None else None
+    eng.call("eng_rmsnorm_f32", dx.ptr, dw.ptr if dw else None, dy.ptr, rows, cols, EPS, None)
+    eng.sync()
+    return dy.download()
+
+
+def gpu_rmsnorm_linear(eng, x, w, W, fn=None):
+    M, K = x.shape
+    N = W.shape[1]
+    half_w = W.dtype == np.uint16
+    fn = fn or ("eng_rmsnorm_linear_f16w" if half_w else "eng_rmsnorm_linear_f32")
+    dx, dW, dy = eng.upload(x), eng.upload(W), eng.empty((M, N), np.float32)
+    dw = eng.upload(w) if w is not None else None
+    eng.call(fn, dx.ptr, dw.ptr if dw else None, dW.ptr, dy.ptr, M, N, K, EPS, None)
+    eng.sync()
+    return dy.download()
+
+
+def check_dot(got, y64, a, K, what):
+    derived, stat = helpers.dot_bounds(a, y64, K)
+    helpers.assert_within(got, y64, derived, what + " [derived K*u bound]")
+    helpers.assert_within(got, y64, stat, what + " [statistical 16*sqrt(K)*u bound]")
+
+
+def check_rmsnorm_linear(got, y64, x, g, W, K, what):
+    derived, stat = helpers.rmsnorm_linear_bounds(x, g, W, y64, K)
+    helpers.assert_within(got, y64, derived, what + " [derived bound]")
+    helpers.assert_within(got, y64, stat, what + " [statistical bound]")
+
+
+# ------------------------------------------------------------- tier 1 golden
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("matmul")])
+def test_matmul_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = gpu_matmul(gpu, x["A"], x["B"])
+    # golden is float32-rounded: its rounding is one more u|y|
+    y = helpers.expected(c)
+    check_dot(got, y, helpers.absdot(x["A"], x["B"]) + np.abs(y), c["params"]["K"], stem)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv")])
+def test_gemv_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = gpu_gemv(gpu, x["A"], x["x"])
+    y = helpers.expected(c)
+    check_dot(got, y, helpers.absdot(x["x"], x["A"]) + np.abs(y), c["params"]["K"], stem)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv_f16w")])
+def test_gemv_f16w_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = gpu_gemv(gpu, x["A"], x["x"])
+    y = helpers.expected(c)
+    check_dot(got, y, helpers.absdot(x["x"], x["A"]) + np.abs(y), c["params"]["K"], stem)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv_fp16")])
+def test_gemv_fp16_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = helpers.as_f64(gpu_gemv(gpu, x["A"], x["x"]))
+    y = helpers.expected(c)
+    K = c["params"]["K"]
+    derived, _ = helpers.dot_bounds(helpers.absdot(x["x"], x["A"]) + np.abs(y), y, K)
+    bound = derived + helpers.U16 * np.abs(y) + 2.0**-25
+    helpers.assert_within(got, y, bound, stem + " [derived bound + half output rounding]")
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm")])
+def test_rmsnorm_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = gpu_rmsnorm(gpu, x["input"], x.get("weight"))
+    y = helpers.expected(c)
+    cols = c["params"]["cols"]
+    # fp32 sum of `cols` squares (cols*u relative, halved by the root) + divide,
+    # root, two multiplies, golden rounding
+    bound = (cols / 2.0 + 6) * helpers.U32 * np.abs(y) + 1e-30
+    helpers.assert_within(got, y, bound, stem)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm_linear")
+                                  + helpers.cases("rmsnorm_linear_f16w")])
+def test_rmsnorm_linear_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = gpu_rmsnorm_linear(gpu, x["input"], x.get("weight"), x["W"])
+    y = helpers.expected(c)
+    check_rmsnorm_linear(got, y, x["input"], x.get("weight"), x["W"], c["params"]["K"], stem)
+
+
+# --------------------------------------------------- tier 2 BASELINE configs
+def test_config1_matmul_512_uniform(gpu, orc):
+    rng = np.random.default_rng(0)
+    A = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    B = rng.uniform(-1, 1, (512, 512)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    y = orc.matmul(A, B).astype(np.float64)
+    check_dot(got, y, helpers.absdot(A, B) + np.abs(y), 512, "config 1 512^3")
+
+
+def test_config2_gemv_f16w_4096(gpu, orc):
+    rng = np.random.default_rng(1)
+    K = N = 4096
+    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(K, dtype=np.float32)
+    got = gpu_gemv(gpu, W, x)
+    y = orc.gemv_f16w(W, x).astype(np.float64)
+    check_dot(got, y, helpers.absdot(x, W) + np.abs(y), K, "config 2 gemv_f16w 4096x4096")
+
+
+def test_config3_rmsnorm_linear_f16w(gpu, orc):
+    rng = np.random.default_rng(2)
+    K, N = 4096, 11008
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear(gpu, x, g, W)
+    y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, W, K, "config 3 rmsnorm_linear_f16w 4096x11008")
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (512, 11008, 4096), (512, 4096, 11008)])
+def test_config4_matmul_sampled_rows(gpu, orc, M, N, K):
+    rng = np.random.default_rng(3)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    rows = np.unique(np.concatenate([[0, 1, 127, 128, M - 1], rng.integers(0, M, 3)]))
+    y = orc.matmul(A[rows], B).astype(np.float64)
+    check_dot(got[rows], y, helpers.absdot(A[rows], B) + np.abs(y), K, f"config 4 {M}x{N}x{K} rows {rows}")
+    # Column sums as a second, full-matrix property: sum_i C[i, :] = (sum_i A[i, :]) . B
+    colsum = got.astype(np.float64).sum(axis=0)
+    ref = A.astype(np.float64).sum(axis=0) @ B.astype(np.float64)
+    bound = (K + M) * helpers.U32 * (np.abs(A).astype(np.float64).sum(axis=0) @ np.abs(B).astype(np.float64))
+    helpers.assert_within(colsum, ref, bound, f"config 4 {M}x{N}x{K} column sums")
+
+
+# -------------------------------------------------------- odd / fallback paths
+@pytest.mark.parametrize("M,N,K", [(3, 7, 11), (65, 137, 73), (129, 257, 65), (1, 65, 127),
+                                   (71, 97, 113), (2, 5, 1), (300, 8, 4), (130, 130, 33)])
+def test_matmul_non_tile_multiples(gpu, orc, M, N, K):
+    i = np.arange(M * K, dtype=np.float32)
+    j = np.arange(K * N, dtype=np.float32)
+    A = (np.sin((i + 1) * 0.1) / np.sqrt(K)).astype(np.float32).reshape(M, K)
+    B = (np.cos((j + 1) * 0.1) / np.sqrt(K)).astype(np.float32).reshape(K, N)
+    got = gpu_matmul(gpu, A, B)
+    y = orc.matmul(A, B).astype(np.float64)
+    check_dot(got, y, helpers.absdot(A, B) + np.abs(y), K, f"matmul {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("N,K,dtype", [(127, 31, "f32"), (73, 125, "f16w"), (4100, 4096, "f16w"),
+                                       (11008, 4096, "f32"), (8, 20000, "f16w"), (1, 1, "f32"),
+                                       (3000, 7, "f16"), (64, 1, "f16w")])
+def test_gemv_shapes_against_oracle(gpu, orc, N, K, dtype):
+    rng = np.random.default_rng(N * 7 + K)
+    A = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    x = rng.standard_normal(K, dtype=np.float32)
+    if dtype == "f32":
+        got, y = gpu_gemv(gpu, A, x), orc.gemv(A, x)
+        check_dot(got, y.astype(np.float64), helpers.absdot(x, A) + np.abs(y), K, f"gemv {N}x{K}")
+    elif dtype == "f16w":
+        A16 = orc.f32_to_f16(A)
+        got, y = gpu_gemv(gpu, A16, x), orc.gemv_f16w(A16, x)
+        check_dot(got, y.astype(np.float64), helpers.absdot(x, A16) + np.abs(y), K, f"gemv_f16w {N}x{K}")
+    else:
+        A16, x16 = orc.f32_to_f16(A), orc.f32_to_f16(x)
+        got = helpers.as_f64(gpu_gemv(gpu, A16, x16))
+        y = helpers.as_f64(x16) @ helpers.as_f64(A16)
+        derived, _ = helpers.dot_bounds(helpers.absdot(x16, A16), y, K)
+        helpers.assert_within(got, y, derived + helpers.U16 * np.abs(y) + 2.0**-25, f"gemv_fp16 {N}x{K}")
+
+
+def test_misaligned_pointers_take_the_scalar_path(gpu, orc):
+    """A weight pointer off 16-byte alignment must still give the right answer."""
+    rng = np.random.default_rng(12)
+    K, N = 512, 1024
+    A = (rng.standard_normal((K, N)) / np.sqrt(K)).astype(np.float32)
+    x = rng.standard_normal(K, dtype=np.float32)
+    dbig = gpu.upload(np.concatenate([[0.0], A.ravel()]).astype(np.float32))
+    dx, dy = gpu.upload(x), gpu.empty(N, np.float32)
+    gpu.call("eng_gemv_f32", dbig.ptr + 4, dx.ptr, dy.ptr, N, K, None)
+    gpu.sync()
+    y = orc.gemv(A, x).astype(np.float64)
+    check_dot(dy.download(), y, helpers.absdot(x, A) + np.abs(y), K, "misaligned gemv")
+    Ab = np.concatenate([[0.0], A.ravel()]).astype(np.float32)
+    B = (rng.standard_normal((K, 96)) / np.sqrt(K)).astype(np.float32)
+    dA, dB, dC = gpu.upload(Ab), gpu.upload(B), gpu.empty((K // 2, 96), np.float32)
+    gpu.call("eng_matmul_f32", dA.ptr + 4, dB.ptr, dC.ptr, K // 2, 96, K, None)
+    gpu.sync()
+    Am = A.ravel()[: (K // 2) * K].reshape(K // 2, K)
+    y = orc.matmul(Am, B).astype(np.float64)
+    check_dot(dC.download(), y, helpers.absdot(Am, B) + np.abs(y), K, "misaligned matmul")
+
+
+# ------------------------------------------------------------------ properties
+def test_results_are_deterministic(gpu):
+    rng = np.random.default_rng(13)
+    K, N = 4096, 11008
+    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    a = gpu_rmsnorm_linear(gpu, x, g, W)
+    b = gpu_rmsnorm_linear(gpu, x, g, W)
+    assert np.array_equal(a, b)
+    A = rng.uniform(-1, 1, (700, 900)).astype(np.float32)
+    B = rng.uniform(-1, 1, (900, 600)).astype(np.float32)
+    assert np.array_equal(gpu_matmul(gpu, A, B), gpu_matmul(gpu, A, B))
+
+
+def test_matmul_m1_is_gemv_bit_exact(gpu):
+    rng = np.random.default_rng(14)
+    A = rng.standard_normal((2048, 3000), dtype=np.float32)
+    x = rng.standard_normal(2048, dtype=np.float32)
+    assert np.array_equal(gpu_matmul(gpu, x[None, :], A)[0], gpu_gemv(gpu, A, x))
+
+
+def test_gemv_is_linear_in_x(gpu):
+    rng = np.random.default_rng(15)
+    K, N = 4096, 4096
+    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x1 = rng.standard_normal(K, dtype=np.float32)
+    x2 = rng.standard_normal(K, dtype=np.float32)
+    y1, y2, y12 = gpu_gemv(gpu, W, x1), gpu_gemv(gpu, W, x2), gpu_gemv(gpu, W, x1 + x2)
+    a = helpers.absdot(np.abs(x1) + np.abs(x2), W)
+    helpers.assert_within(y12, y1.astype(np.float64) + y2, 2 * 16 * np.sqrt(K) * helpers.U32 * a,
+                          "gemv(x1 + x2) = gemv(x1) + gemv(x2)")
+    assert np.all(gpu_gemv(gpu, W, np.zeros(K, np.float32)) == 0.0)
+
+
+def test_rmsnorm_linear_fused_equals_separate(gpu):
+    rng = np.random.default_rng(16)
+    for M in (1, 32):
+        x = rng.standard_normal((M, 512), dtype=np.float32)
+        g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
+        W = (rng.standard_normal((512, 256)) / np.sqrt(512)).astype(np.float32)
+        fused = gpu_rmsnorm_linear(gpu, x, g, W)
+        sep = gpu_matmul(gpu, gpu_rmsnorm(gpu, x, g), W) if M > 1 else gpu_gemv(gpu, W, gpu_rmsnorm(gpu, x, g)[0])[None]
+        y = helpers.rms_scale64(x) * helpers.as_f64(x) * g @ W.astype(np.float64)
+        check_rmsnorm_linear(fused, y, x, g, W, 512, f"fused M={M}")
+        check_rmsnorm_linear(sep, y, x, g, W, 512, f"separate M={M}")
+        direct = gpu_rmsnorm_linear(gpu, x, g, W, fn="eng_rmsnorm_linear_fused_direct_f32")
+        assert np.array_equal(direct, fused)
+
+
+def test_rmsnorm_linear_null_weight_equals_unit_weight(gpu):
+    rng = np.random.default_rng(17)
+    for M in (1, 32):
+        x = rng.standard_normal((M, 512), dtype=np.float32)
+        W = (rng.standard_normal((512, 256)) / np.sqrt(512)).astype(np.float32)
+        assert np.array_equal(gpu_rmsnorm_linear(gpu, x, None, W),
+                              gpu_rmsnorm_linear(gpu, x, np.ones(512, np.float32), W))
+
+
+def test_rmsnorm_zero_row_is_zero(gpu):
+    assert np.all(gpu_rmsnorm(gpu, np.zeros((2, 256), np.float32), None) == 0.0)
+    W = np.ones((256, 64), np.float32)
+    assert np.all(gpu_rmsnorm_linear(gpu, np.zeros((1, 256), np.float32), None, W) == 0.0)
+    assert np.all(gpu_rmsnorm_linear(gpu, np.zeros((3, 256), np.float32), None, W) == 0.0)
+
+
+# ---------------------------------------------------------------- contracts
+def test_k_zero_zero_fills_and_empty_is_untouched(gpu):
+    poison = np.full(12, 7.0, np.float32)
+    d1 = gpu.upload(np.zeros(4, np.float32))
+    for fn, args in (("eng_matmul_f32", (4, 3, 0)), ("eng_gemv_f32", (12, 0)), ("eng_gemv_f16w", (12, 0))):
+        dy = gpu.upload(poison)
+        gpu.call(fn, d1.ptr, d1.ptr, dy.ptr, *args, None)
+        gpu.sync()
+        assert np.all(dy.download() == 0.0), fn
+    dh = gpu.upload(np.full(13, 0x4700, np.uint16))  # 7.0 in half
+    gpu.call("eng_gemv_f16", d1.ptr, d1.ptr, dh.ptr, 13, 0, None)
+    gpu.sync()
+    assert np.all(dh.download() == 0)
+    # rmsnorm_linear with any zero dimension, and N == 0 GEMVs, write nothing.
+    dy = gpu.upload(poison)
+    gpu.call("eng_rmsnorm_linear_f32", d1.ptr, None, d1.ptr, dy.ptr, 4, 3, 0, EPS, None)
+    gpu.call("eng_gemv_f32", d1.ptr, d1.ptr, dy.ptr, 0, 5, None)
+    gpu.call("eng_matmul_f32", d1.ptr, d1.ptr, dy.ptr, 0, 3, 5, None)
+    gpu.sync()
+    assert np.all(dy.download() == 7.0)
+
+
+def test_split_k_workspace_survives_shape_changes_and_streams(gpu, orc):
+    """Many GEMVs of varying shape on two streams share per-stream workspaces."""
+    rng = np.random.default_rng(18)
+    shapes = [(4096, 4096), (11008, 4096), (4096, 11008), (64, 8192), (1000, 3000)]
+    cases = []
+    for N, K in shapes:
+        A = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal(K, dtype=np.float32)
+        cases.append((N, K, A, x, gpu.upload(A), gpu.upload(x), gpu.empty(N, np.float32)))
+    streams = [gpu.stream(), gpu.stream()]
+    try:
+        for rep in range(3):
+            for i, (N, K, _, _, dA, dx, dy) in enumerate(cases):
+                gpu.call("eng_gemv_f16w", dA.ptr, dx.ptr, dy.ptr, N, K, streams[(i + rep) % 2].handle)
+        for s in streams:
+            s.sync()
+        for N, K, A, x, _, _, dy in cases:
+            y = orc.gemv_f16w(A, x).astype(np.float64)
+            check_dot(dy.download(), y, helpers.absdot(x, A) + np.abs(y), K, f"stream gemv {N}x{K}")
+    finally:
+        for s in streams:
+            s.destroy()

@@ -1,0 +1,238 @@
+"""Pins the CPU oracle (oracle/liboracle.so) before it is trusted as the checker.
+
+Against: the float64 golden fixtures (reference case tables), closed forms,
+exact rational brute force on tiny shapes, NumPy's IEEE float16, and planted
+mistakes (oracle/liboracle_mut<N>.so) that each check must catch.
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+import helpers
+
+EPS = 1e-5
+
+
+def oracle_bound(a, y64, K):
+    """Double-accumulated oracle vs float64 golden: output rounding + double sum."""
+    return helpers.U32 * np.abs(y64) + 2.0 * K * 2.0**-53 * a + 1e-300
+
+
+# --------------------------------------------------------------- run helpers
+def run_matmul(orc, c):
+    x = helpers.inputs(c)
+    return orc.matmul(x["A"], x["B"]), x
+
+
+def check_matmul(orc, c):
+    got, x = run_matmul(orc, c)
+    exp = helpers.expected(c)
+    K = c["params"]["K"]
+    # The golden is float32-rounded: allow its rounding as well.
+    bound = oracle_bound(helpers.absdot(x["A"], x["B"]), exp, K) + helpers.U32 * np.abs(exp)
+    return helpers.assert_within(got, exp, bound, c["stem"])
+
+
+def check_gemv(orc, c):
+    x = helpers.inputs(c)
+    got = orc.gemv(x["A"], x["x"])
+    exp = helpers.expected(c)
+    bound = oracle_bound(helpers.absdot(x["x"], x["A"]), exp, c["params"]["K"]) + helpers.U32 * np.abs(exp)
+    return helpers.assert_within(got, exp, bound, c["stem"])
+
+
+def check_rmsnorm(orc, c):
+    x = helpers.inputs(c)
+    got = orc.rmsnorm(x["input"], x.get("weight"), EPS)
+    exp = helpers.expected(c)
+    # scale rounded to float, then two float multiplies, then the golden's rounding
+    bound = 5 * helpers.U32 * np.abs(exp) + 1e-30
+    return helpers.assert_within(got, exp, bound, c["stem"])
+
+
+def check_rmsnorm_linear(orc, c):
+    x = helpers.inputs(c)
+    got = orc.rmsnorm_linear(x["input"], x.get("weight"), x["W"], EPS)
+    exp = helpers.expected(c)
+    K = c["params"]["K"]
+    s = helpers.rms_scale64(x["input"])
+    g = 1.0 if "weight" not in x else helpers.as_f64(x["weight"])
+    a = s * (np.abs(helpers.as_f64(x["input"]) * g) @ np.abs(helpers.as_f64(x["W"])))
+    # temp[k] carries ~3 float roundings (scale, two multiplies): 4u relative per term.
+    bound = 4 * helpers.U32 * a + 2 * helpers.U32 * np.abs(exp) + 2.0 * K * 2.0**-53 * a
+    return helpers.assert_within(got, exp, bound, c["stem"])
+
+
+# ------------------------------------------------------------------- goldens
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("matmul")])
+def test_matmul_matches_golden(orc, stem):
+    check_matmul(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv")])
+def test_gemv_matches_golden(orc, stem):
+    check_gemv(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv_fp16")])
+def test_gemv_fp16_matches_golden(orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = helpers.as_f64(orc.gemv_fp16(x["A"], x["x"]))
+    exp = helpers.expected(c)
+    # half output rounding (half an ulp, 2^-11 relative, 2^-25 absolute near 0)
+    bound = helpers.U16 * np.abs(exp) + 2.0**-25 + helpers.U32 * np.abs(exp)
+    helpers.assert_within(got, exp, bound, stem)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv_f16w")])
+def test_gemv_f16w_matches_golden(orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = orc.gemv_f16w(x["A"], x["x"])
+    exp = helpers.expected(c)
+    bound = oracle_bound(helpers.absdot(x["x"], x["A"]), exp, c["params"]["K"]) + helpers.U32 * np.abs(exp)
+    helpers.assert_within(got, exp, bound, stem)
+    # Same numbers as the fp32 GEMV over the decoded matrix, bit for bit.
+    assert np.array_equal(got, orc.gemv(orc.f16_to_f32(x["A"]), x["x"]))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm")])
+def test_rmsnorm_matches_golden(orc, stem):
+    check_rmsnorm(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm_linear")
+                                  + helpers.cases("rmsnorm_linear_f16w")])
+def test_rmsnorm_linear_matches_golden(orc, stem):
+    check_rmsnorm_linear(orc, helpers.case(stem))
+
+
+def test_golden_inputs_are_reproducible():
+    """Every fixture input regenerates to the recorded SHA-256."""
+    for c in helpers.manifest()["cases"]:
+        helpers.inputs(c)
+
+
+# -------------------------------------------------------------- closed forms
+def test_matmul_identity_is_a_copy(orc):
+    rng = np.random.default_rng(5)
+    A = rng.standard_normal((37, 53), dtype=np.float32)
+    assert np.array_equal(orc.matmul(A, np.eye(53, dtype=np.float32)), A)
+
+
+def test_matmul_all_ones_gives_k(orc):
+    for K in (1, 7, 1000, 4097):
+        C = orc.matmul(np.ones((3, K), np.float32), np.ones((K, 5), np.float32))
+        assert np.all(C == K)
+
+
+def test_matmul_exact_rational_brute_force(orc):
+    rng = np.random.default_rng(11)
+    for M, N, K in ((1, 1, 1), (3, 4, 5), (2, 7, 3)):
+        A = rng.standard_normal((M, K), dtype=np.float32)
+        B = rng.standard_normal((K, N), dtype=np.float32)
+        C = orc.matmul(A, B)
+        for i in range(M):
+            for j in range(N):
+                exact = sum(Fraction(float(A[i, k])) * Fraction(float(B[k, j])) for k in range(K))
+                # products of floats are exact in double; a few double sums then one
+                # rounding to float: equal to the correctly rounded value within 1 ulp
+                assert abs(Fraction(float(C[i, j])) - exact) <= Fraction(abs(float(exact))) * Fraction(2, 2**24)
+
+
+def test_gemv_is_matmul_at_m1_bit_exact(orc):
+    rng = np.random.default_rng(6)
+    A = rng.standard_normal((300, 77), dtype=np.float32)
+    x = rng.standard_normal(300, dtype=np.float32)
+    assert np.array_equal(orc.gemv(A, x), orc.matmul(x[None, :], A)[0])
+
+
+def test_gemv_of_zero_input_is_zero(orc):
+    out = orc.gemv(np.ones((128, 64), np.float32), np.zeros(128, np.float32))
+    assert np.all(out == 0.0)
+
+
+def test_gemv_fp16_small_integers_are_exact(orc):
+    # Sums of small integer products are exact in every format involved.
+    A = orc.f32_to_f16(np.arange(12, dtype=np.float32).reshape(4, 3) - 5)
+    x = orc.f32_to_f16(np.array([1, -2, 3, 1], np.float32))
+    got = orc.f16_to_f32(orc.gemv_fp16(A, x))
+    Af = orc.f16_to_f32(A).astype(np.float64)
+    assert np.array_equal(got, (np.array([1, -2, 3, 1.0]) @ Af).astype(np.float32))
+
+
+def test_rmsnorm_zero_row_is_zero_not_nan(orc):
+    out = orc.rmsnorm(np.zeros((2, 256), np.float32), None, EPS)
+    assert np.all(out == 0.0)
+
+
+def test_rmsnorm_null_weight_equals_unit_weight(orc):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((5, 300), dtype=np.float32)
+    assert np.array_equal(orc.rmsnorm(x, None, EPS), orc.rmsnorm(x, np.ones(300, np.float32), EPS))
+    W = rng.standard_normal((300, 40), dtype=np.float32)
+    assert np.array_equal(orc.rmsnorm_linear(x, None, W, EPS),
+                          orc.rmsnorm_linear(x, np.ones(300, np.float32), W, EPS))
+
+
+def test_rmsnorm_linear_is_rmsnorm_then_matmul(orc):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((9, 200), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(200)).astype(np.float32)
+    W = rng.standard_normal((200, 33), dtype=np.float32)
+    assert np.array_equal(orc.rmsnorm_linear(x, g, W, EPS), orc.matmul(orc.rmsnorm(x, g, EPS), W))
+    W16 = orc.f32_to_f16(W)
+    assert np.array_equal(orc.rmsnorm_linear(x, g, W16, EPS),
+                          orc.rmsnorm_linear(x, g, orc.f16_to_f32(W16), EPS))
+
+
+# ---------------------------------------------------------------------- half
+def test_half_to_float_exhaustive(orc):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = orc.f16_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def half_probe_floats() -> np.ndarray:
+    rng = np.random.default_rng(9)
+    sampled = rng.integers(0, 2**32, size=1 << 24, dtype=np.uint64).astype(np.uint32)
+    # every float next to a half rounding boundary (+-1 ulp around each midpoint)
+    h = np.arange(0, 0x7C00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32).view(np.uint32)
+    edges = np.concatenate([mids - 1, mids, mids + 1, np.array([0x477FF000, 0x477FEFFF, 0x33000000,
+                                                                  0x33000001, 0x7F800000, 0x7FC00000], np.uint32)])
+    allb = np.concatenate([sampled, edges, edges | 0x80000000]).astype(np.uint32)
+    return allb.view(np.float32)
+
+
+def test_float_to_half_matches_numpy(orc):
+    f = half_probe_floats()
+    with np.errstate(over="ignore"):
+        ref = f.astype(np.float16)
+    got = orc.f32_to_f16(f)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got.view(np.float16)), nan)
+    assert np.array_equal(got[~nan], ref[~nan].view(np.uint16))
+
+
+# ------------------------------------------------------------ planted mistakes
+@pytest.mark.parametrize("mutation,check", [
+    (1, lambda o: check_matmul(o, helpers.case("matmul__128x64x256"))),
+    (2, lambda o: check_gemv(o, helpers.case("gemv__256x4096"))),
+    (3, lambda o: check_rmsnorm(o, helpers.case("rmsnorm__1x4096_w"))),
+    (4, lambda o: check_rmsnorm_linear(o, helpers.case("rmsnorm_linear__32x256x512_w"))),
+    (5, lambda o: test_float_to_half_matches_numpy(o)),
+])
+def test_planted_mistakes_are_caught(mutation, check):
+    mutant = helpers.oracle(mutation)
+    assert mutant.mutation() == mutation
+    with pytest.raises(AssertionError):
+        check(mutant)
