@@ -66,15 +66,13 @@ inline bool aligned_to(const void* p, std::uintptr_t bytes) {
 // capture these launches in a HIP graph).
 void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 
-// Per-(device, stream) reduction workspace of the split-K GEMV. Counters are
-// zero when handed out and every kernel that uses them leaves them at zero.
+// Per-(device, stream) workspace of the split-K GEMV: launches on one stream
+// run in order, so consecutive calls can reuse it without synchronisation.
 struct GemvWorkspace {
-  float* partials = nullptr;      // [capacity_partials] fp32 partial sums
-  float* partial_ss = nullptr;    // [capacity_ss] fp32 partial sums of squares
-  unsigned* counters = nullptr;   // [capacity_counters] arrival counters
+  float* partials = nullptr;    // [capacity_partials] fp32 partial sums
+  float* partial_ss = nullptr;  // [capacity_ss] fp32 partial sums of squares
   std::size_t capacity_partials = 0;
   std::size_t capacity_ss = 0;
-  std::size_t capacity_counters = 0;
 };
 GemvWorkspace& gemv_workspace(hipStream_t stream);
 void release_gemv_workspace(hipStream_t stream);

@@ -22,11 +22,9 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(unsigned char* __restric
   for (std::size_t i = pre + nvec * 16 + tid; i < bytes; i += stride) p[i] = 0;
 }
 
-// Workspace sizes: 4 MiB of fp32 partials bounds nsplit * N; the counter array
-// bounds the number of column blocks that can use split-K.
+// Workspace sizes: 4 MiB of fp32 partials bounds nsplit * N.
 constexpr std::size_t kPartials = std::size_t{1} << 20;
-constexpr std::size_t kPartialSs = std::size_t{1} << 16;
-constexpr std::size_t kCounters = std::size_t{1} << 14;
+constexpr std::size_t kPartialSs = std::size_t{1} << 12;
 
 struct Key {
   int device;
@@ -65,16 +63,10 @@ GemvWorkspace& gemv_workspace(hipStream_t stream) {
   GemvWorkspace ws;
   ws.capacity_partials = kPartials;
   ws.capacity_ss = kPartialSs;
-  ws.capacity_counters = kCounters;
-  const std::size_t bytes =
-      (kPartials + kPartialSs) * sizeof(float) + kCounters * sizeof(unsigned);
   void* base = nullptr;
-  ENG_HIP_CHECK(hipMalloc(&base, bytes));
+  ENG_HIP_CHECK(hipMalloc(&base, (kPartials + kPartialSs) * sizeof(float)));
   ws.partials = static_cast<float*>(base);
   ws.partial_ss = ws.partials + kPartials;
-  ws.counters = reinterpret_cast<unsigned*>(ws.partial_ss + kPartialSs);
-  // Counters start at zero; the kernels that use them leave them at zero.
-  fill_zero_async(ws.counters, kCounters * sizeof(unsigned), stream);
   return m.emplace(Key{dev, stream}, ws).first->second;
 }
 

@@ -25,6 +25,7 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace eng {
 namespace {
@@ -42,23 +43,42 @@ constexpr int BS = BN + 4;   // B tile row stride in LDS (floats)
 constexpr int kGroupM = 8;   // tile-rows per raster group
 constexpr int kXcds = 8;
 
+// Global -> register staging of a B tile, K x N layout (B[k][n], rows along N):
+// 32 rows of 128 elements.
 template <typename BT>
 struct BLoad;
 template <>
 struct BLoad<float> {
-  // 32 rows x 128 floats: 4 loads of 4 floats per thread.
-  static constexpr int kLoads = 4;
+  static constexpr int kLoads = 4;   // 4 x float4 per thread
   static constexpr int kVec = 4;
-  static constexpr int kThreadsPerRow = BN / kVec;          // 32
+  static constexpr int kThreadsPerRow = BN / kVec;                // 32
   static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 8
 };
 template <>
 struct BLoad<_Float16> {
-  // 32 rows x 128 halves: 2 loads of 8 halves per thread.
+  static constexpr int kLoads = 2;   // 2 x 8 halves per thread
+  static constexpr int kVec = 8;
+  static constexpr int kThreadsPerRow = BN / kVec;                // 16
+  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 16
+};
+
+// Staging of a B tile given N x K (B^T[n][k], rows along K): 128 rows of 32
+// elements, the same shape as an A tile.
+template <typename BT>
+struct BtLoad;
+template <>
+struct BtLoad<float> {
+  static constexpr int kLoads = 4;
+  static constexpr int kVec = 4;
+  static constexpr int kThreadsPerRow = BK / kVec;                // 8
+  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 32
+};
+template <>
+struct BtLoad<_Float16> {
   static constexpr int kLoads = 2;
   static constexpr int kVec = 8;
-  static constexpr int kThreadsPerRow = BN / kVec;          // 16
-  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 16
+  static constexpr int kThreadsPerRow = BK / kVec;                // 4
+  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 64
 };
 
 // Workgroup id -> (tile_m, tile_n). Workgroups are handed to XCDs round-robin,
@@ -80,13 +100,16 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
   tn = in_group / gm;
 }
 
-template <typename BT, bool VA, bool VB, bool RMS>
+// BNK: B is given as B^T, row-major [N x K]; its tile is staged like an A
+// tile (n rows, k contiguous) and its fragments are read like A's.
+template <typename BT, bool BNK, bool VA, bool VB, bool RMS>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C,
     const float* __restrict__ gamma, int M, int N, int K, float eps, int tiles_m, int tiles_n) {
-  using BL = BLoad<BT>;
+  using BL = typename std::conditional<BNK, BtLoad<BT>, BLoad<BT>>::type;
+  constexpr int kBTile = BNK ? BN * AS : BK * BS;
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
-  __shared__ __attribute__((aligned(16))) float Bs[2][BK * BS];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kBTile];
   __shared__ float row_scale[RMS ? BM : 1];
 
   const int t = threadIdx.x;
@@ -135,10 +158,35 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   auto load_b = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < BL::kLoads; ++i) {
-      const int krow = k0 + b_row + BL::kRowsPerLoad * i;
-      const int nc = n0 + b_col;
 #pragma unroll
       for (int e = 0; e < BL::kVec; ++e) rb[i][e] = 0.0f;
+      if constexpr (BNK) {
+        const int n = n0 + b_row + BL::kRowsPerLoad * i;
+        const int kc = k0 + b_col;
+        if (n < N) {
+          const BT* src = B + static_cast<long long>(n) * K + kc;
+          if constexpr (VB) {
+            if (kc < K) {
+              if constexpr (BL::kVec == 4) {
+                const floatx4 v = *reinterpret_cast<const floatx4*>(src);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) rb[i][e] = v[e];
+              } else {
+                const halfx8 v = *reinterpret_cast<const halfx8*>(src);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) rb[i][e] = static_cast<float>(v[e]);
+              }
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < BL::kVec; ++e)
+              if (kc + e < K) rb[i][e] = static_cast<float>(src[e]);
+          }
+        }
+        continue;
+      }
+      const int krow = k0 + b_row + BL::kRowsPerLoad * i;
+      const int nc = n0 + b_col;
       if (krow < K) {
         const BT* src = B + static_cast<long long>(krow) * N + nc;
         if constexpr (VB) {
@@ -178,7 +226,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     }
 #pragma unroll
     for (int i = 0; i < BL::kLoads; ++i) {
-      float* dst = &Bs[buf][(b_row + BL::kRowsPerLoad * i) * BS + b_col];
+      float* dst = &Bs[buf][(b_row + BL::kRowsPerLoad * i) * (BNK ? AS : BS) + b_col];
 #pragma unroll
       for (int e = 0; e < BL::kVec; e += 4) {
         const floatx4 v = {rb[i][e], rb[i][e + 1], rb[i][e + 2], rb[i][e + 3]};
@@ -219,9 +267,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     float bf[2][16];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const float* src = &Bs[cur][(lg * 16) * BS + wn * 64 + nb * 32 + li];
+      if constexpr (BNK) {
+        const float* src = &Bs[cur][(wn * 64 + nb * 32 + li) * AS + lg * 16];
 #pragma unroll
-      for (int s = 0; s < 16; ++s) bf[nb][s] = src[s * BS];
+        for (int q = 0; q < 4; ++q) {
+          const floatx4 v = *reinterpret_cast<const floatx4*>(src + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[nb][4 * q + e] = v[e];
+        }
+      } else {
+        const float* src = &Bs[cur][(lg * 16) * BS + wn * 64 + nb * 32 + li];
+#pragma unroll
+        for (int s = 0; s < 16; ++s) bf[nb][s] = src[s * BS];
+      }
     }
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -270,11 +328,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 }
 
-template <typename BT, bool RMS>
+template <typename BT, bool BNK, bool RMS>
 void run_gemm(const GemmArgs& a, hipStream_t stream) {
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
   const bool va = (a.K % 4 == 0) && aligned_to(a.A, 16);
-  const bool vb = (a.N % kBVec == 0) && aligned_to(a.B, 16);
+  // B rows run along N ([K x N]) or along K ([N x K]).
+  const bool vb = ((BNK ? a.K : a.N) % kBVec == 0) && aligned_to(a.B, 16);
   const int M = static_cast<int>(a.M);
   const int N = static_cast<int>(a.N);
   const int K = static_cast<int>(a.K);
@@ -285,7 +344,7 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
 #define ENG_GEMM_LAUNCH(VA_, VB_)                                                       \
-  gemm_f32_mfma_kernel<BT, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(               \
+  gemm_f32_mfma_kernel<BT, BNK, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(          \
       a.A, B, a.C, a.gamma, M, N, K, a.eps, tiles_m, tiles_n)
   if (va && vb) {
     ENG_GEMM_LAUNCH(true, true);
@@ -300,22 +359,31 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
+template <typename BT, bool BNK>
+void run_gemm_rms(const GemmArgs& a, hipStream_t stream) {
+  if (a.rms) {
+    run_gemm<BT, BNK, true>(a, stream);
+  } else {
+    run_gemm<BT, BNK, false>(a, stream);
+  }
+}
+
 }  // namespace
 
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_CHECK(a.M <= 0x7fffffffLL && a.N <= 0x7fffffffLL && a.K <= 0x7fffffffLL,
             "matmul: dimensions must fit in 31 bits");
   if (a.b == Elem::F32) {
-    if (a.rms) {
-      run_gemm<float, true>(a, stream);
+    if (a.b_nk) {
+      run_gemm_rms<float, true>(a, stream);
     } else {
-      run_gemm<float, false>(a, stream);
+      run_gemm_rms<float, false>(a, stream);
     }
   } else {
-    if (a.rms) {
-      run_gemm<_Float16, true>(a, stream);
+    if (a.b_nk) {
+      run_gemm_rms<_Float16, true>(a, stream);
     } else {
-      run_gemm<_Float16, false>(a, stream);
+      run_gemm_rms<_Float16, false>(a, stream);
     }
   }
 }

@@ -1,0 +1,318 @@
+// gemv_kernels.hpp -- device code of the decode GEMV family (out[N] = x[K] . W[K x N]).
+//
+// Workgroup -> work mapping (W row-major [K x N], rows contiguous along N):
+//   * a workgroup owns a column slab of CW = LPR * VEC columns and a range of
+//     rows: all K rows (direct mode), or one of `nsplit` row chunks (partial
+//     mode, for shapes with too few slabs to fill the GPU);
+//   * inside a wave, LPR lanes cover one row segment with 16-byte loads (VEC
+//     elements each) and the 64 / LPR lane groups take consecutive rows, so a
+//     wave load instruction reads 64 / LPR rows x 16 * LPR bytes; the WAVES
+//     waves take the following rows and the loop keeps U loads per lane in
+//     flight;
+//   * workgroups are handed to the 8 XCDs round-robin; the id -> slab map is
+//     renumbered so each XCD walks a contiguous band of slabs, and slabs narrower
+//     than a 128-byte line share their lines inside one XCD's L2.
+// Sums are folded across lane groups with cross-lane shuffles and across waves
+// through LDS, always in the same order. Partial mode writes fp32 partial
+// sums (and per-chunk sums of squares) that gemv_reduce_kernel combines in
+// chunk order, so results never depend on scheduling and no workgroup waits
+// on another.
+// RMSNorm fusion: sum_k (x_k s g_k) W_kn = s * sum_k (x_k g_k) W_kn with the
+// row scale s = 1/sqrt(mean(x^2) + eps): the kernel streams W against x * g,
+// sums x^2 over the rows it reads anyway, and applies s last.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace eng {
+namespace gemv {
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return static_cast<float>(v);
+}
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) {
+  return static_cast<T>(v);  // float -> _Float16 rounds to nearest even
+}
+
+template <typename T, int VEC>
+struct RawVec {
+  typedef T type __attribute__((ext_vector_type(VEC)));
+};
+template <typename T>
+struct RawVec<T, 1> {
+  typedef T type;
+};
+
+template <int VEC, typename V>
+__device__ __forceinline__ float lane_elem(const V& v, int e) {
+  if constexpr (VEC == 1) {
+    return static_cast<float>(v);
+  } else {
+    return static_cast<float>(v[e]);
+  }
+}
+
+__device__ __forceinline__ float rms_scale(float sumsq, long long K, float eps) {
+  return 1.0f / sqrtf(sumsq / static_cast<float>(K) + eps);
+}
+
+// Workgroup id -> logical index so that XCD x (ids x, x + 8, ...) gets a
+// contiguous range of logical indices. A bijection on [0, total).
+__device__ __forceinline__ long long xcd_contiguous(long long wg, long long total) {
+  constexpr long long kXcds = 8;
+  const long long q = total / kXcds;
+  const long long r = total % kXcds;
+  const long long xcd = wg % kXcds;
+  return xcd * q + (xcd < r ? xcd : r) + wg / kXcds;
+}
+
+template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool NT,
+          bool RMS, bool PARTIAL>
+__global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
+    const WT* __restrict__ W, const XT* __restrict__ x, const float* __restrict__ gamma,
+    YT* __restrict__ y, long long N, long long K, long long kchunk, long long ncb,
+    float* __restrict__ part, float* __restrict__ part_ss, float eps) {
+  constexpr int RPW = 64 / LPR;       // rows per wave load
+  constexpr int STEP = WAVES * RPW;   // rows per load of all waves
+  constexpr int CW = LPR * VEC;       // columns per workgroup
+  constexpr int THREADS = WAVES * 64;
+  using V = typename RawVec<WT, VEC>::type;
+
+  __shared__ float red[WAVES][CW];
+  __shared__ float red_ss[WAVES];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int seg = lane % LPR;
+  const int rg = lane / LPR;
+
+  const long long total = static_cast<long long>(gridDim.x);
+  const long long logical = xcd_contiguous(blockIdx.x, total);
+  const long long cb = logical % ncb;
+  const long long s = logical / ncb;
+
+  const long long col0 = cb * CW + static_cast<long long>(seg) * VEC;
+  const bool col_ok = col0 < N;  // VEC > 1 implies N % VEC == 0
+  const long long row_begin = s * kchunk;
+  const long long row_end = row_begin + kchunk < K ? row_begin + kchunk : K;
+
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
+  float ss = 0.0f;
+
+  const WT* wcol = W + col0;
+  for (long long base = row_begin + wave * RPW + rg; base < row_end;
+       base += static_cast<long long>(STEP) * U) {
+    V raw[U];
+    float xv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long r = base + static_cast<long long>(u) * STEP;
+      const bool ok = r < row_end;
+      float xr = ok ? to_f32(x[r]) : 0.0f;
+      if constexpr (RMS) {
+        ss = fmaf(xr, xr, ss);
+        if (gamma != nullptr && ok) xr *= gamma[r];
+      }
+      xv[u] = xr;
+      if (ok && col_ok) {
+        const V* p = reinterpret_cast<const V*>(wcol + r * N);
+        if constexpr (NT) {
+          raw[u] = __builtin_nontemporal_load(p);
+        } else {
+          raw[u] = *p;
+        }
+      } else {
+        raw[u] = V{};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = fmaf(xv[u], lane_elem<VEC>(raw[u], e), acc[e]);
+    }
+  }
+
+  // Lanes with the same `seg` hold the same columns: fold the row groups.
+#pragma unroll
+  for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], off);
+    if constexpr (RMS) ss += __shfl_xor(ss, off);
+  }
+  if (rg == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[wave][seg * VEC + e] = acc[e];
+  }
+  if (RMS && lane == 0) red_ss[wave] = ss;
+  __syncthreads();
+
+  float wg_ss = 0.0f;
+  if constexpr (RMS) {
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) wg_ss += red_ss[w];
+  }
+  const float scale = (RMS && !PARTIAL) ? rms_scale(wg_ss, K, eps) : 1.0f;
+
+  for (int c = t; c < CW; c += THREADS) {
+    const long long col = cb * CW + c;
+    if (col < N) {
+      float v = red[0][c];
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) v += red[w][c];
+      if constexpr (PARTIAL) {
+        part[s * N + col] = v;
+      } else {
+        if constexpr (RMS) v *= scale;
+        y[col] = from_f32<YT>(v);
+      }
+    }
+  }
+  if constexpr (PARTIAL && RMS) {
+    if (cb == 0 && t == 0) part_ss[s] = wg_ss;
+  }
+}
+
+// y[col] = scale * sum_{s < nsplit} part[s][col]. A workgroup owns 64 columns;
+// its 4 waves each sum a contiguous quarter of the splits in split order (8
+// independent loads in flight per lane), and the quarters are combined as
+// ((q0 + q1) + q2) + q3, so the association is fixed for a given nsplit.
+template <typename YT, bool RMS>
+__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part,
+                                                          const float* __restrict__ part_ss,
+                                                          YT* __restrict__ y, long long N,
+                                                          long long K, int nsplit, float eps) {
+  __shared__ float quarter[4][64];
+  const int c = threadIdx.x & 63;
+  const int g = threadIdx.x >> 6;
+  const long long col = static_cast<long long>(blockIdx.x) * 64 + c;
+  const int per = (nsplit + 3) / 4;
+  const int s0 = g * per;
+  const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
+  float v = 0.0f;
+  if (col < N) {
+    int s = s0;
+    for (; s + 8 <= s1; s += 8) {
+      float t[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) t[i] = part[static_cast<long long>(s + i) * N + col];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v += t[i];
+    }
+    for (; s < s1; ++s) v += part[static_cast<long long>(s) * N + col];
+  }
+  quarter[g][c] = v;
+  __syncthreads();
+  if (g != 0 || col >= N) return;
+  float out = ((quarter[0][c] + quarter[1][c]) + quarter[2][c]) + quarter[3][c];
+  if constexpr (RMS) {
+    float tot = 0.0f;
+    for (int s = 0; s < nsplit; ++s) tot += part_ss[s];
+    out *= rms_scale(tot, K, eps);
+  }
+  y[col] = from_f32<YT>(out);
+}
+
+// Output-major weights: y[n] = sum_k W[n][k] * xs[k] with W row-major [N x K]
+// (xs = x * gamma, times the RMS row scale when RMS). Each wave owns R
+// consecutive output rows; lane l reads 16-byte pieces l, l + 64, ... of each
+// row (a wave load instruction is 1 KiB contiguous per row) together with the
+// matching x values, keeps U steps of loads in flight, and folds its lanes
+// with shuffles at the end. No partial sums leave the wave. With RMS the wave
+// also sums x^2 over the x values it reads anyway.
+template <typename WT, int VEC, int R, int U, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W,
+                                                        const float* __restrict__ x,
+                                                        const float* __restrict__ gamma,
+                                                        float* __restrict__ y, long long N,
+                                                        long long K, float eps) {
+  using V = typename RawVec<WT, VEC>::type;
+  using XV = typename RawVec<float, VEC>::type;
+  constexpr int PIECE = 64 * VEC;  // elements per wave step
+  const int lane = threadIdx.x & 63;
+  const long long wave = (static_cast<long long>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  const long long n0 = wave * R;
+  if (n0 >= N) return;
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  float ss = 0.0f;
+  const WT* rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = W + (n0 + r < N ? n0 + r : n0) * K;
+
+  for (long long k0 = static_cast<long long>(lane) * VEC; k0 < K; k0 += static_cast<long long>(PIECE) * U) {
+    V w[U][R];
+    XV xv[U];
+    XV gv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long k = k0 + static_cast<long long>(u) * PIECE;
+      const bool ok = k < K;  // VEC > 1 implies K % VEC == 0
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if constexpr (VEC == 1) {
+          w[u][r] = ok ? rows[r][k] : WT(0);
+        } else {
+          w[u][r] = ok ? *reinterpret_cast<const V*>(rows[r] + k) : V{};
+        }
+      }
+      if constexpr (VEC == 1) {
+        xv[u] = ok ? x[k] : 0.0f;
+        if constexpr (RMS) gv[u] = (ok && gamma != nullptr) ? gamma[k] : 1.0f;
+      } else {
+        xv[u] = ok ? *reinterpret_cast<const XV*>(x + k) : XV{};
+        if constexpr (RMS) {
+          if (gamma != nullptr && ok) {
+            gv[u] = *reinterpret_cast<const XV*>(gamma + k);
+          } else {
+            gv[u] = XV{} + 1.0f;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float xe;
+        float ge = 1.0f;
+        if constexpr (VEC == 1) {
+          xe = xv[u];
+          if constexpr (RMS) ge = gv[u];
+        } else {
+          xe = xv[u][e];
+          if constexpr (RMS) ge = gv[u][e];
+        }
+        if constexpr (RMS) {
+          ss = fmaf(xe, xe, ss);
+          xe *= ge;
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = fmaf(xe, lane_elem<VEC>(w[u][r], e), acc[r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += __shfl_xor(acc[r], off);
+    if constexpr (RMS) ss += __shfl_xor(ss, off);
+  }
+  if (lane == 0) {
+    const float scale = RMS ? rms_scale(ss, K, eps) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (n0 + r < N) y[n0 + r] = RMS ? acc[r] * scale : acc[r];
+    }
+  }
+}
+
+}  // namespace gemv
+}  // namespace eng

@@ -11,11 +11,13 @@ namespace eng {
 
 enum class Elem { F32, F16 };
 
-// out[N] = sum_k xs_k * W[k][n]  with  xs_k = x_k * gamma_k (gamma optional);
+// out[N] = sum_k xs_k * W[k][n]  with  xs_k = x_k * gamma_k (gamma optional)
+// (or sum_k W[n][k] xs_k when w_nk);
 // with rms, out is further multiplied by 1/sqrt(sum_k x_k^2 / K + eps).
 struct GemvArgs {
   const void* W = nullptr;
   Elem w = Elem::F32;
+  bool w_nk = false;  // W stored output-major [N x K]: y = W . x
   const void* x = nullptr;
   Elem x_elem = Elem::F32;
   const float* gamma = nullptr;
@@ -35,6 +37,7 @@ struct GemmArgs {
   const float* A = nullptr;
   const void* B = nullptr;
   Elem b = Elem::F32;
+  bool b_nk = false;  // B given as [N x K] (C = A . B^T)
   float* C = nullptr;
   std::int64_t M = 0;
   std::int64_t N = 0;

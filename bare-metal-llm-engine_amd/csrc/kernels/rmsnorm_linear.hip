@@ -8,14 +8,15 @@
 // GEMV with the sum of squares reduced alongside the dot products, M > 1 runs
 // the MFMA GEMM with gamma applied while A is staged and s_r applied in the
 // epilogue. Preconditions, messages and the "any zero dimension is a no-op"
-// rule are the reference's.
+// rule are the reference's. The *_nk entries take W output-major [N x K]
+// (out = RMSNorm(in) . W^T), the layout the decode path streams best.
 #include "launch.hpp"
 
 namespace eng {
 namespace {
 
 void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W, Elem w_elem,
-                        float* out, int64_t M, int64_t N, int64_t K, float eps,
+                        bool nk, float* out, int64_t M, int64_t N, int64_t K, float eps,
                         eng_stream stream) {
   ENG_CHECK(M >= 0 && N >= 0 && K >= 0, "rmsnorm_linear: negative dimension");
   ENG_CHECK(in != nullptr && W != nullptr && out != nullptr,
@@ -27,6 +28,7 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     GemvArgs g;
     g.W = W;
     g.w = w_elem;
+    g.w_nk = nk;
     g.x = in;
     g.gamma = rms_weight;
     g.y = out;
@@ -41,6 +43,7 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
   g.A = in;
   g.B = W;
   g.b = w_elem;
+  g.b_nk = nk;
   g.C = out;
   g.M = M;
   g.N = N;
@@ -59,7 +62,7 @@ extern "C" {
 int eng_rmsnorm_linear_f32(const float* in, const float* rms_weight, const float* W, float* out,
                            int64_t M, int64_t N, int64_t K, float eps, eng_stream stream) {
   return eng::guarded([&] {
-    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, out, M, N, K, eps, stream);
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, false, out, M, N, K, eps, stream);
   });
 }
 
@@ -67,7 +70,7 @@ int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_
                             float* out, int64_t M, int64_t N, int64_t K, float eps,
                             eng_stream stream) {
   return eng::guarded([&] {
-    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F16, out, M, N, K, eps, stream);
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F16, false, out, M, N, K, eps, stream);
   });
 }
 
@@ -75,7 +78,23 @@ int eng_rmsnorm_linear_fused_direct_f32(const float* in, const float* rms_weight
                                         const float* W, float* out, int64_t M, int64_t N,
                                         int64_t K, float eps, eng_stream stream) {
   return eng::guarded([&] {
-    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, out, M, N, K, eps, stream);
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, false, out, M, N, K, eps, stream);
+  });
+}
+
+int eng_rmsnorm_linear_f16w_nk(const float* in, const float* rms_weight, const eng_half* W,
+                               float* out, int64_t M, int64_t N, int64_t K, float eps,
+                               eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F16, true, out, M, N, K, eps, stream);
+  });
+}
+
+int eng_rmsnorm_linear_f32_nk(const float* in, const float* rms_weight, const float* W,
+                              float* out, int64_t M, int64_t N, int64_t K, float eps,
+                              eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_any(in, rms_weight, W, eng::Elem::F32, true, out, M, N, K, eps, stream);
   });
 }
 

@@ -155,12 +155,14 @@ def gemm_row(name, ms, M, N, K):
             "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "flops_per_call": 2 * M * N * K}
 
 
-def bench_gemv_f16w(eng, timer, steps, warmup, rotate=32, K=4096, N=4096, seed=1):
+def bench_gemv_f16w(eng, timer, steps, warmup, rotate=32, K=4096, N=4096, seed=1, nk=False):
+    """nk=False: reference layout out = x . W[K x N] (eng_gemv_f16w);
+    nk=True: y = W[N x K] . x, W row-major out x in (eng_gemv_f16w_nk)."""
     rng = np.random.default_rng(seed)
-    Ws = rotating(eng, rand_f16(rng, (K, N)), rotate)
+    Ws = rotating(eng, rand_f16(rng, (N, K) if nk else (K, N)), rotate)
     dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
     dy = eng.empty(N, np.float32)
-    fn = eng.lib.eng_gemv_f16w
+    fn = eng.lib.eng_gemv_f16w_nk if nk else eng.lib.eng_gemv_f16w
 
     def launch(i, s):
         rc = fn(Ws[i % rotate].ptr, dx.ptr, dy.ptr, N, K, s)
@@ -177,21 +179,28 @@ def secondary_rows(eng, timer) -> list:
     rows = []
     rng = np.random.default_rng(7)
 
-    # config 2 warm: the same 32 MiB matrix every call (Infinity-Cache resident).
-    ms, nb = bench_gemv_f16w(eng, timer, 400, 50, rotate=1)
-    rows.append(hbm_row("gemv_f16w 4096x4096 warm (cache-resident, not HBM)", ms, nb))
+    # config 2 in both weight layouts, cold, and warm (the same 32 MiB matrix
+    # every call: Infinity-Cache resident, not an HBM figure).
+    for nk, tag in ((False, "reference layout x.W[KxN], eng_gemv_f16w"),
+                    (True, "output-major y=W[NxK].x, eng_gemv_f16w_nk")):
+        ms, nb = bench_gemv_f16w(eng, timer, 640, 64, nk=nk)
+        rows.append(hbm_row(f"config 2 gemv fp16-W 4096x4096 cold, {tag}", ms, nb))
+        ms, nb = bench_gemv_f16w(eng, timer, 400, 50, rotate=1, nk=nk)
+        rows.append(hbm_row(f"config 2 gemv fp16-W 4096x4096 WARM (cache-resident), {tag}", ms, nb))
 
-    # config 3: fused RMSNorm + linear, fp16 W [4096 x 11008], cold (12 x 86 MiB).
+    # config 3: fused RMSNorm + linear, fp16 W, K=4096, N=11008, cold (12 x 86 MiB).
     K, N, R = 4096, 11008, 12
-    Ws = rotating(eng, rand_f16(np.random.default_rng(2), (K, N)), R)
     dx = eng.upload(np.random.default_rng(2).standard_normal(K, dtype=np.float32))
     dg = eng.upload((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
     dy = eng.empty(N, np.float32)
-    f = eng.lib.eng_rmsnorm_linear_f16w
-    ms = timer.run(lambda i, s: f(dx.ptr, dg.ptr, Ws[i % R].ptr, dy.ptr, 1, N, K, 1e-5, s), 240, 24)
-    rows.append(hbm_row("rmsnorm_linear_f16w 1x11008x4096 cold (config 3)", ms, 2 * K * N + 8 * K + 4 * N))
-    for w in Ws:
-        w.free()
+    for nk, f, tag in ((False, eng.lib.eng_rmsnorm_linear_f16w, "reference layout W[KxN]"),
+                       (True, eng.lib.eng_rmsnorm_linear_f16w_nk, "output-major W[NxK]")):
+        Ws = rotating(eng, rand_f16(np.random.default_rng(2), (N, K) if nk else (K, N)), R)
+        ms = timer.run(lambda i, s: f(dx.ptr, dg.ptr, Ws[i % R].ptr, dy.ptr, 1, N, K, 1e-5, s), 240, 24)
+        rows.append(hbm_row(f"config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, {tag}", ms,
+                            2 * K * N + 8 * K + 4 * N))
+        for w in Ws:
+            w.free()
 
     # Reference-API GEMVs: fp32 gemv and half-I/O gemv_fp16, 4096x4096, cold.
     K = N = 4096
@@ -237,12 +246,16 @@ def secondary_rows(eng, timer) -> list:
     return rows
 
 
-def bench_llama_stack(eng, timer, tokens=10, warmup=3) -> dict:
-    """Config 5: 32 layers of q,k,v,o [4096x4096], gate/up [4096x11008] via
-    rmsnorm_linear, down [11008x4096]; fp16 weights, fp32 activations."""
+def bench_llama_stack(eng, timer, tokens=10, warmup=3, nk=False) -> dict:
+    """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
+    rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
+    nk=False stores every weight [in x out] (reference layout), nk=True [out x in]."""
     H, F, L = 4096, 11008, 32
     rng = np.random.default_rng(4)
-    sq, gu, dn = rand_f16(rng, (H, H)), rand_f16(rng, (H, F)), rand_f16(rng, (F, H))
+    if nk:
+        sq, gu, dn = rand_f16(rng, (H, H)), rand_f16(rng, (F, H)), rand_f16(rng, (H, F))
+    else:
+        sq, gu, dn = rand_f16(rng, (H, H)), rand_f16(rng, (H, F)), rand_f16(rng, (F, H))
     src = {"sq": eng.upload(sq), "gu": eng.upload(gu), "dn": eng.upload(dn)}
     layers = []
     for _ in range(L):
@@ -259,7 +272,10 @@ def bench_llama_stack(eng, timer, tokens=10, warmup=3) -> dict:
     g = eng.upload((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
     q, k, v, o = (eng.empty(H, np.float32) for _ in range(4))
     gate, up = eng.empty(F, np.float32), eng.empty(F, np.float32)
-    gv, rl = eng.lib.eng_gemv_f16w, eng.lib.eng_rmsnorm_linear_f16w
+    if nk:
+        gv, rl = eng.lib.eng_gemv_f16w_nk, eng.lib.eng_rmsnorm_linear_f16w_nk
+    else:
+        gv, rl = eng.lib.eng_gemv_f16w, eng.lib.eng_rmsnorm_linear_f16w
 
     def token(_i, s):
         for lay in layers:
@@ -279,7 +295,9 @@ def bench_llama_stack(eng, timer, tokens=10, warmup=3) -> dict:
     for lay in layers:
         for d in lay.values():
             d.free()
-    row = hbm_row("llama7b-shape decode linear stack, 32 layers, per token (config 5)", ms, wbytes + abytes)
+    layout = "output-major W[out x in]" if nk else "reference layout W[in x out]"
+    row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
+                  ms, wbytes + abytes)
     row["launches_per_token"] = 7 * L
     row["host_ms_per_token"] = round(host_ms, 3)
     return row
@@ -320,7 +338,8 @@ def main() -> int:
     secondary = []
     if not args.quick:
         secondary = secondary_rows(eng, timer)
-        secondary.append(bench_llama_stack(eng, timer))
+        secondary.append(bench_llama_stack(eng, timer, nk=False))
+        secondary.append(bench_llama_stack(eng, timer, nk=True))
         for r in secondary:
             log(json.dumps(r))
 

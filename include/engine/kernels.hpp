@@ -90,6 +90,29 @@ inline void gemv_fp16(const half* A, const float* x, float* out, std::int64_t N,
   ENGINE_ABI_CHECK(eng_gemv_f16w(detail::bits(A), x, out, N, K, stream));
 }
 
+/// Output-major weights (additive; no reference counterpart): y[N] = W[N x K] * x[K].
+inline void gemv_nk(const half* W, const float* x, float* y, std::int64_t N, std::int64_t K,
+                    hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_gemv_f16w_nk(detail::bits(W), x, y, N, K, stream));
+}
+inline void gemv_nk(const float* W, const float* x, float* y, std::int64_t N, std::int64_t K,
+                    hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_gemv_f32_nk(W, x, y, N, K, stream));
+}
+
+/// Output-major weights: out[M x N] = RMSNorm(in[M x K], rms_weight, eps) * W[N x K]^T.
+inline void rmsnorm_linear_nk(const float* in, const float* rms_weight, const half* W, float* out,
+                              std::int64_t M, std::int64_t N, std::int64_t K, float eps,
+                              hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_rmsnorm_linear_f16w_nk(in, rms_weight, detail::bits(W), out, M, N, K, eps, stream));
+}
+inline void rmsnorm_linear_nk(const float* in, const float* rms_weight, const float* W, float* out,
+                              std::int64_t M, std::int64_t N, std::int64_t K, float eps,
+                              hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_rmsnorm_linear_f32_nk(in, rms_weight, W, out, M, N, K, eps, stream));
+}
+
 }  // namespace hip
 
 // Call sites written against the reference use engine::cuda::...

@@ -217,6 +217,26 @@ int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_
                             float* out, int64_t M, int64_t N, int64_t K, float eps,
                             eng_stream stream);
 
+/* Output-major weights (no reference counterpart; additive). W is row-major
+ * [N x K] -- one contiguous row of K weights per output, the layout of the
+ * decode configurations "y = W.x, W [out x in]" -- and
+ *   y[N] = W[N x K] . x[K]                                 (eng_gemv_*_nk)
+ *   out[M x N] = RMSNorm(in[M x K], rms_weight, eps) . W^T  (eng_rmsnorm_linear_*_nk)
+ * Same preconditions, messages and zero-size rules as the reference-layout
+ * functions above (K == 0: the GEMVs zero-fill, rmsnorm_linear writes nothing).
+ * Each output row is one contiguous stream, so M == 1 needs no split-K
+ * reduction; M > 1 runs the FP32 MFMA GEMM with B read as B^T. */
+int eng_gemv_f16w_nk(const eng_half* W, const float* x, float* y, int64_t N, int64_t K,
+                     eng_stream stream);
+int eng_gemv_f32_nk(const float* W, const float* x, float* y, int64_t N, int64_t K,
+                    eng_stream stream);
+int eng_rmsnorm_linear_f16w_nk(const float* in, const float* rms_weight, const eng_half* W,
+                               float* out, int64_t M, int64_t N, int64_t K, float eps,
+                               eng_stream stream);
+int eng_rmsnorm_linear_f32_nk(const float* in, const float* rms_weight, const float* W,
+                              float* out, int64_t M, int64_t N, int64_t K, float eps,
+                              eng_stream stream);
+
 /* Replaces engine::cuda::rmsnorm_linear_fused_direct
  * (reference include/engine/kernels.hpp:101-104, kernels/rmsnorm_linear.cu:143-171),
  * the benchmarking entry that forces the fused kernel for every M. Here every

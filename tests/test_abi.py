@@ -72,6 +72,12 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_rmsnorm_linear_f16w", P, P, P, P, 4, 4, -1, 1e-5, None), 1, "negative"),
     (("eng_rmsnorm_linear_f16w", P, P, P, P, 4, 4, 4, -1.0, None), 1, "eps must be non-negative"),
     (("eng_rmsnorm_linear_fused_direct_f32", P, P, P, P, 4, 4, 4, float("nan"), None), 1, "eps"),
+    (("eng_gemv_f16w_nk", None, P, P, 4, 4, None), 1, "A is null"),
+    (("eng_gemv_f16w_nk", P, P, P, 4, -1, None), 1, "non-negative"),
+    (("eng_gemv_f32_nk", P, None, P, 4, 4, None), 1, "x is null"),
+    (("eng_rmsnorm_linear_f16w_nk", P, P, None, P, 2, 2, 2, 1e-5, None), 1, "null device pointer"),
+    (("eng_rmsnorm_linear_f32_nk", P, P, P, P, 2, -2, 2, 1e-5, None), 1, "negative dimension"),
+    (("eng_rmsnorm_linear_f32_nk", P, P, P, P, 2, 2, 2, -1e-5, None), 1, "eps"),
 ])
 def test_preconditions_fail_before_launch(eng, call, code, substr):
     name, *args = call
@@ -94,6 +100,9 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_rmsnorm_linear_f32", P, None, P, P, 8, 0, 8, 1e-5, None),
     ("eng_rmsnorm_linear_f32", P, P, P, P, 8, 8, 0, 1e-5, None),
     ("eng_rmsnorm_linear_f16w", P, P, P, P, 8, 8, 0, 1e-5, None),
+    ("eng_gemv_f16w_nk", P, P, P, 0, 8, None),
+    ("eng_rmsnorm_linear_f16w_nk", P, P, P, P, 8, 0, 8, 1e-5, None),
+    ("eng_rmsnorm_linear_f32_nk", P, P, P, P, 0, 8, 8, 1e-5, None),
 ])
 def test_empty_work_is_a_no_op(eng, call):
     name, *args = call

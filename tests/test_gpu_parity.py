@@ -354,3 +354,134 @@ def test_split_k_workspace_survives_shape_changes_and_streams(gpu, orc):
     finally:
         for s in streams:
             s.destroy()
+
+
+# ------------------------------------------------- output-major ([N x K]) path
+def gpu_gemv_nk(eng, W, x):
+    N, K = W.shape
+    dW, dx, dy = eng.upload(W), eng.upload(x), eng.empty(N, np.float32)
+    fn = "eng_gemv_f16w_nk" if W.dtype == np.uint16 else "eng_gemv_f32_nk"
+    eng.call(fn, dW.ptr, dx.ptr, dy.ptr, N, K, None)
+    eng.sync()
+    return dy.download()
+
+
+def gpu_rmsnorm_linear_nk(eng, x, g, W):
+    M, K = x.shape
+    N = W.shape[0]
+    fn = "eng_rmsnorm_linear_f16w_nk" if W.dtype == np.uint16 else "eng_rmsnorm_linear_f32_nk"
+    dx, dW, dy = eng.upload(x), eng.upload(W), eng.empty((M, N), np.float32)
+    dg = eng.upload(g) if g is not None else None
+    eng.call(fn, dx.ptr, dg.ptr if dg else None, dW.ptr, dy.ptr, M, N, K, EPS, None)
+    eng.sync()
+    return dy.download()
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("gemv_f16w")])
+def test_gemv_f16w_nk_matches_golden(gpu, stem):
+    """The golden's A is [K x N]; its transpose is the output-major W."""
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    W = np.ascontiguousarray(x["A"].T)
+    got = gpu_gemv_nk(gpu, W, x["x"])
+    y = helpers.expected(c)
+    check_dot(got, y, helpers.absdot(x["x"], x["A"]) + np.abs(y), c["params"]["K"], stem + " (nk)")
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm_linear_f16w")
+                                  + helpers.cases("rmsnorm_linear")])
+def test_rmsnorm_linear_nk_matches_golden(gpu, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    W = np.ascontiguousarray(x["W"].T)
+    got = gpu_rmsnorm_linear_nk(gpu, x["input"], x.get("weight"), W)
+    y = helpers.expected(c)
+    check_rmsnorm_linear(got, y, x["input"], x.get("weight"), x["W"], c["params"]["K"], stem + " (nk)")
+
+
+def test_config2_gemv_f16w_nk_4096(gpu, orc):
+    """BASELINE config 2 as written: y = W.x, W [4096 x 4096] fp16 row-major."""
+    rng = np.random.default_rng(1)
+    N = K = 4096
+    W = (0.02 * rng.standard_normal((N, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(K, dtype=np.float32)
+    got = gpu_gemv_nk(gpu, W, x)
+    Wt = np.ascontiguousarray(W.T)
+    y = orc.gemv_f16w(Wt, x).astype(np.float64)
+    check_dot(got, y, helpers.absdot(x, Wt) + np.abs(y), K, "config 2 nk")
+
+
+def test_config3_rmsnorm_linear_f16w_nk(gpu, orc):
+    """BASELINE config 3 as written: W [11008 x 4096] fp16 row-major."""
+    rng = np.random.default_rng(2)
+    N, K = 11008, 4096
+    x = rng.standard_normal((1, K), dtype=np.float32)
+    g = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((N, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
+    Wt = np.ascontiguousarray(W.T)
+    y = orc.rmsnorm_linear(x, g, Wt, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, Wt, K, "config 3 nk")
+
+
+@pytest.mark.parametrize("N,K,dtype", [(4096, 11008, "f16"), (7, 13, "f16"), (33, 1000, "f32"),
+                                       (4097, 4096, "f16"), (1, 8, "f16"), (300, 4100, "f32")])
+def test_gemv_nk_shapes_against_oracle(gpu, orc, N, K, dtype):
+    rng = np.random.default_rng(N + 3 * K)
+    Wf = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    x = rng.standard_normal(K, dtype=np.float32)
+    W = orc.f32_to_f16(Wf) if dtype == "f16" else Wf
+    got = gpu_gemv_nk(gpu, W, x)
+    Wt = np.ascontiguousarray(W.T)
+    y = (orc.gemv_f16w(Wt, x) if dtype == "f16" else orc.gemv(Wt, x)).astype(np.float64)
+    check_dot(got, y, helpers.absdot(x, Wt) + np.abs(y), K, f"gemv nk {N}x{K} {dtype}")
+
+
+def test_gemv_nk_misaligned_x_takes_scalar_path(gpu, orc):
+    rng = np.random.default_rng(21)
+    N, K = 256, 2048
+    W = orc.f32_to_f16(rng.standard_normal((N, K), dtype=np.float32) / 45)
+    x = rng.standard_normal(K, dtype=np.float32)
+    dW = gpu.upload(W)
+    dxb = gpu.upload(np.concatenate([[0.0], x]).astype(np.float32))
+    dy = gpu.empty(N, np.float32)
+    gpu.call("eng_gemv_f16w_nk", dW.ptr, dxb.ptr + 4, dy.ptr, N, K, None)
+    gpu.sync()
+    Wt = np.ascontiguousarray(W.T)
+    y = orc.gemv_f16w(Wt, x).astype(np.float64)
+    check_dot(dy.download(), y, helpers.absdot(x, Wt) + np.abs(y), K, "misaligned x nk")
+
+
+@pytest.mark.parametrize("M,N,K,dtype", [(32, 256, 512, "f16"), (17, 127, 31, "f32"), (512, 4096, 4096, "f16"),
+                                         (130, 300, 200, "f32"), (3, 11008, 4096, "f16")])
+def test_rmsnorm_linear_nk_prefill_against_oracle(gpu, orc, M, N, K, dtype):
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Wf = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    W = orc.f32_to_f16(Wf) if dtype == "f16" else Wf
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
+    Wt = np.ascontiguousarray(W.T)
+    rows = np.unique(np.linspace(0, M - 1, min(M, 8)).astype(int))
+    y = orc.rmsnorm_linear(x[rows], g, Wt, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, Wt, K, f"rmsnorm_linear nk {M}x{N}x{K} {dtype}")
+
+
+def test_nk_k_zero_contract(gpu):
+    d1 = gpu.upload(np.zeros(4, np.float32))
+    dy = gpu.upload(np.full(12, 7.0, np.float32))
+    gpu.call("eng_gemv_f16w_nk", d1.ptr, d1.ptr, dy.ptr, 12, 0, None)
+    gpu.sync()
+    assert np.all(dy.download() == 0.0)
+    dy = gpu.upload(np.full(12, 7.0, np.float32))
+    gpu.call("eng_rmsnorm_linear_f16w_nk", d1.ptr, None, d1.ptr, dy.ptr, 4, 3, 0, EPS, None)
+    gpu.sync()
+    assert np.all(dy.download() == 7.0)
+
+
+def test_nk_results_are_deterministic(gpu):
+    rng = np.random.default_rng(22)
+    W = (0.02 * rng.standard_normal((11008, 4096), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((1, 4096), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(4096)).astype(np.float32)
+    assert np.array_equal(gpu_rmsnorm_linear_nk(gpu, x, g, W), gpu_rmsnorm_linear_nk(gpu, x, g, W))
