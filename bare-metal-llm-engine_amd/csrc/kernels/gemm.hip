@@ -8,20 +8,24 @@
 // scale multiplies the accumulators in the epilogue.
 //
 // Tiling for wave64 and v_mfma_f32_32x32x2_f32:
-//   * workgroup tile 128 x 128, K step 32, 256 threads = 4 waves in 2 x 2;
-//   * each wave owns 64 x 64 = 2 x 2 MFMA blocks of 32 x 32 (64 fp32
-//     accumulators per lane);
+//   * workgroup tile BM x BN (128 x 128, 128 x 64 or 64 x 64), K step 32,
+//     256 threads = 4 waves in 2 x 2, each wave owning (BM/2) x (BN/2) as
+//     32 x 32 MFMA blocks;
 //   * operand layout of the instruction: lane l supplies A[l % 32][k] and
 //     B[k][l % 32] with k = l / 32 of the pair; accumulator v of lane l is
 //     C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32]. Within a 32-deep K tile the
 //     instruction at step s pairs k = s (lanes 0-31) with k = 16 + s (lanes
 //     32-63), so each lane reads a contiguous 16-float run of its A row
-//     (ds_read_b128) and a 16-row column of B (ds_read_b32, conflict-free);
+//     (ds_read_b128) and a 16-row column of B (ds_read_b32, conflict-free) --
+//     or, when B is given transposed ([N x K]), a 16-float run of its B row;
 //   * A and B tiles are double-buffered in LDS with 4-float row padding; the
 //     next tile's global loads are issued before the current tile's MFMAs;
 //   * the workgroup -> tile map is XCD-aware: consecutive workgroup ids go to
 //     different XCDs, so ids are regrouped so each XCD works on a contiguous
-//     band of tiles (grouped 8 tile-rows deep) and shares A/B panels in its L2.
+//     band of tiles (grouped 8 tile-rows deep) and shares A/B panels in its L2;
+//   * the tile shape is chosen per call so the grid covers the 256 CUs evenly
+//     (small-M shapes such as 512 x 4096 x 11008 would leave half the CUs idle
+//     with 128 x 128 tiles).
 #include "launch.hpp"
 
 #include <algorithm>
@@ -34,51 +38,22 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
-constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 32;
 constexpr int kThreads = 256;
-constexpr int AS = BK + 4;   // A tile row stride in LDS (floats)
-constexpr int BS = BN + 4;   // B tile row stride in LDS (floats)
+constexpr int AS = BK + 4;   // row stride (floats) of k-contiguous tiles in LDS
 constexpr int kGroupM = 8;   // tile-rows per raster group
 constexpr int kXcds = 8;
 
-// Global -> register staging of a B tile, K x N layout (B[k][n], rows along N):
-// 32 rows of 128 elements.
-template <typename BT>
-struct BLoad;
-template <>
-struct BLoad<float> {
-  static constexpr int kLoads = 4;   // 4 x float4 per thread
-  static constexpr int kVec = 4;
-  static constexpr int kThreadsPerRow = BN / kVec;                // 32
-  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 8
-};
-template <>
-struct BLoad<_Float16> {
-  static constexpr int kLoads = 2;   // 2 x 8 halves per thread
-  static constexpr int kVec = 8;
-  static constexpr int kThreadsPerRow = BN / kVec;                // 16
-  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 16
-};
-
-// Staging of a B tile given N x K (B^T[n][k], rows along K): 128 rows of 32
-// elements, the same shape as an A tile.
-template <typename BT>
-struct BtLoad;
-template <>
-struct BtLoad<float> {
-  static constexpr int kLoads = 4;
-  static constexpr int kVec = 4;
-  static constexpr int kThreadsPerRow = BK / kVec;                // 8
-  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 32
-};
-template <>
-struct BtLoad<_Float16> {
-  static constexpr int kLoads = 2;
-  static constexpr int kVec = 8;
-  static constexpr int kThreadsPerRow = BK / kVec;                // 4
-  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;  // 64
+// Global -> register staging of a B tile: 16-byte vectors, `kLoads` per thread.
+// K x N layout: BK rows of BN elements; N x K layout: BN rows of BK elements.
+template <typename BT, bool BNK, int BN>
+struct BStage {
+  static constexpr int kVec = 16 / static_cast<int>(sizeof(BT));
+  static constexpr int kRowLen = BNK ? BK : BN;
+  static constexpr int kThreadsPerRow = kRowLen / kVec;
+  static constexpr int kRowsPerLoad = kThreads / kThreadsPerRow;
+  static constexpr int kLoads = (BNK ? BN : BK) / kRowsPerLoad;
+  static_assert(kLoads >= 1 && kLoads * kRowsPerLoad == (BNK ? BN : BK), "B staging shape");
 };
 
 // Workgroup id -> (tile_m, tile_n). Workgroups are handed to XCDs round-robin,
@@ -102,12 +77,18 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
 
 // BNK: B is given as B^T, row-major [N x K]; its tile is staged like an A
 // tile (n rows, k contiguous) and its fragments are read like A's.
-template <typename BT, bool BNK, bool VA, bool VB, bool RMS>
+template <int BM, int BN, typename BT, bool BNK, bool VA, bool VB, bool RMS>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C,
     const float* __restrict__ gamma, int M, int N, int K, float eps, int tiles_m, int tiles_n) {
-  using BL = typename std::conditional<BNK, BtLoad<BT>, BLoad<BT>>::type;
-  constexpr int kBTile = BNK ? BN * AS : BK * BS;
+  using BL = BStage<BT, BNK, BN>;
+  constexpr int WM = BM / 2;       // rows per wave
+  constexpr int WN = BN / 2;       // columns per wave
+  constexpr int MB = WM / 32;      // MFMA blocks per wave, along M
+  constexpr int NB = WN / 32;      // ... along N
+  constexpr int A_LOADS = BM / 32; // float4 A loads per thread per K tile
+  constexpr int BSK = BN + 4;      // row stride of a K x N B tile
+  constexpr int kBTile = BNK ? BN * AS : BK * BSK;
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][kBTile];
   __shared__ float row_scale[RMS ? BM : 1];
@@ -131,13 +112,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   const int b_row = t / BL::kThreadsPerRow;            // + kRowsPerLoad * i
   const int b_col = (t % BL::kThreadsPerRow) * BL::kVec;
 
-  floatx4 ra[4];
+  floatx4 ra[A_LOADS];
   float rb[BL::kLoads][BL::kVec];
-  float ss[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float ss[A_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i) ss[i] = 0.0f;
 
   auto load_a = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < A_LOADS; ++i) {
       const int row = m0 + a_row + 32 * i;
       const int kc = k0 + a_col;
       floatx4 v = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -160,37 +143,15 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     for (int i = 0; i < BL::kLoads; ++i) {
 #pragma unroll
       for (int e = 0; e < BL::kVec; ++e) rb[i][e] = 0.0f;
-      if constexpr (BNK) {
-        const int n = n0 + b_row + BL::kRowsPerLoad * i;
-        const int kc = k0 + b_col;
-        if (n < N) {
-          const BT* src = B + static_cast<long long>(n) * K + kc;
-          if constexpr (VB) {
-            if (kc < K) {
-              if constexpr (BL::kVec == 4) {
-                const floatx4 v = *reinterpret_cast<const floatx4*>(src);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) rb[i][e] = v[e];
-              } else {
-                const halfx8 v = *reinterpret_cast<const halfx8*>(src);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) rb[i][e] = static_cast<float>(v[e]);
-              }
-            }
-          } else {
-#pragma unroll
-            for (int e = 0; e < BL::kVec; ++e)
-              if (kc + e < K) rb[i][e] = static_cast<float>(src[e]);
-          }
-        }
-        continue;
-      }
-      const int krow = k0 + b_row + BL::kRowsPerLoad * i;
-      const int nc = n0 + b_col;
-      if (krow < K) {
-        const BT* src = B + static_cast<long long>(krow) * N + nc;
+      // (r, c): row and first column of this thread's vector in B's storage.
+      const int r = (BNK ? n0 : k0) + b_row + BL::kRowsPerLoad * i;
+      const int c = (BNK ? k0 : n0) + b_col;
+      const int rows = BNK ? N : K;
+      const int cols = BNK ? K : N;
+      if (r < rows) {
+        const BT* src = B + static_cast<long long>(r) * cols + c;
         if constexpr (VB) {
-          if (nc < N) {
+          if (c < cols) {
             if constexpr (BL::kVec == 4) {
               const floatx4 v = *reinterpret_cast<const floatx4*>(src);
 #pragma unroll
@@ -204,29 +165,38 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
         } else {
 #pragma unroll
           for (int e = 0; e < BL::kVec; ++e)
-            if (nc + e < N) rb[i][e] = static_cast<float>(src[e]);
+            if (c + e < cols) rb[i][e] = static_cast<float>(src[e]);
         }
       }
     }
   };
 
   auto store_tiles = [&](int buf, int k0) {
+    floatx4 g = {1.0f, 1.0f, 1.0f, 1.0f};
+    if constexpr (RMS) {
+      if (gamma != nullptr) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+        for (int e = 0; e < 4; ++e) {
+          const int k = k0 + a_col + e;
+          g[e] = k < K ? gamma[k] : 0.0f;
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
       floatx4 v = ra[i];
       if constexpr (RMS) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           ss[i] = fmaf(v[e], v[e], ss[i]);
-          const int k = k0 + a_col + e;
-          if (gamma != nullptr && k < K) v[e] *= gamma[k];
+          v[e] *= g[e];
         }
       }
       *reinterpret_cast<floatx4*>(&As[buf][(a_row + 32 * i) * AS + a_col]) = v;
     }
 #pragma unroll
     for (int i = 0; i < BL::kLoads; ++i) {
-      float* dst = &Bs[buf][(b_row + BL::kRowsPerLoad * i) * (BNK ? AS : BS) + b_col];
+      float* dst = &Bs[buf][(b_row + BL::kRowsPerLoad * i) * (BNK ? AS : BSK) + b_col];
 #pragma unroll
       for (int e = 0; e < BL::kVec; e += 4) {
         const floatx4 v = {rb[i][e], rb[i][e + 1], rb[i][e + 2], rb[i][e + 3]};
@@ -235,11 +205,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     }
   };
 
-  floatx16 acc[2][2];
+  floatx16 acc[MB][NB];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
 
@@ -257,18 +227,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     }
 
     // This wave's operand fragments for the whole 32-deep tile.
-    floatx4 af[2][4];
+    floatx4 af[MB][4];
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const float* src = &As[cur][(wm * 64 + mb * 32 + li) * AS + lg * 16];
+    for (int mb = 0; mb < MB; ++mb) {
+      const float* src = &As[cur][(wm * WM + mb * 32 + li) * AS + lg * 16];
 #pragma unroll
       for (int q = 0; q < 4; ++q) af[mb][q] = *reinterpret_cast<const floatx4*>(src + 4 * q);
     }
-    float bf[2][16];
+    float bf[NB][16];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       if constexpr (BNK) {
-        const float* src = &Bs[cur][(wn * 64 + nb * 32 + li) * AS + lg * 16];
+        const float* src = &Bs[cur][(wn * WN + nb * 32 + li) * AS + lg * 16];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const floatx4 v = *reinterpret_cast<const floatx4*>(src + 4 * q);
@@ -276,18 +246,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
           for (int e = 0; e < 4; ++e) bf[nb][4 * q + e] = v[e];
         }
       } else {
-        const float* src = &Bs[cur][(lg * 16) * BS + wn * 64 + nb * 32 + li];
+        const float* src = &Bs[cur][(lg * 16) * BSK + wn * WN + nb * 32 + li];
 #pragma unroll
-        for (int s = 0; s < 16; ++s) bf[nb][s] = src[s * BS];
+        for (int s = 0; s < 16; ++s) bf[nb][s] = src[s * BSK];
       }
     }
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         const float a = af[mb][s >> 2][s & 3];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
+        for (int nb = 0; nb < NB; ++nb)
           acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bf[nb][s], acc[mb][nb], 0, 0, 0);
       }
     }
@@ -299,7 +269,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   if constexpr (RMS) {
     // The 8 lanes t..t+7 staged the same A row: fold their sums of squares.
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < A_LOADS; ++i) {
       float v = ss[i];
       v += __shfl_xor(v, 1);
       v += __shfl_xor(v, 2);
@@ -310,13 +280,13 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb) {
+  for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int col = n0 + wn * 64 + nb * 32 + li;
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = n0 + wn * WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int rl = wm * 64 + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        const int rl = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
         const int row = m0 + rl;
         if (row < M && col < N) {
           float out = acc[mb][nb][v];
@@ -328,7 +298,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 }
 
-template <typename BT, bool BNK, bool RMS>
+template <int BM, int BN, typename BT, bool BNK, bool RMS>
 void run_gemm(const GemmArgs& a, hipStream_t stream) {
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
   const bool va = (a.K % 4 == 0) && aligned_to(a.A, 16);
@@ -344,7 +314,7 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
 #define ENG_GEMM_LAUNCH(VA_, VB_)                                                       \
-  gemm_f32_mfma_kernel<BT, BNK, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(          \
+  gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(  \
       a.A, B, a.C, a.gamma, M, N, K, a.eps, tiles_m, tiles_n)
   if (va && vb) {
     ENG_GEMM_LAUNCH(true, true);
@@ -359,12 +329,47 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
+// Tile shape: the largest of 128 x 128, 128 x 64, 64 x 64 whose makespan (rounds
+// of one tile per CU, times the tile's share of the work) is not worse than a
+// smaller shape's. Smaller tiles re-read A and B more, so ties go to the larger.
+enum class Tile { T128x128, T128x64, T64x64 };
+
+Tile choose_tile(long long M, long long N) {
+  const long long cus = device_cu_count();
+  auto makespan = [&](long long bm, long long bn) {
+    const long long tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const long long rounds = (tiles + cus - 1) / cus;
+    return static_cast<double>(rounds) * static_cast<double>(bm * bn) / (128.0 * 128.0);
+  };
+  const double t1 = makespan(128, 128);
+  const double t2 = makespan(128, 64);
+  const double t3 = makespan(64, 64);
+  if (t1 <= t2 && t1 <= t3) return Tile::T128x128;
+  if (t2 <= t3) return Tile::T128x64;
+  return Tile::T64x64;
+}
+
+template <typename BT, bool BNK, bool RMS>
+void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
+  switch (choose_tile(a.M, a.N)) {
+    case Tile::T128x128:
+      run_gemm<128, 128, BT, BNK, RMS>(a, stream);
+      break;
+    case Tile::T128x64:
+      run_gemm<128, 64, BT, BNK, RMS>(a, stream);
+      break;
+    case Tile::T64x64:
+      run_gemm<64, 64, BT, BNK, RMS>(a, stream);
+      break;
+  }
+}
+
 template <typename BT, bool BNK>
 void run_gemm_rms(const GemmArgs& a, hipStream_t stream) {
   if (a.rms) {
-    run_gemm<BT, BNK, true>(a, stream);
+    run_gemm_tiled<BT, BNK, true>(a, stream);
   } else {
-    run_gemm<BT, BNK, false>(a, stream);
+    run_gemm_tiled<BT, BNK, false>(a, stream);
   }
 }
 

@@ -90,11 +90,14 @@ void dispatch_kn(const GemvArgs& a, hipStream_t stream) {
   }
 }
 
-// Output-major configuration: two rows per wave, 8 x 1 KiB loads per row in flight.
+// Output-major configuration: 8 x 1 KiB loads per row in flight, one row per
+// wave (measured best on gfx950 against 2 or 4 rows per wave, 4 or 16 loads,
+// and x staged in LDS) -- two rows per wave with RMSNorm, which streams gamma
+// beside x and so gains more from sharing those loads between rows.
 template <typename WT, bool RMS>
 void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
   constexpr int VMAX = 16 / static_cast<int>(sizeof(WT));
-  constexpr int R = 2;
+  constexpr int R = RMS ? 2 : 1;
   const long long waves = (a.N + R - 1) / R;
   const long long wgs = (waves + 3) / 4;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");

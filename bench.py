@@ -2,13 +2,15 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
 
-Headline: the fp16-weight decode GEMV out[N] = x[K] . W[K x N]
-with K = N = 4096, fp32 x / out, batch 1. One step is one GEMV launch over one
-weight matrix; the W steps are spread over 32 distinct 32 MiB weight buffers
-(1 GiB) so every launch reads cold weights (the MI355X Infinity Cache holds
-256 MB). `value` is algorithmic bytes (2KN + 4K + 4N per launch) over the
-event-timed region, in GB/s. All inputs are synthetic and already resident in
-HBM when timing starts.
+Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
+y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
+through eng_gemv_f16w_nk. One step is one GEMV launch over one weight matrix;
+the steps are spread over 32 distinct 32 MiB weight buffers (1 GiB) so every
+launch reads cold weights (the MI355X Infinity Cache holds 256 MB). `value` is
+algorithmic bytes (2KN + 4K + 4N per launch) over the event-timed region, in
+GB/s. All inputs are synthetic and already resident in HBM when timing starts.
+The same GEMV through the reference-layout entry (eng_gemv_f16w, out = x . A
+with A [in x out]) is reported in "secondary".
 
 Also reported on the same JSON line (key "secondary"): the other BASELINE
 configs -- fused RMSNorm+linear at K=4096, N=11008 (config 3), the FP32 GEMMs
@@ -36,8 +38,29 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
 METRIC = "decode GEMV HBM GB/s (% of peak); FP32 GEMM TFLOP/s at 4096^3 (% MFMA peak)"
 
 
+HEADLINE_KERNEL = "eng::gemv::gemv_rows_kernel<_Float16, 8, 1, 8, false>"
+TRAFFIC_PROFILE = os.path.join("profiles", "gemv_rows_f16w_4096x4096_cold.md")
+
+
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the headline kernel from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (copy-kernel calibrated), or None when the
+    summary is missing or covers a different kernel."""
+    import re
+
+    try:
+        with open(os.path.join(REPO, TRAFFIC_PROFILE)) as f:
+            text = f.read()
+    except OSError:
+        return None
+    if HEADLINE_KERNEL not in text:
+        return None
+    m = re.search(r"^traffic_bytes_per_launch: (\d+)\s*$", text, re.M)
+    return int(m.group(1)) if m else None
 
 
 def load_package():
@@ -331,9 +354,9 @@ def main() -> int:
     log(eng.device_summary())
     timer = Timer(eng, pkg)
 
-    ms, nbytes = bench_gemv_f16w(eng, timer, args.steps, args.warmup)
+    ms, nbytes = bench_gemv_f16w(eng, timer, args.steps, args.warmup, nk=True)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"config 2 gemv_f16w 4096x4096 cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s")
+    log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s")
 
     secondary = []
     if not args.quick:
@@ -357,8 +380,10 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded numpy; weights ~N(0,0.02^2) fp16, x ~N(0,1) fp32), resident in HBM",
         "config": {
-            "workload": ("BASELINE config 2: fp16-weight decode GEMV out[N]=x[K].W[KxN], K=N=4096, "
-                         "x/out fp32, fp32 accumulate, batch 1, cold weights (32 rotating 32 MiB buffers)"),
+            "workload": ("BASELINE config 2: fp16-weight decode GEMV y=W.x, W [4096x4096] fp16 row-major "
+                         "(out x in), x/y fp32, fp32 accumulate, batch 1, seed 1, cold weights "
+                         "(32 rotating 32 MiB buffers); entry point eng_gemv_f16w_nk. The reference-"
+                         "layout entry (eng_gemv_f16w, out=x.A with A [in x out]) is in 'secondary'"),
             "weight_dtype": "f16",
             "bytes_per_step": nbytes,
             "parallelism": "single GPU",
@@ -369,8 +394,10 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "gemv_splitk_kernel<_Float16,float,float,8,8,false>",
+            "traffic": profiled_traffic(),
+            "traffic_source": TRAFFIC_PROFILE + " (rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
+                              "scaled by the counters of a 32 MiB device copy)",
+            "kernel": HEADLINE_KERNEL,
             "achieved_from": "algorithmic bytes per launch / event-timed average launch duration on the launch stream",
         },
         "cpu_baseline": cpu,
