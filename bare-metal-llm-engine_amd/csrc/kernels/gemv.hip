@@ -11,18 +11,21 @@
 // workgroup, which costs far more than the second launch.
 //
 // Output-major layout, y[N] = W[N x K] . x[K] (the *_nk entry points):
-// gemv_rows_kernel, one wave per pair of output rows streaming contiguous
-// rows; no partial sums and a single launch.
+// each wave streams whole contiguous rows (gemv_rows_kernel, x read from the
+// caches; gemv_rows_lds_kernel, x * gamma staged once per workgroup in LDS);
+// no partial sums and a single launch.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
 #include <algorithm>
+#include <cstddef>
 
 namespace eng {
 namespace {
 
 using gemv::gemv_reduce_kernel;
 using gemv::gemv_rows_kernel;
+using gemv::gemv_rows_lds_kernel;
 using gemv::gemv_stream_kernel;
 
 // Reference-layout configuration: row segments of LPR lanes x 16 bytes.
@@ -61,13 +64,13 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   const XT* x = static_cast<const XT*>(a.x);
   YT* y = static_cast<YT*>(a.y);
   if (nsplit == 1) {
-    gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, false, RMS, false>
+    gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, false>
         <<<static_cast<unsigned>(ncb), WAVES * 64, 0, stream>>>(W, x, a.gamma, y, N, K, K, ncb,
                                                                  nullptr, nullptr, a.eps);
     ENG_LAUNCH_CHECK();
     return;
   }
-  gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, false, RMS, true>
+  gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true>
       <<<static_cast<unsigned>(ncb * nsplit), WAVES * 64, 0, stream>>>(
           W, x, a.gamma, y, N, K, kchunk, ncb, ws->partials, ws->partial_ss, a.eps);
   ENG_LAUNCH_CHECK();
@@ -90,30 +93,72 @@ void dispatch_kn(const GemvArgs& a, hipStream_t stream) {
   }
 }
 
-// Output-major configuration: 8 x 1 KiB loads per row in flight, one row per
-// wave (measured best on gfx950 against 2 or 4 rows per wave, 4 or 16 loads,
-// and x staged in LDS) -- two rows per wave with RMSNorm, which streams gamma
-// beside x and so gains more from sharing those loads between rows.
+// Output-major launches: 256-thread workgroups of 4 waves, R rows per wave.
+template <typename WT, int VEC, int R, int U, bool RMS>
+void launch_rows(const GemvArgs& a, hipStream_t stream) {
+  const long long wgs = ((a.N + R - 1) / R + 3) / 4;
+  ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
+  gemv_rows_kernel<WT, VEC, R, U, RMS><<<static_cast<unsigned>(wgs), 256, 0, stream>>>(
+      static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
+      static_cast<float*>(a.y), a.N, a.K, a.eps);
+  ENG_LAUNCH_CHECK();
+}
+
+template <typename WT, int R, bool RMS>
+void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t stream) {
+  constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
+  const long long wgs = ((a.N + R - 1) / R + 3) / 4;
+  ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
+  gemv_rows_lds_kernel<WT, VEC, R, 4, RMS>
+      <<<static_cast<unsigned>(wgs), 256, lds_bytes, stream>>>(
+          static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
+          static_cast<float*>(a.y), a.N, a.K, a.eps);
+  ENG_LAUNCH_CHECK();
+}
+
+// Output-major configuration, from sweeps on MI355X at the decode shapes
+// (cold weights): one wave per row fills the GPU once when N <= 16 x CUs
+// (4 waves per SIMD), and 4 x 1 KiB loads per row in flight is then best;
+// beyond that 8 in flight. For fp16 weights the x (and gamma) stream is
+// larger than the weight row it meets, and once it no longer stays in the
+// vector L1 (RMSNorm's x and gamma, or K > 4096) or rows outnumber resident
+// waves, staging x * gamma in LDS per workgroup wins 3-8%: one row per wave
+// unless N > 16 x CUs with RMSNorm or K > 4096 without (2 rows share each LDS
+// read). fp32 weights stay on the register kernel (2 rows per wave with
+// RMSNorm), where the LDS variant measured slower.
 template <typename WT, bool RMS>
 void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
   constexpr int VMAX = 16 / static_cast<int>(sizeof(WT));
-  constexpr int R = RMS ? 2 : 1;
-  const long long waves = (a.N + R - 1) / R;
-  const long long wgs = (waves + 3) / 4;
-  ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
   const bool vec_ok = (a.K % VMAX == 0) && aligned_to(a.W, 16) && aligned_to(a.x, 16) &&
                       (a.gamma == nullptr || aligned_to(a.gamma, 16));
-  const WT* W = static_cast<const WT*>(a.W);
-  const float* x = static_cast<const float*>(a.x);
-  float* y = static_cast<float*>(a.y);
-  if (vec_ok) {
-    gemv_rows_kernel<WT, VMAX, R, 8, RMS><<<static_cast<unsigned>(wgs), 256, 0, stream>>>(
-        W, x, a.gamma, y, a.N, a.K, a.eps);
-  } else {
-    gemv_rows_kernel<WT, 1, R, 8, RMS><<<static_cast<unsigned>(wgs), 256, 0, stream>>>(
-        W, x, a.gamma, y, a.N, a.K, a.eps);
+  if (!vec_ok) {
+    launch_rows<WT, 1, RMS ? 2 : 1, 8, RMS>(a, stream);
+    return;
   }
-  ENG_LAUNCH_CHECK();
+  const long long one_round = 16LL * device_cu_count();
+  if constexpr (sizeof(WT) == 2) {
+    constexpr long long kPiece = 64 * VMAX;
+    constexpr long long kMaxLds = 64 * 1024;
+    const long long padded = (a.K + kPiece - 1) / kPiece * kPiece;
+    const bool fits = padded * 4 <= kMaxLds;
+    if (fits && (RMS || a.N > one_round || a.K > 4096)) {
+      const bool two = RMS ? a.N > one_round : a.K > 4096;
+      const std::size_t lds = static_cast<std::size_t>(padded) * 4;
+      if (two) {
+        launch_rows_lds<WT, 2, RMS>(a, lds, stream);
+      } else {
+        launch_rows_lds<WT, 1, RMS>(a, lds, stream);
+      }
+      return;
+    }
+  }
+  if constexpr (RMS) {
+    launch_rows<WT, VMAX, 2, 8, true>(a, stream);
+  } else if (sizeof(WT) == 2 && a.N <= one_round) {
+    launch_rows<WT, VMAX, 1, 4, false>(a, stream);
+  } else {
+    launch_rows<WT, VMAX, 1, 8, false>(a, stream);
+  }
 }
 
 }  // namespace

@@ -257,10 +257,12 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W
       const bool ok = k < K;  // VEC > 1 implies K % VEC == 0
 #pragma unroll
       for (int r = 0; r < R; ++r) {
+        // Weights are read once per call: nontemporal loads keep them from
+        // displacing x (re-read by every wave) in the caches.
         if constexpr (VEC == 1) {
-          w[u][r] = ok ? rows[r][k] : WT(0);
+          w[u][r] = ok ? __builtin_nontemporal_load(rows[r] + k) : WT(0);
         } else {
-          w[u][r] = ok ? *reinterpret_cast<const V*>(rows[r] + k) : V{};
+          w[u][r] = ok ? __builtin_nontemporal_load(reinterpret_cast<const V*>(rows[r] + k)) : V{};
         }
       }
       if constexpr (VEC == 1) {
@@ -307,6 +309,132 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W
   }
   if (lane == 0) {
     const float scale = RMS ? rms_scale(ss, K, eps) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (n0 + r < N) y[n0 + r] = RMS ? acc[r] * scale : acc[r];
+    }
+  }
+}
+
+// LDS slot of element k of the activation vector for gemv_rows_lds_kernel.
+// A wave step covers PIECE = 64 * VEC elements, lane l taking elements
+// l*VEC .. l*VEC+VEC-1; the slot order stores, per piece, the first 4 of
+// every lane's elements, then the next 4, so each 16-byte LDS read of a wave
+// is contiguous across lanes (no bank conflicts). For VEC == 4 this is the
+// identity.
+template <int VEC>
+__device__ __forceinline__ int lds_slot(int k) {
+  constexpr int PIECE = 64 * VEC;
+  const int p = k / PIECE;
+  const int r = k - p * PIECE;
+  const int l = r / VEC;
+  const int e = r - l * VEC;
+  return p * PIECE + (e >> 2) * 256 + l * 4 + (e & 3);
+}
+
+// Output-major GEMV with the activation vector staged once per workgroup.
+// Same arithmetic contract as gemv_rows_kernel (y[n] = s * sum_k W[n][k] *
+// x[k] * g[k]), for when x (and gamma) are too large to stay in the vector L1
+// across the rows a CU streams: the workgroup loads x, multiplies gamma in,
+// sums x^2 and writes xs = x * gamma into LDS (zero-padded to whole pieces),
+// then each wave streams its R rows against LDS, U loads per row in flight.
+// (Issuing weight loads ahead of the staging measured slower: vector loads
+// complete in order, so the staging then waits for HBM.)
+// Requires K % VEC == 0 and 16-byte aligned W, x and gamma; the caller sizes
+// dynamic LDS as round_up(K, 64 * VEC) floats.
+template <typename WT, int VEC, int R, int U, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict__ W,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            float* __restrict__ y, long long N,
+                                                            long long K, float eps) {
+  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
+  using V = typename RawVec<WT, VEC>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 64 * VEC;
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
+  const bool active = n0 < N;
+  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
+
+  const WT* rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = W + (active && n0 + r < N ? n0 + r : 0) * K;
+
+  auto load_step = [&](int p0, V (&w)[U][R]) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long k = static_cast<long long>(p0 + u) * PIECE + lane * VEC;
+      const bool ok = active && k < K;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        w[u][r] = ok ? __builtin_nontemporal_load(reinterpret_cast<const V*>(rows[r] + k)) : V{};
+      }
+    }
+  };
+
+  // Stage xs = x * gamma (4 floats per thread per pass) and sum x^2.
+  float ss = 0.0f;
+  const int padded = npieces * PIECE;
+  for (int k = tid * 4; k < padded; k += 1024) {
+    F4 v = F4{};
+    if (k < K) {
+      v = *reinterpret_cast<const F4*>(x + k);
+      if constexpr (RMS) {
+        ss = fmaf(v[0], v[0], ss);
+        ss = fmaf(v[1], v[1], ss);
+        ss = fmaf(v[2], v[2], ss);
+        ss = fmaf(v[3], v[3], ss);
+        if (gamma != nullptr) v *= *reinterpret_cast<const F4*>(gamma + k);
+      }
+    }
+    *reinterpret_cast<F4*>(xs + lds_slot<VEC>(k)) = v;
+  }
+  if constexpr (RMS) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if (lane == 0) wave_ss[wave] = ss;
+  }
+  __syncthreads();
+  if (!active) return;
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int p0 = 0; p0 < npieces; p0 += U) {
+    V cur[U][R];
+    load_step(p0, cur);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (p0 + u >= npieces) break;  // wave-uniform
+      const float* base = xs + (p0 + u) * PIECE + lane * 4;
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        const F4 a = *reinterpret_cast<const F4*>(base + h * 256);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            acc[r] = fmaf(a[e], static_cast<float>(cur[u][r][h * 4 + e]), acc[r]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += __shfl_xor(acc[r], off);
+  }
+  if (lane == 0) {
+    float scale = 1.0f;
+    if constexpr (RMS) {
+      scale = rms_scale(((wave_ss[0] + wave_ss[1]) + wave_ss[2]) + wave_ss[3], K, eps);
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (n0 + r < N) y[n0 + r] = RMS ? acc[r] * scale : acc[r];

@@ -437,6 +437,36 @@ def test_gemv_nk_shapes_against_oracle(gpu, orc, N, K, dtype):
     check_dot(got, y, helpers.absdot(x, Wt) + np.abs(y), K, f"gemv nk {N}x{K} {dtype}")
 
 
+@pytest.mark.parametrize("N,K,rms,gamma", [
+    (5, 8, True, True),          # K below one 512-element piece
+    (333, 1000, True, True),     # ragged last piece, N not a multiple of 4 rows
+    (333, 1000, True, False),    # null gain
+    (4099, 520, True, True),     # N beyond one resident round: 2 rows per wave, odd N
+    (64, 16384, True, True),     # largest K whose staged vector fits 64 KiB of LDS
+    (64, 16392, True, True),     # just past it: register kernel fallback
+    (300, 8200, False, False),   # K > 4096 without RMSNorm: 2 rows per wave
+    (5000, 1000, False, False),  # many rows, small K: 1 row per wave
+    (64, 20000, False, False),   # LDS does not fit: register kernel, 4 loads in flight
+])
+def test_nk_fp16_kernel_selection_against_oracle(gpu, orc, N, K, rms, gamma):
+    """Every output-major fp16 launch variant (LDS-staged x, register x,
+    fallbacks) against the oracle at the shapes that select it."""
+    rng = np.random.default_rng(7 * N + K)
+    W = orc.f32_to_f16(rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K))
+    Wt = np.ascontiguousarray(W.T)
+    if rms:
+        x = rng.standard_normal((1, K), dtype=np.float32)
+        g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if gamma else None
+        got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
+        y = orc.rmsnorm_linear(x, g, Wt, EPS).astype(np.float64)
+        check_rmsnorm_linear(got, y, x, g, Wt, K, f"rmsnorm_linear nk {N}x{K}")
+    else:
+        x = rng.standard_normal(K, dtype=np.float32)
+        got = gpu_gemv_nk(gpu, W, x)
+        y = orc.gemv_f16w(Wt, x).astype(np.float64)
+        check_dot(got, y, helpers.absdot(x, Wt) + np.abs(y), K, f"gemv nk {N}x{K}")
+
+
 def test_gemv_nk_misaligned_x_takes_scalar_path(gpu, orc):
     rng = np.random.default_rng(21)
     N, K = 256, 2048
