@@ -1,6 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
+                    [--only config2,config3,refapi,gemm,stack]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -16,9 +17,13 @@ Also reported on the same JSON line (key "secondary"): the other BASELINE
 configs -- fused RMSNorm+linear at K=4096, N=11008 (config 3), the FP32 GEMMs
 (config 4), the 32-layer Llama-7B-shape decode linear stack (config 5) -- the
 reference API's fp32 / half-I/O GEMVs and warm-cache rows, each with its
-roofline fraction. The CPU baseline runs the scalar C oracle (a restatement
-of the reference's src/cpu_ref, double accumulation) on one pinned core
-before the GPU is touched.
+roofline fraction. Secondary rows follow the reference harness's protocol:
+warm-up, batches of back-to-back calls sized to ~1.5 ms (at most 256), 15
+batches, per-call median with p25 / p75 and IQR % (flagged "noisy" above
+10%). The CPU baseline runs the scalar C oracle (a restatement of the
+reference's src/cpu_ref, double accumulation) on one pinned core before the
+GPU is touched: config 2 for `cpu_baseline.value`, configs 1, 3, 4, 5 in
+`cpu_baseline.per_config`.
 """
 
 from __future__ import annotations
@@ -79,41 +84,118 @@ def load_package():
 
 
 # ------------------------------------------------------------ CPU baseline
-def cpu_baseline(seconds: float = 10.0) -> dict:
-    """The scalar oracle's fp16-weight GEMV (config 2 shape) on one core."""
-    sys.path.insert(0, os.path.join(REPO, "tests"))
-    import helpers
-
-    orc = helpers.oracle(0)
-    rng = np.random.default_rng(1)
-    K = N = 4096
-    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
-    x = rng.standard_normal(K, dtype=np.float32)
-    cpus = sorted(os.sched_getaffinity(0))
-    core = cpus[0]
-    old = os.sched_getaffinity(0)
-    os.sched_setaffinity(0, {core})
-    try:
-        orc.gemv_f16w(W, x)  # warm-up
-        times = []
-        t_end = time.perf_counter() + seconds
-        while time.perf_counter() < t_end and len(times) < 200:
-            t0 = time.perf_counter()
-            orc.gemv_f16w(W, x)
-            times.append(time.perf_counter() - t0)
-    finally:
-        os.sched_setaffinity(0, old)
-    med = float(np.median(times))
-    nbytes = 2 * K * N + 4 * K + 4 * N
-    cpu_model = "unknown"
+def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
                 if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                    return line.split(":", 1)[1].strip()
     except OSError:
         pass
+    return "unknown"
+
+
+def _time_cpu(fn, reps: int, seconds: float, warm: bool = True) -> list:
+    """Wall time of `fn` per call: one warm-up (unless `warm` is False, for
+    multi-second calls), then at least `reps` calls and at most `seconds` of
+    them (the reference's time_cpu protocol)."""
+    if warm:
+        fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < reps or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def _tiled(rng, shape, kind):
+    """Cheap CPU-baseline inputs: a 1 Mi-element random block repeated to
+    `shape` (scalar-loop timings do not depend on the values)."""
+    n = 1 << 20
+    if kind == "f16":
+        base = (0.02 * rng.standard_normal(n, dtype=np.float32)).astype(np.float16).view(np.uint16)
+    else:
+        base = rng.uniform(-1, 1, n).astype(np.float32)
+    return np.resize(base, shape)
+
+
+def cpu_baseline(seconds: float = 10.0) -> dict:
+    """The scalar C oracle on one pinned core, per BASELINE config: config 2
+    (the headline, fp16-weight GEMV) over ~`seconds`, then configs 1, 3, 4
+    (sampled rows) and 5 (one layer) at >= 3 calls each."""
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import helpers
+
+    orc = helpers.oracle(0)
+    cpus = sorted(os.sched_getaffinity(0))
+    core = cpus[0]
+    old = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {core})
+    rows = []
+    try:
+        rng = np.random.default_rng(1)
+        K = N = 4096
+        W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal(K, dtype=np.float32)
+        times = _time_cpu(lambda: orc.gemv_f16w(W, x), 3, seconds)
+        med = float(np.median(times))
+        nbytes = 2 * K * N + 4 * K + 4 * N
+
+        # config 1: 512^3 GEMM.
+        r = np.random.default_rng(0)
+        A = r.uniform(-1, 1, (512, 512)).astype(np.float32)
+        B = r.uniform(-1, 1, (512, 512)).astype(np.float32)
+        t = float(np.median(_time_cpu(lambda: orc.matmul(A, B), 3, 0.0)))
+        rows.append({"config": 1, "what": "matmul 512^3", "ms_per_call": round(t * 1e3, 2),
+                     "GFLOP/s": round(2 * 512 ** 3 / t / 1e9, 3)})
+
+        # config 3: rmsnorm_linear, fp16 W [K=4096 x N=11008].
+        r = np.random.default_rng(2)
+        K3, N3 = 4096, 11008
+        x3 = r.standard_normal((1, K3), dtype=np.float32)
+        g3 = (1 + 0.1 * r.standard_normal(K3)).astype(np.float32)
+        W3 = _tiled(r, (K3, N3), "f16")
+        t = float(np.median(_time_cpu(lambda: orc.rmsnorm_linear(x3, g3, W3, 1e-5), 3, 0.0, warm=False)))
+        b3 = 2 * K3 * N3 + 8 * K3 + 4 * N3
+        rows.append({"config": 3, "what": "rmsnorm_linear fp16-W 1x11008x4096",
+                     "ms_per_call": round(t * 1e3, 2), "GB/s": round(b3 / t / 1e9, 4)})
+        del W3
+
+        # config 4: 512x11008x4096 on 4 sampled rows of A, extrapolated to 512.
+        r = np.random.default_rng(3)
+        A4 = r.uniform(-1, 1, (4, 4096)).astype(np.float32)
+        B4 = _tiled(r, (4096, 11008), "f32")
+        t = float(np.median(_time_cpu(lambda: orc.matmul(A4, B4), 3, 0.0, warm=False))) * (512 / 4)
+        rows.append({"config": 4, "what": "matmul 512x11008x4096 (4 of 512 rows timed, x128)",
+                     "ms_per_call": round(t * 1e3, 1), "GFLOP/s": round(2 * 512 * 11008 * 4096 / t / 1e9, 3)})
+        del B4
+
+        # config 5: one decoder layer's linear stack, reported x32 per token.
+        r = np.random.default_rng(4)
+        H, F = 4096, 11008
+        sq = _tiled(r, (H, H), "f16")
+        gu = _tiled(r, (H, F), "f16")
+        dn = _tiled(r, (F, H), "f16")
+        xh = r.standard_normal(H, dtype=np.float32)
+        g5 = (1 + 0.1 * r.standard_normal(H)).astype(np.float32)
+
+        def layer():
+            q = orc.gemv_f16w(sq, xh)
+            orc.gemv_f16w(sq, xh)
+            orc.gemv_f16w(sq, xh)
+            o = orc.gemv_f16w(sq, q)
+            gate = orc.rmsnorm_linear(o[None, :], g5, gu, 1e-5)
+            orc.rmsnorm_linear(o[None, :], g5, gu, 1e-5)
+            orc.gemv_f16w(dn, gate[0])
+
+        t = float(np.median(_time_cpu(layer, 3, 0.0, warm=False))) * 32
+        b5 = 12963053568
+        rows.append({"config": 5, "what": "llama7b-shape decode linear stack (1 layer timed, x32)",
+                     "ms_per_token": round(t * 1e3, 1), "GB/s": round(b5 / t / 1e9, 4)})
+    finally:
+        os.sched_setaffinity(0, old)
     return {
         "value": round(nbytes / med / 1e9, 4),
         "unit": "GB/s",
@@ -121,31 +203,73 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
         "kind": "port",
         "sample": (f"{len(times)} calls of the config-2 GEMV (4096x4096 fp16 W, fp32 x/y) by the "
                    f"scalar C oracle (oracle/oracle.c orc_gemv_f16w, double accumulation), pinned "
-                   f"to core {core} of {len(cpus)} on '{cpu_model}'; median {med * 1e3:.1f} ms/call"),
+                   f"to core {core} of {len(cpus)} on '{_cpu_model()}'; median {med * 1e3:.1f} ms/call"),
+        "per_config": rows,
+        "per_config_note": ("configs 1, 3, 4, 5 by the same oracle on the same core; their large weight "
+                            "matrices are a 1 Mi-element random block repeated to shape (timing does not "
+                            "depend on the values); config 4 times 4 of 512 rows, config 5 one layer"),
     }
 
 
 # --------------------------------------------------------------- GPU timing
+def _stats(samples: list) -> dict:
+    """Median and spread of per-call times (ms), as the reference's harness
+    reports them (bench_harness.hpp: median, p25/p75, IQR %, flagged > 10%)."""
+    a = np.sort(np.asarray(samples, dtype=np.float64))
+    med = float(np.median(a))
+    p25, p75 = (float(v) for v in np.percentile(a, [25, 75]))
+    iqr = 100.0 * (p75 - p25) / med if med > 0 else 0.0
+    return {"median_ms": med, "p25_ms": p25, "p75_ms": p75, "iqr_pct": round(iqr, 2),
+            "samples": len(a), "noisy": iqr > 10.0}
+
+
 class Timer:
     def __init__(self, eng, pkg):
         self.eng = eng
         self.stream = eng.stream(pkg.STREAM_NON_BLOCKING)
         self.e0 = eng.event()
         self.e1 = eng.event()
+        self.calls = 0
 
-    def run(self, launch, steps: int, warmup: int) -> float:
-        """Average ms per launch over `steps` back-to-back launches on one stream."""
-        for i in range(warmup):
-            launch(i, self.stream.handle)
-        self.stream.sync()
-        self.eng.sync()
+    def _window(self, launch, n: int) -> float:
         self.e0.record(self.stream)
-        for i in range(steps):
-            launch(warmup + i, self.stream.handle)
+        for _ in range(n):
+            launch(self.calls, self.stream.handle)
+            self.calls += 1
         self.e1.record(self.stream)
         self.e1.sync()
+        return self.e0.elapsed_ms(self.e1)
+
+    def run(self, launch, steps: int, warmup: int) -> float:
+        """Average ms per launch over exactly `steps` back-to-back launches on
+        one stream, after `warmup` untimed ones."""
+        for _ in range(warmup):
+            launch(self.calls, self.stream.handle)
+            self.calls += 1
+        self.stream.sync()
         self.eng.sync()
-        return self.e0.elapsed_ms(self.e1) / steps
+        ms = self._window(launch, steps) / steps
+        self.eng.sync()
+        return ms
+
+    def sampled(self, launch, samples: int = 15, target_ms: float = 1.5, max_batch: int = 256,
+                warmup_ms: float = 20.0) -> dict:
+        """The reference's protocol: warm up for >= `warmup_ms`, size a batch of
+        back-to-back calls to ~`target_ms` (at most `max_batch`), time
+        `samples` batches; per-call median / quartiles / IQR %."""
+        t_end = time.perf_counter() + warmup_ms * 1e-3
+        n = 0
+        while time.perf_counter() < t_end or n < 2:
+            launch(self.calls, self.stream.handle)
+            self.calls += 1
+            n += 1
+        self.stream.sync()
+        one = self._window(launch, 4) / 4
+        batch = int(max(1, min(max_batch, round(target_ms / max(one, 1e-6)))))
+        per_call = [self._window(launch, batch) / batch for _ in range(samples)]
+        st = _stats(per_call)
+        st["batch"] = batch
+        return st
 
 
 def rand_f16(rng, shape, std=0.02):
@@ -163,54 +287,73 @@ def rotating(eng, host, count):
     return bufs
 
 
-def hbm_row(name, ms, nbytes, extra=None):
+def _spread(st: dict) -> dict:
+    return {"p25_us": round(st["p25_ms"] * 1e3, 3), "p75_us": round(st["p75_ms"] * 1e3, 3),
+            "iqr_pct": st["iqr_pct"], "samples": st["samples"], "batch": st["batch"],
+            **({"noisy": True} if st["noisy"] else {})}
+
+
+def hbm_row(name, st, nbytes, extra=None):
+    """Row for an HBM-bound call timed by Timer.sampled (median per call)."""
+    ms = st["median_ms"]
     gbs = nbytes / (ms * 1e-3) / 1e9
     row = {"name": name, "us_per_call": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
            "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": nbytes}
+    row.update(_spread(st))
     if extra:
         row.update(extra)
     return row
 
 
-def gemm_row(name, ms, M, N, K):
+def gemm_row(name, st, M, N, K):
+    ms = st["median_ms"]
     tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
-    return {"name": name, "ms_per_call": round(ms, 4), "TFLOP/s": round(tf, 2),
-            "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "flops_per_call": 2 * M * N * K}
+    row = {"name": name, "ms_per_call": round(ms, 4), "TFLOP/s": round(tf, 2),
+           "frac_fp32_mfma_peak": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "flops_per_call": 2 * M * N * K}
+    row.update(_spread(st))
+    return row
 
 
-def bench_gemv_f16w(eng, timer, steps, warmup, rotate=32, K=4096, N=4096, seed=1, nk=False):
-    """nk=False: reference layout out = x . W[K x N] (eng_gemv_f16w);
+class GemvF16w:
+    """Config-2-shaped fp16-weight GEMV over `rotate` distinct weight copies.
+    nk=False: reference layout out = x . W[K x N] (eng_gemv_f16w);
     nk=True: y = W[N x K] . x, W row-major out x in (eng_gemv_f16w_nk)."""
-    rng = np.random.default_rng(seed)
-    Ws = rotating(eng, rand_f16(rng, (N, K) if nk else (K, N)), rotate)
-    dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
-    dy = eng.empty(N, np.float32)
-    fn = eng.lib.eng_gemv_f16w_nk if nk else eng.lib.eng_gemv_f16w
 
-    def launch(i, s):
-        rc = fn(Ws[i % rotate].ptr, dx.ptr, dy.ptr, N, K, s)
+    def __init__(self, eng, rotate=32, K=4096, N=4096, seed=1, nk=False):
+        rng = np.random.default_rng(seed)
+        self.eng, self.rotate, self.K, self.N = eng, rotate, K, N
+        self.Ws = rotating(eng, rand_f16(rng, (N, K) if nk else (K, N)), rotate)
+        self.dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
+        self.dy = eng.empty(N, np.float32)
+        self.fn = eng.lib.eng_gemv_f16w_nk if nk else eng.lib.eng_gemv_f16w
+        self.nbytes = 2 * K * N + 4 * K + 4 * N
+
+    def __call__(self, i, s):
+        rc = self.fn(self.Ws[i % self.rotate].ptr, self.dx.ptr, self.dy.ptr, self.N, self.K, s)
         if rc:
-            raise RuntimeError(eng.last_error())
+            raise RuntimeError(self.eng.last_error())
 
-    ms = timer.run(launch, steps, warmup)
-    for w in Ws:
-        w.free()
-    return ms, 2 * K * N + 4 * K + 4 * N
+    def free(self):
+        for w in self.Ws:
+            w.free()
 
 
-def secondary_rows(eng, timer) -> list:
+def rows_config2(eng, timer) -> list:
     rows = []
-    rng = np.random.default_rng(7)
-
     # config 2 in both weight layouts, cold, and warm (the same 32 MiB matrix
     # every call: Infinity-Cache resident, not an HBM figure).
     for nk, tag in ((False, "reference layout x.W[KxN], eng_gemv_f16w"),
                     (True, "output-major y=W[NxK].x, eng_gemv_f16w_nk")):
-        ms, nb = bench_gemv_f16w(eng, timer, 640, 64, nk=nk)
-        rows.append(hbm_row(f"config 2 gemv fp16-W 4096x4096 cold, {tag}", ms, nb))
-        ms, nb = bench_gemv_f16w(eng, timer, 400, 50, rotate=1, nk=nk)
-        rows.append(hbm_row(f"config 2 gemv fp16-W 4096x4096 WARM (cache-resident), {tag}", ms, nb))
+        for rotate, temp in ((32, "cold"), (1, "WARM (cache-resident)")):
+            g = GemvF16w(eng, rotate=rotate, nk=nk)
+            rows.append(hbm_row(f"config 2 gemv fp16-W 4096x4096 {temp}, {tag}", timer.sampled(g), g.nbytes))
+            g.free()
+    return rows
 
+
+def rows_config3(eng, timer) -> list:
+    rows = []
+    rng = np.random.default_rng(7)
     # config 3: fused RMSNorm + linear, fp16 W, K=4096, N=11008, cold (12 x 86 MiB).
     K, N, R = 4096, 11008, 12
     dx = eng.upload(np.random.default_rng(2).standard_normal(K, dtype=np.float32))
@@ -219,12 +362,17 @@ def secondary_rows(eng, timer) -> list:
     for nk, f, tag in ((False, eng.lib.eng_rmsnorm_linear_f16w, "reference layout W[KxN]"),
                        (True, eng.lib.eng_rmsnorm_linear_f16w_nk, "output-major W[NxK]")):
         Ws = rotating(eng, rand_f16(np.random.default_rng(2), (N, K) if nk else (K, N)), R)
-        ms = timer.run(lambda i, s: f(dx.ptr, dg.ptr, Ws[i % R].ptr, dy.ptr, 1, N, K, 1e-5, s), 240, 24)
-        rows.append(hbm_row(f"config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, {tag}", ms,
+        st = timer.sampled(lambda i, s: f(dx.ptr, dg.ptr, Ws[i % R].ptr, dy.ptr, 1, N, K, 1e-5, s))
+        rows.append(hbm_row(f"config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, {tag}", st,
                             2 * K * N + 8 * K + 4 * N))
         for w in Ws:
             w.free()
+    return rows
 
+
+def rows_reference_api(eng, timer) -> list:
+    rows = []
+    rng = np.random.default_rng(8)
     # Reference-API GEMVs: fp32 gemv and half-I/O gemv_fp16, 4096x4096, cold.
     K = N = 4096
     R = 16
@@ -232,28 +380,34 @@ def secondary_rows(eng, timer) -> list:
     dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
     dy = eng.empty(N, np.float32)
     f = eng.lib.eng_gemv_f32
-    ms = timer.run(lambda i, s: f(Wf[i % R].ptr, dx.ptr, dy.ptr, N, K, s), 160, 16)
-    rows.append(hbm_row("gemv (fp32 W) 4096x4096 cold", ms, 4 * K * N + 8 * K))
+    st = timer.sampled(lambda i, s: f(Wf[i % R].ptr, dx.ptr, dy.ptr, N, K, s))
+    rows.append(hbm_row("gemv (fp32 W) 4096x4096 cold", st, 4 * K * N + 8 * K))
     for w in Wf:
         w.free()
     Wh = rotating(eng, rand_f16(rng, (K, N)), 32)
     dxh = eng.upload(rng.standard_normal(K, dtype=np.float32).astype(np.float16).view(np.uint16))
     dyh = eng.empty(N, np.uint16)
     f = eng.lib.eng_gemv_f16
-    ms = timer.run(lambda i, s: f(Wh[i % 32].ptr, dxh.ptr, dyh.ptr, N, K, s), 320, 32)
-    rows.append(hbm_row("gemv_fp16 (half x/out) 4096x4096 cold", ms, 2 * K * N + 4 * K))
+    st = timer.sampled(lambda i, s: f(Wh[i % 32].ptr, dxh.ptr, dyh.ptr, N, K, s))
+    rows.append(hbm_row("gemv_fp16 (half x/out) 4096x4096 cold", st, 2 * K * N + 4 * K))
     for w in Wh:
         w.free()
+    return rows
 
-    # config 4: FP32 GEMMs on MFMA.
+
+def rows_gemm(eng, timer) -> list:
+    rows = []
+    rng = np.random.default_rng(9)
+    # configs 1 and 4: FP32 GEMMs on MFMA.
     f = eng.lib.eng_matmul_f32
-    for M, N, K, reps in ((4096, 4096, 4096, 20), (512, 11008, 4096, 40), (512, 4096, 11008, 40)):
-        r3 = np.random.default_rng(3)
+    for cfg, M, N, K, seed in ((1, 512, 512, 512, 0), (4, 4096, 4096, 4096, 3), (4, 512, 11008, 4096, 3),
+                               (4, 512, 4096, 11008, 3)):
+        r3 = np.random.default_rng(seed)
         dA = eng.upload(r3.uniform(-1, 1, (M, K)).astype(np.float32))
         dB = eng.upload(r3.uniform(-1, 1, (K, N)).astype(np.float32))
         dC = eng.empty((M, N), np.float32)
-        ms = timer.run(lambda i, s: f(dA.ptr, dB.ptr, dC.ptr, M, N, K, s), reps, 3)
-        rows.append(gemm_row(f"matmul_f32 {M}x{N}x{K} (config 4)", ms, M, N, K))
+        st = timer.sampled(lambda i, s: f(dA.ptr, dB.ptr, dC.ptr, M, N, K, s))
+        rows.append(gemm_row(f"matmul_f32 {M}x{N}x{K} (config {cfg})", st, M, N, K))
         dA.free(), dB.free(), dC.free()
 
     # Reference bench shape: rmsnorm_linear (fp32 W) at M = 512, 4096 x 4096.
@@ -263,13 +417,21 @@ def secondary_rows(eng, timer) -> list:
     dW = eng.upload((rng.standard_normal((K, N), dtype=np.float32) / 64).astype(np.float32))
     dC = eng.empty((M, N), np.float32)
     f = eng.lib.eng_rmsnorm_linear_f32
-    ms = timer.run(lambda i, s: f(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s), 40, 3)
-    rows.append(gemm_row("rmsnorm_linear_f32 512x4096x4096 (fused MFMA GEMM)", ms, M, N, K))
+    st = timer.sampled(lambda i, s: f(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
+    rows.append(gemm_row("rmsnorm_linear_f32 512x4096x4096 (fused MFMA GEMM)", st, M, N, K))
     dA.free(), dg.free(), dW.free(), dC.free()
     return rows
 
 
-def bench_llama_stack(eng, timer, tokens=10, warmup=3, nk=False) -> dict:
+def rows_stack(eng, timer) -> list:
+    return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True)]
+
+
+GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
+          "gemm": rows_gemm, "stack": rows_stack}
+
+
+def bench_llama_stack(eng, timer, nk=False) -> dict:
     """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
     rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
     nk=False stores every weight [in x out] (reference layout), nk=True [out x in]."""
@@ -310,9 +472,7 @@ def bench_llama_stack(eng, timer, tokens=10, warmup=3, nk=False) -> dict:
             rl(o.ptr, g.ptr, lay["up"].ptr, up.ptr, 1, F, H, 1e-5, s)
             gv(lay["down"].ptr, gate.ptr, xh.ptr, H, F, s)
 
-    t0 = time.perf_counter()
-    ms = timer.run(token, tokens, warmup)
-    host_ms = (time.perf_counter() - t0) * 1e3 / (tokens + warmup)
+    st = timer.sampled(token, samples=10)
     wbytes = L * (4 * H * H + 3 * H * F) * 2
     abytes = L * (4 * (4 * H + 4 * H) + 2 * (8 * H + 4 * F) + (4 * F + 4 * H))
     for lay in layers:
@@ -320,9 +480,8 @@ def bench_llama_stack(eng, timer, tokens=10, warmup=3, nk=False) -> dict:
             d.free()
     layout = "output-major W[out x in]" if nk else "reference layout W[in x out]"
     row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
-                  ms, wbytes + abytes)
+                  st, wbytes + abytes)
     row["launches_per_token"] = 7 * L
-    row["host_ms_per_token"] = round(host_ms, 3)
     return row
 
 
@@ -333,6 +492,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary rows)")
+    ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
+                    + ", ".join(GROUPS) + " (default: all)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -354,17 +515,24 @@ def main() -> int:
     log(eng.device_summary())
     timer = Timer(eng, pkg)
 
-    ms, nbytes = bench_gemv_f16w(eng, timer, args.steps, args.warmup, nk=True)
+    head = GemvF16w(eng, nk=True)
+    nbytes = head.nbytes
+    ms = timer.run(head, args.steps, args.warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s")
+    spread = None if args.quick else _spread(timer.sampled(head))
+    head.free()
 
     secondary = []
     if not args.quick:
-        secondary = secondary_rows(eng, timer)
-        secondary.append(bench_llama_stack(eng, timer, nk=False))
-        secondary.append(bench_llama_stack(eng, timer, nk=True))
-        for r in secondary:
-            log(json.dumps(r))
+        groups = [g for g in args.only.split(",") if g] or list(GROUPS)
+        for g in groups:
+            if g not in GROUPS:
+                log(f"unknown group {g!r}; choose from {', '.join(GROUPS)}")
+                return 2
+            for r in GROUPS[g](eng, timer):
+                log(json.dumps(r))
+                secondary.append(r)
 
     line = {
         "metric": METRIC,
@@ -399,6 +567,10 @@ def main() -> int:
                               "scaled by the counters of a 32 MiB device copy)",
             "kernel": HEADLINE_KERNEL,
             "achieved_from": "algorithmic bytes per launch / event-timed average launch duration on the launch stream",
+        },
+        "timing": {
+            "value_from": f"{args.steps} back-to-back launches between two HIP events, after {args.warmup} warm-up",
+            "spread": spread,
         },
         "cpu_baseline": cpu,
         "secondary": secondary,
