@@ -107,6 +107,12 @@ SIGNATURES = {
     "eng_gemv_f32_nk": [_p, _p, _p, _i64, _i64, _p],
     "eng_rmsnorm_linear_f16w_nk": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_f32_nk": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_vector_add_f32": [_p, _p, _p, _i64, _p],
+    "eng_residual_rmsnorm_f32": [_p, _p, _p, _p, _p, _i64, _i64, _f, _p],
+    "eng_swiglu_f32": [_p, _p, _p, _i64, _p],
+    "eng_swiglu_f16": [_p, _p, _p, _i64, _p],
+    "eng_rmsnorm_linear_swiglu_f16w_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_rmsnorm_linear_swiglu_f32_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
 }
 STRING_FUNCTIONS = ("eng_last_error", "eng_build_info")
 

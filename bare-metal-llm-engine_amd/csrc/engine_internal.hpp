@@ -77,6 +77,24 @@ struct GemvWorkspace {
 GemvWorkspace& gemv_workspace(hipStream_t stream);
 void release_gemv_workspace(hipStream_t stream);
 
+// Stream-ordered scratch from the process-wide device pool (the reference's
+// ScopedPoolBuffer, include/engine/pool_allocator.hpp:97-148): returned to the
+// pool on destruction with an event on `stream`, so the block is handed out
+// again only after the work queued on that stream has finished.
+class PoolScratch {
+ public:
+  PoolScratch(std::size_t bytes, hipStream_t stream);
+  ~PoolScratch();
+  PoolScratch(const PoolScratch&) = delete;
+  PoolScratch& operator=(const PoolScratch&) = delete;
+  void* get() const { return ptr_; }
+
+ private:
+  eng_pool pool_ = nullptr;
+  void* ptr_ = nullptr;
+  hipStream_t stream_ = nullptr;
+};
+
 }  // namespace eng
 
 #define ENG_CHECK(cond, msg)                                                           \

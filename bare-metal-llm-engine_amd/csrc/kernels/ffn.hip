@@ -1,0 +1,114 @@
+// ffn.hip -- fused RMSNorm + gate / up projections + SwiGLU, the first half of
+// a Llama FFN, with output-major weights Wg, Wu [N x K]:
+//   act[r][n] = SiLU(xn[r] . Wg[n]) * (xn[r] . Wu[n]),  xn = RMSNorm(in) * gamma.
+// The reference composes this from rmsnorm, two GEMVs / GEMMs and swiglu
+// (tests/test_kernels.cu:2867-2898; its ADR 0006 defers fusing gate / up /
+// SwiGLU on one weight stream). Decode (M == 1, 16-byte aligned operands, K
+// up to 16384) runs gemv_rows_glu_kernel: one launch that stages x * gamma in
+// LDS, streams each output's gate and up rows together and applies SiLU in the
+// epilogue, so gate and up never reach memory. Other shapes compute gate and
+// up with the fused RMSNorm+linear launchers (GEMV or MFMA GEMM) into pooled,
+// stream-ordered scratch and finish with the SwiGLU kernel. Preconditions and
+// messages follow rmsnorm_linear; any zero dimension writes nothing.
+#include "gemv_kernels.hpp"
+#include "launch.hpp"
+
+#include <cstddef>
+
+namespace eng {
+namespace {
+
+template <typename WT>
+void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg, const WT* Wu,
+                              float* act, int64_t M, int64_t N, int64_t K, float eps,
+                              Elem elem, eng_stream stream) {
+  ENG_CHECK(M >= 0 && N >= 0 && K >= 0, "rmsnorm_linear_swiglu: negative dimension");
+  ENG_CHECK(in != nullptr && Wg != nullptr && Wu != nullptr && act != nullptr,
+            "rmsnorm_linear_swiglu: null device pointer");
+  ENG_CHECK(eps >= 0.0f, "rmsnorm_linear_swiglu: eps must be non-negative");
+  if (M == 0 || N == 0 || K == 0) return;
+  hipStream_t s = as_stream(stream);
+
+  constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
+  constexpr long long kPiece = 64 * VEC;
+  constexpr long long kMaxLds = 64 * 1024;
+  const long long padded = (K + kPiece - 1) / kPiece * kPiece;
+  const bool fused = M == 1 && K % VEC == 0 && padded * 4 <= kMaxLds && aligned_to(Wg, 16) &&
+                     aligned_to(Wu, 16) && aligned_to(in, 16) &&
+                     (gamma == nullptr || aligned_to(gamma, 16));
+  if (fused) {
+    const long long wgs = (N + 3) / 4;  // one output (its gate and up rows) per wave
+    ENG_CHECK(wgs <= 0x7fffffffLL, "rmsnorm_linear_swiglu: N too large for one launch");
+    gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true>
+        <<<static_cast<unsigned>(wgs), 256, static_cast<std::size_t>(padded) * 4, s>>>(
+            Wg, Wu, in, gamma, act, N, K, eps);
+    ENG_LAUNCH_CHECK();
+    return;
+  }
+
+  const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
+  PoolScratch scratch(2 * mn * sizeof(float), s);
+  float* gate = static_cast<float*>(scratch.get());
+  float* up = gate + mn;
+  for (int half = 0; half < 2; ++half) {
+    const void* W = half == 0 ? static_cast<const void*>(Wg) : static_cast<const void*>(Wu);
+    float* out = half == 0 ? gate : up;
+    if (M == 1) {
+      GemvArgs g;
+      g.W = W;
+      g.w = elem;
+      g.w_nk = true;
+      g.x = in;
+      g.gamma = gamma;
+      g.y = out;
+      g.N = N;
+      g.K = K;
+      g.rms = true;
+      g.eps = eps;
+      launch_gemv(g, s);
+    } else {
+      GemmArgs g;
+      g.A = in;
+      g.B = W;
+      g.b = elem;
+      g.b_nk = true;
+      g.C = out;
+      g.M = M;
+      g.N = N;
+      g.K = K;
+      g.gamma = gamma;
+      g.rms = true;
+      g.eps = eps;
+      launch_gemm(g, s);
+    }
+  }
+  launch_swiglu_f32(gate, up, act, static_cast<long long>(mn), s);
+}
+
+}  // namespace
+}  // namespace eng
+
+extern "C" {
+
+int eng_rmsnorm_linear_swiglu_f16w_nk(const float* in, const float* rms_weight,
+                                      const eng_half* W_gate, const eng_half* W_up, float* act,
+                                      int64_t M, int64_t N, int64_t K, float eps,
+                                      eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_swiglu_nk(in, rms_weight, reinterpret_cast<const _Float16*>(W_gate),
+                                  reinterpret_cast<const _Float16*>(W_up), act, M, N, K, eps,
+                                  eng::Elem::F16, stream);
+  });
+}
+
+int eng_rmsnorm_linear_swiglu_f32_nk(const float* in, const float* rms_weight,
+                                     const float* W_gate, const float* W_up, float* act,
+                                     int64_t M, int64_t N, int64_t K, float eps,
+                                     eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_swiglu_nk(in, rms_weight, W_gate, W_up, act, M, N, K, eps,
+                                  eng::Elem::F32, stream);
+  });
+}
+
+}  // extern "C"

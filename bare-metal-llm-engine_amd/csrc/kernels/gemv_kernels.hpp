@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W
   }
 }
 
-// LDS slot of element k of the activation vector for gemv_rows_lds_kernel.
+// LDS slot of element k of the activation vector for the LDS-staged kernels.
 // A wave step covers PIECE = 64 * VEC elements, lane l taking elements
 // l*VEC .. l*VEC+VEC-1; the slot order stores, per piece, the first 4 of
 // every lane's elements, then the next 4, so each 16-byte LDS read of a wave
@@ -332,52 +332,20 @@ __device__ __forceinline__ int lds_slot(int k) {
   return p * PIECE + (e >> 2) * 256 + l * 4 + (e & 3);
 }
 
-// Output-major GEMV with the activation vector staged once per workgroup.
-// Same arithmetic contract as gemv_rows_kernel (y[n] = s * sum_k W[n][k] *
-// x[k] * g[k]), for when x (and gamma) are too large to stay in the vector L1
-// across the rows a CU streams: the workgroup loads x, multiplies gamma in,
-// sums x^2 and writes xs = x * gamma into LDS (zero-padded to whole pieces),
-// then each wave streams its R rows against LDS, U loads per row in flight.
-// (Issuing weight loads ahead of the staging measured slower: vector loads
-// complete in order, so the staging then waits for HBM.)
-// Requires K % VEC == 0 and 16-byte aligned W, x and gamma; the caller sizes
-// dynamic LDS as round_up(K, 64 * VEC) floats.
-template <typename WT, int VEC, int R, int U, bool RMS>
-__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict__ W,
-                                                            const float* __restrict__ x,
-                                                            const float* __restrict__ gamma,
-                                                            float* __restrict__ y, long long N,
-                                                            long long K, float eps) {
-  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
-  using V = typename RawVec<WT, VEC>::type;
+// Workgroup-cooperative staging for the LDS kernels (256 threads): writes
+// xs = x * gamma (gamma optional, applied only with RMS) into LDS slots,
+// zero-padded to whole pieces, sums x^2 across the workgroup (RMS) into
+// *total_ss, and ends with a barrier. K % 4 == 0 and 16-byte aligned x /
+// gamma are required. The sum is folded in a fixed order (lanes by shuffle,
+// then waves 0..3), so every workgroup computes the same value.
+template <int VEC, bool RMS>
+__device__ __forceinline__ void stage_xs(const float* __restrict__ x,
+                                         const float* __restrict__ gamma, long long K,
+                                         int npieces, float* xs, float* wave_ss,
+                                         float* total_ss) {
   using F4 = typename RawVec<float, 4>::type;
   constexpr int PIECE = 64 * VEC;
-  extern __shared__ float xs[];
-  __shared__ float wave_ss[4];
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
-  const bool active = n0 < N;
-  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
-
-  const WT* rows[R];
-#pragma unroll
-  for (int r = 0; r < R; ++r) rows[r] = W + (active && n0 + r < N ? n0 + r : 0) * K;
-
-  auto load_step = [&](int p0, V (&w)[U][R]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const long long k = static_cast<long long>(p0 + u) * PIECE + lane * VEC;
-      const bool ok = active && k < K;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        w[u][r] = ok ? __builtin_nontemporal_load(reinterpret_cast<const V*>(rows[r] + k)) : V{};
-      }
-    }
-  };
-
-  // Stage xs = x * gamma (4 floats per thread per pass) and sum x^2.
   float ss = 0.0f;
   const int padded = npieces * PIECE;
   for (int k = tid * 4; k < padded; k += 1024) {
@@ -397,17 +365,35 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict
   if constexpr (RMS) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if (lane == 0) wave_ss[wave] = ss;
+    if ((tid & 63) == 0) wave_ss[tid >> 6] = ss;
   }
   __syncthreads();
-  if (!active) return;
+  if constexpr (RMS) *total_ss = ((wave_ss[0] + wave_ss[1]) + wave_ss[2]) + wave_ss[3];
+}
 
-  float acc[R];
+// acc[j] = sum_k rows[j][k] * xs[k] over this lane's elements (the caller
+// folds the lanes): NR weight rows streamed with 16-byte nontemporal loads,
+// U loads per row in flight, against the staged vector in LDS.
+template <typename WT, int VEC, int NR, int U>
+__device__ __forceinline__ void dot_rows_lds(const WT* const (&rows)[NR], const float* xs,
+                                             long long K, int npieces, int lane,
+                                             float (&acc)[NR]) {
+  using V = typename RawVec<WT, VEC>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 64 * VEC;
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
   for (int p0 = 0; p0 < npieces; p0 += U) {
-    V cur[U][R];
-    load_step(p0, cur);
+    V cur[U][NR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long k = static_cast<long long>(p0 + u) * PIECE + lane * VEC;
+      const bool ok = k < K;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        cur[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const V*>(rows[j] + k)) : V{};
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if (p0 + u >= npieces) break;  // wave-uniform
@@ -418,8 +404,8 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
 #pragma unroll
-          for (int r = 0; r < R; ++r) {
-            acc[r] = fmaf(a[e], static_cast<float>(cur[u][r][h * 4 + e]), acc[r]);
+          for (int j = 0; j < NR; ++j) {
+            acc[j] = fmaf(a[e], static_cast<float>(cur[u][j][h * 4 + e]), acc[j]);
           }
         }
       }
@@ -428,16 +414,100 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] += __shfl_xor(acc[r], off);
+    for (int j = 0; j < NR; ++j) acc[j] += __shfl_xor(acc[j], off);
   }
+}
+
+// Output-major GEMV with the activation vector staged once per workgroup.
+// Same arithmetic contract as gemv_rows_kernel (y[n] = s * sum_k W[n][k] *
+// x[k] * g[k]), for when x (and gamma) are too large to stay in the vector L1
+// across the rows a CU streams: the workgroup stages x * gamma in LDS
+// (stage_xs), then each wave streams its R rows against LDS, U loads per row
+// in flight (dot_rows_lds). (Issuing weight loads ahead of the staging
+// measured slower: vector loads complete in order, so the staging then waits
+// for HBM.) Requires K % VEC == 0 and 16-byte aligned W, x and gamma; the
+// caller sizes dynamic LDS as round_up(K, 64 * VEC) floats.
+template <typename WT, int VEC, int R, int U, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict__ W,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            float* __restrict__ y, long long N,
+                                                            long long K, float eps) {
+  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
+  constexpr int PIECE = 64 * VEC;
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
+  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
+
+  float total_ss = 0.0f;
+  stage_xs<VEC, RMS>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
+  if (n0 >= N) return;
+
+  const WT* rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) rows[r] = W + (n0 + r < N ? n0 + r : n0) * K;
+  float acc[R];
+  dot_rows_lds<WT, VEC, R, U>(rows, xs, K, npieces, lane, acc);
   if (lane == 0) {
-    float scale = 1.0f;
-    if constexpr (RMS) {
-      scale = rms_scale(((wave_ss[0] + wave_ss[1]) + wave_ss[2]) + wave_ss[3], K, eps);
-    }
+    const float scale = RMS ? rms_scale(total_ss, K, eps) : 1.0f;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (n0 + r < N) y[n0 + r] = RMS ? acc[r] * scale : acc[r];
+    }
+  }
+}
+
+// SiLU(g) * u with SiLU(g) = g / (1 + e^-g) (reference src/cpu_ref/swiglu_cpu.cpp:
+// 23-25): fp32 exp and a correctly rounded divide; large negative g gives
+// g / inf = -0, large positive g gives g.
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
+// Fused RMSNorm + gate / up projections + SwiGLU for decode (M = 1),
+// output-major weights Wg, Wu [N x K]:
+//   act[n] = SiLU(s * Wg[n] . xs) * (s * Wu[n] . xs),  xs = x * gamma.
+// The staged vector is shared by both projections; each wave streams the
+// gate and up rows of its R outputs together (2R weight streams), so the
+// intermediate gate / up vectors never reach memory and the FFN saves a
+// launch. Same requirements as gemv_rows_lds_kernel.
+template <typename WT, int VEC, int R, int U, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_glu_kernel(const WT* __restrict__ Wg,
+                                                            const WT* __restrict__ Wu,
+                                                            const float* __restrict__ x,
+                                                            const float* __restrict__ gamma,
+                                                            float* __restrict__ act, long long N,
+                                                            long long K, float eps) {
+  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
+  constexpr int PIECE = 64 * VEC;
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
+  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
+
+  float total_ss = 0.0f;
+  stage_xs<VEC, RMS>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
+  if (n0 >= N) return;
+
+  const WT* rows[2 * R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const long long n = n0 + r < N ? n0 + r : n0;
+    rows[r] = Wg + n * K;
+    rows[R + r] = Wu + n * K;
+  }
+  float acc[2 * R];
+  dot_rows_lds<WT, VEC, 2 * R, U>(rows, xs, K, npieces, lane, acc);
+  if (lane == 0) {
+    const float scale = RMS ? rms_scale(total_ss, K, eps) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (n0 + r < N) act[n0 + r] = swiglu_f32(acc[r] * scale, acc[R + r] * scale);
     }
   }
 }

@@ -52,6 +52,10 @@ void launch_gemm(const GemmArgs& a, hipStream_t stream);
 void launch_rmsnorm(const float* in, const float* weight, float* out, long long rows,
                     long long cols, float eps, hipStream_t stream);
 
+// out[i] = SiLU(g[i]) * u[i] in fp32.
+void launch_swiglu_f32(const float* g, const float* u, float* out, long long n,
+                       hipStream_t stream);
+
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 

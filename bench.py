@@ -1,7 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,stack]
+                    [--only config2,config3,refapi,gemm,ffn,stack]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -423,18 +423,76 @@ def rows_gemm(eng, timer) -> list:
     return rows
 
 
+def rows_ffn(eng, timer) -> list:
+    """The ops either side of the linear layers, and the fused gate/up + SwiGLU."""
+    rows = []
+    rng = np.random.default_rng(10)
+    H, F = 4096, 11008
+    # residual_rmsnorm: decode row and a prefill batch (reads x, residual, gain;
+    # writes sum and norm).
+    for R in (1, 128):
+        dx = eng.upload(rng.standard_normal((R, H), dtype=np.float32))
+        dr = eng.upload(rng.standard_normal((R, H), dtype=np.float32))
+        dw = eng.upload((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        dn, dsum = eng.empty((R, H), np.float32), eng.empty((R, H), np.float32)
+        f = eng.lib.eng_residual_rmsnorm_f32
+        st = timer.sampled(lambda i, s: f(dx.ptr, dr.ptr, dw.ptr, dn.ptr, dsum.ptr, R, H, 1e-5, s))
+        rows.append(hbm_row(f"residual_rmsnorm {R}x{H}", st, 16 * R * H + 4 * H))
+        for d in (dx, dr, dw, dn, dsum):
+            d.free()
+    # swiglu over a decode row and a prefill batch of the FFN width.
+    for R in (1, 128):
+        dg = eng.upload(rng.standard_normal(R * F, dtype=np.float32))
+        du = eng.upload(rng.standard_normal(R * F, dtype=np.float32))
+        do = eng.empty(R * F, np.float32)
+        f = eng.lib.eng_swiglu_f32
+        st = timer.sampled(lambda i, s: f(dg.ptr, du.ptr, do.ptr, R * F, s))
+        rows.append(hbm_row(f"swiglu {R}x{F}", st, 12 * R * F))
+        for d in (dg, du, do):
+            d.free()
+    # Config-5 gate/up + SwiGLU at decode, cold (6 rotating pairs of 86 MiB):
+    # one fused launch vs rmsnorm_linear x2 + swiglu.
+    RW = 6
+    base = rand_f16(rng, (F, H))
+    Wg = rotating(eng, base, RW)
+    Wu = rotating(eng, base, RW)
+    dx = eng.upload(rng.standard_normal(H, dtype=np.float32))
+    dgm = eng.upload((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    dgate, dup, dact = (eng.empty(F, np.float32) for _ in range(3))
+    nbytes = 2 * 2 * H * F + 8 * H + 4 * F
+    glu = eng.lib.eng_rmsnorm_linear_swiglu_f16w_nk
+    st = timer.sampled(lambda i, s: glu(dx.ptr, dgm.ptr, Wg[i % RW].ptr, Wu[i % RW].ptr, dact.ptr,
+                                        1, F, H, 1e-5, s))
+    rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, fused (1 launch)", st, nbytes))
+    rl, sw = eng.lib.eng_rmsnorm_linear_f16w_nk, eng.lib.eng_swiglu_f32
+
+    def unfused(i, s):
+        rl(dx.ptr, dgm.ptr, Wg[i % RW].ptr, dgate.ptr, 1, F, H, 1e-5, s)
+        rl(dx.ptr, dgm.ptr, Wu[i % RW].ptr, dup.ptr, 1, F, H, 1e-5, s)
+        sw(dgate.ptr, dup.ptr, dact.ptr, F, s)
+
+    st = timer.sampled(unfused)
+    rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, unfused (3 launches)", st, nbytes))
+    for d in Wg + Wu + [dx, dgm, dgate, dup, dact]:
+        d.free()
+    return rows
+
+
 def rows_stack(eng, timer) -> list:
-    return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True)]
+    return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True),
+            bench_llama_stack(eng, timer, nk=True, fused_glu=True)]
 
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
-          "gemm": rows_gemm, "stack": rows_stack}
+          "gemm": rows_gemm, "ffn": rows_ffn, "stack": rows_stack}
 
 
-def bench_llama_stack(eng, timer, nk=False) -> dict:
+def bench_llama_stack(eng, timer, nk=False, fused_glu=False) -> dict:
     """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
     rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
-    nk=False stores every weight [in x out] (reference layout), nk=True [out x in]."""
+    nk=False stores every weight [in x out] (reference layout), nk=True [out x in].
+    fused_glu=True (output-major only) runs gate, up and SwiGLU as one launch
+    and feeds SiLU(gate) * up to the down projection (6 launches per layer)."""
     H, F, L = 4096, 11008, 32
     rng = np.random.default_rng(4)
     if nk:
@@ -462,14 +520,19 @@ def bench_llama_stack(eng, timer, nk=False) -> dict:
     else:
         gv, rl = eng.lib.eng_gemv_f16w, eng.lib.eng_rmsnorm_linear_f16w
 
+    glu = eng.lib.eng_rmsnorm_linear_swiglu_f16w_nk
+
     def token(_i, s):
         for lay in layers:
             gv(lay["q"].ptr, xh.ptr, q.ptr, H, H, s)
             gv(lay["k"].ptr, xh.ptr, k.ptr, H, H, s)
             gv(lay["v"].ptr, xh.ptr, v.ptr, H, H, s)
             gv(lay["o"].ptr, v.ptr, o.ptr, H, H, s)
-            rl(o.ptr, g.ptr, lay["gate"].ptr, gate.ptr, 1, F, H, 1e-5, s)
-            rl(o.ptr, g.ptr, lay["up"].ptr, up.ptr, 1, F, H, 1e-5, s)
+            if fused_glu:
+                glu(o.ptr, g.ptr, lay["gate"].ptr, lay["up"].ptr, gate.ptr, 1, F, H, 1e-5, s)
+            else:
+                rl(o.ptr, g.ptr, lay["gate"].ptr, gate.ptr, 1, F, H, 1e-5, s)
+                rl(o.ptr, g.ptr, lay["up"].ptr, up.ptr, 1, F, H, 1e-5, s)
             gv(lay["down"].ptr, gate.ptr, xh.ptr, H, F, s)
 
     st = timer.sampled(token, samples=10)
@@ -479,9 +542,11 @@ def bench_llama_stack(eng, timer, nk=False) -> dict:
         for d in lay.values():
             d.free()
     layout = "output-major W[out x in]" if nk else "reference layout W[in x out]"
+    if fused_glu:
+        layout += ", gate/up + SwiGLU fused"
     row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
                   st, wbytes + abytes)
-    row["launches_per_token"] = 7 * L
+    row["launches_per_token"] = (6 if fused_glu else 7) * L
     return row
 
 

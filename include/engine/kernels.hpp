@@ -113,6 +113,49 @@ inline void rmsnorm_linear_nk(const float* in, const float* rms_weight, const fl
   ENGINE_ABI_CHECK(eng_rmsnorm_linear_f32_nk(in, rms_weight, W, out, M, N, K, eps, stream));
 }
 
+/// out[i] = a[i] + b[i], bit-exact (reference kernels.hpp:47-50).
+inline void vector_add(const float* a, const float* b, float* out, std::int64_t n,
+                       hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_vector_add_f32(a, b, out, n, stream));
+}
+
+/// sum_out = x + residual; norm_out = RMSNorm(sum_out, weight, eps); `weight`
+/// may be nullptr (reference kernels.hpp:106-112).
+inline void residual_rmsnorm(const float* x, const float* residual, const float* weight,
+                             float* norm_out, float* sum_out, std::int64_t rows,
+                             std::int64_t cols, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_residual_rmsnorm_f32(x, residual, weight, norm_out, sum_out, rows, cols, eps, stream));
+}
+
+/// out[i] = SiLU(gate[i]) * up[i] (reference kernels.hpp:138-142).
+inline void swiglu(const float* gate, const float* up, float* out, std::int64_t n,
+                   hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_swiglu_f32(gate, up, out, n, stream));
+}
+inline void swiglu_fp16(const half* gate, const half* up, half* out, std::int64_t n,
+                        hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_swiglu_f16(detail::bits(gate), detail::bits(up), detail::bits(out), n, stream));
+}
+
+/// Gate / up half of a SwiGLU FFN with output-major weights [N x K]:
+/// act = SiLU(RMSNorm(in) * W_gate^T) * (RMSNorm(in) * W_up^T). One launch at
+/// M == 1 (additive; the reference composes rmsnorm, two GEMVs and swiglu).
+inline void rmsnorm_linear_swiglu_nk(const float* in, const float* rms_weight, const half* W_gate,
+                                     const half* W_up, float* act, std::int64_t M, std::int64_t N,
+                                     std::int64_t K, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_rmsnorm_linear_swiglu_f16w_nk(in, rms_weight, detail::bits(W_gate),
+                                                     detail::bits(W_up), act, M, N, K, eps,
+                                                     stream));
+}
+inline void rmsnorm_linear_swiglu_nk(const float* in, const float* rms_weight, const float* W_gate,
+                                     const float* W_up, float* act, std::int64_t M, std::int64_t N,
+                                     std::int64_t K, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_rmsnorm_linear_swiglu_f32_nk(in, rms_weight, W_gate, W_up, act, M, N, K, eps, stream));
+}
+
 }  // namespace hip
 
 // Call sites written against the reference use engine::cuda::...

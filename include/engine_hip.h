@@ -246,6 +246,51 @@ int eng_rmsnorm_linear_fused_direct_f32(const float* in, const float* rms_weight
                                         const float* W, float* out, int64_t M, int64_t N,
                                         int64_t K, float eps, eng_stream stream);
 
+/* ------------------------------------------------------------------------
+ * The ops either side of the linear layers (SwiGLU FFN, residual stream).
+ * ---------------------------------------------------------------------- */
+
+/* out[i] = a[i] + b[i], bit-exact fp32 addition. n < 0 -> "n must be
+ * non-negative"; n == 0 returns before the pointer check; null -> "null device
+ * pointer". Replaces engine::cuda::vector_add
+ * (reference include/engine/kernels.hpp:47-50, kernels/vector_add.cu:119-149). */
+int eng_vector_add_f32(const float* a, const float* b, float* out, int64_t n, eng_stream stream);
+
+/* sum_out = x + residual (bit-exact); norm_out = sum_out / sqrt(mean(sum_out^2)
+ * + eps) * weight, per row of [rows x cols]; weight may be NULL, the other
+ * pointers may not ("null device pointer"); "negative dimension"; "eps must be
+ * non-negative"; rows or cols == 0 writes nothing. Replaces
+ * engine::cuda::residual_rmsnorm (reference include/engine/kernels.hpp:106-112,
+ * kernels/residual_rmsnorm.cu:124-150). */
+int eng_residual_rmsnorm_f32(const float* x, const float* residual, const float* weight,
+                             float* norm_out, float* sum_out, int64_t rows, int64_t cols,
+                             float eps, eng_stream stream);
+
+/* out[i] = SiLU(gate[i]) * up[i], SiLU(g) = g / (1 + exp(-g)), fp32 (and half
+ * in / out with fp32 arithmetic, rounded to nearest even). "gate is null" /
+ * "up is null" / "out is null"; "n must be non-negative"; n == 0 is a no-op.
+ * Replace engine::cuda::swiglu / swiglu_fp16
+ * (reference include/engine/kernels.hpp:138-142, kernels/swiglu.cu:155-227). */
+int eng_swiglu_f32(const float* gate, const float* up, float* out, int64_t n, eng_stream stream);
+int eng_swiglu_f16(const eng_half* gate, const eng_half* up, eng_half* out, int64_t n,
+                   eng_stream stream);
+
+/* act[M x N] = SiLU(xn . Wg^T) * (xn . Wu^T), xn = RMSNorm(in[M x K], rms_weight,
+ * eps), with output-major W_gate, W_up [N x K]: the gate / up half of a SwiGLU
+ * FFN in one call (no reference counterpart: the reference composes rmsnorm,
+ * two GEMV / GEMMs and swiglu, tests/test_kernels.cu:2867-2898). Decode
+ * (M == 1) is a single fused launch; other shapes use pooled scratch for gate
+ * and up. rms_weight may be NULL. Messages: "negative dimension", "null device
+ * pointer", "eps must be non-negative"; any zero dimension writes nothing. */
+int eng_rmsnorm_linear_swiglu_f16w_nk(const float* in, const float* rms_weight,
+                                      const eng_half* W_gate, const eng_half* W_up, float* act,
+                                      int64_t M, int64_t N, int64_t K, float eps,
+                                      eng_stream stream);
+int eng_rmsnorm_linear_swiglu_f32_nk(const float* in, const float* rms_weight,
+                                     const float* W_gate, const float* W_up, float* act,
+                                     int64_t M, int64_t N, int64_t K, float eps,
+                                     eng_stream stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

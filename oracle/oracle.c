@@ -26,6 +26,23 @@
  *                         ones, planted dropped-gain mutation must be caught.
  *   orc_rmsnorm_linear_f16w  equality with orc_rmsnorm_linear on the
  *                         half-decoded matrix.
+ *   orc_vector_add        exact: a + b is one float rounding, compared bit for
+ *                         bit with NumPy float32 addition.
+ *   orc_residual_rmsnorm  golden vectors (RESIDUAL_RMSNORM_SHAPES), zeros give
+ *                         zeros not NaN, NULL weight == ones, sum_out bit-exact
+ *                         x + residual, equality with orc_rmsnorm of the sum;
+ *                         planted dropped-residual mutation must be caught.
+ *   orc_swiglu            golden vectors (SWIGLU_SIZES, NumPy float64 with the
+ *                         overflow-safe sigmoid), closed forms silu(0) = 0,
+ *                         up = 0 gives 0, silu(g) - silu(-g) == g, large |g|
+ *                         limits; planted sign-flipped sigmoid must be caught.
+ *   orc_swiglu_fp16       golden vectors with half output rounding, exact
+ *                         agreement with orc_swiglu of the decoded halves
+ *                         rounded to half.
+ *   orc_rmsnorm_linear_swiglu(_f16w)  bit-exact equality with orc_rmsnorm_linear
+ *                         (gate and up) followed by orc_swiglu.
+ *   orc_ffn_subblock      golden vectors (FFN_SUBBLOCK_CASES), equality with the
+ *                         composition of the pinned functions.
  *   half conversions      all 65536 half -> float against NumPy float16,
  *                         float -> half against NumPy on 2^24 sampled floats
  *                         plus every boundary case; planted truncation
@@ -235,4 +252,112 @@ void orc_rmsnorm_linear(const float* in, const float* rms_weight, const float* W
 void orc_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const uint16_t* W,
                              float* out, int64_t M, int64_t N, int64_t K, float eps) {
   rmsnorm_linear_any(in, rms_weight, NULL, W, out, M, N, K, eps);
+}
+
+/* ------------------------------------------------------ elementwise ops */
+
+void orc_vector_add(const float* a, const float* b, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = a[i] + b[i];
+}
+
+void orc_residual_rmsnorm(const float* x, const float* residual, const float* weight,
+                          float* norm_out, float* sum_out, int64_t rows, int64_t cols, float eps) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * cols;
+    const float* rr = residual != NULL ? residual + r * cols : NULL;
+    float* dn = norm_out + r * cols;
+    float* ds = sum_out != NULL ? sum_out + r * cols : NULL;
+    double sumsq = 0.0;
+    for (int64_t c = 0; c < cols; ++c) {
+#if ORC_MUTATION == 7
+      /* planted mistake: the residual is not added */
+      const float s = xr[c];
+      (void)rr;
+#else
+      const float s = xr[c] + (rr != NULL ? rr[c] : 0.0f);
+#endif
+      if (ds != NULL) ds[c] = s;
+      sumsq += (double)s * (double)s;
+    }
+    const float scale = (float)(1.0 / sqrt(sumsq / (double)cols + (double)eps));
+    for (int64_t c = 0; c < cols; ++c) {
+#if ORC_MUTATION == 7
+      const float s = xr[c];
+#else
+      const float s = xr[c] + (rr != NULL ? rr[c] : 0.0f);
+#endif
+      const float w = weight != NULL ? weight[c] : 1.0f;
+      dn[c] = s * scale * w;
+    }
+  }
+}
+
+static double silu64(double g) {
+#if ORC_MUTATION == 6
+  /* planted mistake: sigmoid with the wrong sign */
+  return g / (1.0 + exp(g));
+#else
+  return g / (1.0 + exp(-g));
+#endif
+}
+
+void orc_swiglu(const float* gate, const float* up, float* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = (float)(silu64((double)gate[i]) * (double)up[i]);
+}
+
+void orc_swiglu_fp16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double g = (double)orc_half_to_float(gate[i]);
+    const double u = (double)orc_half_to_float(up[i]);
+    out[i] = orc_float_to_half((float)(silu64(g) * u));
+  }
+}
+
+static void rmsnorm_linear_swiglu_any(const float* in, const float* rms_weight, const float* Wgf,
+                                      const float* Wuf, const uint16_t* Wgh, const uint16_t* Wuh,
+                                      float* act, int64_t M, int64_t N, int64_t K, float eps) {
+  const size_t n = (size_t)(M > 0 ? M : 1) * (size_t)(N > 0 ? N : 1);
+  float* gate = (float*)malloc(n * sizeof(float));
+  float* up = (float*)malloc(n * sizeof(float));
+  if (gate == NULL || up == NULL) abort();
+  rmsnorm_linear_any(in, rms_weight, Wgf, Wgh, gate, M, N, K, eps);
+  rmsnorm_linear_any(in, rms_weight, Wuf, Wuh, up, M, N, K, eps);
+  orc_swiglu(gate, up, act, M * N);
+  free(gate);
+  free(up);
+}
+
+void orc_rmsnorm_linear_swiglu(const float* in, const float* rms_weight, const float* Wg,
+                               const float* Wu, float* act, int64_t M, int64_t N, int64_t K,
+                               float eps) {
+  rmsnorm_linear_swiglu_any(in, rms_weight, Wg, Wu, NULL, NULL, act, M, N, K, eps);
+}
+
+void orc_rmsnorm_linear_swiglu_f16w(const float* in, const float* rms_weight, const uint16_t* Wg,
+                                    const uint16_t* Wu, float* act, int64_t M, int64_t N,
+                                    int64_t K, float eps) {
+  rmsnorm_linear_swiglu_any(in, rms_weight, NULL, NULL, Wg, Wu, act, M, N, K, eps);
+}
+
+void orc_ffn_subblock(const float* h, const float* ffn_norm_w, const float* Wg, const float* Wu,
+                      const float* Wd, float* out, int64_t S, int64_t D, int64_t F, float eps) {
+  const size_t sd = (size_t)(S > 0 ? S : 1) * (size_t)(D > 0 ? D : 1);
+  const size_t sf = (size_t)(S > 0 ? S : 1) * (size_t)(F > 0 ? F : 1);
+  float* hn = (float*)malloc(sd * sizeof(float));
+  float* gate = (float*)malloc(sf * sizeof(float));
+  float* up = (float*)malloc(sf * sizeof(float));
+  float* act = (float*)malloc(sf * sizeof(float));
+  float* down = (float*)malloc(sd * sizeof(float));
+  if (!hn || !gate || !up || !act || !down) abort();
+  orc_rmsnorm(h, ffn_norm_w, hn, S, D, eps);
+  orc_matmul(hn, Wg, gate, S, F, D);
+  orc_matmul(hn, Wu, up, S, F, D);
+  orc_swiglu(gate, up, act, S * F);
+  orc_matmul(act, Wd, down, S, D, F);
+  orc_vector_add(h, down, out, S * D);
+  free(hn);
+  free(gate);
+  free(up);
+  free(act);
+  free(down);
 }

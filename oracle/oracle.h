@@ -47,6 +47,41 @@ void orc_rmsnorm_linear(const float* in, const float* rms_weight, const float* W
 void orc_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const uint16_t* W,
                              float* out, int64_t M, int64_t N, int64_t K, float eps);
 
+/* out[i] = a[i] + b[i] (reference src/cpu_ref/vector_add_cpu.cpp:8-12). */
+void orc_vector_add(const float* a, const float* b, float* out, int64_t n);
+
+/* sum = x + residual (float), written to sum_out when it is not NULL;
+ * norm_out = sum / sqrt(mean(sum^2) + eps) * weight with the mean in double and
+ * the scale rounded to float (reference src/cpu_ref/residual_rmsnorm_cpu.cpp:19-50).
+ * residual, weight and sum_out may be NULL. */
+void orc_residual_rmsnorm(const float* x, const float* residual, const float* weight,
+                          float* norm_out, float* sum_out, int64_t rows, int64_t cols, float eps);
+
+/* out[i] = g / (1 + exp(-g)) * u in double, rounded to float
+ * (reference src/cpu_ref/swiglu_cpu.cpp:15-27). */
+void orc_swiglu(const float* gate, const float* up, float* out, int64_t n);
+
+/* Half gate / up / out, the same double formula, output rounded to half
+ * (reference src/cpu_ref/swiglu_cpu.cpp:29-41). */
+void orc_swiglu_fp16(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t n);
+
+/* act = swiglu(rmsnorm_linear(in, w, Wg), rmsnorm_linear(in, w, Wu)) with
+ * Wg, Wu [K x N] (fp32, or half when the _f16w form): the gate / up projections
+ * of a SwiGLU FFN, stated as the reference composes them (tests/test_kernels.cu:
+ * 2900-2915: rmsnorm, matmul x2, swiglu). */
+void orc_rmsnorm_linear_swiglu(const float* in, const float* rms_weight, const float* Wg,
+                               const float* Wu, float* act, int64_t M, int64_t N, int64_t K,
+                               float eps);
+void orc_rmsnorm_linear_swiglu_f16w(const float* in, const float* rms_weight, const uint16_t* Wg,
+                                    const uint16_t* Wu, float* act, int64_t M, int64_t N,
+                                    int64_t K, float eps);
+
+/* The SwiGLU FFN sub-block (reference tests/test_kernels.cu:2900-2915,
+ * run_ffn_subblock_cpu): out = h + swiglu(n.Wg, n.Wu).Wd with n = rmsnorm(h, w);
+ * h [S x D], Wg / Wu [D x F], Wd [F x D]. */
+void orc_ffn_subblock(const float* h, const float* ffn_norm_w, const float* Wg, const float* Wu,
+                      const float* Wd, float* out, int64_t S, int64_t D, int64_t F, float eps);
+
 /* IEEE-754 binary16 conversions: half -> float exact; float -> half rounds to
  * nearest, ties to even (the rounding of the reference's CUDA build,
  * include/engine/half.hpp:28-32). */

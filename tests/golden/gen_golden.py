@@ -7,6 +7,9 @@ tools/gen_reference.py:401-440 for shapes, :668-741 for distributions):
 inputs ~ N(0, 1), matrices scaled by 1/sqrt(K), RMSNorm gains ~ 1 + N(0, 0.1^2),
 eps = 1e-5. Added cases: BASELINE config 1 (512^3, U[-1, 1], seed 0) and the
 fp16-weight variants with fp32 activations (gemv_f16w, rmsnorm_linear_f16w).
+The FFN-side ops follow :410-415 (residual_rmsnorm), :451 (swiglu) and
+:488-491 / :906-928 (FFN sub-block); the fused gate/up + SwiGLU cases are this
+build's own.
 
 Inputs are not stored: each is rebuilt from its generator spec by
 tests/golden/detgen.py and checked against the SHA-256 recorded here.
@@ -41,6 +44,14 @@ RMSNORM_LINEAR_SHAPES = [
 ]
 GEMV_SHAPES = [(256, 4096), (768, 256), (127, 31), (64, 128)]
 GEMV_FP16_SHAPES = [(64, 64), (128, 256), (73, 125), (256, 4096)]
+# reference tools/gen_reference.py:410-415, :451, :488-491
+RESIDUAL_RMSNORM_SHAPES = [(1, 4096, True), (128, 4096, True), (32, 127, True), (32, 4096, False)]
+SWIGLU_SIZES = [1, 65, 1024, 4096, 11008]
+FFN_SUBBLOCK_CASES = [("prefill_s16_d512_ffn1408", 16, 512, 1408), ("decode_s1_d512_ffn1408", 1, 512, 1408)]
+# Fused gate/up + SwiGLU of the FFN (no reference counterpart): decode, prefill, ragged.
+RMSNORM_LINEAR_SWIGLU_SHAPES = [(1, 1408, 512, True), (16, 1408, 512, True), (3, 257, 100, False)]
+# reference :379 without its 1 Mi case (tests check large sizes against float32 addition)
+VECTOR_ADD_SIZES = [1, 31, 32, 33, 255, 256, 257, 4096]
 
 
 def f64(a: np.ndarray, dtype: str) -> np.ndarray:
@@ -48,6 +59,13 @@ def f64(a: np.ndarray, dtype: str) -> np.ndarray:
     if dtype == "f16":
         return a.view(np.float16).astype(np.float64)
     return a.astype(np.float64)
+
+
+def silu64(g: np.ndarray) -> np.ndarray:
+    """g * sigmoid(g) with the overflow-safe sigmoid of the reference's generator
+    (tools/gen_reference.py:158-163)."""
+    e = np.exp(-np.abs(g))
+    return g * np.where(g >= 0.0, 1.0 / (1.0 + e), e / (1.0 + e))
 
 
 def rms_rows(x64: np.ndarray, w64) -> np.ndarray:
@@ -67,12 +85,15 @@ class Builder:
         self.next_seed += 1
         return s
 
-    def add(self, stem, op, params, specs, expected):
+    def add(self, stem, op, params, specs, expected, extra=None):
         inputs = {}
         for name, s in specs.items():
             arr = detgen.make(s)
             inputs[name] = dict(s, sha256=detgen.digest(arr))
-        engref.write(HERE / "data" / f"{stem}.bin", {"expected": expected.astype(np.float32)})
+        tensors = {"expected": expected.astype(np.float32)}
+        for name, arr in (extra or {}).items():
+            tensors[name] = arr.astype(np.float32)
+        engref.write(HERE / "data" / f"{stem}.bin", tensors)
         self.cases.append({"stem": stem, "op": op, "params": params, "inputs": inputs})
 
     def build(self):
@@ -132,6 +153,70 @@ class Builder:
                 A = f64(detgen.make(specs["A"]), "f16")
                 x = f64(detgen.make(specs["x"]), xdt)
                 self.add(f"{tag}__{n}x{k}", tag, {"N": n, "K": k}, specs, x @ A)
+
+        self.build_ffn_ops()
+
+    def build_ffn_ops(self):
+        """The ops either side of the linear layers (SwiGLU FFN)."""
+        for n in VECTOR_ADD_SIZES:
+            specs = {"a": self.spec("normal", (n,)), "b": self.spec("normal", (n,))}
+            a, b = (f64(detgen.make(specs[x]), "f32") for x in ("a", "b"))
+            self.add(f"vector_add__n{n}", "vector_add", {"n": n}, specs, a + b)
+
+        for rows, cols, with_w in RESIDUAL_RMSNORM_SHAPES:
+            specs = {"x": self.spec("normal", (rows, cols)), "residual": self.spec("normal", (rows, cols))}
+            if with_w:
+                specs["weight"] = self.spec("normal", (cols,), mean=1.0, std=0.1)
+            x = f64(detgen.make(specs["x"]), "f32")
+            r = f64(detgen.make(specs["residual"]), "f32")
+            w = f64(detgen.make(specs["weight"]), "f32") if with_w else None
+            sfx = "w" if with_w else "now"
+            self.add(f"residual_rmsnorm__{rows}x{cols}_{sfx}", "residual_rmsnorm",
+                     {"rows": rows, "cols": cols, "eps": EPS}, specs, rms_rows(x + r, w))
+        specs = {"x": self.spec("zeros", (2, 256)), "residual": self.spec("zeros", (2, 256))}
+        self.add("residual_rmsnorm__zeros", "residual_rmsnorm", {"rows": 2, "cols": 256, "eps": EPS},
+                 specs, np.zeros((2, 256)))
+
+        for dt, tag in (("f32", "swiglu"), ("f16", "swiglu_fp16")):
+            for n in SWIGLU_SIZES:
+                specs = {"gate": self.spec("normal", (n,), dtype=dt), "up": self.spec("normal", (n,), dtype=dt)}
+                g, u = (f64(detgen.make(specs[x]), dt) for x in ("gate", "up"))
+                self.add(f"{tag}__n{n}", tag, {"n": n}, specs, silu64(g) * u)
+
+        for wdt, tag in (("f32", "rmsnorm_linear_swiglu"), ("f16", "rmsnorm_linear_swiglu_f16w")):
+            for m, n, k, with_w in RMSNORM_LINEAR_SWIGLU_SHAPES:
+                sc = 1.0 / np.sqrt(max(k, 1))
+                specs = {
+                    "input": self.spec("normal", (m, k)),
+                    "Wg": self.spec("normal", (k, n), dtype=wdt, std=sc),
+                    "Wu": self.spec("normal", (k, n), dtype=wdt, std=sc),
+                }
+                if with_w:
+                    specs["weight"] = self.spec("normal", (k,), mean=1.0, std=0.1)
+                x = f64(detgen.make(specs["input"]), "f32")
+                Wg = f64(detgen.make(specs["Wg"]), wdt)
+                Wu = f64(detgen.make(specs["Wu"]), wdt)
+                w = f64(detgen.make(specs["weight"]), "f32") if with_w else None
+                xn = rms_rows(x, w)
+                gate, up = xn @ Wg, xn @ Wu
+                sfx = "w" if with_w else "now"
+                self.add(f"{tag}__{m}x{n}x{k}_{sfx}", tag, {"M": m, "N": n, "K": k, "eps": EPS},
+                         specs, silu64(gate) * up, extra={"gate": gate, "up": up})
+
+        for name, s_q, d, f in FFN_SUBBLOCK_CASES:
+            specs = {
+                "x": self.spec("normal", (s_q, d)),
+                "ffn_rms_w": self.spec("normal", (d,), mean=1.0, std=0.1),
+                "w_gate": self.spec("normal", (d, f), std=1.0 / np.sqrt(d)),
+                "w_up": self.spec("normal", (d, f), std=1.0 / np.sqrt(d)),
+                "w_down": self.spec("normal", (f, d), std=1.0 / np.sqrt(f)),
+            }
+            x, w, wg, wu, wd = (f64(detgen.make(specs[k]), "f32")
+                                for k in ("x", "ffn_rms_w", "w_gate", "w_up", "w_down"))
+            xn = rms_rows(x, w)
+            act = silu64(xn @ wg) * (xn @ wu)
+            self.add(f"ffn_subblock__{name}", "ffn_subblock", {"S": s_q, "D": d, "F": f, "eps": EPS},
+                     specs, x + act @ wd, extra={"act": act})
 
 
 def main() -> None:

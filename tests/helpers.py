@@ -84,6 +84,13 @@ class Oracle:
             "orc_rmsnorm_linear_f16w": [p, p, p, p, i64, i64, i64, f],
             "orc_f16_to_f32": [p, p, i64],
             "orc_f32_to_f16": [p, p, i64],
+            "orc_vector_add": [p, p, p, i64],
+            "orc_residual_rmsnorm": [p, p, p, p, p, i64, i64, f],
+            "orc_swiglu": [p, p, p, i64],
+            "orc_swiglu_fp16": [p, p, p, i64],
+            "orc_rmsnorm_linear_swiglu": [p, p, p, p, p, i64, i64, i64, f],
+            "orc_rmsnorm_linear_swiglu_f16w": [p, p, p, p, p, i64, i64, i64, f],
+            "orc_ffn_subblock": [p, p, p, p, p, p, i64, i64, i64, f],
         }
         for name, args in sig.items():
             fn = getattr(lib, name)
@@ -154,6 +161,66 @@ class Oracle:
            out.ctypes.data, M, N, K, eps)
         return out
 
+    @staticmethod
+    def _p(a):
+        return None if a is None else a.ctypes.data
+
+    def vector_add(self, a, b):
+        a, b = self._c(a, np.float32), self._c(b, np.float32)
+        out = np.empty_like(a)
+        self.lib.orc_vector_add(a.ctypes.data, b.ctypes.data, out.ctypes.data, a.size)
+        return out
+
+    def residual_rmsnorm(self, x, residual, w, eps, want_sum=True):
+        """(norm_out, sum_out); residual and w may be None, want_sum=False
+        passes a NULL sum_out (sum_out is then None)."""
+        x = self._c(x, np.float32)
+        rows, cols = x.shape
+        r = None if residual is None else self._c(residual, np.float32)
+        wp = None if w is None else self._c(w, np.float32)
+        norm = np.empty_like(x)
+        sm = np.empty_like(x) if want_sum else None
+        self.lib.orc_residual_rmsnorm(x.ctypes.data, self._p(r), self._p(wp), norm.ctypes.data,
+                                      self._p(sm), rows, cols, eps)
+        return norm, sm
+
+    def swiglu(self, g, u):
+        g, u = self._c(g, np.float32), self._c(u, np.float32)
+        out = np.empty_like(g)
+        self.lib.orc_swiglu(g.ctypes.data, u.ctypes.data, out.ctypes.data, g.size)
+        return out
+
+    def swiglu_fp16(self, g16, u16):
+        g16, u16 = self._c(g16, np.uint16), self._c(u16, np.uint16)
+        out = np.empty_like(g16)
+        self.lib.orc_swiglu_fp16(g16.ctypes.data, u16.ctypes.data, out.ctypes.data, g16.size)
+        return out
+
+    def rmsnorm_linear_swiglu(self, x, w, Wg, Wu, eps):
+        """Wg, Wu [K x N] (float32, or uint16 half bits)."""
+        x = self._c(x, np.float32)
+        M, K = x.shape
+        half = Wg.dtype == np.uint16
+        dt = np.uint16 if half else np.float32
+        Wg, Wu = self._c(Wg, dt), self._c(Wu, dt)
+        N = Wg.shape[1]
+        out = np.empty((M, N), np.float32)
+        wp = None if w is None else self._c(w, np.float32)
+        fn = self.lib.orc_rmsnorm_linear_swiglu_f16w if half else self.lib.orc_rmsnorm_linear_swiglu
+        fn(x.ctypes.data, self._p(wp), Wg.ctypes.data, Wu.ctypes.data, out.ctypes.data, M, N, K, eps)
+        return out
+
+    def ffn_subblock(self, h, w, Wg, Wu, Wd, eps):
+        h = self._c(h, np.float32)
+        S, D = h.shape
+        F = Wg.shape[1]
+        Wg, Wu, Wd = (self._c(a, np.float32) for a in (Wg, Wu, Wd))
+        wp = None if w is None else self._c(w, np.float32)
+        out = np.empty_like(h)
+        self.lib.orc_ffn_subblock(h.ctypes.data, self._p(wp), Wg.ctypes.data, Wu.ctypes.data,
+                                  Wd.ctypes.data, out.ctypes.data, S, D, F, eps)
+        return out
+
     def f32_to_f16(self, a):
         a = self._c(a, np.float32)
         out = np.empty(a.shape, np.uint16)
@@ -204,8 +271,8 @@ def inputs(c: dict) -> dict:
     return out
 
 
-def expected(c: dict) -> np.ndarray:
-    return engref.read(GOLDEN / "data" / f"{c['stem']}.bin")["expected"].astype(np.float64)
+def expected(c: dict, name: str = "expected") -> np.ndarray:
+    return engref.read(GOLDEN / "data" / f"{c['stem']}.bin")[name].astype(np.float64)
 
 
 def as_f64(a: np.ndarray) -> np.ndarray:

@@ -26,7 +26,9 @@ def test_header_declares_the_hot_path_entry_points():
     names = declared_functions()
     for fn in ("eng_matmul_f32", "eng_gemv_f32", "eng_gemv_f16", "eng_gemv_f16w",
                "eng_rmsnorm_f32", "eng_rmsnorm_linear_f32", "eng_rmsnorm_linear_f16w",
-               "eng_rmsnorm_linear_fused_direct_f32", "eng_last_error"):
+               "eng_rmsnorm_linear_fused_direct_f32", "eng_last_error", "eng_vector_add_f32",
+               "eng_residual_rmsnorm_f32", "eng_swiglu_f32", "eng_swiglu_f16",
+               "eng_rmsnorm_linear_swiglu_f16w_nk", "eng_rmsnorm_linear_swiglu_f32_nk"):
         assert fn in names
 
 
@@ -78,6 +80,26 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_rmsnorm_linear_f16w_nk", P, P, None, P, 2, 2, 2, 1e-5, None), 1, "null device pointer"),
     (("eng_rmsnorm_linear_f32_nk", P, P, P, P, 2, -2, 2, 1e-5, None), 1, "negative dimension"),
     (("eng_rmsnorm_linear_f32_nk", P, P, P, P, 2, 2, 2, -1e-5, None), 1, "eps"),
+    (("eng_vector_add_f32", P, P, P, -1, None), 1, "vector_add: n must be non-negative"),
+    (("eng_vector_add_f32", None, P, P, 4, None), 1, "vector_add: null device pointer"),
+    (("eng_vector_add_f32", P, P, None, 4, None), 1, "null"),
+    (("eng_residual_rmsnorm_f32", P, P, P, P, P, -1, 4, 1e-5, None), 1, "residual_rmsnorm: negative dimension"),
+    (("eng_residual_rmsnorm_f32", P, P, P, P, P, 4, -1, 1e-5, None), 1, "negative dimension"),
+    (("eng_residual_rmsnorm_f32", None, P, P, P, P, 2, 2, 1e-5, None), 1, "null device pointer"),
+    (("eng_residual_rmsnorm_f32", P, None, P, P, P, 2, 2, 1e-5, None), 1, "null"),
+    (("eng_residual_rmsnorm_f32", P, P, P, None, P, 2, 2, 1e-5, None), 1, "null"),
+    (("eng_residual_rmsnorm_f32", P, P, P, P, None, 2, 2, 1e-5, None), 1, "null"),
+    (("eng_residual_rmsnorm_f32", P, P, P, P, P, 4, 4, -1.0, None), 1, "eps"),
+    (("eng_swiglu_f32", None, P, P, 4, None), 1, "swiglu: gate is null"),
+    (("eng_swiglu_f32", P, None, P, 4, None), 1, "swiglu: up is null"),
+    (("eng_swiglu_f32", P, P, None, 4, None), 1, "swiglu: out is null"),
+    (("eng_swiglu_f32", P, P, P, -1, None), 1, "swiglu: n must be non-negative"),
+    (("eng_swiglu_f16", None, P, P, 4, None), 1, "swiglu_fp16: gate is null"),
+    (("eng_swiglu_f16", P, P, P, -1, None), 1, "swiglu_fp16: n must be non-negative"),
+    (("eng_rmsnorm_linear_swiglu_f16w_nk", P, P, None, P, P, 1, 4, 4, 1e-5, None), 1, "null device pointer"),
+    (("eng_rmsnorm_linear_swiglu_f16w_nk", P, P, P, None, P, 1, 4, 4, 1e-5, None), 1, "null"),
+    (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, -4, 4, 1e-5, None), 1, "negative dimension"),
+    (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 4, 4, -1.0, None), 1, "eps"),
 ])
 def test_preconditions_fail_before_launch(eng, call, code, substr):
     name, *args = call
@@ -103,6 +125,13 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_gemv_f16w_nk", P, P, P, 0, 8, None),
     ("eng_rmsnorm_linear_f16w_nk", P, P, P, P, 8, 0, 8, 1e-5, None),
     ("eng_rmsnorm_linear_f32_nk", P, P, P, P, 0, 8, 8, 1e-5, None),
+    ("eng_vector_add_f32", None, None, None, 0, None),
+    ("eng_residual_rmsnorm_f32", P, P, None, P, P, 0, 8, 1e-5, None),
+    ("eng_residual_rmsnorm_f32", P, P, P, P, P, 8, 0, 1e-5, None),
+    ("eng_swiglu_f32", P, P, P, 0, None),
+    ("eng_swiglu_f16", P, P, P, 0, None),
+    ("eng_rmsnorm_linear_swiglu_f16w_nk", P, None, P, P, P, 1, 0, 8, 1e-5, None),
+    ("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 8, 0, 1e-5, None),
 ])
 def test_empty_work_is_a_no_op(eng, call):
     name, *args = call

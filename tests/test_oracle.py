@@ -67,7 +67,113 @@ def check_rmsnorm_linear(orc, c):
     return helpers.assert_within(got, exp, bound, c["stem"])
 
 
+def check_residual_rmsnorm(orc, c):
+    x = helpers.inputs(c)
+    norm, sm = orc.residual_rmsnorm(x["x"], x["residual"], x.get("weight"), EPS)
+    exp = helpers.expected(c)
+    # sum rounded to float (u), scale from the rounded sums (u), scale to float,
+    # two float multiplies, the golden's rounding: 6u relative.
+    helpers.assert_within(norm, exp, 6 * helpers.U32 * np.abs(exp) + 1e-30, c["stem"])
+    # sum_out is one float addition: bit-exact with NumPy's float32 add.
+    assert np.array_equal(sm, x["x"] + x["residual"]), c["stem"] + " sum_out"
+
+
+def check_swiglu(orc, c):
+    x = helpers.inputs(c)
+    got = orc.swiglu(x["gate"], x["up"])
+    exp = helpers.expected(c)
+    # double evaluation then one float rounding, plus the golden's float32 rounding
+    return helpers.assert_within(got, exp, 2 * helpers.U32 * np.abs(exp) + 2.0**-149, c["stem"])
+
+
+def swiglu_bound(g64, u64, dg, du, act64):
+    """|d act| for act = silu(g) u given |d g| <= dg, |d u| <= du (|silu'| < 1.1)."""
+    silu = g64 / (1.0 + np.exp(-g64))
+    return 1.1 * np.abs(u64) * dg + np.abs(silu) * du + dg * du + 2 * helpers.U32 * np.abs(act64)
+
+
+def check_rmsnorm_linear_swiglu(orc, c):
+    x = helpers.inputs(c)
+    got = orc.rmsnorm_linear_swiglu(x["input"], x.get("weight"), x["Wg"], x["Wu"], EPS)
+    exp, g64, u64 = (helpers.expected(c, n) for n in ("expected", "gate", "up"))
+    K = c["params"]["K"]
+    s = helpers.rms_scale64(x["input"])
+    gw = 1.0 if "weight" not in x else helpers.as_f64(x["weight"])
+    xs = np.abs(helpers.as_f64(x["input"]) * gw)
+    ag = s * (xs @ np.abs(helpers.as_f64(x["Wg"])))
+    au = s * (xs @ np.abs(helpers.as_f64(x["Wu"])))
+    dg = 4 * helpers.U32 * ag + 2 * helpers.U32 * np.abs(g64) + 2.0 * K * 2.0**-53 * ag
+    du = 4 * helpers.U32 * au + 2 * helpers.U32 * np.abs(u64) + 2.0 * K * 2.0**-53 * au
+    return helpers.assert_within(got, exp, swiglu_bound(g64, u64, dg, du, exp), c["stem"])
+
+
 # ------------------------------------------------------------------- goldens
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("vector_add")])
+def test_vector_add_is_float32_addition(orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got = orc.vector_add(x["a"], x["b"])
+    assert np.array_equal(got, x["a"] + x["b"])
+    assert np.array_equal(got.astype(np.float64), helpers.expected(c).astype(np.float32).astype(np.float64))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("residual_rmsnorm")])
+def test_residual_rmsnorm_matches_golden(orc, stem):
+    check_residual_rmsnorm(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("swiglu")])
+def test_swiglu_matches_golden(orc, stem):
+    check_swiglu(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("swiglu_fp16")])
+def test_swiglu_fp16_matches_golden(orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    got16 = orc.swiglu_fp16(x["gate"], x["up"])
+    exp = helpers.expected(c)
+    bound = helpers.U16 * np.abs(exp) + 2.0**-25 + 2 * helpers.U32 * np.abs(exp)
+    helpers.assert_within(helpers.as_f64(got16), exp, bound, stem)
+    # the fp32 formula on the decoded halves, rounded to half: bit for bit
+    ref = orc.f32_to_f16(orc.swiglu(orc.f16_to_f32(x["gate"]), orc.f16_to_f32(x["up"])))
+    assert np.array_equal(got16, ref)
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm_linear_swiglu")
+                                  + helpers.cases("rmsnorm_linear_swiglu_f16w")])
+def test_rmsnorm_linear_swiglu_matches_golden(orc, stem):
+    check_rmsnorm_linear_swiglu(orc, helpers.case(stem))
+
+
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("ffn_subblock")])
+def test_ffn_subblock_matches_golden(orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    S, D, F = (c["params"][k] for k in ("S", "D", "F"))
+    got = orc.ffn_subblock(x["x"], x["ffn_rms_w"], x["w_gate"], x["w_up"], x["w_down"], EPS)
+    # The same numbers as the composition of the individually pinned functions.
+    hn = orc.rmsnorm(x["x"], x["ffn_rms_w"], EPS)
+    act = orc.swiglu(orc.matmul(hn, x["w_gate"]), orc.matmul(hn, x["w_up"]))
+    assert np.array_equal(got, orc.vector_add(x["x"], orc.matmul(act, x["w_down"])))
+    # Against the float64 golden: error of act (gate / up as in rmsnorm_linear,
+    # propagated through SwiGLU), carried through the down projection.
+    exp, act64 = helpers.expected(c), helpers.expected(c, "act")
+    h64, w64 = helpers.as_f64(x["x"]), helpers.as_f64(x["ffn_rms_w"])
+    s = helpers.rms_scale64(x["x"])
+    xs = s * np.abs(h64 * w64)
+    g64 = (s * h64 * w64) @ helpers.as_f64(x["w_gate"])
+    u64 = (s * h64 * w64) @ helpers.as_f64(x["w_up"])
+    ag, au = xs @ np.abs(helpers.as_f64(x["w_gate"])), xs @ np.abs(helpers.as_f64(x["w_up"]))
+    dg = 4 * helpers.U32 * ag + 2 * helpers.U32 * np.abs(g64) + 2.0 * D * 2.0**-53 * ag
+    du = 4 * helpers.U32 * au + 2 * helpers.U32 * np.abs(u64) + 2.0 * D * 2.0**-53 * au
+    dact = swiglu_bound(g64, u64, dg, du, act64)
+    wd = np.abs(helpers.as_f64(x["w_down"]))
+    down_bound = dact @ wd + (helpers.U32 + 2.0 * F * 2.0**-53) * (np.abs(act64) @ wd)
+    bound = down_bound + 2 * helpers.U32 * np.abs(exp)
+    helpers.assert_within(got, exp, bound, stem)
+
+
 @pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("matmul")])
 def test_matmul_matches_golden(orc, stem):
     check_matmul(orc, helpers.case(stem))
@@ -191,6 +297,55 @@ def test_rmsnorm_linear_is_rmsnorm_then_matmul(orc):
                           orc.rmsnorm_linear(x, g, orc.f16_to_f32(W16), EPS))
 
 
+def test_residual_rmsnorm_closed_forms(orc):
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5, 300), dtype=np.float32)
+    r = rng.standard_normal((5, 300), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(300)).astype(np.float32)
+    norm, sm = orc.residual_rmsnorm(x, r, g, EPS)
+    # == rmsnorm of the float sum, bit for bit; NULL sum_out changes nothing
+    assert np.array_equal(norm, orc.rmsnorm(x + r, g, EPS))
+    assert np.array_equal(orc.residual_rmsnorm(x, r, g, EPS, want_sum=False)[0], norm)
+    # NULL weight == ones; NULL residual == rmsnorm of x
+    assert np.array_equal(orc.residual_rmsnorm(x, r, None, EPS)[0],
+                          orc.residual_rmsnorm(x, r, np.ones(300, np.float32), EPS)[0])
+    assert np.array_equal(orc.residual_rmsnorm(x, None, g, EPS)[0], orc.rmsnorm(x, g, EPS))
+    z = np.zeros((2, 64), np.float32)
+    nz, sz = orc.residual_rmsnorm(z, z, None, EPS)
+    assert np.all(nz == 0.0) and np.all(sz == 0.0)
+
+
+def test_swiglu_closed_forms(orc):
+    rng = np.random.default_rng(12)
+    g = rng.standard_normal(1000, dtype=np.float32) * 4
+    u = rng.standard_normal(1000, dtype=np.float32)
+    assert np.all(orc.swiglu(np.zeros(1000, np.float32), u) == 0.0)
+    assert np.all(orc.swiglu(g, np.zeros(1000, np.float32)) == 0.0)
+    # silu(g) - silu(-g) == g: sigmoid(g) + sigmoid(-g) == 1
+    one = np.ones(1000, np.float32)
+    d = orc.swiglu(g, one).astype(np.float64) - orc.swiglu(-g, one).astype(np.float64)
+    helpers.assert_within(d, g.astype(np.float64), 2 * helpers.U32 * (np.abs(g) + 1e-30) * 2,
+                          "silu(g) - silu(-g)")
+    # far tails: silu(50) rounds to 50, silu(-50) is ~ -1e-20
+    big = np.full(4, 50.0, np.float32)
+    assert np.array_equal(orc.swiglu(big, u[:4]), (big * u[:4]).astype(np.float32))
+    assert np.all(np.abs(orc.swiglu(-big, one[:4])) < 1e-19)
+    # fp16 form on the same values
+    g16, u16 = orc.f32_to_f16(g), orc.f32_to_f16(u)
+    assert np.all(orc.swiglu_fp16(np.zeros(1000, np.uint16), u16) & 0x7FFF == 0)
+
+
+def test_rmsnorm_linear_swiglu_is_the_composition(orc):
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal((4, 96), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(96)).astype(np.float32)
+    Wg = rng.standard_normal((96, 50), dtype=np.float32) / 10
+    Wu = rng.standard_normal((96, 50), dtype=np.float32) / 10
+    for W1, W2 in ((Wg, Wu), (orc.f32_to_f16(Wg), orc.f32_to_f16(Wu))):
+        ref = orc.swiglu(orc.rmsnorm_linear(x, g, W1, EPS), orc.rmsnorm_linear(x, g, W2, EPS))
+        assert np.array_equal(orc.rmsnorm_linear_swiglu(x, g, W1, W2, EPS), ref)
+
+
 # ---------------------------------------------------------------------- half
 def test_half_to_float_exhaustive(orc):
     bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
@@ -230,6 +385,8 @@ def test_float_to_half_matches_numpy(orc):
     (3, lambda o: check_rmsnorm(o, helpers.case("rmsnorm__1x4096_w"))),
     (4, lambda o: check_rmsnorm_linear(o, helpers.case("rmsnorm_linear__32x256x512_w"))),
     (5, lambda o: test_float_to_half_matches_numpy(o)),
+    (6, lambda o: check_swiglu(o, helpers.case("swiglu__n1024"))),
+    (7, lambda o: check_residual_rmsnorm(o, helpers.case("residual_rmsnorm__1x4096_w"))),
 ])
 def test_planted_mistakes_are_caught(mutation, check):
     mutant = helpers.oracle(mutation)
