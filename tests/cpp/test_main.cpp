@@ -94,6 +94,37 @@ TEST(cpu_contract, empty_work_is_a_no_op_not_an_error) {
   for (float v : g_dummy_f) EXPECT_EQ(v, 0.0f);
 }
 
+TEST(cpu_contract, ffn_side_launchers_keep_the_reference_contract) {
+  float* p = g_dummy_f;
+  engine::half* ph = g_dummy_h;
+  // reference tests/test_kernels.cu:1679-1839, the rows for these launchers
+  EXPECT_THROWS_MSG(engine::cuda::vector_add(p, p, p, -1), "non-negative");
+  EXPECT_THROWS_MSG(engine::cuda::vector_add(nullptr, p, p, 4), "null");
+  EXPECT_NO_THROW(engine::cuda::vector_add(nullptr, nullptr, nullptr, 0));
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, p, p, p, p, -1, 4, 1e-5f), "negative");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, p, p, p, p, 4, -1, 1e-5f), "negative");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, p, p, p, p, 4, 4, -1.0f), "eps");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(nullptr, p, p, p, p, 2, 2, 1e-5f), "null");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, nullptr, p, p, p, 2, 2, 1e-5f), "null");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, p, p, nullptr, p, 2, 2, 1e-5f), "null");
+  EXPECT_THROWS_MSG(engine::cuda::residual_rmsnorm(p, p, p, p, nullptr, 2, 2, 1e-5f), "null");
+  EXPECT_NO_THROW(engine::cuda::residual_rmsnorm(p, p, nullptr, p, p, 0, 0, 1e-5f));
+  EXPECT_NO_THROW(engine::cuda::residual_rmsnorm(p, p, p, p, p, 0, 8, 1e-5f));
+  EXPECT_NO_THROW(engine::cuda::residual_rmsnorm(p, p, p, p, p, 8, 0, 1e-5f));
+  EXPECT_THROWS_MSG(engine::cuda::swiglu(p, p, p, -1), "non-negative");
+  EXPECT_THROWS_MSG(engine::cuda::swiglu_fp16(ph, ph, ph, -1), "non-negative");
+  EXPECT_THROWS_MSG(engine::cuda::swiglu(nullptr, p, p, 4), "null");
+  EXPECT_THROWS_MSG(engine::cuda::swiglu(p, nullptr, p, 4), "null");
+  EXPECT_THROWS_MSG(engine::cuda::swiglu(p, p, nullptr, 4), "null");
+  EXPECT_THROWS_MSG(engine::cuda::swiglu_fp16(nullptr, ph, ph, 4), "null");
+  EXPECT_NO_THROW(engine::cuda::swiglu(p, p, p, 0));
+  EXPECT_NO_THROW(engine::cuda::swiglu_fp16(ph, ph, ph, 0));
+  EXPECT_THROWS_MSG(engine::cuda::rmsnorm_linear_swiglu_nk(p, p, ph, ph, p, 1, -1, 4, 1e-5f),
+                    "negative");
+  EXPECT_NO_THROW(engine::cuda::rmsnorm_linear_swiglu_nk(p, nullptr, p, p, p, 1, 8, 0, 1e-5f));
+  for (float v : g_dummy_f) EXPECT_EQ(v, 0.0f);
+}
+
 TEST(cpu_contract, error_message_layout) {
   try {
     engine::cuda::gemv(nullptr, g_dummy_f, g_dummy_f, 4, 4);
@@ -472,6 +503,65 @@ TEST(gpu_kernels, rmsnorm_linear_multi_stream) {
       if (!(std::fabs(got[j] - runs[i].expected[j]) <= runs[i].bound[j])) ++bad;
     EXPECT_EQ(bad, 0);
   }
+}
+
+TEST(gpu_kernels, ffn_sub_block_through_cpp_api) {
+  // The decode FFN as the engine runs it: fused gate/up + SwiGLU, down
+  // projection, residual add; against a double-precision host reference.
+  require_gpu(ctx);
+  const std::int64_t D = 256, F = 704;
+  const float eps = 1e-5f;
+  std::vector<float> h(D), w(D), Wg(F * D), Wu(F * D), Wd(D * F);
+  std::uint64_t state = 7;
+  auto next = [&state]() {
+    state = state * 6364136223846793005ULL + 1442695040888963407ULL;
+    return static_cast<float>(static_cast<double>(state >> 11) * 0x1p-53 * 2.0 - 1.0);
+  };
+  for (auto& v : h) v = next();
+  for (auto& v : w) v = 1.0f + 0.1f * next();
+  for (auto& v : Wg) v = next() / 16.0f;
+  for (auto& v : Wu) v = next() / 16.0f;
+  for (auto& v : Wd) v = next() / 26.0f;
+  engine::DeviceBuffer<float> dh(h), dw(w), dWg(Wg), dWu(Wu), dWd(Wd);
+  engine::DeviceBuffer<float> act(F), down(D), out(D), sum(D), norm(D);
+  engine::cuda::rmsnorm_linear_swiglu_nk(dh.get(), dw.get(), dWg.get(), dWu.get(), act.get(), 1, F,
+                                         D, eps);
+  engine::cuda::gemv_nk(dWd.get(), act.get(), down.get(), D, F);
+  engine::cuda::vector_add(dh.get(), down.get(), out.get(), D);
+  engine::cuda::residual_rmsnorm(dh.get(), down.get(), dw.get(), norm.get(), sum.get(), 1, D, eps);
+  ENGINE_ABI_CHECK(eng_device_sync());
+
+  double ss = 0.0;
+  for (float v : h) ss += static_cast<double>(v) * v;
+  const double s = 1.0 / std::sqrt(ss / D + eps);
+  std::vector<double> a(F);
+  for (std::int64_t n = 0; n < F; ++n) {
+    double g = 0.0, u = 0.0;
+    for (std::int64_t k = 0; k < D; ++k) {
+      const double xs = h[k] * s * w[k];
+      g += xs * Wg[n * D + k];
+      u += xs * Wu[n * D + k];
+    }
+    a[n] = g / (1.0 + std::exp(-g)) * u;
+  }
+  const std::vector<float> got_out = out.download();
+  const std::vector<float> got_sum = sum.download();
+  const std::vector<float> got_down = down.download();
+  int bad = 0;
+  for (std::int64_t d = 0; d < D; ++d) {
+    double dn = 0.0, dabs = 0.0;
+    for (std::int64_t f = 0; f < F; ++f) {
+      dn += a[f] * Wd[d * F + f];
+      dabs += std::fabs(a[f] * Wd[d * F + f]);
+    }
+    // generous derived bound: (D + F) u over the absolute sums of both stages
+    const double bound = (D + F + 8) * 0x1p-24 * (dabs + std::fabs(h[d]) + 1.0);
+    if (!(std::fabs(got_out[d] - (h[d] + dn)) <= bound)) ++bad;
+    // residual_rmsnorm's sum_out is the same fp32 addition as vector_add
+    if (got_sum[d] != h[d] + got_down[d]) ++bad;
+  }
+  EXPECT_EQ(bad, 0);
+  EXPECT_TRUE(got_out == got_sum);
 }
 
 }  // namespace
