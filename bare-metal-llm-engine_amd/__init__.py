@@ -113,6 +113,12 @@ SIGNATURES = {
     "eng_swiglu_f16": [_p, _p, _p, _i64, _p],
     "eng_rmsnorm_linear_swiglu_f16w_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_swiglu_f32_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_attention_decode_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, ctypes.c_int, _p],
+    "eng_attention_decode_with_mode_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f,
+                                           ctypes.c_int, ctypes.c_int, _p],
+    "eng_cast_f32_to_f16": [_p, _p, _i64, _p],
+    "eng_cast_f16_to_f32": [_p, _p, _i64, _p],
+    "eng_kv_cache_write_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
 }
 STRING_FUNCTIONS = ("eng_last_error", "eng_build_info")
 

@@ -1,0 +1,462 @@
+// attention.hip -- single-token decode attention over an fp16 KV cache
+// (FlashDecoding; reference kernels/attention_decode.cu, ADR 0013), and the
+// bridge kernels that connect the fp32 linear path to it (reference
+// kernels/attention_bridge.cu): fp32 <-> fp16 casts and the KV-cache append.
+//
+// Layouts (reference include/engine/kernels.hpp:160-194): q / out [n_heads, D]
+// fp16; K / V head-major, key j of KV head h at h * kv_head_stride + j * D;
+// query head h reads KV head h / (n_heads / n_kv_heads).
+//
+// Work mapping on gfx950: one 256-thread workgroup per (group of G query heads
+// sharing a KV head, KV split). A lane owns 8 consecutive dims (one 16-byte
+// load of K and of V), so D / 8 lanes cover a key and one wave load reads 64 /
+// (D / 8) keys (4 at D = 128, 8 at D = 64) as 1 KiB contiguous. Each K / V
+// byte is read once for all G heads of the group. Each lane keeps an online
+// softmax state (m, l, o[8]) per head; U key steps are processed as a chunk
+// (scores first, one rescale per chunk). States merge exactly -- weights
+// exp(m_i - m) -- across the key lanes of a wave by shuffles, across the 4
+// waves through LDS, and across splits in flash_decode_reduce_kernel, always
+// in a fixed order. Splits write fp32 (o, m, l) partials to pooled,
+// stream-ordered scratch.
+#include "gemv_kernels.hpp"
+#include "launch.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstddef>
+#include <string>
+
+namespace eng {
+namespace {
+
+using H8 = gemv::RawVec<_Float16, 8>::type;
+constexpr int kThreads = 256;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+template <bool VEC>
+__device__ __forceinline__ H8 load_h8(const _Float16* p) {
+  if constexpr (VEC) {
+    return __builtin_nontemporal_load(reinterpret_cast<const H8*>(p));
+  } else {
+    H8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = p[e];
+    return r;
+  }
+}
+
+// exp(a - b) as a merge weight; 0 for an empty state (a == -inf).
+__device__ __forceinline__ float merge_weight(float a, float b) {
+  return a > kNegInf ? expf(a - b) : 0.0f;
+}
+
+template <int D, int G, int U, bool VEC, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void flash_decode_split_kernel(
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k,
+    const _Float16* __restrict__ v, _Float16* __restrict__ out, float* __restrict__ part_o,
+    float* __restrict__ part_ml, long long kv_len, long long group_size,
+    long long kv_head_stride, float scale, int nsplit) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  constexpr int LPK = D / 8;       // lanes per key
+  constexpr int KPW = 64 / LPK;    // keys per wave load
+  constexpr int STEP = 4 * KPW;    // keys per workgroup load
+  __shared__ float s_m[4][G];
+  __shared__ float s_l[4][G];
+  __shared__ float s_o[4][G][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int sub = lane / LPK;
+  const int d0 = (lane % LPK) * 8;
+  const long long h0 = static_cast<long long>(blockIdx.x) * G;
+  const long long kvh = h0 / group_size;
+  const int split = static_cast<int>(blockIdx.y);
+  const long long j0 = kv_len * split / nsplit;
+  const long long j1 = kv_len * (split + 1) / nsplit;
+
+  float qf[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[g][e] = static_cast<float>(q[(h0 + g) * D + d0 + e]);
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+
+  const _Float16* kh = k + kvh * kv_head_stride + d0;
+  const _Float16* vh = v + kvh * kv_head_stride + d0;
+  // The loop bound depends on the wave only, so every lane runs the shuffles.
+  for (long long jb = j0 + static_cast<long long>(wave) * KPW; jb < j1;
+       jb += static_cast<long long>(STEP) * U) {
+    H8 kr[U], vr[U];
+    bool ok[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long j = jb + static_cast<long long>(u) * STEP + sub;
+      ok[u] = j < j1;
+      kr[u] = ok[u] ? load_h8<VEC>(kh + j * D) : H8{};
+      vr[u] = ok[u] ? load_h8<VEC>(vh + j * D) : H8{};
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[U];
+      float cm = kNegInf;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = fmaf(qf[g][e], static_cast<float>(kr[u][e]), part);
+#pragma unroll
+        for (int off = LPK / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
+        s[u] = ok[u] ? part * scale : kNegInf;
+        cm = fmaxf(cm, s[u]);
+      }
+      const float mn = fmaxf(m[g], cm);
+      if (mn > kNegInf) {
+        const float alpha = merge_weight(m[g], mn);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float p = merge_weight(s[u], mn);
+          l[g] += p;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, static_cast<float>(vr[u][e]), o[g][e]);
+        }
+        m[g] = mn;
+      }
+    }
+  }
+
+  // Merge the key lanes of the wave (lanes with the same dims, other keys).
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo = __shfl_xor(l[g], off);
+      const float mn = fmaxf(m[g], mo);
+      const float sa = merge_weight(m[g], mn);
+      const float sb = merge_weight(mo, mn);
+      l[g] = l[g] * sa + lo * sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float oo = __shfl_xor(o[g][e], off);
+        o[g][e] = o[g][e] * sa + oo * sb;
+      }
+      m[g] = mn;
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wave][g][d0 + e] = o[g][e];
+      if (lane == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int g = idx / D;
+    const int d = idx - g * D;
+    const float mb = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
+    float lb = 0.0f, ob = 0.0f;
+    if (mb > kNegInf) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float wt = merge_weight(s_m[w][g], mb);
+        lb = fmaf(s_l[w][g], wt, lb);
+        ob = fmaf(s_o[w][g][d], wt, ob);
+      }
+    }
+    const long long h = h0 + g;
+    if constexpr (PARTIAL) {
+      const long long slot = h * nsplit + split;
+      part_o[slot * D + d] = ob;
+      if (d == 0) {
+        part_ml[2 * slot] = mb;
+        part_ml[2 * slot + 1] = lb;
+      }
+    } else {
+      out[h * D + d] = static_cast<_Float16>(lb > 0.0f ? ob / lb : 0.0f);
+    }
+  }
+}
+
+// out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = exp(m_s - max m),
+// splits combined in order; one workgroup of D threads per head.
+template <int D>
+__global__ __launch_bounds__(D) void flash_decode_reduce_kernel(const float* __restrict__ part_o,
+                                                                const float* __restrict__ part_ml,
+                                                                _Float16* __restrict__ out,
+                                                                int nsplit) {
+  const long long h = blockIdx.x;
+  const int d = threadIdx.x;
+  const long long base = h * nsplit;
+  float mg = kNegInf;
+  for (int s = 0; s < nsplit; ++s) mg = fmaxf(mg, part_ml[2 * (base + s)]);
+  float lg = 0.0f, og = 0.0f;
+  if (mg > kNegInf) {
+    for (int s = 0; s < nsplit; ++s) {
+      const float w = merge_weight(part_ml[2 * (base + s)], mg);
+      lg = fmaf(part_ml[2 * (base + s) + 1], w, lg);
+      og = fmaf(part_o[(base + s) * D + d], w, og);
+    }
+  }
+  out[h * D + d] = static_cast<_Float16>(lg > 0.0f ? og / lg : 0.0f);
+}
+
+// Splits when the caller passes split_kv = 0: about two workgroups per CU
+// across all head groups, at least 256 keys per split, at most 256 splits.
+int auto_splits(long long kv_len, long long head_blocks) {
+  const long long cus = device_cu_count();
+  const long long wanted = (2 * cus + head_blocks - 1) / head_blocks;
+  const long long by_len = kv_len / 256;
+  return static_cast<int>(std::max(1LL, std::min({wanted, by_len, 256LL})));
+}
+
+struct DecodeArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  _Float16* out;
+  long long kv_len, n_heads, group_size, kv_head_stride;
+  float scale;
+  int splits;
+};
+
+template <int D, int G, bool VEC>
+void run_decode(const DecodeArgs& a, hipStream_t s) {
+  constexpr int U = 2;
+  const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
+  if (a.splits == 1) {
+    flash_decode_split_kernel<D, G, U, VEC, false><<<grid, kThreads, 0, s>>>(
+        a.q, a.k, a.v, a.out, nullptr, nullptr, a.kv_len, a.group_size, a.kv_head_stride,
+        a.scale, 1);
+    ENG_LAUNCH_CHECK();
+    return;
+  }
+  const std::size_t slots = static_cast<std::size_t>(a.n_heads) * a.splits;
+  PoolScratch scratch(slots * (D + 2) * sizeof(float), s);
+  float* part_o = static_cast<float*>(scratch.get());
+  float* part_ml = part_o + slots * D;
+  flash_decode_split_kernel<D, G, U, VEC, true><<<grid, kThreads, 0, s>>>(
+      a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+      a.scale, a.splits);
+  ENG_LAUNCH_CHECK();
+  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), D, 0, s>>>(
+      part_o, part_ml, a.out, a.splits);
+  ENG_LAUNCH_CHECK();
+}
+
+template <int D, bool VEC>
+void run_decode_g(const DecodeArgs& a, int G, hipStream_t s) {
+  switch (G) {
+    case 8: run_decode<D, 8, VEC>(a, s); break;
+    case 4: run_decode<D, 4, VEC>(a, s); break;
+    case 2: run_decode<D, 2, VEC>(a, s); break;
+    default: run_decode<D, 1, VEC>(a, s); break;
+  }
+}
+
+void attention_decode_any(const eng_half* q, const eng_half* k, const eng_half* v, eng_half* out,
+                          int64_t kv_len, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                          int64_t kv_head_stride, float scale, int split_kv, bool share_gqa_kv,
+                          eng_stream stream) {
+  // Precondition order and messages: reference kernels/attention_decode.cu:590-607.
+  ENG_CHECK(q != nullptr, "attention_decode: q is null");
+  ENG_CHECK(k != nullptr, "attention_decode: k is null");
+  ENG_CHECK(v != nullptr, "attention_decode: v is null");
+  ENG_CHECK(out != nullptr, "attention_decode: out is null");
+  ENG_CHECK(kv_len >= 0, "attention_decode: kv_len must be non-negative");
+  ENG_CHECK(n_heads > 0, "attention_decode: n_heads must be positive");
+  ENG_CHECK(n_kv_heads > 0, "attention_decode: n_kv_heads must be positive");
+  ENG_CHECK(n_heads % n_kv_heads == 0,
+            "attention_decode: n_heads must be divisible by n_kv_heads");
+  ENG_CHECK(head_dim == 64 || head_dim == 128, "attention_decode: head_dim must be 64 or 128");
+  ENG_CHECK(std::isfinite(scale), "attention_decode: scale must be finite");
+  ENG_CHECK(split_kv >= 0, "attention_decode: split_kv must be non-negative");
+  const int64_t min_stride = kv_len > 0 ? kv_len * head_dim : 0;
+  ENG_CHECK(kv_head_stride >= min_stride,
+            "attention_decode: kv_head_stride < kv_len * head_dim");
+  hipStream_t s = as_stream(stream);
+  if (kv_len == 0) {
+    fill_zero_async(out, static_cast<std::size_t>(n_heads * head_dim) * sizeof(eng_half), s);
+    return;
+  }
+  ENG_CHECK(n_heads <= 0x7fffffffLL, "attention_decode: n_heads too large for one launch");
+
+  DecodeArgs a;
+  a.q = reinterpret_cast<const _Float16*>(q);
+  a.k = reinterpret_cast<const _Float16*>(k);
+  a.v = reinterpret_cast<const _Float16*>(v);
+  a.out = reinterpret_cast<_Float16*>(out);
+  a.kv_len = kv_len;
+  a.n_heads = n_heads;
+  a.group_size = n_heads / n_kv_heads;
+  a.kv_head_stride = kv_head_stride;
+  a.scale = scale;
+  // Query heads per workgroup: the largest of 8, 4, 2 dividing the GQA group
+  // when K / V are shared across it, otherwise one.
+  int G = 1;
+  if (share_gqa_kv) {
+    for (int cand : {8, 4, 2}) {
+      if (a.group_size % cand == 0) {
+        G = cand;
+        break;
+      }
+    }
+  }
+  const int req = split_kv == 0 ? auto_splits(kv_len, n_heads / G) : split_kv;
+  a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 65535})));
+  const bool vec = aligned_to(k, 16) && aligned_to(v, 16) && kv_head_stride % 8 == 0;
+  if (head_dim == 64) {
+    if (vec) {
+      run_decode_g<64, true>(a, G, s);
+    } else {
+      run_decode_g<64, false>(a, G, s);
+    }
+  } else {
+    if (vec) {
+      run_decode_g<128, true>(a, G, s);
+    } else {
+      run_decode_g<128, false>(a, G, s);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ bridge
+__global__ __launch_bounds__(kThreads) void cast_f32_to_f16_kernel(const float* __restrict__ in,
+                                                                   _Float16* __restrict__ out,
+                                                                   long long n) {
+  const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += stride) {
+    out[i] = static_cast<_Float16>(in[i]);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void cast_f16_to_f32_kernel(const _Float16* __restrict__ in,
+                                                                   float* __restrict__ out,
+                                                                   long long n) {
+  const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < n;
+       i += stride) {
+    out[i] = static_cast<float>(in[i]);
+  }
+}
+
+// Token-major new K / V [s_new, n_kv_heads, D] -> head-major caches
+// [n_kv_heads, kv_max_seq_len, D] at positions pos_offset ...
+__global__ __launch_bounds__(kThreads) void kv_cache_write_kernel(
+    const _Float16* __restrict__ k_new, const _Float16* __restrict__ v_new,
+    _Float16* __restrict__ k_cache, _Float16* __restrict__ v_cache, long long s_new,
+    long long n_kv_heads, long long D, long long pos_offset, long long kv_max_seq_len) {
+  const long long total = s_new * n_kv_heads * D;
+  const long long stride = static_cast<long long>(gridDim.x) * kThreads;
+  for (long long i = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x; i < total;
+       i += stride) {
+    const long long d = i % D;
+    const long long th = i / D;
+    const long long h = th % n_kv_heads;
+    const long long t = th / n_kv_heads;
+    const long long dst = (h * kv_max_seq_len + pos_offset + t) * D + d;
+    k_cache[dst] = k_new[i];
+    v_cache[dst] = v_new[i];
+  }
+}
+
+unsigned bridge_grid(long long n) {
+  const long long wanted = 8LL * device_cu_count();
+  return static_cast<unsigned>(std::max(1LL, std::min((n + kThreads - 1) / kThreads, wanted)));
+}
+
+}  // namespace
+}  // namespace eng
+
+using eng::guarded;
+
+extern "C" {
+
+int eng_attention_decode_f16(const eng_half* q, const eng_half* k, const eng_half* v,
+                             eng_half* out, int64_t kv_len, int64_t n_heads, int64_t n_kv_heads,
+                             int64_t head_dim, int64_t kv_head_stride, float scale, int split_kv,
+                             eng_stream stream) {
+  return guarded([&] {
+    eng::attention_decode_any(q, k, v, out, kv_len, n_heads, n_kv_heads, head_dim,
+                              kv_head_stride, scale, split_kv, true, stream);
+  });
+}
+
+int eng_attention_decode_with_mode_f16(const eng_half* q, const eng_half* k, const eng_half* v,
+                                       eng_half* out, int64_t kv_len, int64_t n_heads,
+                                       int64_t n_kv_heads, int64_t head_dim,
+                                       int64_t kv_head_stride, float scale, int split_kv,
+                                       int share_gqa_kv, eng_stream stream) {
+  return guarded([&] {
+    eng::attention_decode_any(q, k, v, out, kv_len, n_heads, n_kv_heads, head_dim,
+                              kv_head_stride, scale, split_kv, share_gqa_kv != 0, stream);
+  });
+}
+
+int eng_cast_f32_to_f16(const float* in, eng_half* out, int64_t n, eng_stream stream) {
+  return guarded([&] {
+    ENG_CHECK(n >= 0, "cast_f32_to_f16: n must be non-negative");
+    if (n == 0) return;
+    ENG_CHECK(in != nullptr, "cast_f32_to_f16: in is null");
+    ENG_CHECK(out != nullptr, "cast_f32_to_f16: out is null");
+    eng::cast_f32_to_f16_kernel<<<eng::bridge_grid(n), eng::kThreads, 0, eng::as_stream(stream)>>>(
+        in, reinterpret_cast<_Float16*>(out), n);
+    ENG_LAUNCH_CHECK();
+  });
+}
+
+int eng_cast_f16_to_f32(const eng_half* in, float* out, int64_t n, eng_stream stream) {
+  return guarded([&] {
+    ENG_CHECK(n >= 0, "cast_f16_to_f32: n must be non-negative");
+    if (n == 0) return;
+    ENG_CHECK(in != nullptr, "cast_f16_to_f32: in is null");
+    ENG_CHECK(out != nullptr, "cast_f16_to_f32: out is null");
+    eng::cast_f16_to_f32_kernel<<<eng::bridge_grid(n), eng::kThreads, 0, eng::as_stream(stream)>>>(
+        reinterpret_cast<const _Float16*>(in), out, n);
+    ENG_LAUNCH_CHECK();
+  });
+}
+
+int eng_kv_cache_write_f16(const eng_half* k_new, const eng_half* v_new, eng_half* k_cache,
+                           eng_half* v_cache, int64_t s_new, int64_t n_kv_heads, int64_t head_dim,
+                           int64_t pos_offset, int64_t kv_max_seq_len, eng_stream stream) {
+  return guarded([&] {
+    // Precondition order and messages: reference kernels/attention_bridge.cu:86-103.
+    ENG_CHECK(s_new >= 0, "kv_cache_write: s_new must be non-negative");
+    ENG_CHECK(n_kv_heads > 0, "kv_cache_write: n_kv_heads must be positive");
+    ENG_CHECK(head_dim > 0, "kv_cache_write: head_dim must be positive");
+    ENG_CHECK(pos_offset >= 0, "kv_cache_write: pos_offset must be non-negative");
+    ENG_CHECK(kv_max_seq_len >= pos_offset + s_new,
+              "kv_cache_write: kv_max_seq_len < pos_offset + s_new");
+    if (s_new == 0) return;
+    ENG_CHECK(k_new != nullptr && v_new != nullptr, "kv_cache_write: k_new/v_new is null");
+    ENG_CHECK(k_cache != nullptr && v_cache != nullptr, "kv_cache_write: k_cache/v_cache is null");
+    const long long total = s_new * n_kv_heads * head_dim;
+    eng::kv_cache_write_kernel<<<eng::bridge_grid(total), eng::kThreads, 0,
+                                 eng::as_stream(stream)>>>(
+        reinterpret_cast<const _Float16*>(k_new), reinterpret_cast<const _Float16*>(v_new),
+        reinterpret_cast<_Float16*>(k_cache), reinterpret_cast<_Float16*>(v_cache), s_new,
+        n_kv_heads, head_dim, pos_offset, kv_max_seq_len);
+    ENG_LAUNCH_CHECK();
+  });
+}
+
+}  // extern "C"

@@ -156,6 +156,53 @@ inline void rmsnorm_linear_swiglu_nk(const float* in, const float* rms_weight, c
       eng_rmsnorm_linear_swiglu_f32_nk(in, rms_weight, W_gate, W_up, act, M, N, K, eps, stream));
 }
 
+namespace detail {
+
+/// FlashDecoding with GQA K / V sharing switched explicitly (reference
+/// kernels.hpp:169-174, for ablations).
+inline void attention_decode_with_mode(const half* q, const half* k, const half* v, half* out,
+                                       std::int64_t kv_len, std::int64_t n_heads,
+                                       std::int64_t n_kv_heads, std::int64_t head_dim,
+                                       std::int64_t kv_head_stride, float scale, int split_kv,
+                                       bool share_gqa_kv, hipStream_t stream) {
+  ENGINE_ABI_CHECK(eng_attention_decode_with_mode_f16(
+      bits(q), bits(k), bits(v), bits(out), kv_len, n_heads, n_kv_heads, head_dim,
+      kv_head_stride, scale, split_kv, share_gqa_kv ? 1 : 0, stream));
+}
+
+/// fp32 -> fp16 and back, elementwise (reference kernels.hpp:176-180).
+inline void cast_f32_to_f16(const float* in, half* out, std::int64_t n,
+                            hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_cast_f32_to_f16(in, bits(out), n, stream));
+}
+inline void cast_f16_to_f32(const half* in, float* out, std::int64_t n,
+                            hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_cast_f16_to_f32(bits(in), out, n, stream));
+}
+
+/// Token-major K / V -> head-major KV caches (reference kernels.hpp:182-188).
+inline void kv_cache_write(const half* k_new, const half* v_new, half* k_cache, half* v_cache,
+                           std::int64_t s_new, std::int64_t n_kv_heads, std::int64_t head_dim,
+                           std::int64_t pos_offset, std::int64_t kv_max_seq_len,
+                           hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_kv_cache_write_f16(bits(k_new), bits(v_new), bits(k_cache), bits(v_cache),
+                                          s_new, n_kv_heads, head_dim, pos_offset,
+                                          kv_max_seq_len, stream));
+}
+
+}  // namespace detail
+
+/// Single-token decode attention, split-KV FlashDecoding over an fp16 KV
+/// cache; split_kv = 0 chooses the split count (reference kernels.hpp:190-194).
+inline void attention_decode(const half* q, const half* k, const half* v, half* out,
+                             std::int64_t kv_len, std::int64_t n_heads, std::int64_t n_kv_heads,
+                             std::int64_t head_dim, std::int64_t kv_head_stride, float scale,
+                             int split_kv = 0, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_attention_decode_f16(detail::bits(q), detail::bits(k), detail::bits(v),
+                                            detail::bits(out), kv_len, n_heads, n_kv_heads,
+                                            head_dim, kv_head_stride, scale, split_kv, stream));
+}
+
 }  // namespace hip
 
 // Call sites written against the reference use engine::cuda::...

@@ -291,6 +291,49 @@ int eng_rmsnorm_linear_swiglu_f32_nk(const float* in, const float* rms_weight,
                                      int64_t M, int64_t N, int64_t K, float eps,
                                      eng_stream stream);
 
+/* ------------------------------------------------------------------------
+ * Decode attention over an fp16 KV cache, and its bridge kernels.
+ * ---------------------------------------------------------------------- */
+
+/* Single-token decode attention with split-KV FlashDecoding: for each query
+ * head h, out[h] = softmax(scale * K_g . q[h]) . V_g over keys 0..kv_len-1 of
+ * KV head g = h / (n_heads / n_kv_heads). q / out [n_heads, head_dim] half;
+ * K / V head-major, key j of KV head g at g * kv_head_stride + j * head_dim.
+ * split_kv = 0 picks the split count; the query heads of a GQA group share
+ * each K / V load. Messages (order as the reference): "q is null", "k is
+ * null", "v is null", "out is null", "kv_len must be non-negative", "n_heads
+ * must be positive", "n_kv_heads must be positive", "n_heads must be divisible
+ * by n_kv_heads", "head_dim must be 64 or 128", "scale must be finite",
+ * "split_kv must be non-negative", "kv_head_stride < kv_len * head_dim";
+ * kv_len == 0 zero-fills out. Replaces engine::cuda::attention_decode
+ * (reference include/engine/kernels.hpp:190-194, kernels/attention_decode.cu:
+ * 632-715); the _with_mode form replaces detail::attention_decode_with_mode
+ * (kernels.hpp:169-174), share_gqa_kv = 0 giving one query head per workgroup. */
+int eng_attention_decode_f16(const eng_half* q, const eng_half* k, const eng_half* v,
+                             eng_half* out, int64_t kv_len, int64_t n_heads, int64_t n_kv_heads,
+                             int64_t head_dim, int64_t kv_head_stride, float scale, int split_kv,
+                             eng_stream stream);
+int eng_attention_decode_with_mode_f16(const eng_half* q, const eng_half* k, const eng_half* v,
+                                       eng_half* out, int64_t kv_len, int64_t n_heads,
+                                       int64_t n_kv_heads, int64_t head_dim,
+                                       int64_t kv_head_stride, float scale, int split_kv,
+                                       int share_gqa_kv, eng_stream stream);
+
+/* Elementwise fp32 <-> fp16 (round to nearest even); n < 0 -> "n must be
+ * non-negative", n == 0 returns before the pointer checks. Replace
+ * engine::cuda::detail::cast_f32_to_f16 / cast_f16_to_f32
+ * (reference include/engine/kernels.hpp:176-180, kernels/attention_bridge.cu:64-84). */
+int eng_cast_f32_to_f16(const float* in, eng_half* out, int64_t n, eng_stream stream);
+int eng_cast_f16_to_f32(const eng_half* in, float* out, int64_t n, eng_stream stream);
+
+/* Scatter token-major k_new / v_new [s_new, n_kv_heads, head_dim] into
+ * head-major caches [n_kv_heads, kv_max_seq_len, head_dim] at positions
+ * pos_offset .. pos_offset + s_new - 1. Replaces engine::cuda::detail::kv_cache_write
+ * (reference include/engine/kernels.hpp:182-188, kernels/attention_bridge.cu:86-110). */
+int eng_kv_cache_write_f16(const eng_half* k_new, const eng_half* v_new, eng_half* k_cache,
+                           eng_half* v_cache, int64_t s_new, int64_t n_kv_heads, int64_t head_dim,
+                           int64_t pos_offset, int64_t kv_max_seq_len, eng_stream stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -43,6 +43,12 @@
  *                         (gate and up) followed by orc_swiglu.
  *   orc_ffn_subblock      golden vectors (FFN_SUBBLOCK_CASES), equality with the
  *                         composition of the pinned functions.
+ *   orc_attention         golden vectors (the reference's ATTENTION_CASES decode
+ *                         rows), closed forms (one key gives its value row,
+ *                         q = 0 gives the mean of the value rows, a dominant
+ *                         key gives its value row, key order does not matter),
+ *                         NumPy float64 softmax on random heads; planted wrong
+ *                         GQA head mapping must be caught.
  *   half conversions      all 65536 half -> float against NumPy float16,
  *                         float -> half against NumPy on 2^24 sampled floats
  *                         plus every boundary case; planted truncation
@@ -360,4 +366,73 @@ void orc_ffn_subblock(const float* h, const float* ffn_norm_w, const float* Wg, 
   free(up);
   free(act);
   free(down);
+}
+
+/* ------------------------------------------------------------ attention */
+
+int orc_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                  int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t n_kv_heads,
+                  int64_t head_dim, int64_t kv_head_stride, float scale, int64_t q_pos_offset,
+                  int is_causal, float* out_lse) {
+  if (q == NULL || k == NULL || v == NULL || out == NULL) return -1;
+  if (s_q < 0 || s_kv < 0 || q_pos_offset < 0 || n_heads <= 0 || n_kv_heads <= 0) return -1;
+  if (n_heads % n_kv_heads != 0 || (head_dim != 64 && head_dim != 128)) return -1;
+  if (!isfinite(scale)) return -1;
+  if (kv_head_stride < (s_kv > 0 ? s_kv * head_dim : 0)) return -1;
+  const int64_t rows = s_q * n_heads;
+  if (s_kv == 0) {
+    for (int64_t i = 0; i < rows * head_dim; ++i) out[i] = 0;
+    if (out_lse != NULL)
+      for (int64_t r = 0; r < rows; ++r) out_lse[r] = -INFINITY;
+    return 0;
+  }
+  const int64_t group = n_heads / n_kv_heads;
+  double* scores = (double*)malloc((size_t)s_kv * sizeof(double));
+  double* acc = (double*)malloc((size_t)head_dim * sizeof(double));
+  if (scores == NULL || acc == NULL) abort();
+  for (int64_t i = 0; i < s_q; ++i) {
+    const int64_t last = is_causal ? (q_pos_offset + i < s_kv - 1 ? q_pos_offset + i : s_kv - 1)
+                                   : s_kv - 1;
+    for (int64_t h = 0; h < n_heads; ++h) {
+      const int64_t row = i * n_heads + h;
+      const uint16_t* qr = q + row * head_dim;
+      uint16_t* orow = out + row * head_dim;
+#if ORC_MUTATION == 8
+      /* planted mistake: query head h reads KV head h % n_kv_heads */
+      const int64_t hk = h % n_kv_heads;
+      (void)group;
+#else
+      const int64_t hk = h / group;
+#endif
+      const uint16_t* kh = k + hk * kv_head_stride;
+      const uint16_t* vh = v + hk * kv_head_stride;
+      double m = -INFINITY;
+      for (int64_t j = 0; j <= last; ++j) {
+        double dot = 0.0;
+        for (int64_t d = 0; d < head_dim; ++d)
+          dot += (double)orc_half_to_float(qr[d]) * (double)orc_half_to_float(kh[j * head_dim + d]);
+        scores[j] = dot * (double)scale;
+        if (scores[j] > m) m = scores[j];
+      }
+      if (last < 0 || !(m > -INFINITY)) {
+        for (int64_t d = 0; d < head_dim; ++d) orow[d] = 0;
+        if (out_lse != NULL) out_lse[row] = -INFINITY;
+        continue;
+      }
+      double sum = 0.0;
+      for (int64_t d = 0; d < head_dim; ++d) acc[d] = 0.0;
+      for (int64_t j = 0; j <= last; ++j) {
+        const double w = exp(scores[j] - m);
+        sum += w;
+        for (int64_t d = 0; d < head_dim; ++d)
+          acc[d] += w * (double)orc_half_to_float(vh[j * head_dim + d]);
+      }
+      const double inv = 1.0 / sum;
+      for (int64_t d = 0; d < head_dim; ++d) orow[d] = orc_float_to_half((float)(acc[d] * inv));
+      if (out_lse != NULL) out_lse[row] = (float)(m + log(sum));
+    }
+  }
+  free(scores);
+  free(acc);
+  return 0;
 }

@@ -82,6 +82,19 @@ void orc_rmsnorm_linear_swiglu_f16w(const float* in, const float* rms_weight, co
 void orc_ffn_subblock(const float* h, const float* ffn_norm_w, const float* Wg, const float* Wu,
                       const float* Wd, float* out, int64_t S, int64_t D, int64_t F, float eps);
 
+/* Multi-head / grouped-query attention with half q, k, v, out and a float64
+ * two-pass softmax (reference src/cpu_ref/attention_cpu.cpp:84-155):
+ * q / out [s_q, n_heads, head_dim]; k / v [n_kv_heads, kv_head_stride] with
+ * key j of KV head h at h * kv_head_stride + j * head_dim; query head h reads
+ * KV head h / (n_heads / n_kv_heads); causal rows see keys j <= q_pos_offset + i.
+ * out_lse (may be NULL) receives m + log(sum exp) per row, -inf for an empty row.
+ * Returns 0, or -1 when the arguments break the reference's preconditions
+ * (nothing is written then). */
+int orc_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                  int64_t s_q, int64_t s_kv, int64_t n_heads, int64_t n_kv_heads,
+                  int64_t head_dim, int64_t kv_head_stride, float scale, int64_t q_pos_offset,
+                  int is_causal, float* out_lse);
+
 /* IEEE-754 binary16 conversions: half -> float exact; float -> half rounds to
  * nearest, ties to even (the rounding of the reference's CUDA build,
  * include/engine/half.hpp:28-32). */

@@ -52,6 +52,16 @@ FFN_SUBBLOCK_CASES = [("prefill_s16_d512_ffn1408", 16, 512, 1408), ("decode_s1_d
 RMSNORM_LINEAR_SWIGLU_SHAPES = [(1, 1408, 512, True), (16, 1408, 512, True), (3, 257, 100, False)]
 # reference :379 without its 1 Mi case (tests check large sizes against float32 addition)
 VECTOR_ADD_SIZES = [1, 31, 32, 33, 255, 256, 257, 4096]
+# reference :466-477 -- the decode rows (s_q = 1) plus two causal prefill rows
+# that pin the general oracle: (name, s_q, s_kv, n_heads, n_kv_heads, head_dim, q_pos_offset, causal)
+ATTENTION_CASES = [
+    ("s1_h1_d64_causal", 1, 1, 1, 1, 64, 0, True),
+    ("s1_kv31_h4_d64_nocausal", 1, 31, 4, 4, 64, 0, False),
+    ("s1_kv257_h32_kv4_d64_decode", 1, 257, 32, 4, 64, 256, False),
+    ("s1_kv513_h8_kv2_d128_decode", 1, 513, 8, 2, 128, 512, False),
+    ("s17_h8_kv2_d64_causal", 17, 17, 8, 2, 64, 0, True),
+    ("s33_kv65_h8_kv2_d128_off32_causal", 33, 65, 8, 2, 128, 32, True),
+]
 
 
 def f64(a: np.ndarray, dtype: str) -> np.ndarray:
@@ -66,6 +76,28 @@ def silu64(g: np.ndarray) -> np.ndarray:
     (tools/gen_reference.py:158-163)."""
     e = np.exp(-np.abs(g))
     return g * np.where(g >= 0.0, 1.0 / (1.0 + e), e / (1.0 + e))
+
+
+def attention64(q, k, v, scale, q_pos_offset, causal):
+    """float64 two-pass softmax attention (reference gen_reference.py attention):
+    q [s_q, H, D], k / v [H_kv, s_kv, D] -> (out [s_q, H, D], lse [s_q, H])."""
+    s_q, H, D = q.shape
+    H_kv, s_kv, _ = k.shape
+    group = H // H_kv
+    out = np.zeros((s_q, H, D))
+    lse = np.full((s_q, H), -np.inf)
+    for i in range(s_q):
+        last = min(s_kv - 1, q_pos_offset + i) if causal else s_kv - 1
+        if last < 0:
+            continue
+        for h in range(H):
+            kh, vh = k[h // group, : last + 1], v[h // group, : last + 1]
+            s = (kh @ q[i, h]) * scale
+            m = s.max()
+            w = np.exp(s - m)
+            out[i, h] = (w @ vh) / w.sum()
+            lse[i, h] = m + np.log(w.sum())
+    return out, lse
 
 
 def rms_rows(x64: np.ndarray, w64) -> np.ndarray:
@@ -217,6 +249,18 @@ class Builder:
             act = silu64(xn @ wg) * (xn @ wu)
             self.add(f"ffn_subblock__{name}", "ffn_subblock", {"S": s_q, "D": d, "F": f, "eps": EPS},
                      specs, x + act @ wd, extra={"act": act})
+
+        for name, s_q, s_kv, H, H_kv, D, off, causal in ATTENTION_CASES:
+            specs = {
+                "q": self.spec("normal", (s_q, H, D), dtype="f16"),
+                "k": self.spec("normal", (H_kv, s_kv, D), dtype="f16"),
+                "v": self.spec("normal", (H_kv, s_kv, D), dtype="f16"),
+            }
+            q, k, v = (f64(detgen.make(specs[x]), "f16") for x in ("q", "k", "v"))
+            out, lse = attention64(q, k, v, 1.0 / np.sqrt(D), off, causal)
+            self.add(f"attention__{name}", "attention",
+                     {"s_q": s_q, "s_kv": s_kv, "n_heads": H, "n_kv_heads": H_kv, "head_dim": D,
+                      "q_pos_offset": off, "is_causal": causal}, specs, out, extra={"lse": lse})
 
 
 def main() -> None:

@@ -92,6 +92,9 @@ class Oracle:
             "orc_rmsnorm_linear_swiglu_f16w": [p, p, p, p, p, i64, i64, i64, f],
             "orc_ffn_subblock": [p, p, p, p, p, p, i64, i64, i64, f],
         }
+        lib.orc_attention.argtypes = [p, p, p, p, i64, i64, i64, i64, i64, i64, f, i64,
+                                      ctypes.c_int, p]
+        lib.orc_attention.restype = ctypes.c_int
         for name, args in sig.items():
             fn = getattr(lib, name)
             fn.argtypes = args
@@ -220,6 +223,22 @@ class Oracle:
         self.lib.orc_ffn_subblock(h.ctypes.data, self._p(wp), Wg.ctypes.data, Wu.ctypes.data,
                                   Wd.ctypes.data, out.ctypes.data, S, D, F, eps)
         return out
+
+    def attention(self, q, k, v, n_heads, n_kv_heads, head_dim, s_kv, kv_head_stride, scale,
+                  q_pos_offset=0, is_causal=False, want_lse=False):
+        """Half q [s_q, H, D] and k / v (flat, kv_head_stride elements per KV
+        head); returns half out [s_q, H, D] (and fp32 lse [s_q, H])."""
+        q = self._c(q, np.uint16)
+        k, v = self._c(k, np.uint16), self._c(v, np.uint16)
+        s_q = q.size // (n_heads * head_dim)
+        out = np.empty((s_q, n_heads, head_dim), np.uint16)
+        lse = np.empty((s_q, n_heads), np.float32) if want_lse else None
+        rc = self.lib.orc_attention(q.ctypes.data, k.ctypes.data, v.ctypes.data, out.ctypes.data,
+                                    s_q, s_kv, n_heads, n_kv_heads, head_dim, kv_head_stride,
+                                    scale, q_pos_offset, int(is_causal), self._p(lse))
+        if rc != 0:
+            raise ValueError("orc_attention: precondition failed")
+        return (out, lse) if want_lse else out
 
     def f32_to_f16(self, a):
         a = self._c(a, np.float32)

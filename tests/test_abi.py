@@ -100,6 +100,29 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_rmsnorm_linear_swiglu_f16w_nk", P, P, P, None, P, 1, 4, 4, 1e-5, None), 1, "null"),
     (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, -4, 4, 1e-5, None), 1, "negative dimension"),
     (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 4, 4, -1.0, None), 1, "eps"),
+    (("eng_attention_decode_f16", None, P, P, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "attention_decode: q is null"),
+    (("eng_attention_decode_f16", P, None, P, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "k is null"),
+    (("eng_attention_decode_f16", P, P, None, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "v is null"),
+    (("eng_attention_decode_f16", P, P, P, None, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "out is null"),
+    (("eng_attention_decode_f16", P, P, P, P, -1, 8, 2, 64, 256, 0.125, 0, None), 1, "kv_len must be non-negative"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 0, 2, 64, 256, 0.125, 0, None), 1, "n_heads must be positive"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 8, 0, 64, 256, 0.125, 0, None), 1, "n_kv_heads must be positive"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 6, 4, 64, 256, 0.125, 0, None), 1, "divisible by n_kv_heads"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 8, 2, 32, 128, 0.125, 0, None), 1, "head_dim must be 64 or 128"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 8, 2, 64, 256, float("inf"), 0, None), 1, "scale must be finite"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 8, 2, 64, 256, 0.125, -1, None), 1, "split_kv must be non-negative"),
+    (("eng_attention_decode_f16", P, P, P, P, 4, 8, 2, 64, 255, 0.125, 0, None), 1, "kv_head_stride < kv_len * head_dim"),
+    (("eng_attention_decode_with_mode_f16", P, P, P, P, 4, 8, 2, 128, 256, 0.125, 0, 0, None), 1, "kv_head_stride"),
+    (("eng_cast_f32_to_f16", P, P, -1, None), 1, "cast_f32_to_f16: n must be non-negative"),
+    (("eng_cast_f32_to_f16", None, P, 4, None), 1, "in is null"),
+    (("eng_cast_f16_to_f32", P, None, 4, None), 1, "cast_f16_to_f32: out is null"),
+    (("eng_kv_cache_write_f16", P, P, P, P, -1, 2, 64, 0, 8, None), 1, "s_new must be non-negative"),
+    (("eng_kv_cache_write_f16", P, P, P, P, 1, 0, 64, 0, 8, None), 1, "n_kv_heads must be positive"),
+    (("eng_kv_cache_write_f16", P, P, P, P, 1, 2, 0, 0, 8, None), 1, "head_dim must be positive"),
+    (("eng_kv_cache_write_f16", P, P, P, P, 1, 2, 64, -1, 8, None), 1, "pos_offset must be non-negative"),
+    (("eng_kv_cache_write_f16", P, P, P, P, 4, 2, 64, 5, 8, None), 1, "kv_max_seq_len < pos_offset + s_new"),
+    (("eng_kv_cache_write_f16", None, P, P, P, 1, 2, 64, 0, 8, None), 1, "k_new/v_new is null"),
+    (("eng_kv_cache_write_f16", P, P, P, None, 1, 2, 64, 0, 8, None), 1, "k_cache/v_cache is null"),
 ])
 def test_preconditions_fail_before_launch(eng, call, code, substr):
     name, *args = call
@@ -132,6 +155,9 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_swiglu_f16", P, P, P, 0, None),
     ("eng_rmsnorm_linear_swiglu_f16w_nk", P, None, P, P, P, 1, 0, 8, 1e-5, None),
     ("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 8, 0, 1e-5, None),
+    ("eng_cast_f32_to_f16", None, None, 0, None),
+    ("eng_cast_f16_to_f32", None, None, 0, None),
+    ("eng_kv_cache_write_f16", None, None, None, None, 0, 2, 64, 3, 3, None),
 ])
 def test_empty_work_is_a_no_op(eng, call):
     name, *args = call

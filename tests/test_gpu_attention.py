@@ -1,0 +1,265 @@
+"""GPU parity of decode attention (FlashDecoding over an fp16 KV cache) and
+its bridge kernels, called through the C-ABI, against the float64 golden
+fixtures (the reference's decode attention cases) and the C oracle.
+
+Two tolerances are checked everywhere:
+* the reference's own decode tolerance (tests/test_kernels.cu:292-296):
+  |got - exp| <= 1.5 * 2^-10 + 4 * s_kv * 2^-23 + 2 * 2^-10 * |exp|;
+* a derived bound (u = 2^-24): with w_j = exp(s_j - max s), the fp32 scores
+  carry |ds_j| <= (D + 1) u scale sum_d |q_d k_jd| =: e_j, so the weights carry
+  at most 2 max_j e_j + 4u relative error (their difference in the exponent,
+  exp's own rounding); the fp32 sums of p_j v_j and p_j add (s_kv + 16) u
+  relative to sum_j w_j |v_j|; the output adds half rounding 2^-11 |y| + 2^-25:
+      |got - y| <= 2^-11 |y| + 2^-25
+                   + (2 max e + (s_kv + 24) u) (sum_j w_j |v_j| / sum_j w_j + |y|).
+Long sequences (8K / 32K keys) also use the reference's output-scaled
+tolerance (test_kernels.cu:2565-2640): rtol = 2^-9, atol = rtol * rms(out).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+U = helpers.U32
+
+
+def decode64(q, k, v, H, Hkv, D, L, stride, scale):
+    """float64 decode attention and the derived bound; q [H, D] / k / v flat
+    half bits with `stride` elements per KV head."""
+    q64 = helpers.as_f64(q).reshape(H, D)
+    k64 = helpers.as_f64(k).reshape(Hkv, -1)
+    v64 = helpers.as_f64(v).reshape(Hkv, -1)
+    group = H // Hkv
+    y = np.zeros((H, D))
+    bound = np.zeros((H, D))
+    for h in range(H):
+        kh = k64[h // group, : L * D].reshape(L, D)
+        vh = v64[h // group, : L * D].reshape(L, D)
+        s = kh @ q64[h] * scale
+        w = np.exp(s - s.max())
+        y[h] = (w @ vh) / w.sum()
+        e = (D + 1) * U * scale * (np.abs(kh) @ np.abs(q64[h]))
+        mag = (w @ np.abs(vh)) / w.sum() + np.abs(y[h])
+        bound[h] = helpers.U16 * np.abs(y[h]) + 2.0**-25 + (2 * e.max() + (L + 24) * U) * mag
+    return y, bound
+
+
+def reference_tol(exp, s_kv):
+    return 1.5 * 2.0**-10 + 4.0 * s_kv * 2.0**-23 + 2.0 * 2.0**-10 * np.abs(exp)
+
+
+def gpu_decode(eng, q, k, v, L, H, Hkv, D, stride, scale, split_kv=0, share=None, out_fill=None,
+               k_offset=0):
+    dq, dk, dv = eng.upload(q), eng.upload(k), eng.upload(v)
+    dout = eng.empty((H, D), np.uint16)
+    if out_fill is not None:
+        dout.upload(np.full((H, D), out_fill, np.uint16))
+    if share is None:
+        eng.call("eng_attention_decode_f16", dq.ptr, dk.ptr + 2 * k_offset, dv.ptr + 2 * k_offset,
+                 dout.ptr, L, H, Hkv, D, stride, scale, split_kv, None)
+    else:
+        eng.call("eng_attention_decode_with_mode_f16", dq.ptr, dk.ptr + 2 * k_offset,
+                 dv.ptr + 2 * k_offset, dout.ptr, L, H, Hkv, D, stride, scale, split_kv,
+                 int(share), None)
+    eng.sync()
+    return dout.download()
+
+
+def check_decode(got16, q, k, v, H, Hkv, D, L, stride, scale, orc, what):
+    got = helpers.as_f64(got16).reshape(H, D)
+    y, bound = decode64(q, k, v, H, Hkv, D, L, stride, scale)
+    helpers.assert_within(got, y, bound, what + " [derived bound]")
+    helpers.assert_within(got, y, reference_tol(y, L), what + " [reference tolerance]")
+    ref = helpers.as_f64(orc.attention(q, k, v, H, Hkv, D, L, stride, scale)).reshape(H, D)
+    helpers.assert_within(got, ref, bound + helpers.U16 * np.abs(ref) + 2.0**-25, what + " [vs oracle]")
+    return got
+
+
+def rand_half(orc, rng, shape, amp=1.0):
+    return orc.f32_to_f16((amp * rng.standard_normal(shape)).astype(np.float32))
+
+
+# ------------------------------------------------------------------ goldens
+DECODE_STEMS = [c["stem"] for c in helpers.cases("attention") if c["params"]["s_q"] == 1]
+
+
+@pytest.mark.parametrize("stem", DECODE_STEMS)
+@pytest.mark.parametrize("split_kv", [0, 1, 8])
+def test_attention_decode_matches_golden(gpu, orc, stem, split_kv):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    P = c["params"]
+    H, Hkv, D, L = P["n_heads"], P["n_kv_heads"], P["head_dim"], P["s_kv"]
+    scale = 1.0 / np.sqrt(D)
+    got = gpu_decode(gpu, x["q"], x["k"], x["v"], L, H, Hkv, D, L * D, scale, split_kv)
+    exp = helpers.expected(c).reshape(H, D)
+    helpers.assert_within(helpers.as_f64(got), exp, reference_tol(exp, L), f"{stem} split={split_kv} golden")
+    check_decode(got, x["q"], x["k"], x["v"], H, Hkv, D, L, L * D, scale, orc, f"{stem} split={split_kv}")
+
+
+def test_attention_decode_splits_and_edges(gpu, orc):
+    """Reference attention_decode_splits_and_contracts, GPU part."""
+    c = helpers.case("attention__s1_kv513_h8_kv2_d128_decode")
+    x = helpers.inputs(c)
+    q, k, v = x["q"], x["k"], x["v"]
+    H, Hkv, D, L = 8, 2, 128, 513
+    sc = 1.0 / np.sqrt(D)
+    s1 = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, 1)
+    s8 = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, 8)
+    _, bound = decode64(q, k, v, H, Hkv, D, L, L * D, sc)
+    helpers.assert_within(helpers.as_f64(s1), helpers.as_f64(s8).reshape(s1.shape),
+                          2 * bound.reshape(s1.shape), "split 1 vs 8")
+    # kv_len = 3 < split_kv = 16 (clamped), kv_len = 1 (exactly the value row)
+    got3 = gpu_decode(gpu, q, k, v, 3, H, Hkv, D, L * D, sc, 16)
+    check_decode(got3, q, k, v, H, Hkv, D, 3, L * D, sc, orc, "kv_len 3 < split 16")
+    got1 = gpu_decode(gpu, q, k, v, 1, H, Hkv, D, L * D, sc, 0)
+    vv = v.reshape(Hkv, L, D)
+    for h in range(H):
+        assert np.array_equal(got1[h], vv[h // 4, 0]), h
+    # kv_len = 0 zero-fills (output prefilled with 5.0)
+    got0 = gpu_decode(gpu, q, k, v, 0, H, Hkv, D, 0, sc, 4, out_fill=0x4500)
+    assert np.all(got0 == 0)
+    # one query head per workgroup (no GQA sharing), split 8
+    ns = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, 8, share=False)
+    check_decode(ns, q, k, v, H, Hkv, D, L, L * D, sc, orc, "per-head split 8")
+
+
+def test_attention_decode_concurrent_streams_reuse_scratch(gpu, orc):
+    c = helpers.case("attention__s1_kv513_h8_kv2_d128_decode")
+    x = helpers.inputs(c)
+    q, k, v = x["q"], x["k"], x["v"]
+    H, Hkv, D, L = 8, 2, 128, 513
+    sc = 1.0 / np.sqrt(D)
+    dq, dk, dv = gpu.upload(q), gpu.upload(k), gpu.upload(v)
+    da, db = gpu.empty((H, D), np.uint16), gpu.empty((H, D), np.uint16)
+    sa, sb = gpu.stream(), gpu.stream()
+    try:
+        for _ in range(4):
+            gpu.call("eng_attention_decode_f16", dq.ptr, dk.ptr, dv.ptr, da.ptr, L, H, Hkv, D, L * D,
+                     sc, 8, sa.handle)
+            gpu.call("eng_attention_decode_f16", dq.ptr, dk.ptr, dv.ptr, db.ptr, 257, H, Hkv, D, L * D,
+                     sc, 8, sb.handle)
+        sa.sync()
+        sb.sync()
+    finally:
+        sa.destroy()
+        sb.destroy()
+    check_decode(da.download(), q, k, v, H, Hkv, D, L, L * D, sc, orc, "stream A")
+    check_decode(db.download(), q, k, v, H, Hkv, D, 257, L * D, sc, orc, "stream B (kv_len 257)")
+
+
+# --------------------------------------------------------- model shapes
+@pytest.mark.parametrize("H,Hkv,D,L,split", [
+    (32, 32, 128, 2048, 0),   # Llama-2-7B, MHA
+    (32, 4, 64, 2048, 0),     # TinyLlama, GQA 8
+    (32, 4, 64, 2048, 1),     # one split per head group
+    (12, 3, 128, 1000, 0),    # GQA 4, ragged
+    (10, 5, 64, 777, 3),      # GQA 2
+    (6, 6, 64, 300, 0),       # short sequence: one split
+])
+def test_attention_decode_shapes_against_oracle(gpu, orc, H, Hkv, D, L, split):
+    rng = np.random.default_rng(H * 1000 + L)
+    q = rand_half(orc, rng, (H, D))
+    k = rand_half(orc, rng, (Hkv, L, D))
+    v = rand_half(orc, rng, (Hkv, L, D))
+    sc = 1.0 / np.sqrt(D)
+    got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split)
+    check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"decode H={H}/{Hkv} D={D} L={L}")
+
+
+def test_attention_decode_unaligned_cache_takes_scalar_loads(gpu, orc):
+    """K / V not 16-byte aligned, and a head stride that is not a multiple of 8."""
+    rng = np.random.default_rng(41)
+    H, Hkv, D, L = 8, 2, 64, 300
+    stride = L * D + 3
+    q = rand_half(orc, rng, (H, D))
+    k = np.zeros(Hkv * stride + 1, np.uint16)
+    v = np.zeros(Hkv * stride + 1, np.uint16)
+    kk = rand_half(orc, rng, (Hkv, L, D))
+    vv = rand_half(orc, rng, (Hkv, L, D))
+    for h in range(Hkv):
+        k[1 + h * stride: 1 + h * stride + L * D] = kk[h].ravel()
+        v[1 + h * stride: 1 + h * stride + L * D] = vv[h].ravel()
+    sc = 1.0 / np.sqrt(D)
+    got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, stride, sc, 0, k_offset=1)
+    check_decode(got, q, k[1:], v[1:], H, Hkv, D, L, stride, sc, orc, "unaligned cache")
+
+
+@pytest.mark.parametrize("L", [8192, 32768])
+def test_attention_decode_long_sequence(gpu, orc, L):
+    """Reference attention_decode_long_sequence: GQA 8:1, D = 64, a strided
+    KV cache padded with NaN past kv_len (never read), O(1) outputs."""
+    rng = np.random.default_rng(L)
+    H, Hkv, D = 8, 1, 64
+    stride = (L + 17) * D
+    nan16 = np.uint16(0x7E00)
+    sc = 1.0 / np.sqrt(D)
+    q = rand_half(orc, rng, (H, D), 0.5)
+    kk = rand_half(orc, rng, (L, D), 0.5)
+    pos = np.linspace(-1, 1, L)[:, None]
+    vv = orc.f32_to_f16((0.5 + 0.5 * pos + 0.25 * rng.standard_normal((L, D))).astype(np.float32))
+
+    def cache(body):
+        c = np.full(Hkv * stride, nan16, np.uint16)
+        c[: L * D] = body.ravel()
+        return c
+
+    k, v = cache(kk), cache(vv)
+    ref = helpers.as_f64(orc.attention(q, k, v, H, Hkv, D, L, stride, sc)).reshape(H, D)
+    rtol = 2.0**-9
+    atol = rtol * max(1e-3, float(np.sqrt(np.mean(ref**2))))
+    for split, share in ((0, True), (1, True), (0, False)):
+        got = helpers.as_f64(gpu_decode(gpu, q, k, v, L, H, Hkv, D, stride, sc, split, share=share))
+        assert np.isfinite(got).all()
+        helpers.assert_within(got, ref, atol + rtol * np.abs(ref), f"L={L} split={split} share={share}")
+    # needles: one key far above the rest, at the last position, then two equal
+    # needles in different splits (cross-split merge)
+    qn = orc.f32_to_f16(np.full((H, D), 0.5, np.float32))
+    for js in ((L - 1,), (17, L - 1)):
+        kn = np.zeros((L, D), np.float32)
+        for j in js:
+            kn[j] = 8.0
+        vn = orc.f32_to_f16((rng.standard_normal((L, D))).astype(np.float32))
+        target = helpers.as_f64(vn[list(js)]).mean(axis=0)
+        got = helpers.as_f64(gpu_decode(gpu, qn, cache(orc.f32_to_f16(kn)), cache(vn), L, H, Hkv, D,
+                                        stride, sc, 0)).reshape(H, D)
+        for h in range(H):
+            helpers.assert_within(got[h], target, rtol * (1 + np.abs(target)), f"needle {js} h={h}")
+
+
+# ------------------------------------------------------------------- bridge
+def test_cast_kernels_are_exact(gpu, orc):
+    rng = np.random.default_rng(42)
+    f = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 1000,
+                        np.array([65504.0, 65520.0, 1e-8, -0.0, np.inf], np.float32)])
+    d_in, d_h = gpu.upload(f), gpu.empty(f.shape, np.uint16)
+    gpu.call("eng_cast_f32_to_f16", d_in.ptr, d_h.ptr, f.size, None)
+    gpu.sync()
+    with np.errstate(over="ignore"):
+        assert np.array_equal(d_h.download(), f.astype(np.float16).view(np.uint16))
+    bits = np.arange(0, 0x7C00, dtype=np.uint16)
+    d_b, d_f = gpu.upload(bits), gpu.empty(bits.shape, np.float32)
+    gpu.call("eng_cast_f16_to_f32", d_b.ptr, d_f.ptr, bits.size, None)
+    gpu.sync()
+    assert np.array_equal(d_f.download(), bits.view(np.float16).astype(np.float32))
+
+
+def test_kv_cache_write_scatters_token_major_to_head_major(gpu):
+    rng = np.random.default_rng(43)
+    s_new, Hkv, D, max_seq, pos = 5, 3, 64, 40, 11
+    kn = rng.integers(0, 0x7BFF, (s_new, Hkv, D)).astype(np.uint16)
+    vn = rng.integers(0, 0x7BFF, (s_new, Hkv, D)).astype(np.uint16)
+    kc = np.full((Hkv, max_seq, D), 7, np.uint16)
+    vc = np.full((Hkv, max_seq, D), 9, np.uint16)
+    dkn, dvn, dkc, dvc = gpu.upload(kn), gpu.upload(vn), gpu.upload(kc), gpu.upload(vc)
+    gpu.call("eng_kv_cache_write_f16", dkn.ptr, dvn.ptr, dkc.ptr, dvc.ptr, s_new, Hkv, D, pos, max_seq, None)
+    gpu.sync()
+    ek, ev = kc.copy(), vc.copy()
+    ek[:, pos:pos + s_new] = kn.transpose(1, 0, 2)
+    ev[:, pos:pos + s_new] = vn.transpose(1, 0, 2)
+    assert np.array_equal(dkc.download(), ek)
+    assert np.array_equal(dvc.download(), ev)

@@ -107,7 +107,77 @@ def check_rmsnorm_linear_swiglu(orc, c):
     return helpers.assert_within(got, exp, swiglu_bound(g64, u64, dg, du, exp), c["stem"])
 
 
+def run_attention(orc, c):
+    x = helpers.inputs(c)
+    P = c["params"]
+    D, s_kv = P["head_dim"], P["s_kv"]
+    return orc.attention(x["q"], x["k"], x["v"], P["n_heads"], P["n_kv_heads"], D, s_kv, s_kv * D,
+                         1.0 / np.sqrt(D), P["q_pos_offset"], P["is_causal"], want_lse=True)
+
+
+def check_attention(orc, c):
+    out, lse = run_attention(orc, c)
+    exp = helpers.expected(c).reshape(out.shape)
+    # double softmax then half rounding (half an ulp) against the float32-stored golden
+    bound = helpers.U16 * np.abs(exp) + 2.0**-25 + 2 * helpers.U32 * np.abs(exp)
+    helpers.assert_within(helpers.as_f64(out), exp, bound, c["stem"])
+    else_ = helpers.expected(c, "lse")
+    helpers.assert_within(lse, else_, 2 * helpers.U32 * np.abs(else_) + 1e-30, c["stem"] + " lse")
+
+
 # ------------------------------------------------------------------- goldens
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("attention")])
+def test_attention_matches_golden(orc, stem):
+    check_attention(orc, helpers.case(stem))
+
+
+def test_attention_closed_forms(orc):
+    rng = np.random.default_rng(14)
+    H, Hkv, D, L = 8, 2, 128, 40
+    f16 = lambda a: orc.f32_to_f16(np.asarray(a, np.float32))
+    q = f16(rng.standard_normal((1, H, D)))
+    k = f16(rng.standard_normal((Hkv, L, D)))
+    v = f16(rng.standard_normal((Hkv, L, D)))
+    sc = 1.0 / np.sqrt(D)
+    # one key: the output is that key's value row, exactly
+    o1 = orc.attention(q, k, v, H, Hkv, D, 1, L * D, sc)
+    for h in range(H):
+        assert np.array_equal(o1[0, h], v[h // 4, 0])
+    # q = 0: every score is 0, the output is the mean value row
+    o0 = orc.attention(np.zeros_like(q), k, v, H, Hkv, D, L, L * D, sc)
+    mean = helpers.as_f64(v).mean(axis=1)
+    for h in range(H):
+        assert np.array_equal(o0[0, h], orc.f32_to_f16(mean[h // 4].astype(np.float32)))
+    # a dominant key (score ~ +1e4 above the rest) selects its value row
+    kd = k.copy()
+    kd[:, 17] = f16(np.sign(helpers.as_f64(q[0, ::4])) * 8.0)
+    od = orc.attention(q, kd, v, H, Hkv, D, L, L * D, 1.0)
+    for h in range(0, H, 4):
+        assert np.array_equal(od[0, h], v[h // 4, 17])
+    # key order does not matter (up to one half ulp from the double sums)
+    perm = rng.permutation(L)
+    op = orc.attention(q, k[:, perm], v[:, perm], H, Hkv, D, L, L * D, sc)
+    o = orc.attention(q, k, v, H, Hkv, D, L, L * D, sc)
+    helpers.assert_within(helpers.as_f64(op), helpers.as_f64(o),
+                          helpers.U16 * np.abs(helpers.as_f64(o)) * 2 + 2.0**-24, "key permutation")
+    # strided KV heads and GQA mapping against NumPy float64
+    stride = (L + 5) * D
+    kp = np.zeros((Hkv, L + 5, D), np.uint16)
+    vp = np.zeros((Hkv, L + 5, D), np.uint16)
+    kp[:, :L], vp[:, :L] = k, v
+    os_ = orc.attention(q, kp, vp, H, Hkv, D, L, stride, sc)
+    q64, k64, v64 = (helpers.as_f64(a) for a in (q, k, v))
+    for h in range(H):
+        s = k64[h // 4] @ q64[0, h] * sc
+        w = np.exp(s - s.max())
+        ref = (w @ v64[h // 4]) / w.sum()
+        helpers.assert_within(helpers.as_f64(os_[0, h]), ref, helpers.U16 * np.abs(ref) + 2.0**-25,
+                              f"strided head {h}")
+    # the empty sequence writes zeros and -inf lse
+    oe, le = orc.attention(q, k, v, H, Hkv, D, 0, 0, sc, want_lse=True)
+    assert np.all(oe == 0) and np.all(np.isneginf(le))
+
+
 @pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("vector_add")])
 def test_vector_add_is_float32_addition(orc, stem):
     c = helpers.case(stem)
@@ -387,6 +457,7 @@ def test_float_to_half_matches_numpy(orc):
     (5, lambda o: test_float_to_half_matches_numpy(o)),
     (6, lambda o: check_swiglu(o, helpers.case("swiglu__n1024"))),
     (7, lambda o: check_residual_rmsnorm(o, helpers.case("residual_rmsnorm__1x4096_w"))),
+    (8, lambda o: check_attention(o, helpers.case("attention__s1_kv257_h32_kv4_d64_decode"))),
 ])
 def test_planted_mistakes_are_caught(mutation, check):
     mutant = helpers.oracle(mutation)
