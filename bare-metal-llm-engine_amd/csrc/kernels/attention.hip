@@ -12,11 +12,12 @@
 // load of K and of V), so D / 8 lanes cover a key and one wave load reads 64 /
 // (D / 8) keys (4 at D = 128, 8 at D = 64) as 1 KiB contiguous. Each K / V
 // byte is read once for all G heads of the group. Each lane keeps an online
-// softmax state (m, l, o[8]) per head; U key steps are processed as a chunk
-// (scores first, one rescale per chunk). States merge exactly -- weights
-// exp(m_i - m) -- across the key lanes of a wave by shuffles, across the 4
-// waves through LDS, and across splits in flash_decode_reduce_kernel, always
-// in a fixed order. Splits write fp32 (o, m, l) partials to pooled,
+// softmax state (m, l, o[8]) per head in the log2 domain; U key steps are
+// processed as a chunk (scores first, one rescale per chunk). Key-lane dot
+// products are summed with DPP; states merge exactly -- weights 2^(m_i - m)
+// -- across the key lanes of a wave by shuffles, across the 4 waves through
+// LDS, and across splits in flash_decode_reduce_kernel, always in a fixed
+// order. Splits write fp32 (o, m, l) partials to pooled,
 // stream-ordered scratch.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
@@ -45,9 +46,30 @@ __device__ __forceinline__ H8 load_h8(const _Float16* p) {
   }
 }
 
-// exp(a - b) as a merge weight; 0 for an empty state (a == -inf).
+// Scores and softmax states are kept in the log2 domain (scores scaled by
+// scale * log2(e)), so every weight is one hardware exp2: 2^(a - b), 0 for an
+// empty state (a == -inf). The output o / l is the same ratio.
+constexpr float kLog2e = 1.4426950408889634f;
 __device__ __forceinline__ float merge_weight(float a, float b) {
-  return a > kNegInf ? expf(a - b) : 0.0f;
+  return a > kNegInf ? __builtin_amdgcn_exp2f(a - b) : 0.0f;
+}
+
+// Sum over the LPK (8 or 16) consecutive lanes that hold one key, left in
+// every one of them: DPP quad_perm xor-1 and xor-2, then row_half_mirror
+// (lane i <- 7 - i within 8 lanes) and, for 16 lanes, row_mirror (i <- 15 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false);
+  return x + __builtin_bit_cast(float, y);
+}
+template <int LPK>
+__device__ __forceinline__ float sum_key_lanes(float x) {
+  static_assert(LPK == 8 || LPK == 16, "8 or 16 lanes per key");
+  x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = dpp_add<0x141>(x);  // row_half_mirror
+  if constexpr (LPK == 16) x = dpp_add<0x140>(x);  // row_mirror
+  return x;
 }
 
 template <int D, int G, int U, bool VEC, bool PARTIAL>
@@ -74,6 +96,7 @@ __global__ __launch_bounds__(kThreads) void flash_decode_split_kernel(
   const int split = static_cast<int>(blockIdx.y);
   const long long j0 = kv_len * split / nsplit;
   const long long j1 = kv_len * (split + 1) / nsplit;
+  const float scale2 = scale * kLog2e;
 
   float qf[G][8];
 #pragma unroll
@@ -113,9 +136,8 @@ __global__ __launch_bounds__(kThreads) void flash_decode_split_kernel(
         float part = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) part = fmaf(qf[g][e], static_cast<float>(kr[u][e]), part);
-#pragma unroll
-        for (int off = LPK / 2; off > 0; off >>= 1) part += __shfl_xor(part, off);
-        s[u] = ok[u] ? part * scale : kNegInf;
+        part = sum_key_lanes<LPK>(part);
+        s[u] = ok[u] ? part * scale2 : kNegInf;
         cm = fmaxf(cm, s[u]);
       }
       const float mn = fmaxf(m[g], cm);
@@ -195,34 +217,272 @@ __global__ __launch_bounds__(kThreads) void flash_decode_split_kernel(
   }
 }
 
-// out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = exp(m_s - max m),
-// splits combined in order; one workgroup of D threads per head.
-template <int D>
-__global__ __launch_bounds__(D) void flash_decode_reduce_kernel(const float* __restrict__ part_o,
-                                                                const float* __restrict__ part_ml,
-                                                                _Float16* __restrict__ out,
-                                                                int nsplit) {
-  const long long h = blockIdx.x;
-  const int d = threadIdx.x;
-  const long long base = h * nsplit;
-  float mg = kNegInf;
-  for (int s = 0; s < nsplit; ++s) mg = fmaxf(mg, part_ml[2 * (base + s)]);
-  float lg = 0.0f, og = 0.0f;
-  if (mg > kNegInf) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float w = merge_weight(part_ml[2 * (base + s)], mg);
-      lg = fmaf(part_ml[2 * (base + s) + 1], w, lg);
-      og = fmaf(part_o[(base + s) * D + d], w, og);
+// GQA decode with K / V tiles staged in LDS: one 256-thread workgroup per (KV
+// head's group of G query heads, split). All threads copy a tile of T = 4096
+// / D keys of K and V (16 KB) from HBM into LDS, double-buffered: the copy of
+// tile t + 1 is in flight while tile t is computed, one barrier per tile. Wave
+// w owns HPW = G / 4 query heads (G = 8: 2, G = 4: 1) or, for G = 2, one head
+// and every other half-tile (WPH = 2 waves per head); its lanes read K / V
+// rows from LDS (16 bytes per lane, a wave read is 1 KiB contiguous) and keep
+// the online softmax state of their heads only, so K / V bytes leave HBM once
+// per group while the registers hold G / 4 heads, not G.
+template <int D, int G, bool VEC, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void flash_decode_gqa_lds_kernel(
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k,
+    const _Float16* __restrict__ v, _Float16* __restrict__ out, float* __restrict__ part_o,
+    float* __restrict__ part_ml, long long kv_len, long long group_size,
+    long long kv_head_stride, float scale, int nsplit) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(G == 2 || G == 4 || G == 8, "GQA group of 2, 4 or 8 heads");
+  constexpr int LPK = D / 8;                 // lanes per key
+  constexpr int KPW = 64 / LPK;              // keys per wave read
+  constexpr int T = 4096 / D;                // keys per tile
+  constexpr int HPW = G >= 4 ? G / 4 : 1;    // heads per wave
+  constexpr int WPH = 4 / (G / HPW);         // waves per head
+  constexpr int KEYS = T / WPH;              // keys of a tile per wave
+  constexpr int U = KEYS / KPW;              // wave reads per tile
+  constexpr int CHUNKS = 2 * T * LPK;        // 16-byte chunks of a K + V tile
+  constexpr int CPT = CHUNKS / kThreads;     // chunks per thread
+  static_assert(CHUNKS % kThreads == 0 && U >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) _Float16 tile[2][2][T][D];
+  __shared__ float s_m[4][HPW];
+  __shared__ float s_l[4][HPW];
+  __shared__ float s_o[4][HPW][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int sub = lane / LPK;
+  const int d0 = (lane % LPK) * 8;
+  const int hslot = wave % (G / HPW);        // which HPW heads of the group
+  const int kslice = wave / (G / HPW);       // which key slice of each tile
+  const long long hg0 = static_cast<long long>(blockIdx.x) * G;
+  const long long kvh = hg0 / group_size;
+  const int split = static_cast<int>(blockIdx.y);
+  const long long j0 = kv_len * split / nsplit;
+  const long long j1 = kv_len * (split + 1) / nsplit;
+  const long long ntiles = (j1 - j0 + T - 1) / T;
+  const float scale2 = scale * kLog2e;
+
+  float qf[HPW][8];
+#pragma unroll
+  for (int g = 0; g < HPW; ++g) {
+    const long long h = hg0 + hslot * HPW + g;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[g][e] = static_cast<float>(q[h * D + d0 + e]);
+  }
+  float m[HPW], l[HPW], o[HPW][8];
+#pragma unroll
+  for (int g = 0; g < HPW; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+
+  const _Float16* kb = k + kvh * kv_head_stride;
+  const _Float16* vb = v + kvh * kv_head_stride;
+  H8 stage[CPT];
+  auto fetch = [&](long long t) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      const int sel = c / (T * LPK);
+      const int r = c - sel * (T * LPK);
+      const int key = r / LPK;
+      const int col = r - key * LPK;
+      const long long j = j0 + t * T + key;
+      const _Float16* src = (sel == 0 ? kb : vb) + j * D + col * 8;
+      stage[i] = j < j1 ? load_h8<VEC>(src) : H8{};
+    }
+  };
+  auto commit = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + i * kThreads;
+      const int sel = c / (T * LPK);
+      const int r = c - sel * (T * LPK);
+      const int key = r / LPK;
+      const int col = r - key * LPK;
+      *reinterpret_cast<H8*>(&tile[buf][sel][key][col * 8]) = stage[i];
+    }
+  };
+
+  if (ntiles > 0) {
+    fetch(0);
+    commit(0);
+  }
+  __syncthreads();
+  for (long long t = 0; t < ntiles; ++t) {
+    const int buf = static_cast<int>(t & 1);
+    if (t + 1 < ntiles) fetch(t + 1);
+    const long long tbase = j0 + t * T;
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+      float s[U];
+      float cm = kNegInf;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int key = kslice * KEYS + u * KPW + sub;
+        const H8 kr = *reinterpret_cast<const H8*>(&tile[buf][0][key][d0]);
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part = fmaf(qf[g][e], static_cast<float>(kr[e]), part);
+        part = sum_key_lanes<LPK>(part);
+        s[u] = tbase + key < j1 ? part * scale2 : kNegInf;
+        cm = fmaxf(cm, s[u]);
+      }
+      const float mn = fmaxf(m[g], cm);
+      if (mn > kNegInf) {
+        const float alpha = merge_weight(m[g], mn);
+        l[g] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int key = kslice * KEYS + u * KPW + sub;
+          const float p = merge_weight(s[u], mn);
+          const H8 vr = *reinterpret_cast<const H8*>(&tile[buf][1][key][d0]);
+          l[g] += p;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, static_cast<float>(vr[e]), o[g][e]);
+        }
+        m[g] = mn;
+      }
+    }
+    if (t + 1 < ntiles) commit(buf ^ 1);
+    __syncthreads();
+  }
+
+  // Merge the key lanes of the wave.
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo = __shfl_xor(l[g], off);
+      const float mn = fmaxf(m[g], mo);
+      const float sa = merge_weight(m[g], mn);
+      const float sb = merge_weight(mo, mn);
+      l[g] = l[g] * sa + lo * sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float oo = __shfl_xor(o[g][e], off);
+        o[g][e] = o[g][e] * sa + oo * sb;
+      }
+      m[g] = mn;
     }
   }
-  out[h * D + d] = static_cast<_Float16>(lg > 0.0f ? og / lg : 0.0f);
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wave][g][d0 + e] = o[g][e];
+      if (lane == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Combine the WPH waves of each head (in wave order) and write.
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int gh = idx / D;                  // head within the group
+    const int d = idx - gh * D;
+    const int hs = gh / HPW;                 // head slot
+    const int g = gh - hs * HPW;
+    float mb = kNegInf;
+#pragma unroll
+    for (int w = 0; w < WPH; ++w) mb = fmaxf(mb, s_m[hs + w * (G / HPW)][g]);
+    float lb = 0.0f, ob = 0.0f;
+    if (mb > kNegInf) {
+#pragma unroll
+      for (int w = 0; w < WPH; ++w) {
+        const int ww = hs + w * (G / HPW);
+        const float wt = merge_weight(s_m[ww][g], mb);
+        lb = fmaf(s_l[ww][g], wt, lb);
+        ob = fmaf(s_o[ww][g][d], wt, ob);
+      }
+    }
+    const long long h = hg0 + gh;
+    if constexpr (PARTIAL) {
+      const long long slot = h * nsplit + split;
+      part_o[slot * D + d] = ob;
+      if (d == 0) {
+        part_ml[2 * slot] = mb;
+        part_ml[2 * slot + 1] = lb;
+      }
+    } else {
+      out[h * D + d] = static_cast<_Float16>(lb > 0.0f ? ob / lb : 0.0f);
+    }
+  }
 }
 
-// Splits when the caller passes split_kv = 0: about two workgroups per CU
-// across all head groups, at least 256 keys per split, at most 256 splits.
+// out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = 2^(m_s - max m).
+// One 256-thread workgroup per head: thread (c, d), c = tid / D, merges the
+// states of splits c, c + C, ... (C = 256 / D) online -- independent loads,
+// unrolled so several are in flight -- and the C slice states then merge in
+// slice order through LDS: one pass over the partials, one barrier.
+template <int D>
+__global__ __launch_bounds__(kThreads) void flash_decode_reduce_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    _Float16* __restrict__ out, int nsplit) {
+  constexpr int C = kThreads / D;
+  __shared__ float s_o[C][D];
+  __shared__ float s_m[C];
+  __shared__ float s_l[C];
+  const int tid = threadIdx.x;
+  const int c = tid / D;
+  const int d = tid - c * D;
+  const long long base = static_cast<long long>(blockIdx.x) * nsplit;
+  float m = kNegInf, l = 0.0f, o = 0.0f;
+#pragma unroll 8
+  for (int sp = c; sp < nsplit; sp += C) {
+    const float ms = part_ml[2 * (base + sp)];
+    const float ls = part_ml[2 * (base + sp) + 1];
+    const float os = part_o[(base + sp) * D + d];
+    const float mn = fmaxf(m, ms);
+    if (mn > kNegInf) {
+      const float wa = merge_weight(m, mn);
+      const float wb = merge_weight(ms, mn);
+      l = l * wa + ls * wb;
+      o = o * wa + os * wb;
+      m = mn;
+    }
+  }
+  s_o[c][d] = o;
+  if (d == 0) {
+    s_m[c] = m;
+    s_l[c] = l;
+  }
+  __syncthreads();
+  if (tid < D) {
+    float mg = kNegInf;
+#pragma unroll
+    for (int cc = 0; cc < C; ++cc) mg = fmaxf(mg, s_m[cc]);
+    float lg = 0.0f, og = 0.0f;
+    if (mg > kNegInf) {
+#pragma unroll
+      for (int cc = 0; cc < C; ++cc) {
+        const float w = merge_weight(s_m[cc], mg);
+        lg = fmaf(s_l[cc], w, lg);
+        og = fmaf(s_o[cc][tid], w, og);
+      }
+    }
+    out[static_cast<long long>(blockIdx.x) * D + tid] =
+        static_cast<_Float16>(lg > 0.0f ? og / lg : 0.0f);
+  }
+}
+
+// Splits when the caller passes split_kv = 0: about one workgroup per CU
+// across all head groups, at least 256 keys per split, at most 256 splits
+// (a sweep on MI355X over the reference's decode shapes -- 32/4 heads at
+// D = 64 and 32/32 at D = 128, 512 to 32768 keys, cold caches -- put the best
+// split count there or within 3% of it for every shape from 2048 keys up).
 int auto_splits(long long kv_len, long long head_blocks) {
   const long long cus = device_cu_count();
-  const long long wanted = (2 * cus + head_blocks - 1) / head_blocks;
+  const long long wanted = (cus + head_blocks - 1) / head_blocks;
   const long long by_len = kv_len / 256;
   return static_cast<int>(std::max(1LL, std::min({wanted, by_len, 256LL})));
 }
@@ -237,26 +497,36 @@ struct DecodeArgs {
   int splits;
 };
 
+// One query head per workgroup (MHA, or GQA sharing switched off): the
+// register kernel with 8 key steps in flight per lane. GQA groups: the
+// LDS-tile kernel.
+template <int D, int G, bool VEC, bool PARTIAL>
+void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
+  if constexpr (G == 1) {
+    flash_decode_split_kernel<D, 1, 8, VEC, PARTIAL><<<grid, kThreads, 0, s>>>(
+        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+        a.scale, a.splits);
+  } else {
+    flash_decode_gqa_lds_kernel<D, G, VEC, PARTIAL><<<grid, kThreads, 0, s>>>(
+        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+        a.scale, a.splits);
+  }
+  ENG_LAUNCH_CHECK();
+}
+
 template <int D, int G, bool VEC>
 void run_decode(const DecodeArgs& a, hipStream_t s) {
-  constexpr int U = 2;
-  const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
   if (a.splits == 1) {
-    flash_decode_split_kernel<D, G, U, VEC, false><<<grid, kThreads, 0, s>>>(
-        a.q, a.k, a.v, a.out, nullptr, nullptr, a.kv_len, a.group_size, a.kv_head_stride,
-        a.scale, 1);
-    ENG_LAUNCH_CHECK();
+    launch_split<D, G, VEC, false>(a, nullptr, nullptr, s);
     return;
   }
   const std::size_t slots = static_cast<std::size_t>(a.n_heads) * a.splits;
   PoolScratch scratch(slots * (D + 2) * sizeof(float), s);
   float* part_o = static_cast<float*>(scratch.get());
   float* part_ml = part_o + slots * D;
-  flash_decode_split_kernel<D, G, U, VEC, true><<<grid, kThreads, 0, s>>>(
-      a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
-      a.scale, a.splits);
-  ENG_LAUNCH_CHECK();
-  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), D, 0, s>>>(
+  launch_split<D, G, VEC, true>(a, part_o, part_ml, s);
+  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), kThreads, 0, s>>>(
       part_o, part_ml, a.out, a.splits);
   ENG_LAUNCH_CHECK();
 }
@@ -319,8 +589,11 @@ void attention_decode_any(const eng_half* q, const eng_half* k, const eng_half* 
       }
     }
   }
+  // Explicit requests are clamped to kv_len (as the reference does) and to
+  // 256 (more splits only add partial states to merge); the result does not
+  // depend on the split count beyond rounding.
   const int req = split_kv == 0 ? auto_splits(kv_len, n_heads / G) : split_kv;
-  a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 65535})));
+  a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 256})));
   const bool vec = aligned_to(k, 16) && aligned_to(v, 16) && kv_head_stride % 8 == 0;
   if (head_dim == 64) {
     if (vec) {

@@ -1,7 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,ffn,stack]
+                    [--only config2,config3,refapi,gemm,ffn,attention,stack]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -478,13 +478,51 @@ def rows_ffn(eng, timer) -> list:
     return rows
 
 
+def rows_attention(eng, timer) -> list:
+    """Decode attention at the reference's benchmark shapes (bench_kernels.cu:
+    1079-1092): TinyLlama 32/4 heads at D = 64 and Llama-2-7B 32/32 at D = 128,
+    cold KV caches (about 1 GiB of rotating copies). Bytes: K and V once plus
+    q and out, 2 (2 H_kv L D + 2 H D)."""
+    rows = []
+    rng = np.random.default_rng(11)
+    f = eng.lib.eng_attention_decode_with_mode_f16
+    cases = [(512, 32, 4, 64), (2048, 32, 4, 64), (8192, 32, 4, 64), (16384, 32, 4, 64),
+             (32768, 32, 4, 64), (512, 32, 32, 128), (2048, 32, 32, 128), (8192, 32, 32, 128)]
+    for L, H, Hkv, D in cases:
+        elems = 2 * Hkv * L * D
+        nslots = max(2, (1 << 30) // (2 * elems) + 1)
+        kv = rotating(eng, (0.5 * rng.standard_normal(elems, dtype=np.float32)).astype(np.float16).view(np.uint16),
+                      nslots)
+        dq = eng.upload((0.5 * rng.standard_normal(H * D, dtype=np.float32)).astype(np.float16).view(np.uint16))
+        do = eng.empty(H * D, np.uint16)
+        sc = 1.0 / np.sqrt(D)
+        nbytes = 2 * (2 * Hkv * L * D + 2 * H * D)
+        arch = "TinyLlama" if Hkv == 4 else "Llama-2-7B"
+        variants = [("auto splits", 0, 1)]
+        if L >= 8192:
+            variants.append(("split_kv=1", 1, 1))
+        if Hkv == 4 and L == 32768:
+            variants.append(("no GQA sharing", 0, 0))
+        for tag, sp, share in variants:
+            def launch(i, s, sp=sp, share=share):
+                kp = kv[i % nslots].ptr
+                rc = f(dq.ptr, kp, kp + 2 * Hkv * L * D, do.ptr, L, H, Hkv, D, L * D, sc, sp, share, s)
+                if rc:
+                    raise RuntimeError(eng.last_error())
+            rows.append(hbm_row(f"attention_decode {arch} L={L} H={H}/{Hkv} D={D} cold, {tag}",
+                                timer.sampled(launch), nbytes))
+        for d in kv + [dq, do]:
+            d.free()
+    return rows
+
+
 def rows_stack(eng, timer) -> list:
     return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True),
             bench_llama_stack(eng, timer, nk=True, fused_glu=True)]
 
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
-          "gemm": rows_gemm, "ffn": rows_ffn, "stack": rows_stack}
+          "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack}
 
 
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False) -> dict:

@@ -6,12 +6,14 @@ Two tolerances are checked everywhere:
 * the reference's own decode tolerance (tests/test_kernels.cu:292-296):
   |got - exp| <= 1.5 * 2^-10 + 4 * s_kv * 2^-23 + 2 * 2^-10 * |exp|;
 * a derived bound (u = 2^-24): with w_j = exp(s_j - max s), the fp32 scores
-  carry |ds_j| <= (D + 1) u scale sum_d |q_d k_jd| =: e_j, so the weights carry
-  at most 2 max_j e_j + 4u relative error (their difference in the exponent,
-  exp's own rounding); the fp32 sums of p_j v_j and p_j add (s_kv + 16) u
-  relative to sum_j w_j |v_j|; the output adds half rounding 2^-11 |y| + 2^-25:
+  carry |ds_j| <= (D + 1) u scale sum_d |q_d k_jd| =: e_j; the kernel forms
+  weights as 2^((s_j - m) log2 e) with the scale, the subtraction and the
+  hardware exp2 rounding once each (<= 4 u max_j |s_j| + 8 u relative), so the
+  weights carry at most 2 max_j e_j + 4 u max_j |s_j| + 8 u relative error;
+  the fp32 sums of p_j v_j and p_j add (s_kv + 24) u relative to
+  sum_j w_j |v_j|; the output adds half rounding 2^-11 |y| + 2^-25:
       |got - y| <= 2^-11 |y| + 2^-25
-                   + (2 max e + (s_kv + 24) u) (sum_j w_j |v_j| / sum_j w_j + |y|).
+                   + (2 max e + 4 u max |s| + (s_kv + 32) u) (sum_j w_j |v_j| / sum_j w_j + |y|).
 Long sequences (8K / 32K keys) also use the reference's output-scaled
 tolerance (test_kernels.cu:2565-2640): rtol = 2^-9, atol = rtol * rms(out).
 """
@@ -44,7 +46,8 @@ def decode64(q, k, v, H, Hkv, D, L, stride, scale):
         y[h] = (w @ vh) / w.sum()
         e = (D + 1) * U * scale * (np.abs(kh) @ np.abs(q64[h]))
         mag = (w @ np.abs(vh)) / w.sum() + np.abs(y[h])
-        bound[h] = helpers.U16 * np.abs(y[h]) + 2.0**-25 + (2 * e.max() + (L + 24) * U) * mag
+        rel = 2 * e.max() + 4 * U * np.abs(s).max() + (L + 32) * U
+        bound[h] = helpers.U16 * np.abs(y[h]) + 2.0**-25 + rel * mag
     return y, bound
 
 
