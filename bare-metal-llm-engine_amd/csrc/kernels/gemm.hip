@@ -29,6 +29,7 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 namespace eng {
@@ -298,6 +299,262 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 }
 
+// Full-tile fp32 variant fed by direct global -> LDS loads
+// (global_load_lds_dwordx4: lane l of a wave writes 16 bytes at the wave's
+// LDS base + 16 l, from any global address the lane names). No staging
+// registers and no LDS store instructions: the next tile's loads are issued
+// at the top of the K step and land while the MFMAs run; one s_waitcnt and
+// one barrier end the step. LDS tiles are unpadded and the 16-byte chunk
+// positions are XOR-swizzled instead, which the fetch side applies by choosing
+// which global chunk each lane loads:
+//   * k-contiguous tiles (A, and B given [N x K]): chunk c of row r sits at
+//     c ^ ((r >> 1) & 7), so the 16 rows a 16-lane slice of ds_read_b128
+//     touches fall in 16 distinct bank groups;
+//   * [K x N] B tiles: chunk c of row k sits at c ^ (8 ((k >> 4) & 1)), so the
+//     rows k and k + 16 read by the two half-waves of a ds_read_b32 use
+//     disjoint banks.
+// Requires M % BM == N % BN == K % 32 == 0 and 16-byte aligned A, B (and gamma).
+__device__ __forceinline__ int swz_rows(int r) { return (r >> 1) & 7; }
+
+// 16-byte direct global -> LDS load of this lane; the LDS address of lane l is
+// lds + 16 l (lds must be the same in every lane of the wave). The builtin is
+// device-only: the host pass of a kernel template that names it would drop
+// the template's launch stub.
+__device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// Waits until this wave's outstanding memory operations, the direct LDS loads
+// included, have completed.
+__device__ __forceinline__ void wait_all_memory() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_s_waitcnt(0);
+#endif
+}
+__device__ __forceinline__ int swz_kn(int k) { return ((k >> 4) & 1) * 8; }
+
+//
+// The two stages of each operand are separate LDS variables and the K loop is
+// unrolled by two, so every LDS access names its buffer statically. The
+// compiler models a direct load's LDS write per lane and may otherwise fail to
+// prove that a fragment read of the current stage cannot overlap the loads
+// into the other one; it then makes the read wait for the whole next tile.
+// With distinct variables the accesses carry distinct alias scopes.
+//
+// RMS (fused RMSNorm, as in gemm_f32_mfma_kernel): A arrives unscaled. The K
+// tile's 32 gamma values travel with A and B by direct load; gamma multiplies
+// each A fragment value as it feeds the MFMA, the sums of squares of A's rows
+// are accumulated from the same fragment values (waves of column 0 only; the
+// two K halves of a row are joined by one shuffle), and the row scale
+// multiplies the accumulators in the epilogue through LDS.
+template <int BM, int BN, bool BNK, bool RMS>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
+    const float* __restrict__ gamma, float eps, int M, int N, int K, int tiles_m, int tiles_n) {
+  constexpr int WM = BM / 2;
+  constexpr int WN = BN / 2;
+  constexpr int MB = WM / 32;
+  constexpr int NB = WN / 32;
+  constexpr int A_CH = BM * BK / 4;        // 16-byte chunks of an A tile
+  constexpr int B_CH = BN * BK / 4;
+  constexpr int A_INST = A_CH / kThreads;  // chunk loads per thread (= per wave instruction count)
+  constexpr int B_INST = B_CH / kThreads;
+  constexpr int BROW = BN / 4;             // chunks per [K x N] B row
+  constexpr int GN = RMS ? BK : 4;
+  static_assert(A_CH % kThreads == 0 && B_CH % kThreads == 0, "tile shape");
+  __shared__ __attribute__((aligned(1024))) float As0[BM * BK];
+  __shared__ __attribute__((aligned(1024))) float As1[BM * BK];
+  __shared__ __attribute__((aligned(1024))) float Bs0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) float Bs1[BN * BK];
+  __shared__ __attribute__((aligned(16))) float Gs0[GN];
+  __shared__ __attribute__((aligned(16))) float Gs1[GN];
+  __shared__ float row_scale[RMS ? BM : 1];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int li = lane & 31;
+  const int lg = lane >> 5;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
+
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+
+  // Issue the direct loads of K tile kt into one stage. Wave w's j-th
+  // instruction fills chunk slots (4 j + w) * 64 + lane; with RMS, lanes 0-7
+  // of the last wave load the tile's gamma values.
+  auto fetch = [&](float* as, float* bs, float* gs, int kt) {
+    const int k0 = kt * BK;
+    if constexpr (RMS) {
+      if (gamma != nullptr && wave == kThreads / 64 - 1 && lane < BK / 4)
+        lds_dma16(gamma + k0 + 4 * lane, gs);
+    }
+#pragma unroll
+    for (int j = 0; j < A_INST; ++j) {
+      const int slot0 = (4 * j + wave) * 64;
+      const int slot = slot0 + lane;
+      const int r = slot >> 3;
+      const int c = (slot & 7) ^ swz_rows(r);
+      const float* src = A + static_cast<long long>(m0 + r) * K + k0 + 4 * c;
+      lds_dma16(src, as + 4 * slot0);
+    }
+#pragma unroll
+    for (int j = 0; j < B_INST; ++j) {
+      const int slot0 = (4 * j + wave) * 64;
+      const int slot = slot0 + lane;
+      const float* src;
+      if constexpr (BNK) {
+        const int r = slot >> 3;
+        const int c = (slot & 7) ^ swz_rows(r);
+        src = B + static_cast<long long>(n0 + r) * K + k0 + 4 * c;
+      } else {
+        const int k = slot / BROW;
+        const int c = (slot % BROW) ^ swz_kn(k);
+        src = B + static_cast<long long>(k0 + k) * N + n0 + 4 * c;
+      }
+      lds_dma16(src, bs + 4 * slot0);
+    }
+  };
+
+  floatx16 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
+
+  float ss[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.0f;
+
+  // One K step on a resident stage: fragment reads, RMS work, 16 MFMA
+  // k-slices. The A fragment of lane (li, lg) holds k = 16 lg + 4 q + e.
+  auto compute = [&](const float* as, const float* bs, const float* gs) {
+    floatx4 af[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int r = wm * WM + mb * 32 + li;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = (lg * 4 + q) ^ swz_rows(r);
+        af[mb][q] = *reinterpret_cast<const floatx4*>(as + 4 * (r * 8 + c));
+      }
+    }
+    if constexpr (RMS) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const floatx4 g = *reinterpret_cast<const floatx4*>(gs + lg * 16 + 4 * q);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          if (wn == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss[mb] = fmaf(af[mb][q][e], af[mb][q][e], ss[mb]);
+          }
+          af[mb][q] *= g;
+        }
+      }
+    }
+    float bf[NB][16];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      if constexpr (BNK) {
+        const int r = wn * WN + nb * 32 + li;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int c = (lg * 4 + q) ^ swz_rows(r);
+          const floatx4 v = *reinterpret_cast<const floatx4*>(bs + 4 * (r * 8 + c));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bf[nb][4 * q + e] = v[e];
+        }
+      } else {
+        const int n = wn * WN + nb * 32 + li;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+          const int k = lg * 16 + s;
+          const int c = (n >> 2) ^ swz_kn(k);
+          bf[nb][s] = bs[4 * (k * BROW + c) + (n & 3)];
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const float a = af[mb][s >> 2][s & 3];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bf[nb][s], acc[mb][nb], 0, 0, 0);
+      }
+    }
+  };
+
+  // A null gamma is a gain of one: both gamma stages hold ones and are never
+  // fetched into.
+  if constexpr (RMS) {
+    if (gamma == nullptr && t < BK) {
+      Gs0[t] = 1.0f;
+      Gs1[t] = 1.0f;
+    }
+  }
+
+  const int nk = K / BK;
+  fetch(As0, Bs0, Gs0, 0);
+  wait_all_memory();
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    if (kt + 1 < nk) fetch(As1, Bs1, Gs1, kt + 1);
+    compute(As0, Bs0, Gs0);
+    wait_all_memory();  // this wave's loads of the next tile have landed
+    __syncthreads();
+    if (kt + 1 < nk) {
+      if (kt + 2 < nk) fetch(As0, Bs0, Gs0, kt + 2);
+      compute(As1, Bs1, Gs1);
+      wait_all_memory();
+      __syncthreads();
+    }
+  }
+
+  if constexpr (RMS) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const float tot = ss[mb] + __shfl_xor(ss[mb], 32);
+      if (wn == 0 && lg == 0) row_scale[wm * WM + mb * 32 + li] = 1.0f / sqrtf(tot / K + eps);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int col = n0 + wn * WN + nb * 32 + li;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int rl = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        float out = acc[mb][nb][v];
+        if constexpr (RMS) out *= row_scale[rl];
+        C[static_cast<long long>(m0 + rl) * N + col] = out;
+      }
+    }
+  }
+}
+
+// The direct-load kernel can be switched off (ENGINE_GEMM_NO_DMA=1) to
+// compare it with the register-staged kernel on the same shapes.
+bool dma_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_NO_DMA");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
 template <int BM, int BN, typename BT, bool BNK, bool RMS>
 void run_gemm(const GemmArgs& a, hipStream_t stream) {
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
@@ -313,6 +570,17 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
+  if constexpr (std::is_same<BT, float>::value) {
+    const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned_to(a.A, 16) &&
+                      aligned_to(a.B, 16) && (BNK || N % 4 == 0) &&
+                      (!RMS || a.gamma == nullptr || aligned_to(a.gamma, 16));
+    if (full && dma_enabled()) {
+      gemm_f32_mfma_dma_kernel<BM, BN, BNK, RMS><<<grid, kThreads, 0, stream>>>(
+          a.A, B, a.C, a.gamma, a.eps, M, N, K, tiles_m, tiles_n);
+      ENG_LAUNCH_CHECK();
+      return;
+    }
+  }
 #define ENG_GEMM_LAUNCH(VA_, VB_)                                                       \
   gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(  \
       a.A, B, a.C, a.gamma, M, N, K, a.eps, tiles_m, tiles_n)
