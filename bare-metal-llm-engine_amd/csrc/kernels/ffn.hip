@@ -6,9 +6,10 @@
 // SwiGLU on one weight stream). Decode (M == 1, 16-byte aligned operands, K
 // up to 16384) runs gemv_rows_glu_kernel: one launch that stages x * gamma in
 // LDS, streams each output's gate and up rows together and applies SiLU in the
-// epilogue, so gate and up never reach memory. Other shapes compute gate and
-// up with the fused RMSNorm+linear launchers (GEMV or MFMA GEMM) into pooled,
-// stream-ordered scratch and finish with the SwiGLU kernel. Preconditions and
+// epilogue, so gate and up never reach memory. Other decode rows compute gate
+// and up with the fused RMSNorm + GEMV kernels; M > 1 normalises the rows
+// once, runs the MFMA GEMM for gate and for up, all into pooled,
+// stream-ordered scratch, and finishes with the SwiGLU kernel. Preconditions and
 // messages follow rmsnorm_linear; any zero dimension writes nothing.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
@@ -47,9 +48,12 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
   }
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
-  PoolScratch scratch(2 * mn * sizeof(float), s);
-  float* gate = static_cast<float*>(scratch.get());
+  const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
+  PoolScratch scratch((mk + 2 * mn) * sizeof(float), s);
+  float* xn = static_cast<float*>(scratch.get());  // first: the GEMM wants it 16-byte aligned
+  float* gate = xn + mk;
   float* up = gate + mn;
+  if (M > 1) launch_rmsnorm(in, gamma, xn, M, K, eps, s);
   for (int half = 0; half < 2; ++half) {
     const void* W = half == 0 ? static_cast<const void*>(Wg) : static_cast<const void*>(Wu);
     float* out = half == 0 ? gate : up;
@@ -68,7 +72,7 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
       launch_gemv(g, s);
     } else {
       GemmArgs g;
-      g.A = in;
+      g.A = xn;
       g.B = W;
       g.b = elem;
       g.b_nk = true;
@@ -76,9 +80,6 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
       g.M = M;
       g.N = N;
       g.K = K;
-      g.gamma = gamma;
-      g.rms = true;
-      g.eps = eps;
       launch_gemm(g, s);
     }
   }

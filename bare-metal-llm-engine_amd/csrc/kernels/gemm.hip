@@ -1,11 +1,13 @@
 // gemm.hip -- FP32 GEMM on gfx950 matrix cores (C[M x N] = A[M x K] . B[K x N]).
 //
 // Replaces the SIMT register-tiled kernel behind matmul_register_tiled
-// (reference kernels/matmul_register_tiled.cu:48-199) and serves the M > 1
-// case of rmsnorm_linear (reference kernels/rmsnorm_linear.cu:195-199), with
-// the RMSNorm fused in: gamma scales A's columns as they are staged, the row
-// sums of squares are accumulated from the same staged values, and the row
-// scale multiplies the accumulators in the epilogue.
+// (reference kernels/matmul_register_tiled.cu:48-199); it is also the M > 1
+// half of rmsnorm_linear, which, as in the reference
+// (kernels/rmsnorm_linear.cu:191-199), normalises the rows into pooled scratch
+// first. (Fusing the RMSNorm into this kernel -- gamma applied to the A
+// fragments, row sums of squares taken from them -- measured 30% slower than
+// the separate pass at 512 x 4096 x 4096: every N-tile repeats the multiply,
+// and it sits between the LDS read and the MFMA.)
 //
 // Tiling for wave64 and v_mfma_f32_32x32x2_f32:
 //   * workgroup tile BM x BN (128 x 128, 128 x 64 or 64 x 64), K step 32,
@@ -18,8 +20,11 @@
 //     32-63), so each lane reads a contiguous 16-float run of its A row
 //     (ds_read_b128) and a 16-row column of B (ds_read_b32, conflict-free) --
 //     or, when B is given transposed ([N x K]), a 16-float run of its B row;
-//   * A and B tiles are double-buffered in LDS with 4-float row padding; the
-//     next tile's global loads are issued before the current tile's MFMAs;
+//   * full tiles of fp32 operands take gemm_f32_mfma_dma_kernel, which loads
+//     tiles straight into LDS (below); other shapes and fp16 B take
+//     gemm_f32_mfma_kernel, which stages through registers: A and B tiles are
+//     double-buffered in LDS with 4-float row padding and the next tile's
+//     global loads are issued before the current tile's MFMAs;
 //   * the workgroup -> tile map is XCD-aware: consecutive workgroup ids go to
 //     different XCDs, so ids are regrouped so each XCD works on a contiguous
 //     band of tiles (grouped 8 tile-rows deep) and shares A/B panels in its L2;
@@ -78,10 +83,10 @@ __device__ __forceinline__ void tile_of(int wg, int tiles_m, int tiles_n, int& t
 
 // BNK: B is given as B^T, row-major [N x K]; its tile is staged like an A
 // tile (n rows, k contiguous) and its fragments are read like A's.
-template <int BM, int BN, typename BT, bool BNK, bool VA, bool VB, bool RMS>
+template <int BM, int BN, typename BT, bool BNK, bool VA, bool VB>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
-    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C,
-    const float* __restrict__ gamma, int M, int N, int K, float eps, int tiles_m, int tiles_n) {
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
+    int K, int tiles_m, int tiles_n) {
   using BL = BStage<BT, BNK, BN>;
   constexpr int WM = BM / 2;       // rows per wave
   constexpr int WN = BN / 2;       // columns per wave
@@ -92,7 +97,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   constexpr int kBTile = BNK ? BN * AS : BK * BSK;
   __shared__ __attribute__((aligned(16))) float As[2][BM * AS];
   __shared__ __attribute__((aligned(16))) float Bs[2][kBTile];
-  __shared__ float row_scale[RMS ? BM : 1];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -115,9 +119,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
 
   floatx4 ra[A_LOADS];
   float rb[BL::kLoads][BL::kVec];
-  float ss[A_LOADS];
-#pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) ss[i] = 0.0f;
 
   auto load_a = [&](int k0) {
 #pragma unroll
@@ -172,29 +173,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
     }
   };
 
-  auto store_tiles = [&](int buf, int k0) {
-    floatx4 g = {1.0f, 1.0f, 1.0f, 1.0f};
-    if constexpr (RMS) {
-      if (gamma != nullptr) {
+  auto store_tiles = [&](int buf) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int k = k0 + a_col + e;
-          g[e] = k < K ? gamma[k] : 0.0f;
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      floatx4 v = ra[i];
-      if constexpr (RMS) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          ss[i] = fmaf(v[e], v[e], ss[i]);
-          v[e] *= g[e];
-        }
-      }
-      *reinterpret_cast<floatx4*>(&As[buf][(a_row + 32 * i) * AS + a_col]) = v;
-    }
+    for (int i = 0; i < A_LOADS; ++i)
+      *reinterpret_cast<floatx4*>(&As[buf][(a_row + 32 * i) * AS + a_col]) = ra[i];
 #pragma unroll
     for (int i = 0; i < BL::kLoads; ++i) {
       float* dst = &Bs[buf][(b_row + BL::kRowsPerLoad * i) * (BNK ? AS : BSK) + b_col];
@@ -217,7 +199,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   const int nk = (K + BK - 1) / BK;
   load_a(0);
   load_b(0);
-  store_tiles(0, 0);
+  store_tiles(0);
   __syncthreads();
 
   for (int kt = 0; kt < nk; ++kt) {
@@ -263,20 +245,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
       }
     }
 
-    if (kt + 1 < nk) store_tiles(cur ^ 1, (kt + 1) * BK);
-    __syncthreads();
-  }
-
-  if constexpr (RMS) {
-    // The 8 lanes t..t+7 staged the same A row: fold their sums of squares.
-#pragma unroll
-    for (int i = 0; i < A_LOADS; ++i) {
-      float v = ss[i];
-      v += __shfl_xor(v, 1);
-      v += __shfl_xor(v, 2);
-      v += __shfl_xor(v, 4);
-      if ((t & 7) == 0) row_scale[a_row + 32 * i] = 1.0f / sqrtf(v / static_cast<float>(K) + eps);
-    }
+    if (kt + 1 < nk) store_tiles(cur ^ 1);
     __syncthreads();
   }
 
@@ -287,13 +256,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
       const int col = n0 + wn * WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int rl = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
-        const int row = m0 + rl;
-        if (row < M && col < N) {
-          float out = acc[mb][nb][v];
-          if constexpr (RMS) out *= row_scale[rl];
-          C[static_cast<long long>(row) * N + col] = out;
-        }
+        const int row = m0 + wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        if (row < M && col < N) C[static_cast<long long>(row) * N + col] = acc[mb][nb][v];
       }
     }
   }
@@ -313,7 +277,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
 //   * [K x N] B tiles: chunk c of row k sits at c ^ (8 ((k >> 4) & 1)), so the
 //     rows k and k + 16 read by the two half-waves of a ds_read_b32 use
 //     disjoint banks.
-// Requires M % BM == N % BN == K % 32 == 0 and 16-byte aligned A, B (and gamma).
+// Requires M % BM == N % BN == K % 32 == 0 and 16-byte aligned A and B.
 __device__ __forceinline__ int swz_rows(int r) { return (r >> 1) & 7; }
 
 // 16-byte direct global -> LDS load of this lane; the LDS address of lane l is
@@ -342,17 +306,10 @@ __device__ __forceinline__ int swz_kn(int k) { return ((k >> 4) & 1) * 8; }
 // prove that a fragment read of the current stage cannot overlap the loads
 // into the other one; it then makes the read wait for the whole next tile.
 // With distinct variables the accesses carry distinct alias scopes.
-//
-// RMS (fused RMSNorm, as in gemm_f32_mfma_kernel): A arrives unscaled. The K
-// tile's 32 gamma values travel with A and B by direct load; gamma multiplies
-// each A fragment value as it feeds the MFMA, the sums of squares of A's rows
-// are accumulated from the same fragment values (waves of column 0 only; the
-// two K halves of a row are joined by one shuffle), and the row scale
-// multiplies the accumulators in the epilogue through LDS.
-template <int BM, int BN, bool BNK, bool RMS>
+template <int BM, int BN, bool BNK>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C,
-    const float* __restrict__ gamma, float eps, int M, int N, int K, int tiles_m, int tiles_n) {
+    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
+    int K, int tiles_m, int tiles_n) {
   constexpr int WM = BM / 2;
   constexpr int WN = BN / 2;
   constexpr int MB = WM / 32;
@@ -362,15 +319,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
   constexpr int A_INST = A_CH / kThreads;  // chunk loads per thread (= per wave instruction count)
   constexpr int B_INST = B_CH / kThreads;
   constexpr int BROW = BN / 4;             // chunks per [K x N] B row
-  constexpr int GN = RMS ? BK : 4;
   static_assert(A_CH % kThreads == 0 && B_CH % kThreads == 0, "tile shape");
   __shared__ __attribute__((aligned(1024))) float As0[BM * BK];
   __shared__ __attribute__((aligned(1024))) float As1[BM * BK];
   __shared__ __attribute__((aligned(1024))) float Bs0[BN * BK];
   __shared__ __attribute__((aligned(1024))) float Bs1[BN * BK];
-  __shared__ __attribute__((aligned(16))) float Gs0[GN];
-  __shared__ __attribute__((aligned(16))) float Gs1[GN];
-  __shared__ float row_scale[RMS ? BM : 1];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -386,14 +339,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
   const int n0 = tn * BN;
 
   // Issue the direct loads of K tile kt into one stage. Wave w's j-th
-  // instruction fills chunk slots (4 j + w) * 64 + lane; with RMS, lanes 0-7
-  // of the last wave load the tile's gamma values.
-  auto fetch = [&](float* as, float* bs, float* gs, int kt) {
+  // instruction fills chunk slots (4 j + w) * 64 + lane.
+  auto fetch = [&](float* as, float* bs, int kt) {
     const int k0 = kt * BK;
-    if constexpr (RMS) {
-      if (gamma != nullptr && wave == kThreads / 64 - 1 && lane < BK / 4)
-        lds_dma16(gamma + k0 + 4 * lane, gs);
-    }
 #pragma unroll
     for (int j = 0; j < A_INST; ++j) {
       const int slot0 = (4 * j + wave) * 64;
@@ -429,13 +377,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
 
-  float ss[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) ss[mb] = 0.0f;
-
-  // One K step on a resident stage: fragment reads, RMS work, 16 MFMA
-  // k-slices. The A fragment of lane (li, lg) holds k = 16 lg + 4 q + e.
-  auto compute = [&](const float* as, const float* bs, const float* gs) {
+  // One K step on a resident stage: fragment reads and 16 MFMA k-slices.
+  // The A fragment of lane (li, lg) holds k = 16 lg + 4 q + e.
+  auto compute = [&](const float* as, const float* bs) {
     floatx4 af[MB][4];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -444,20 +388,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
       for (int q = 0; q < 4; ++q) {
         const int c = (lg * 4 + q) ^ swz_rows(r);
         af[mb][q] = *reinterpret_cast<const floatx4*>(as + 4 * (r * 8 + c));
-      }
-    }
-    if constexpr (RMS) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const floatx4 g = *reinterpret_cast<const floatx4*>(gs + lg * 16 + 4 * q);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          if (wn == 0) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ss[mb] = fmaf(af[mb][q][e], af[mb][q][e], ss[mb]);
-          }
-          af[mb][q] *= g;
-        }
       }
     }
     float bf[NB][16];
@@ -494,39 +424,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     }
   };
 
-  // A null gamma is a gain of one: both gamma stages hold ones and are never
-  // fetched into.
-  if constexpr (RMS) {
-    if (gamma == nullptr && t < BK) {
-      Gs0[t] = 1.0f;
-      Gs1[t] = 1.0f;
-    }
-  }
-
   const int nk = K / BK;
-  fetch(As0, Bs0, Gs0, 0);
+  fetch(As0, Bs0, 0);
   wait_all_memory();
   __syncthreads();
   for (int kt = 0; kt < nk; kt += 2) {
-    if (kt + 1 < nk) fetch(As1, Bs1, Gs1, kt + 1);
-    compute(As0, Bs0, Gs0);
+    if (kt + 1 < nk) fetch(As1, Bs1, kt + 1);
+    compute(As0, Bs0);
     wait_all_memory();  // this wave's loads of the next tile have landed
     __syncthreads();
     if (kt + 1 < nk) {
-      if (kt + 2 < nk) fetch(As0, Bs0, Gs0, kt + 2);
-      compute(As1, Bs1, Gs1);
+      if (kt + 2 < nk) fetch(As0, Bs0, kt + 2);
+      compute(As1, Bs1);
       wait_all_memory();
       __syncthreads();
     }
-  }
-
-  if constexpr (RMS) {
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const float tot = ss[mb] + __shfl_xor(ss[mb], 32);
-      if (wn == 0 && lg == 0) row_scale[wm * WM + mb * 32 + li] = 1.0f / sqrtf(tot / K + eps);
-    }
-    __syncthreads();
   }
 
 #pragma unroll
@@ -536,10 +448,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
       const int col = n0 + wn * WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int rl = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
-        float out = acc[mb][nb][v];
-        if constexpr (RMS) out *= row_scale[rl];
-        C[static_cast<long long>(m0 + rl) * N + col] = out;
+        const int row = m0 + wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        C[static_cast<long long>(row) * N + col] = acc[mb][nb][v];
       }
     }
   }
@@ -555,7 +465,7 @@ bool dma_enabled() {
   return on;
 }
 
-template <int BM, int BN, typename BT, bool BNK, bool RMS>
+template <int BM, int BN, typename BT, bool BNK>
 void run_gemm(const GemmArgs& a, hipStream_t stream) {
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
   const bool va = (a.K % 4 == 0) && aligned_to(a.A, 16);
@@ -572,18 +482,17 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   const BT* B = static_cast<const BT*>(a.B);
   if constexpr (std::is_same<BT, float>::value) {
     const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned_to(a.A, 16) &&
-                      aligned_to(a.B, 16) && (BNK || N % 4 == 0) &&
-                      (!RMS || a.gamma == nullptr || aligned_to(a.gamma, 16));
+                      aligned_to(a.B, 16) && (BNK || N % 4 == 0);
     if (full && dma_enabled()) {
-      gemm_f32_mfma_dma_kernel<BM, BN, BNK, RMS><<<grid, kThreads, 0, stream>>>(
-          a.A, B, a.C, a.gamma, a.eps, M, N, K, tiles_m, tiles_n);
+      gemm_f32_mfma_dma_kernel<BM, BN, BNK><<<grid, kThreads, 0, stream>>>(a.A, B, a.C, M, N, K,
+                                                                          tiles_m, tiles_n);
       ENG_LAUNCH_CHECK();
       return;
     }
   }
-#define ENG_GEMM_LAUNCH(VA_, VB_)                                                       \
-  gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_, RMS><<<grid, kThreads, 0, stream>>>(  \
-      a.A, B, a.C, a.gamma, M, N, K, a.eps, tiles_m, tiles_n)
+#define ENG_GEMM_LAUNCH(VA_, VB_)                                                  \
+  gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_><<<grid, kThreads, 0, stream>>>(  \
+      a.A, B, a.C, M, N, K, tiles_m, tiles_n)
   if (va && vb) {
     ENG_GEMM_LAUNCH(true, true);
   } else if (va) {
@@ -617,27 +526,18 @@ Tile choose_tile(long long M, long long N) {
   return Tile::T64x64;
 }
 
-template <typename BT, bool BNK, bool RMS>
+template <typename BT, bool BNK>
 void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
   switch (choose_tile(a.M, a.N)) {
     case Tile::T128x128:
-      run_gemm<128, 128, BT, BNK, RMS>(a, stream);
+      run_gemm<128, 128, BT, BNK>(a, stream);
       break;
     case Tile::T128x64:
-      run_gemm<128, 64, BT, BNK, RMS>(a, stream);
+      run_gemm<128, 64, BT, BNK>(a, stream);
       break;
     case Tile::T64x64:
-      run_gemm<64, 64, BT, BNK, RMS>(a, stream);
+      run_gemm<64, 64, BT, BNK>(a, stream);
       break;
-  }
-}
-
-template <typename BT, bool BNK>
-void run_gemm_rms(const GemmArgs& a, hipStream_t stream) {
-  if (a.rms) {
-    run_gemm_tiled<BT, BNK, true>(a, stream);
-  } else {
-    run_gemm_tiled<BT, BNK, false>(a, stream);
   }
 }
 
@@ -648,15 +548,15 @@ void launch_gemm(const GemmArgs& a, hipStream_t stream) {
             "matmul: dimensions must fit in 31 bits");
   if (a.b == Elem::F32) {
     if (a.b_nk) {
-      run_gemm_rms<float, true>(a, stream);
+      run_gemm_tiled<float, true>(a, stream);
     } else {
-      run_gemm_rms<float, false>(a, stream);
+      run_gemm_tiled<float, false>(a, stream);
     }
   } else {
     if (a.b_nk) {
-      run_gemm_rms<_Float16, true>(a, stream);
+      run_gemm_tiled<_Float16, true>(a, stream);
     } else {
-      run_gemm_rms<_Float16, false>(a, stream);
+      run_gemm_tiled<_Float16, false>(a, stream);
     }
   }
 }

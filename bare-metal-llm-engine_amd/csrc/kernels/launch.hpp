@@ -42,9 +42,6 @@ struct GemmArgs {
   std::int64_t M = 0;
   std::int64_t N = 0;
   std::int64_t K = 0;
-  const float* gamma = nullptr;
-  bool rms = false;
-  float eps = 0.0f;
 };
 void launch_gemm(const GemmArgs& a, hipStream_t stream);
 

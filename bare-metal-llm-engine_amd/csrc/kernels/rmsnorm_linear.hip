@@ -3,14 +3,18 @@
 //   out[r][n] = sum_k (in[r][k] * s_r * w_k) * W[k][n],  s_r = 1/sqrt(mean_k in[r][k]^2 + eps)
 //
 // The reference dispatches rmsnorm into pooled scratch and then gemv (M == 1)
-// or the register-tiled GEMM (M > 1). Here both cases are single fused
-// kernels that never materialise the normalised rows: M == 1 runs the split-K
-// GEMV with the sum of squares reduced alongside the dot products, M > 1 runs
-// the MFMA GEMM with gamma applied while A is staged and s_r applied in the
-// epilogue. Preconditions, messages and the "any zero dimension is a no-op"
-// rule are the reference's. The *_nk entries take W output-major [N x K]
+// or the register-tiled GEMM (M > 1). Here M == 1 is one fused launch that
+// never materialises the normalised row (the GEMV kernels with the sum of
+// squares reduced alongside the dot products); M > 1 keeps the reference's
+// structure -- rmsnorm into pooled, stream-ordered scratch, then the MFMA GEMM
+// -- because the normalisation pass is a few microseconds of HBM traffic while
+// applying gamma inside the GEMM repeats the multiply for every N-tile.
+// Preconditions, messages and the "any zero dimension is a no-op" rule are
+// the reference's. The *_nk entries take W output-major [N x K]
 // (out = RMSNorm(in) . W^T), the layout the decode path streams best.
 #include "launch.hpp"
+
+#include <cstddef>
 
 namespace eng {
 namespace {
@@ -39,8 +43,12 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     launch_gemv(g, s);
     return;
   }
+  PoolScratch normed(static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float),
+                     s);
+  float* xn = static_cast<float*>(normed.get());
+  launch_rmsnorm(in, rms_weight, xn, M, K, eps, s);
   GemmArgs g;
-  g.A = in;
+  g.A = xn;
   g.B = W;
   g.b = w_elem;
   g.b_nk = nk;
@@ -48,9 +56,6 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
   g.M = M;
   g.N = N;
   g.K = K;
-  g.gamma = rms_weight;
-  g.rms = true;
-  g.eps = eps;
   launch_gemm(g, s);
 }
 

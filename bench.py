@@ -418,7 +418,8 @@ def rows_gemm(eng, timer) -> list:
     dC = eng.empty((M, N), np.float32)
     f = eng.lib.eng_rmsnorm_linear_f32
     st = timer.sampled(lambda i, s: f(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
-    rows.append(gemm_row("rmsnorm_linear_f32 512x4096x4096 (fused MFMA GEMM)", st, M, N, K))
+    rows.append(gemm_row("rmsnorm_linear_f32 512x4096x4096 (rmsnorm into pooled scratch + MFMA GEMM)",
+                        st, M, N, K))
     dA.free(), dg.free(), dW.free(), dC.free()
     return rows
 

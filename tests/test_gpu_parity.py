@@ -501,8 +501,8 @@ def test_rmsnorm_linear_nk_prefill_against_oracle(gpu, orc, M, N, K, dtype):
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f32_full_tiles_against_oracle(gpu, orc, M, N, K, layout, with_gamma):
-    # Whole 64/128-row tiles with K % 32 == 0 take the direct-to-LDS GEMM,
-    # which applies gamma to A fragments and sums squares from them.
+    # M > 1 normalises into pooled scratch; whole 64/128-row tiles with
+    # K % 32 == 0 then take the direct-to-LDS GEMM.
     rng = np.random.default_rng(7 * M + N + K + (layout == "nk"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
