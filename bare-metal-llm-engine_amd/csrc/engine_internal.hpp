@@ -12,7 +12,9 @@
 
 #include <engine_hip.h>
 
+#include <cstddef>
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -66,16 +68,30 @@ inline bool aligned_to(const void* p, std::uintptr_t bytes) {
 // capture these launches in a HIP graph).
 void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 
-// Per-(device, stream) workspace of the split-K GEMV: launches on one stream
-// run in order, so consecutive calls can reuse it without synchronisation.
-struct GemvWorkspace {
-  float* partials = nullptr;    // [capacity_partials] fp32 partial sums
-  float* partial_ss = nullptr;  // [capacity_ss] fp32 partial sums of squares
-  std::size_t capacity_partials = 0;
-  std::size_t capacity_ss = 0;
+// Per-(device, stream) scratch arena for launchers whose kernels pass partial
+// results to a second kernel on the same stream (split-K GEMV, split-KV
+// attention). Launches on one stream run in order, so a call can reuse the
+// arena as soon as the previous call's launches are queued: no event, no
+// allocation per call. The lease holds the arena's lock until it goes out of
+// scope, so two host threads that share a stream cannot interleave their
+// kernel pairs on it; take it before the first launch that writes the arena
+// and keep it past the last one that reads it. The arena grows to the largest
+// request (growth waits for the stream, then reallocates) and is freed when
+// the stream is destroyed through eng_stream_destroy, or at exit. A launcher
+// takes at most one lease at a time.
+class StreamScratch {
+ public:
+  StreamScratch(hipStream_t stream, std::size_t bytes);
+  ~StreamScratch();
+  StreamScratch(const StreamScratch&) = delete;
+  StreamScratch& operator=(const StreamScratch&) = delete;
+  void* get() const { return ptr_; }
+
+ private:
+  std::mutex* held_ = nullptr;
+  void* ptr_ = nullptr;
 };
-GemvWorkspace& gemv_workspace(hipStream_t stream);
-void release_gemv_workspace(hipStream_t stream);
+void release_stream_scratch(hipStream_t stream);
 
 // Stream-ordered scratch from the process-wide device pool (the reference's
 // ScopedPoolBuffer, include/engine/pool_allocator.hpp:97-148): returned to the

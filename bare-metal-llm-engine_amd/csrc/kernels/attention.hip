@@ -17,8 +17,8 @@
 // products are summed with DPP; states merge exactly -- weights 2^(m_i - m)
 // -- across the key lanes of a wave by shuffles, across the 4 waves through
 // LDS, and across splits in flash_decode_reduce_kernel, always in a fixed
-// order. Splits write fp32 (o, m, l) partials to pooled,
-// stream-ordered scratch.
+// order. Splits write fp32 (o, m, l) partials to the stream's scratch arena
+// (reused in stream order: no allocation or event per call).
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
@@ -31,6 +31,7 @@ namespace eng {
 namespace {
 
 using H8 = gemv::RawVec<_Float16, 8>::type;
+using H2 = gemv::RawVec<_Float16, 2>::type;
 constexpr int kThreads = 256;
 constexpr float kNegInf = -__builtin_huge_valf();
 
@@ -419,16 +420,307 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_lds_kernel(
   }
 }
 
+// Direct-to-LDS variant for 16-byte aligned caches (any G of 1, 2, 4, 8):
+// the same work split and arithmetic as flash_decode_gqa_lds_kernel (G = 1:
+// four waves per head, each a quarter of every tile), but the K / V tiles are
+// loaded straight into LDS (global_load_lds_dwordx4: lane l writes 16 bytes
+// at the wave's LDS base + 16 l) through NST = 4 stages, so three tiles are in
+// flight while one is computed and no registers hold staged data. A tile is
+// T keys of K and of V, each 8 KiB contiguous in the cache; keys past the
+// split's end are loaded from its last key (in bounds, finite) and masked to
+// a -inf score. The stages are separate LDS variables and the tile loop is
+// unrolled by NST, so every LDS access names its stage statically: the
+// compiler then need not make a fragment read wait for the loads in flight
+// into the other stages. Each thread issues the same CPT loads per tile, and
+// waits with vmcnt = CPT x (tiles issued after the one it needs).
+__device__ __forceinline__ void lds_dma16(const _Float16* src, _Float16* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt 7 and lgkmcnt 15
+// are the "don't wait" values).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+
+// Workgroup barrier without a memory fence. __syncthreads() also fences, and
+// the compiler implements that fence with a wait for every load in flight --
+// all stages of the pipeline, not just the tile the next step needs. The
+// tile loop writes no LDS, and each wave waits for its own loads of the next
+// tile before it arrives, so a bare s_barrier is all it needs; the memory
+// clobber keeps the compiler from moving LDS reads across it.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int CPT>
+__device__ __forceinline__ void wait_tiles_after(int outstanding) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  if (outstanding >= 2) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CPT));
+  } else if (outstanding == 1) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT));
+  } else {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  }
+#endif
+}
+
+template <int D, int G, bool PARTIAL>
+__global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k,
+    const _Float16* __restrict__ v, _Float16* __restrict__ out, float* __restrict__ part_o,
+    float* __restrict__ part_ml, long long kv_len, long long group_size,
+    long long kv_head_stride, float scale, int nsplit) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "1, 2, 4 or 8 heads per workgroup");
+  constexpr int NST = 4;                     // pipeline stages
+  constexpr int LPK = D / 8;                 // lanes per key
+  constexpr int KPW = 64 / LPK;              // keys per wave read
+  constexpr int T = 4096 / D;                // keys per tile
+  constexpr int HPW = G >= 4 ? G / 4 : 1;    // heads per wave
+  constexpr int WPH = 4 / (G / HPW);         // waves per head
+  constexpr int KEYS = T / WPH;              // keys of a tile per wave
+  constexpr int U = KEYS / KPW;              // wave reads per tile
+  constexpr int HALF_CHUNKS = T * LPK;       // 16-byte chunks of the K (or V) tile
+  constexpr int CPH = HALF_CHUNKS / kThreads;  // loads per thread per K (or V) tile
+  constexpr int CPT = 2 * CPH;               // loads per thread per tile
+  static_assert(HALF_CHUNKS % kThreads == 0 && U >= 1, "tile shape");
+  // Stage s: K tile at S_s[0, T D), V tile at S_s[T D, 2 T D).
+  __shared__ __attribute__((aligned(1024))) _Float16 S0[2 * T * D], S1[2 * T * D], S2[2 * T * D],
+      S3[2 * T * D];
+  __shared__ float s_m[4][HPW];
+  __shared__ float s_l[4][HPW];
+  __shared__ float s_o[4][HPW][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane / LPK;
+  const int d0 = (lane % LPK) * 8;
+  const int hslot = wave % (G / HPW);        // which HPW heads of the group
+  const int kslice = wave / (G / HPW);       // which key slice of each tile
+  const long long hg0 = static_cast<long long>(blockIdx.x) * G;
+  const long long kvh = hg0 / group_size;
+  const int split = static_cast<int>(blockIdx.y);
+  const long long j0 = kv_len * split / nsplit;
+  const long long j1 = kv_len * (split + 1) / nsplit;
+  const int ntiles = static_cast<int>((j1 - j0 + T - 1) / T);
+  const float scale2 = scale * kLog2e;
+
+  // q stays fp16: the scores are v_dot2 (two exact fp16 products added to an
+  // fp32 accumulator) of q and K pairs.
+  H2 qh[HPW][4];
+#pragma unroll
+  for (int g = 0; g < HPW; ++g) {
+    const long long h = hg0 + hslot * HPW + g;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) qh[g][p] = H2{q[h * D + d0 + 2 * p], q[h * D + d0 + 2 * p + 1]};
+  }
+  float m[HPW], l[HPW], o[HPW][8];
+#pragma unroll
+  for (int g = 0; g < HPW; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.0f;
+  }
+
+  const _Float16* kb = k + kvh * kv_head_stride;
+  const _Float16* vb = v + kvh * kv_head_stride;
+  // Loads of tile t into one stage: the thread's i-th load of the K (V) tile
+  // fills chunk slot (4 i + wave) * 64 + lane, i.e. key slot / LPK, dims
+  // (slot % LPK) * 8 .. + 7.
+  auto fetch = [&](_Float16* st, int t) __attribute__((always_inline)) {
+    _Float16* ks = st;
+    _Float16* vs = st + T * D;
+#pragma unroll
+    for (int i = 0; i < CPH; ++i) {
+      const int slot0 = (4 * i + wave) * 64;
+      const int slot = slot0 + lane;
+      long long j = j0 + static_cast<long long>(t) * T + slot / LPK;
+      j = j < j1 ? j : j1 - 1;
+      const long long off = j * D + (slot % LPK) * 8;
+      lds_dma16(kb + off, ks + 8 * slot0);
+      lds_dma16(vb + off, vs + 8 * slot0);
+    }
+  };
+  // One resident tile. Each K row is read once for the wave's HPW heads;
+  // each head's state is rescaled once; each V row is read and converted to
+  // fp32 once, then accumulated into every head with plain FMAs (a mixed
+  // fp16 x fp32 FMA per head would repeat the conversion at a lower rate).
+  // An all -inf state stays empty: its weights 2^(s - m) are 0.
+  auto compute = [&](const _Float16* st, int t) __attribute__((always_inline)) {
+    const _Float16* ks = st;
+    const _Float16* vs = st + T * D;
+    const long long tbase = j0 + static_cast<long long>(t) * T;
+    float sc[HPW][U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = kslice * KEYS + u * KPW + sub;
+      const bool valid = tbase + key < j1;
+      const H8 kr = *reinterpret_cast<const H8*>(ks + key * D + d0);
+#pragma unroll
+      for (int g = 0; g < HPW; ++g) {
+        float part = 0.0f;
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+          part = __builtin_amdgcn_fdot2(qh[g][p], H2{kr[2 * p], kr[2 * p + 1]}, part, false);
+        part = sum_key_lanes<LPK>(part);
+        sc[g][u] = valid ? part * scale2 : kNegInf;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+      float cm = sc[g][0];
+#pragma unroll
+      for (int u = 1; u < U; ++u) cm = fmaxf(cm, sc[g][u]);
+      const float mn = fmaxf(m[g], cm);
+      const float alpha = merge_weight(m[g], mn);
+      l[g] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+      m[g] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = kslice * KEYS + u * KPW + sub;
+      const H8 vr = *reinterpret_cast<const H8*>(vs + key * D + d0);
+      float vf[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        vf[e] = static_cast<float>(vr[e]);
+        // Materialise the fp32 value once: otherwise the conversion is folded
+        // into a mixed-precision FMA for every head.
+        asm("" : "+v"(vf[e]));
+      }
+#pragma unroll
+      for (int g = 0; g < HPW; ++g) {
+        const float p = merge_weight(sc[g][u], m[g]);
+        l[g] += p;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vf[e], o[g][e]);
+      }
+    }
+  };
+  // Step t on stage S: refill the stage step t - 1 used with tile t + NST - 1,
+  // compute tile t, then wait for tile t + 1 and meet at the barrier.
+  auto step = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
+    if (t + NST - 1 < ntiles) fetch(next, t + NST - 1);
+    compute(st, t);
+    const int last_issued = t + NST - 1 < ntiles - 1 ? t + NST - 1 : ntiles - 1;
+    wait_tiles_after<CPT>(last_issued - (t + 1));
+    barrier_no_fence();
+  };
+
+  // Prologue: tiles 0 .. NST - 2 in flight, tile 0 resident.
+  fetch(S0, 0);
+  if (1 < ntiles) fetch(S1, 1);
+  if (2 < ntiles) fetch(S2, 2);
+  {
+    const int last_issued = ntiles - 1 < NST - 2 ? ntiles - 1 : NST - 2;
+    wait_tiles_after<CPT>(last_issued);
+    barrier_no_fence();
+  }
+  // Steady state (every step refills a stage and leaves two tiles in flight):
+  // no branches around the loads or waits, so the compiler's own wait
+  // analysis stays exact. Then the last tiles, with the general step.
+  auto steady = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
+    fetch(next, t + NST - 1);
+    compute(st, t);
+    wait_tiles_after<CPT>(2);
+    barrier_no_fence();
+  };
+  int t = 0;
+  for (; t + 2 * NST - 2 < ntiles; t += NST) {
+    steady(S0, S3, t);
+    steady(S1, S0, t + 1);
+    steady(S2, S1, t + 2);
+    steady(S3, S2, t + 3);
+  }
+  for (; t < ntiles; t += NST) {
+    step(S0, S3, t);
+    if (t + 1 < ntiles) step(S1, S0, t + 1);
+    if (t + 2 < ntiles) step(S2, S1, t + 2);
+    if (t + 3 < ntiles) step(S3, S2, t + 3);
+  }
+
+  // Merge the key lanes of the wave.
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo = __shfl_xor(l[g], off);
+      const float mn = fmaxf(m[g], mo);
+      const float sa = merge_weight(m[g], mn);
+      const float sb = merge_weight(mo, mn);
+      l[g] = l[g] * sa + lo * sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float oo = __shfl_xor(o[g][e], off);
+        o[g][e] = o[g][e] * sa + oo * sb;
+      }
+      m[g] = mn;
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < HPW; ++g) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_o[wave][g][d0 + e] = o[g][e];
+      if (lane == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Combine the WPH waves of each head (in wave order) and write.
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int gh = idx / D;                  // head within the group
+    const int d = idx - gh * D;
+    const int hs = gh / HPW;                 // head slot
+    const int g = gh - hs * HPW;
+    float mb = kNegInf;
+#pragma unroll
+    for (int w = 0; w < WPH; ++w) mb = fmaxf(mb, s_m[hs + w * (G / HPW)][g]);
+    float lb = 0.0f, ob = 0.0f;
+    if (mb > kNegInf) {
+#pragma unroll
+      for (int w = 0; w < WPH; ++w) {
+        const int ww = hs + w * (G / HPW);
+        const float wt = merge_weight(s_m[ww][g], mb);
+        lb = fmaf(s_l[ww][g], wt, lb);
+        ob = fmaf(s_o[ww][g][d], wt, ob);
+      }
+    }
+    const long long h = hg0 + gh;
+    if constexpr (PARTIAL) {
+      const long long slot = h * nsplit + split;
+      part_o[slot * D + d] = ob;
+      if (d == 0) {
+        part_ml[2 * slot] = mb;
+        part_ml[2 * slot + 1] = lb;
+      }
+    } else {
+      out[h * D + d] = static_cast<_Float16>(lb > 0.0f ? ob / lb : 0.0f);
+    }
+  }
+}
+
 // out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = 2^(m_s - max m).
-// One 256-thread workgroup per head: thread (c, d), c = tid / D, merges the
-// states of splits c, c + C, ... (C = 256 / D) online -- independent loads,
-// unrolled so several are in flight -- and the C slice states then merge in
-// slice order through LDS: one pass over the partials, one barrier.
+// One 1024-thread workgroup per head: thread (c, d), c = tid / D, merges the
+// states of splits c, c + C, ... (C = 1024 / D) online -- independent loads,
+// unrolled so several are in flight; with at most 256 splits a thread walks
+// at most 32 -- and the C slice states then merge in slice order through LDS:
+// one pass over the partials, one barrier. (The merge is latency-bound: with
+// 256 threads per head it took longer than the split kernel at 128+ splits.)
+constexpr int kReduceThreads = 1024;
 template <int D>
-__global__ __launch_bounds__(kThreads) void flash_decode_reduce_kernel(
+__global__ __launch_bounds__(kReduceThreads) void flash_decode_reduce_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     _Float16* __restrict__ out, int nsplit) {
-  constexpr int C = kThreads / D;
+  constexpr int C = kReduceThreads / D;
   __shared__ float s_o[C][D];
   __shared__ float s_m[C];
   __shared__ float s_l[C];
@@ -476,14 +768,14 @@ __global__ __launch_bounds__(kThreads) void flash_decode_reduce_kernel(
 }
 
 // Splits when the caller passes split_kv = 0: about one workgroup per CU
-// across all head groups, at least 256 keys per split, at most 256 splits
-// (a sweep on MI355X over the reference's decode shapes -- 32/4 heads at
-// D = 64 and 32/32 at D = 128, 512 to 32768 keys, cold caches -- put the best
-// split count there or within 3% of it for every shape from 2048 keys up).
+// across all head groups, at least 64 keys per split, at most 256 splits (a
+// sweep on MI355X over the reference's decode shapes -- 32/4 heads at D = 64
+// and 32/32 at D = 128, 512 to 32768 keys, cold caches -- put this choice at
+// the best split count, or within 2% of it, for every shape).
 int auto_splits(long long kv_len, long long head_blocks) {
   const long long cus = device_cu_count();
   const long long wanted = (cus + head_blocks - 1) / head_blocks;
-  const long long by_len = kv_len / 256;
+  const long long by_len = kv_len / 64;
   return static_cast<int>(std::max(1LL, std::min({wanted, by_len, 256LL})));
 }
 
@@ -497,13 +789,18 @@ struct DecodeArgs {
   int splits;
 };
 
-// One query head per workgroup (MHA, or GQA sharing switched off): the
-// register kernel with 8 key steps in flight per lane. GQA groups: the
-// LDS-tile kernel.
+// 16-byte aligned caches: the direct-to-LDS pipelined kernel for every G.
+// Otherwise one query head per workgroup (MHA, or GQA sharing switched off):
+// the register kernel with 8 key steps in flight per lane; GQA groups: the
+// register-staged LDS-tile kernel.
 template <int D, int G, bool VEC, bool PARTIAL>
 void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
-  if constexpr (G == 1) {
+  if constexpr (VEC) {
+    flash_decode_gqa_dma_kernel<D, G, PARTIAL><<<grid, kThreads, 0, s>>>(
+        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+        a.scale, a.splits);
+  } else if constexpr (G == 1) {
     flash_decode_split_kernel<D, 1, 8, VEC, PARTIAL><<<grid, kThreads, 0, s>>>(
         a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
         a.scale, a.splits);
@@ -522,11 +819,11 @@ void run_decode(const DecodeArgs& a, hipStream_t s) {
     return;
   }
   const std::size_t slots = static_cast<std::size_t>(a.n_heads) * a.splits;
-  PoolScratch scratch(slots * (D + 2) * sizeof(float), s);
+  StreamScratch scratch(s, slots * (D + 2) * sizeof(float));
   float* part_o = static_cast<float*>(scratch.get());
   float* part_ml = part_o + slots * D;
   launch_split<D, G, VEC, true>(a, part_o, part_ml, s);
-  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), kThreads, 0, s>>>(
+  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), kReduceThreads, 0, s>>>(
       part_o, part_ml, a.out, a.splits);
   ENG_LAUNCH_CHECK();
 }

@@ -1,7 +1,9 @@
-// common.hip -- zero-fill kernel and the per-stream split-K GEMV workspace.
+// common.hip -- zero-fill kernel and the per-stream scratch arenas.
 #include "../engine_internal.hpp"
 
+#include <algorithm>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <utility>
 
@@ -22,10 +24,6 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(unsigned char* __restric
   for (std::size_t i = pre + nvec * 16 + tid; i < bytes; i += stride) p[i] = 0;
 }
 
-// Workspace sizes: 4 MiB of fp32 partials bounds nsplit * N.
-constexpr std::size_t kPartials = std::size_t{1} << 20;
-constexpr std::size_t kPartialSs = std::size_t{1} << 12;
-
 struct Key {
   int device;
   hipStream_t stream;
@@ -34,9 +32,17 @@ struct Key {
   }
 };
 
-std::mutex g_ws_mu;
-std::map<Key, GemvWorkspace>& workspaces() {
-  static auto* m = new std::map<Key, GemvWorkspace>();  // leaked: no exit-time teardown
+struct Arena {
+  std::mutex mu;  // held by the live lease
+  void* base = nullptr;
+  std::size_t capacity = 0;
+};
+
+constexpr std::size_t kMinArena = std::size_t{1} << 20;
+
+std::mutex g_arenas_mu;  // guards the map, not the arenas
+std::map<Key, std::unique_ptr<Arena>>& arenas() {
+  static auto* m = new std::map<Key, std::unique_ptr<Arena>>();  // leaked: no exit-time teardown
   return *m;
 }
 
@@ -52,36 +58,54 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
-GemvWorkspace& gemv_workspace(hipStream_t stream) {
+StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes) {
   int dev = 0;
   ENG_HIP_CHECK(hipGetDevice(&dev));
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  auto& m = workspaces();
-  auto it = m.find(Key{dev, stream});
-  if (it != m.end()) return it->second;
-
-  GemvWorkspace ws;
-  ws.capacity_partials = kPartials;
-  ws.capacity_ss = kPartialSs;
-  void* base = nullptr;
-  ENG_HIP_CHECK(hipMalloc(&base, (kPartials + kPartialSs) * sizeof(float)));
-  ws.partials = static_cast<float*>(base);
-  ws.partial_ss = ws.partials + kPartials;
-  return m.emplace(Key{dev, stream}, ws).first->second;
+  Arena* arena = nullptr;
+  {
+    std::lock_guard<std::mutex> lock(g_arenas_mu);
+    auto& slot = arenas()[Key{dev, stream}];
+    if (!slot) slot = std::make_unique<Arena>();
+    arena = slot.get();
+  }
+  std::unique_lock<std::mutex> lock(arena->mu);
+  if (bytes > arena->capacity) {
+    // Queued kernels of this stream may still use the old block.
+    if (arena->base != nullptr) {
+      ENG_HIP_CHECK(hipStreamSynchronize(stream));
+      ENG_HIP_CHECK(hipFree(arena->base));
+      arena->base = nullptr;
+      arena->capacity = 0;
+    }
+    const std::size_t want = std::max({bytes, kMinArena, 2 * arena->capacity});
+    ENG_HIP_CHECK(hipMalloc(&arena->base, want));
+    arena->capacity = want;
+  }
+  ptr_ = arena->base;
+  held_ = lock.release();
 }
 
-void release_gemv_workspace(hipStream_t stream) {
+StreamScratch::~StreamScratch() {
+  if (held_ != nullptr) held_->unlock();
+}
+
+void release_stream_scratch(hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
     return;
   }
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  auto& m = workspaces();
-  auto it = m.find(Key{dev, stream});
-  if (it == m.end()) return;
-  (void)hipFree(it->second.partials);
-  m.erase(it);
+  std::unique_ptr<Arena> arena;
+  {
+    std::lock_guard<std::mutex> lock(g_arenas_mu);
+    auto& m = arenas();
+    auto it = m.find(Key{dev, stream});
+    if (it == m.end()) return;
+    arena = std::move(it->second);
+    m.erase(it);
+  }
+  std::lock_guard<std::mutex> lock(arena->mu);  // no lease may be live
+  if (arena->base != nullptr) (void)hipFree(arena->base);
 }
 
 }  // namespace eng

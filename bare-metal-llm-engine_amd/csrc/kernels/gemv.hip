@@ -4,8 +4,8 @@
 // overload, rmsnorm_linear at M == 1; reference kernels/gemv.cu,
 // kernels/gemv_fp16.cu, kernels/rmsnorm_linear.cu): gemv_stream_kernel over
 // 512-byte row segments. When the column slabs alone cannot fill the GPU the
-// rows are split into chunks whose fp32 partial sums go to a per-stream
-// workspace and gemv_reduce_kernel combines them in chunk order. Two launches
+// rows are split into chunks whose fp32 partial sums go to the stream's
+// scratch arena and gemv_reduce_kernel combines them in chunk order. Two launches
 // instead of a "last workgroup reduces" handshake: on gfx950 the agent-scope
 // release/acquire that handshake needs is a full L2 writeback/invalidate per
 // workgroup, which costs far more than the second launch.
@@ -48,13 +48,6 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
     nsplit = std::min(nsplit, (K + STEP * U - 1) / (STEP * U));
     nsplit = std::max(nsplit, 1LL);
   }
-  GemvWorkspace* ws = nullptr;
-  if (nsplit > 1) {
-    ws = &gemv_workspace(stream);
-    nsplit = std::min(nsplit, static_cast<long long>(ws->capacity_partials) / N);
-    nsplit = std::min(nsplit, static_cast<long long>(ws->capacity_ss));
-    nsplit = std::max(nsplit, 1LL);
-  }
   long long kchunk = (K + nsplit - 1) / nsplit;
   kchunk = (kchunk + STEP - 1) / STEP * STEP;
   nsplit = (K + kchunk - 1) / kchunk;
@@ -70,12 +63,16 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
     ENG_LAUNCH_CHECK();
     return;
   }
+  // fp32 partial sums [nsplit x N], then partial sums of squares [nsplit].
+  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * (N + 1) * sizeof(float));
+  float* partials = static_cast<float*>(ws.get());
+  float* partial_ss = partials + nsplit * N;
   gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true>
       <<<static_cast<unsigned>(ncb * nsplit), WAVES * 64, 0, stream>>>(
-          W, x, a.gamma, y, N, K, kchunk, ncb, ws->partials, ws->partial_ss, a.eps);
+          W, x, a.gamma, y, N, K, kchunk, ncb, partials, partial_ss, a.eps);
   ENG_LAUNCH_CHECK();
   gemv_reduce_kernel<YT, RMS><<<static_cast<unsigned>((N + 63) / 64), 256, 0, stream>>>(
-      ws->partials, ws->partial_ss, y, N, K, static_cast<int>(nsplit), a.eps);
+      partials, partial_ss, y, N, K, static_cast<int>(nsplit), a.eps);
   ENG_LAUNCH_CHECK();
 }
 

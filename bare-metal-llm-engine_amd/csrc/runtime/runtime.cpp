@@ -292,10 +292,10 @@ int eng_stream_destroy(eng_stream stream) {
   return guarded([&] {
     if (stream == nullptr) return;
     hipStream_t s = eng::as_stream(stream);
-    // Drain first: the stream's GEMV workspace may still be in use by queued
+    // Drain first: the stream's scratch arena may still be in use by queued
     // kernels, and a later stream can be handed the same handle value.
     ENG_HIP_CHECK(hipStreamSynchronize(s));
-    eng::release_gemv_workspace(s);
+    eng::release_stream_scratch(s);
     ENG_HIP_CHECK(hipStreamDestroy(s));
   });
 }

@@ -174,6 +174,24 @@ def test_attention_decode_shapes_against_oracle(gpu, orc, H, Hkv, D, L, split):
     check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"decode H={H}/{Hkv} D={D} L={L}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_decode_every_pipeline_depth(gpu, orc, D):
+    """One split per head group with 1..12 tiles of 4096 / D keys, the last
+    one ragged: the pipelined kernel's prologue, steady loop and every tail
+    length (and GQA 4 sharing) against the oracle."""
+    rng = np.random.default_rng(D)
+    H, Hkv = 8, 2
+    T = 4096 // D
+    for ntiles in range(1, 13):
+        L = T * ntiles - (5 if ntiles > 1 else 0)
+        q = rand_half(orc, rng, (H, D))
+        k = rand_half(orc, rng, (Hkv, L, D))
+        v = rand_half(orc, rng, (Hkv, L, D))
+        sc = 1.0 / np.sqrt(D)
+        got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, 1)
+        check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"D={D} tiles={ntiles} L={L}")
+
+
 def test_attention_decode_unaligned_cache_takes_scalar_loads(gpu, orc):
     """K / V not 16-byte aligned, and a head stride that is not a multiple of 8."""
     rng = np.random.default_rng(41)

@@ -292,6 +292,9 @@ def test_rmsnorm_linear_fused_equals_separate(gpu):
         check_rmsnorm_linear(sep, y, x, g, W, 512, f"separate M={M}")
         direct = gpu_rmsnorm_linear(gpu, x, g, W, fn="eng_rmsnorm_linear_fused_direct_f32")
         assert np.array_equal(direct, fused)
+        if M > 1:
+            # M > 1 is rmsnorm into scratch, then the GEMM -- the same launches.
+            assert np.array_equal(fused, sep)
 
 
 def test_rmsnorm_linear_null_weight_equals_unit_weight(gpu):
@@ -333,7 +336,7 @@ def test_k_zero_zero_fills_and_empty_is_untouched(gpu):
 
 
 def test_split_k_workspace_survives_shape_changes_and_streams(gpu, orc):
-    """Many GEMVs of varying shape on two streams share per-stream workspaces."""
+    """Many GEMVs of varying shape on two streams share per-stream scratch arenas."""
     rng = np.random.default_rng(18)
     shapes = [(4096, 4096), (11008, 4096), (4096, 11008), (64, 8192), (1000, 3000)]
     cases = []
@@ -354,6 +357,45 @@ def test_split_k_workspace_survives_shape_changes_and_streams(gpu, orc):
     finally:
         for s in streams:
             s.destroy()
+
+
+def test_scratch_arena_with_threads_sharing_one_stream(gpu, orc):
+    """Split-K GEMVs from four host threads on ONE stream. Each call's partial
+    and reduce kernels hold the stream's scratch arena while they are queued,
+    so no call's reduce can read another call's partials; the shapes differ so
+    the arena also grows while other threads wait for it."""
+    import threading
+    rng = np.random.default_rng(19)
+    shapes = [(64, 8192), (1000, 3000), (512, 11008), (2048, 16384)]
+    cases = []
+    for N, K in shapes:
+        A = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+        x = rng.standard_normal(K, dtype=np.float32)
+        cases.append((N, K, A, x, gpu.upload(A), gpu.upload(x), gpu.empty(N, np.float32)))
+    s = gpu.stream()
+    errors = []
+
+    def worker(case):
+        N, K, _, _, dA, dx, dy = case
+        try:
+            for _ in range(25):
+                gpu.call("eng_gemv_f16w", dA.ptr, dx.ptr, dy.ptr, N, K, s.handle)
+        except Exception as e:  # pragma: no cover - reported below
+            errors.append(e)
+
+    try:
+        threads = [threading.Thread(target=worker, args=(c,)) for c in cases]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        s.sync()
+        assert not errors, errors
+        for N, K, A, x, _, _, dy in cases:
+            y = orc.gemv_f16w(A, x).astype(np.float64)
+            check_dot(dy.download(), y, helpers.absdot(x, A) + np.abs(y), K, f"threaded gemv {N}x{K}")
+    finally:
+        s.destroy()
 
 
 # ------------------------------------------------- output-major ([N x K]) path
