@@ -708,6 +708,230 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
   }
 }
 
+// GQA groups at D = 64 on the matrix cores: the same pipeline as
+// flash_decode_gqa_dma_kernel (tiles of T = 64 keys loaded straight into LDS
+// through four stages), but wave w takes the 16 keys of a tile it owns for
+// all G <= 16 heads at once and computes
+//   scores  S^T[16 keys x 16 heads] = K_w . q^T   on v_mfma_f32_16x16x32_f16
+//           (fp16 products are exact in fp32, accumulated in fp32), and
+//   values  O^T[64 dims x 16 heads] += V_w^T . P^T on v_mfma_f32_16x16x4_f32
+//           (V converted to fp32, softmax weights in fp32),
+// with the online softmax in between held per head in registers. Lane l owns
+// head l % 16 (columns G.. are zero queries and are never written).
+// Layouts (checked on the device): A[i][k] is lane i + 16 (k / KPL) element
+// k % KPL, B[k][j] lane j + 16 (k / KPL), D[i][j] lane j + 16 (i / 4) element
+// i % 4, with KPL = 8 (16x16x32 f16) or 1 (16x16x4 f32). Accumulator row
+// rho = 4 g + s of the score block holds key sigma(rho) = 4 s + g of the
+// wave's 16, so that the p . V step s reads its B operand (p of key
+// sigma(4 g + s)) from the lane's own score registers and its A operand from
+// V row sigma(4 g + s): the four lane groups then read rows 4 s .. 4 s + 3,
+// alternating bank halves. Value block mb holds dims 4 i + mb (i = row), so a
+// lane's four blocks read four consecutive dims with one 8-byte LDS read. K
+// tiles are stored with 16-byte chunk c of row r at c ^ ((r >> 1) & 7) (chosen
+// by the load addresses), so the 16 rows one score read touches fall in 16
+// distinct bank groups.
+template <int G, int NW, bool PARTIAL>
+__global__ __launch_bounds__(64 * NW) void flash_decode_gqa_mfma_kernel(
+    const _Float16* __restrict__ q, const _Float16* __restrict__ k,
+    const _Float16* __restrict__ v, _Float16* __restrict__ out, float* __restrict__ part_o,
+    float* __restrict__ part_ml, long long kv_len, long long group_size,
+    long long kv_head_stride, float scale, int nsplit) {
+  static_assert(G >= 2 && G <= 16, "2 to 16 heads per workgroup");
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+  typedef float float4v __attribute__((ext_vector_type(4)));
+  constexpr int D = 64;
+  constexpr int NT = 64 * NW;                // threads
+  constexpr int T = 16 * NW;                 // keys per tile, 16 per wave
+  constexpr int NST = 4;                     // pipeline stages
+  constexpr int CPH = T * D / 8 / NT;        // loads per thread per K (or V) tile
+  constexpr int CPT = 2 * CPH;
+  __shared__ __attribute__((aligned(1024))) _Float16 S0[2 * T * D], S1[2 * T * D], S2[2 * T * D],
+      S3[2 * T * D];
+  __shared__ float s_m[NW][G];
+  __shared__ float s_l[NW][G];
+  __shared__ float s_o[NW][G][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15;                 // head of this lane
+  const int grp = lane >> 4;                 // lane group 0..3
+  const long long hg0 = static_cast<long long>(blockIdx.x) * G;
+  const long long kvh = hg0 / group_size;
+  const int split = static_cast<int>(blockIdx.y);
+  const long long j0 = kv_len * split / nsplit;
+  const long long j1 = kv_len * (split + 1) / nsplit;
+  const int nkeys = static_cast<int>(j1 - j0);  // a split holds at most kv_len / 1 keys < 2^31
+  const int ntiles = (nkeys + T - 1) / T;
+  const float scale2 = scale * kLog2e;
+
+  // q^T as the B operand of the score MFMA: head col, dims 32 ks + 8 grp + j.
+  half8 qb[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      qb[ks][j] = col < G ? q[(hg0 + col) * D + 32 * ks + 8 * grp + j] : static_cast<_Float16>(0.0f);
+  }
+
+  const _Float16* kb = k + kvh * kv_head_stride;
+  const _Float16* vb = v + kvh * kv_head_stride;
+  // Load slot (4 i + wave) * 64 + lane holds row slot / 8, 16-byte chunk
+  // position slot % 8: K chunk (position ^ swizzle), V chunk (position).
+  auto fetch = [&](_Float16* st, int t) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < CPH; ++i) {
+      const int slot0 = (NW * i + wave) * 64;
+      const int slot = slot0 + lane;
+      const int r = slot >> 3;
+      const int pos = slot & 7;
+      long long j = j0 + static_cast<long long>(t) * T + r;
+      j = j < j1 ? j : j1 - 1;
+      lds_dma16(kb + j * D + 8 * (pos ^ ((r >> 1) & 7)), st + 8 * slot0);
+      lds_dma16(vb + j * D + 8 * pos, st + T * D + 8 * slot0);
+    }
+  };
+
+  // Lazy rescaling: weights are taken relative to a reference max m that is
+  // raised (rescaling o and l) only when a tile's max exceeds it by more than
+  // 2^kLazy; the weights then stay <= 2^kLazy, exact in fp32, and the final
+  // o / l is the same ratio.
+  constexpr float kLazy = 8.0f;
+  float m = kNegInf;
+  float lsum = 0.0f;                         // this lane's share of the head's sum
+  float4v o[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) o[mb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const _Float16* st, int t) __attribute__((always_inline)) {
+    // Scores: A row i = key sigma(i) = 16 wave + 4 (i % 4) + i / 4.
+    const int arow = 16 * wave + 4 * (col & 3) + (col >> 2);
+    float4v sc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int c = 4 * ks + grp;
+      const half8 a = *reinterpret_cast<const half8*>(st + arow * D + 8 * (c ^ ((arow >> 1) & 7)));
+      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ks], sc, 0, 0, 0);
+    }
+    // Row 4 grp + s of the block is key 16 wave + 4 s + grp of the tile.
+    const int kbase = t * T + 16 * wave + grp;
+    float sv[4];
+    float mx = kNegInf;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      sv[s] = kbase + 4 * s < nkeys ? sc[s] * scale2 : kNegInf;
+      mx = fmaxf(mx, sv[s]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // Every lane group of a head sees the same mx, so a head's lanes agree.
+    if (__any(mx > m + kLazy)) {
+      const float mn = fmaxf(m, mx);
+      const float alpha = merge_weight(m, mn);
+      m = mn;
+      lsum *= alpha;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) o[mb] *= alpha;
+    }
+    float p[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) p[s] = merge_weight(sv[s], m);
+    lsum += (p[0] + p[1]) + (p[2] + p[3]);
+    // Values: step s, k index grp = key 16 wave + 4 s + grp; dims 4 col + mb.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int vrow = 16 * wave + 4 * s + grp;
+      const half4 h = *reinterpret_cast<const half4*>(st + T * D + vrow * D + 4 * col);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        o[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(static_cast<float>(h[mb]), p[s], o[mb], 0, 0, 0);
+    }
+  };
+  auto step = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
+    if (t + NST - 1 < ntiles) fetch(next, t + NST - 1);
+    compute(st, t);
+    const int last_issued = t + NST - 1 < ntiles - 1 ? t + NST - 1 : ntiles - 1;
+    wait_tiles_after<CPT>(last_issued - (t + 1));
+    barrier_no_fence();
+  };
+  auto steady = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
+    fetch(next, t + NST - 1);
+    compute(st, t);
+    wait_tiles_after<CPT>(2);
+    barrier_no_fence();
+  };
+
+  fetch(S0, 0);
+  if (1 < ntiles) fetch(S1, 1);
+  if (2 < ntiles) fetch(S2, 2);
+  {
+    const int last_issued = ntiles - 1 < NST - 2 ? ntiles - 1 : NST - 2;
+    wait_tiles_after<CPT>(last_issued);
+    barrier_no_fence();
+  }
+  int t = 0;
+  for (; t + 2 * NST - 2 < ntiles; t += NST) {
+    steady(S0, S3, t);
+    steady(S1, S0, t + 1);
+    steady(S2, S1, t + 2);
+    steady(S3, S2, t + 3);
+  }
+  for (; t < ntiles; t += NST) {
+    step(S0, S3, t);
+    if (t + 1 < ntiles) step(S1, S0, t + 1);
+    if (t + 2 < ntiles) step(S2, S1, t + 2);
+    if (t + 3 < ntiles) step(S3, S2, t + 3);
+  }
+
+  // This wave's state per head: sum the four lane groups' shares of l; the
+  // value block mb row i = 4 grp + r is dim 4 i + mb.
+  float lt = lsum + __shfl_xor(lsum, 16);
+  lt += __shfl_xor(lt, 32);
+  if (col < G) {
+    if (grp == 0) {
+      s_m[wave][col] = m;
+      s_l[wave][col] = lt;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_o[wave][col][4 * (4 * grp + r) + mb] = o[mb][r];
+    }
+  }
+  __syncthreads();
+
+  // Merge the NW waves (key slices) of each head, in wave order, and write.
+  for (int idx = tid; idx < G * D; idx += NT) {
+    const int gh = idx / D;
+    const int d = idx - gh * D;
+    float mb = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mb = fmaxf(mb, s_m[w][gh]);
+    float lb = 0.0f, ob = 0.0f;
+    if (mb > kNegInf) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float wt = merge_weight(s_m[w][gh], mb);
+        lb = fmaf(s_l[w][gh], wt, lb);
+        ob = fmaf(s_o[w][gh][d], wt, ob);
+      }
+    }
+    const long long h = hg0 + gh;
+    if constexpr (PARTIAL) {
+      const long long slot = h * nsplit + split;
+      part_o[slot * D + d] = ob;
+      if (d == 0) {
+        part_ml[2 * slot] = mb;
+        part_ml[2 * slot + 1] = lb;
+      }
+    } else {
+      out[h * D + d] = static_cast<_Float16>(lb > 0.0f ? ob / lb : 0.0f);
+    }
+  }
+}
+
 // out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = 2^(m_s - max m).
 // One 1024-thread workgroup per head: thread (c, d), c = tid / D, merges the
 // states of splits c, c + C, ... (C = 1024 / D) online -- independent loads,
@@ -793,10 +1017,19 @@ struct DecodeArgs {
 // Otherwise one query head per workgroup (MHA, or GQA sharing switched off):
 // the register kernel with 8 key steps in flight per lane; GQA groups: the
 // register-staged LDS-tile kernel.
+// Waves per workgroup of the MFMA kernel: 8 waves (128-key tiles) stream a
+// single split 1.3x faster, but at the automatic split counts 4 waves are
+// 5% faster (the per-workgroup prologue and merge dominate short splits).
+constexpr int kMfmaWaves = 4;
+
 template <int D, int G, bool VEC, bool PARTIAL>
 void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
-  if constexpr (VEC) {
+  if constexpr (VEC && D == 64 && G >= 2) {
+    flash_decode_gqa_mfma_kernel<G, kMfmaWaves, PARTIAL><<<grid, 64 * kMfmaWaves, 0, s>>>(
+        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+        a.scale, a.splits);
+  } else if constexpr (VEC) {
     flash_decode_gqa_dma_kernel<D, G, PARTIAL><<<grid, kThreads, 0, s>>>(
         a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
         a.scale, a.splits);
