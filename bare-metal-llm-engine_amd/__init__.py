@@ -79,6 +79,10 @@ SIGNATURES = {
     "eng_stream_wait_event": [_p, _p, ctypes.c_uint],
     "eng_event_create": [_pp, ctypes.c_uint],
     "eng_event_destroy": [_p],
+    "eng_graph_capture_begin": [_p],
+    "eng_graph_capture_end": [_p, _p],
+    "eng_graph_launch": [_p, _p],
+    "eng_graph_destroy": [_p],
     "eng_event_record": [_p, _p],
     "eng_event_query": [_p, _pint],
     "eng_event_sync": [_p],
@@ -229,6 +233,9 @@ class Engine:
     def event(self, flags: int = 0) -> "Event":
         return Event(self, flags)
 
+    def graph(self, stream: "Stream") -> "Graph":
+        return Graph(self, stream)
+
     # -- host fp16 -------------------------------------------------------
     def f32_to_f16(self, a: np.ndarray) -> np.ndarray:
         a = np.ascontiguousarray(a, dtype=np.float32)
@@ -315,6 +322,38 @@ class Stream:
 
     def __exit__(self, *exc):
         self.destroy()
+
+
+class Graph:
+    """A HIP graph captured from the work issued on `stream` inside the
+    `with` block (see eng_graph_capture_begin): replay it with launch()."""
+
+    def __init__(self, eng: Engine, stream: Stream):
+        self.eng = eng
+        self.stream = stream
+        self.handle = None
+
+    def __enter__(self):
+        self.eng.call("eng_graph_capture_begin", self.stream.handle)
+        return self
+
+    def __exit__(self, exc_type, *exc):
+        h = ctypes.c_void_p(0)
+        rc = self.eng.status("eng_graph_capture_end", self.stream.handle, ctypes.byref(h))
+        if exc_type is None:
+            if rc != OK:
+                raise EngineError(rc, self.eng.last_error())
+            self.handle = h.value
+        return False
+
+    def launch(self, stream: "Stream | None" = None) -> None:
+        s = stream or self.stream
+        self.eng.call("eng_graph_launch", self.handle, s.handle)
+
+    def destroy(self) -> None:
+        if self.handle:
+            h, self.handle = self.handle, None
+            self.eng.call("eng_graph_destroy", h)
 
 
 class Event:

@@ -68,9 +68,10 @@ inline bool aligned_to(const void* p, std::uintptr_t bytes) {
 // capture these launches in a HIP graph).
 void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 
-// Per-(device, stream) scratch arena for launchers whose kernels pass partial
-// results to a second kernel on the same stream (split-K GEMV, split-KV
-// attention). Launches on one stream run in order, so a call can reuse the
+// Per-(device, stream) scratch arena for launchers whose kernels pass data to
+// a later kernel of the same call (split-K GEMV and split-KV attention
+// partials, the normalised rows of rmsnorm_linear at M > 1, the FFN's gate /
+// up vectors). Launches on one stream run in order, so a call can reuse the
 // arena as soon as the previous call's launches are queued: no event, no
 // allocation per call. The lease holds the arena's lock until it goes out of
 // scope, so two host threads that share a stream cannot interleave their
@@ -92,24 +93,6 @@ class StreamScratch {
   void* ptr_ = nullptr;
 };
 void release_stream_scratch(hipStream_t stream);
-
-// Stream-ordered scratch from the process-wide device pool (the reference's
-// ScopedPoolBuffer, include/engine/pool_allocator.hpp:97-148): returned to the
-// pool on destruction with an event on `stream`, so the block is handed out
-// again only after the work queued on that stream has finished.
-class PoolScratch {
- public:
-  PoolScratch(std::size_t bytes, hipStream_t stream);
-  ~PoolScratch();
-  PoolScratch(const PoolScratch&) = delete;
-  PoolScratch& operator=(const PoolScratch&) = delete;
-  void* get() const { return ptr_; }
-
- private:
-  eng_pool pool_ = nullptr;
-  void* ptr_ = nullptr;
-  hipStream_t stream_ = nullptr;
-};
 
 }  // namespace eng
 

@@ -8,8 +8,8 @@
 // LDS, streams each output's gate and up rows together and applies SiLU in the
 // epilogue, so gate and up never reach memory. Other decode rows compute gate
 // and up with the fused RMSNorm + GEMV kernels; M > 1 normalises the rows
-// once, runs the MFMA GEMM for gate and for up, all into pooled,
-// stream-ordered scratch, and finishes with the SwiGLU kernel. Preconditions and
+// once, runs the MFMA GEMM for gate and for up, all into the stream's scratch
+// arena, and finishes with the SwiGLU kernel. Preconditions and
 // messages follow rmsnorm_linear; any zero dimension writes nothing.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
@@ -49,7 +49,7 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
   const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
-  PoolScratch scratch((mk + 2 * mn) * sizeof(float), s);
+  StreamScratch scratch(s, (mk + 2 * mn) * sizeof(float));
   float* xn = static_cast<float*>(scratch.get());  // first: the GEMM wants it 16-byte aligned
   float* gate = xn + mk;
   float* up = gate + mn;

@@ -3,7 +3,7 @@
 // Replaces the SIMT register-tiled kernel behind matmul_register_tiled
 // (reference kernels/matmul_register_tiled.cu:48-199); it is also the M > 1
 // half of rmsnorm_linear, which, as in the reference
-// (kernels/rmsnorm_linear.cu:191-199), normalises the rows into pooled scratch
+// (kernels/rmsnorm_linear.cu:191-199), normalises the rows into scratch
 // first. (Fusing the RMSNorm into this kernel -- gamma applied to the A
 // fragments, row sums of squares taken from them -- measured 30% slower than
 // the separate pass at 512 x 4096 x 4096: every N-tile repeats the multiply,

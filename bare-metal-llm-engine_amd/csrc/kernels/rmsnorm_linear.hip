@@ -6,9 +6,11 @@
 // or the register-tiled GEMM (M > 1). Here M == 1 is one fused launch that
 // never materialises the normalised row (the GEMV kernels with the sum of
 // squares reduced alongside the dot products); M > 1 keeps the reference's
-// structure -- rmsnorm into pooled, stream-ordered scratch, then the MFMA GEMM
-// -- because the normalisation pass is a few microseconds of HBM traffic while
-// applying gamma inside the GEMM repeats the multiply for every N-tile.
+// structure -- rmsnorm into scratch, then the MFMA GEMM -- because the
+// normalisation pass is a few microseconds of HBM traffic while applying gamma
+// inside the GEMM repeats the multiply for every N-tile. The scratch is the
+// stream's arena rather than the reference's pooled buffer (stream-ordered
+// reuse without an event per call, and capturable in a HIP graph).
 // Preconditions, messages and the "any zero dimension is a no-op" rule are
 // the reference's. The *_nk entries take W output-major [N x K]
 // (out = RMSNorm(in) . W^T), the layout the decode path streams best.
@@ -43,8 +45,7 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     launch_gemv(g, s);
     return;
   }
-  PoolScratch normed(static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float),
-                     s);
+  StreamScratch normed(s, static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float));
   float* xn = static_cast<float*>(normed.get());
   launch_rmsnorm(in, rms_weight, xn, M, K, eps, s);
   GemmArgs g;

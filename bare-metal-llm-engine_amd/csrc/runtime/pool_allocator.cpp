@@ -236,21 +236,6 @@ int eng_pool_default(eng_pool* pool, int device) {
   });
 }
 
-eng::PoolScratch::PoolScratch(std::size_t bytes, hipStream_t stream) : stream_(stream) {
-  const int rc = eng_pool_default(&pool_, ENG_DEVICE_GPU);
-  ENG_CHECK(rc == ENG_OK, std::string("pool scratch: ") + eng_last_error());
-  ptr_ = eng::pool_allocate(*pool_, bytes);
-}
-
-eng::PoolScratch::~PoolScratch() {
-  if (ptr_ == nullptr) return;
-  try {
-    eng::pool_deallocate(*pool_, ptr_, stream_);
-  } catch (...) {
-    // A failed release leaves the block out of the pool; the destructor must not throw.
-  }
-}
-
 int eng_pool_allocate(eng_pool pool, std::size_t bytes, void** ptr) {
   return guarded([&] {
     ENG_CHECK(pool != nullptr, "eng_pool_allocate: pool is null");

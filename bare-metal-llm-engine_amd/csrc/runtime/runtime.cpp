@@ -327,6 +327,58 @@ int eng_event_destroy(eng_event event) {
   });
 }
 
+namespace {
+struct GraphHandle {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+}  // namespace
+
+int eng_graph_capture_begin(eng_stream stream) {
+  return guarded([&] {
+    ENG_CHECK(stream != nullptr,
+              "eng_graph_capture_begin: capture needs a created stream, not the null stream");
+    ENG_HIP_CHECK(hipStreamBeginCapture(eng::as_stream(stream), hipStreamCaptureModeThreadLocal));
+  });
+}
+
+int eng_graph_capture_end(eng_stream stream, eng_graph* graph) {
+  return guarded([&] {
+    ENG_CHECK(stream != nullptr, "eng_graph_capture_end: stream is null");
+    ENG_CHECK(graph != nullptr, "eng_graph_capture_end: graph is null");
+    *graph = nullptr;
+    hipGraph_t g = nullptr;
+    ENG_HIP_CHECK(hipStreamEndCapture(eng::as_stream(stream), &g));
+    hipGraphExec_t exec = nullptr;
+    const hipError_t err = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (err != hipSuccess) {
+      (void)hipGraphDestroy(g);
+      ENG_HIP_CHECK(err);
+    }
+    *graph = reinterpret_cast<eng_graph>(new GraphHandle{g, exec});
+  });
+}
+
+int eng_graph_launch(eng_graph graph, eng_stream stream) {
+  return guarded([&] {
+    ENG_CHECK(graph != nullptr, "eng_graph_launch: graph is null");
+    ENG_HIP_CHECK(hipGraphLaunch(reinterpret_cast<GraphHandle*>(graph)->exec,
+                                 eng::as_stream(stream)));
+  });
+}
+
+int eng_graph_destroy(eng_graph graph) {
+  return guarded([&] {
+    if (graph == nullptr) return;
+    auto* h = reinterpret_cast<GraphHandle*>(graph);
+    const hipError_t e1 = hipGraphExecDestroy(h->exec);
+    const hipError_t e2 = hipGraphDestroy(h->graph);
+    delete h;
+    ENG_HIP_CHECK(e1);
+    ENG_HIP_CHECK(e2);
+  });
+}
+
 int eng_event_record(eng_event event, eng_stream stream) {
   return guarded([&] {
     ENG_CHECK(event != nullptr, "eng_event_record: event is null");

@@ -519,19 +519,22 @@ def rows_attention(eng, timer) -> list:
 
 def rows_stack(eng, timer) -> list:
     return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True),
-            bench_llama_stack(eng, timer, nk=True, fused_glu=True)]
+            bench_llama_stack(eng, timer, nk=True, fused_glu=True),
+            bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True)]
 
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack}
 
 
-def bench_llama_stack(eng, timer, nk=False, fused_glu=False) -> dict:
+def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False) -> dict:
     """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
     rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
     nk=False stores every weight [in x out] (reference layout), nk=True [out x in].
     fused_glu=True (output-major only) runs gate, up and SwiGLU as one launch
-    and feeds SiLU(gate) * up to the down projection (6 launches per layer)."""
+    and feeds SiLU(gate) * up to the down projection (6 launches per layer).
+    graph=True captures one token's launches into a HIP graph (eng_graph_*)
+    and times its replays."""
     H, F, L = 4096, 11008, 32
     rng = np.random.default_rng(4)
     if nk:
@@ -574,7 +577,16 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False) -> dict:
                 rl(o.ptr, g.ptr, lay["up"].ptr, up.ptr, 1, F, H, 1e-5, s)
             gv(lay["down"].ptr, gate.ptr, xh.ptr, H, F, s)
 
-    st = timer.sampled(token, samples=10)
+    if graph:
+        token(0, timer.stream.handle)         # eager first: capture needs nothing allocated
+        timer.stream.sync()
+        captured = eng.graph(timer.stream)
+        with captured:
+            token(0, timer.stream.handle)
+        st = timer.sampled(lambda i, s: eng.lib.eng_graph_launch(captured.handle, s), samples=10)
+        captured.destroy()
+    else:
+        st = timer.sampled(token, samples=10)
     wbytes = L * (4 * H * H + 3 * H * F) * 2
     abytes = L * (4 * (4 * H + 4 * H) + 2 * (8 * H + 4 * F) + (4 * F + 4 * H))
     for lay in layers:
@@ -583,6 +595,8 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False) -> dict:
     layout = "output-major W[out x in]" if nk else "reference layout W[in x out]"
     if fused_glu:
         layout += ", gate/up + SwiGLU fused"
+    if graph:
+        layout += ", replayed as one HIP graph"
     row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
                   st, wbytes + abytes)
     row["launches_per_token"] = (6 if fused_glu else 7) * L

@@ -109,7 +109,9 @@ int eng_check_last_launch(void);
  * Streams and events. Replace engine::CudaStream / CudaEvent
  * (reference include/engine/cuda_stream.hpp:21-124, src/cuda_stream.cpp:11-38).
  * Streams are created at the default priority. eng_stream_destroy waits for
- * the stream's work and releases the per-stream GEMV reduction workspace.
+ * the stream's work and releases the stream's scratch arena (the device
+ * memory the split-K GEMV, split-KV attention, rmsnorm_linear at M > 1 and the
+ * FFN launchers reuse on that stream; it grows to the largest request).
  * ---------------------------------------------------------------------- */
 int eng_stream_create(eng_stream* stream, unsigned int flags);
 int eng_stream_destroy(eng_stream stream);
@@ -122,6 +124,24 @@ int eng_event_record(eng_event event, eng_stream stream);
 int eng_event_query(eng_event event, int* done);
 int eng_event_sync(eng_event event);
 int eng_event_elapsed_ms(float* ms, eng_event start, eng_event end);
+
+/* ------------------------------------------------------------------------
+ * HIP graph capture of a stream. No counterpart in the reference: for decode
+ * loops that issue the same launches every token (capture once, replay per
+ * token). eng_graph_capture_begin starts recording the work issued on
+ * `stream` (a stream from eng_stream_create, not the null stream) without
+ * running it; eng_graph_capture_end stops, instantiates and returns the graph;
+ * eng_graph_launch replays it on any stream. Every launcher here is
+ * capture-safe once it has run eagerly on that stream at least once with
+ * shapes at least as large (the stream's scratch arena is sized outside the
+ * capture; zero fills are kernels, not memsets). A failed capture returns an
+ * error and leaves no graph; the stream is no longer capturing either way.
+ * ---------------------------------------------------------------------- */
+typedef void* eng_graph;
+int eng_graph_capture_begin(eng_stream stream);
+int eng_graph_capture_end(eng_stream stream, eng_graph* graph);
+int eng_graph_launch(eng_graph graph, eng_stream stream);
+int eng_graph_destroy(eng_graph graph);
 
 /* ------------------------------------------------------------------------
  * Pooled allocator. Replaces engine::PoolAllocator / pool_allocator(Device) /
@@ -279,7 +299,7 @@ int eng_swiglu_f16(const eng_half* gate, const eng_half* up, eng_half* out, int6
  * eps), with output-major W_gate, W_up [N x K]: the gate / up half of a SwiGLU
  * FFN in one call (no reference counterpart: the reference composes rmsnorm,
  * two GEMV / GEMMs and swiglu, tests/test_kernels.cu:2867-2898). Decode
- * (M == 1) is a single fused launch; other shapes use pooled scratch for gate
+ * (M == 1) is a single fused launch; other shapes use scratch for gate
  * and up. rms_weight may be NULL. Messages: "negative dimension", "null device
  * pointer", "eps must be non-negative"; any zero dimension writes nothing. */
 int eng_rmsnorm_linear_swiglu_f16w_nk(const float* in, const float* rms_weight,

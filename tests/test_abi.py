@@ -123,6 +123,10 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_kv_cache_write_f16", P, P, P, P, 4, 2, 64, 5, 8, None), 1, "kv_max_seq_len < pos_offset + s_new"),
     (("eng_kv_cache_write_f16", None, P, P, P, 1, 2, 64, 0, 8, None), 1, "k_new/v_new is null"),
     (("eng_kv_cache_write_f16", P, P, P, None, 1, 2, 64, 0, 8, None), 1, "k_cache/v_cache is null"),
+    (("eng_graph_capture_begin", None), 1, "capture needs a created stream"),
+    (("eng_graph_capture_end", None, P), 1, "eng_graph_capture_end: stream is null"),
+    (("eng_graph_capture_end", P, None), 1, "eng_graph_capture_end: graph is null"),
+    (("eng_graph_launch", None, None), 1, "eng_graph_launch: graph is null"),
 ])
 def test_preconditions_fail_before_launch(eng, call, code, substr):
     name, *args = call
@@ -158,6 +162,7 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_cast_f32_to_f16", None, None, 0, None),
     ("eng_cast_f16_to_f32", None, None, 0, None),
     ("eng_kv_cache_write_f16", None, None, None, None, 0, 2, 64, 3, 3, None),
+    ("eng_graph_destroy", None),
 ])
 def test_empty_work_is_a_no_op(eng, call):
     name, *args = call

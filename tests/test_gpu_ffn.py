@@ -247,7 +247,7 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (1, 1376, 4096, "f16", False),   # one GPU's share of it under 8-way TP; null gain
     (1, 300, 1000, "f16", True),     # ragged last piece
     (1, 257, 1024, "f32", True),     # fp32 weights: fused launch
-    (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with pooled scratch
+    (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with arena scratch
     (1, 64, 20000, "f16", True),     # K past the LDS budget: GEMV fallback
     (5, 200, 512, "f16", True),      # prefill: MFMA GEMMs + SwiGLU kernel
 ])

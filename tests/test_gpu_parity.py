@@ -543,7 +543,7 @@ def test_rmsnorm_linear_nk_prefill_against_oracle(gpu, orc, M, N, K, dtype):
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f32_full_tiles_against_oracle(gpu, orc, M, N, K, layout, with_gamma):
-    # M > 1 normalises into pooled scratch; whole 64/128-row tiles with
+    # M > 1 normalises into scratch; whole 64/128-row tiles with
     # K % 32 == 0 then take the direct-to-LDS GEMM.
     rng = np.random.default_rng(7 * M + N + K + (layout == "nk"))
     x = rng.standard_normal((M, K), dtype=np.float32)
