@@ -105,36 +105,45 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
   for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
   float ss = 0.0f;
 
-  const WT* wcol = W + col0;
+  // Columns past N (whole vectors, as N % VEC == 0 when VEC > 1) read column
+  // 0 instead; their sums are never written.
+  const WT* wsafe = W + (col_ok ? col0 : 0);
   for (long long base = row_begin + wave * RPW + rg; base < row_end;
        base += static_cast<long long>(STEP) * U) {
+    // All of a step's loads (W, x, gamma) are issued before any is used, and
+    // none is conditional: rows past the chunk read its last row (in bounds)
+    // and are zeroed where the products are formed. (Loads complete in
+    // order, so using a value as soon as it is loaded -- or a conditional
+    // load's register reused as the next address -- waits for every weight
+    // load issued before it.)
     V raw[U];
     float xv[U];
+    float gv[U];
+    bool okr[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const long long r = base + static_cast<long long>(u) * STEP;
-      const bool ok = r < row_end;
-      float xr = ok ? to_f32(x[r]) : 0.0f;
-      if constexpr (RMS) {
-        ss = fmaf(xr, xr, ss);
-        if (gamma != nullptr && ok) xr *= gamma[r];
-      }
-      xv[u] = xr;
-      if (ok && col_ok) {
-        const V* p = reinterpret_cast<const V*>(wcol + r * N);
-        if constexpr (NT) {
-          raw[u] = __builtin_nontemporal_load(p);
-        } else {
-          raw[u] = *p;
-        }
+      okr[u] = r < row_end;
+      const long long rr = okr[u] ? r : row_end - 1;
+      xv[u] = to_f32(x[rr]);
+      if constexpr (RMS) gv[u] = gamma != nullptr ? gamma[rr] : 1.0f;
+      const V* p = reinterpret_cast<const V*>(wsafe + rr * N);
+      if constexpr (NT) {
+        raw[u] = __builtin_nontemporal_load(p);
       } else {
-        raw[u] = V{};
+        raw[u] = *p;
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      float xr = okr[u] ? xv[u] : 0.0f;
+      if constexpr (RMS) {
+        ss = fmaf(xr, xr, ss);
+        xr *= gv[u];
+      }
+      const V w = okr[u] ? raw[u] : V{};
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = fmaf(xv[u], lane_elem<VEC>(raw[u], e), acc[e]);
+      for (int e = 0; e < VEC; ++e) acc[e] = fmaf(xr, lane_elem<VEC>(w, e), acc[e]);
     }
   }
 
