@@ -1,7 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,ffn,attention,stack]
+                    [--only config2,config3,refapi,gemm,ffn,attention,stack,stackfused]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -520,21 +520,30 @@ def rows_attention(eng, timer) -> list:
 def rows_stack(eng, timer) -> list:
     return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True),
             bench_llama_stack(eng, timer, nk=True, fused_glu=True),
-            bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True)]
+            bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True),
+            bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
+
+
+def rows_stack_fused(eng, timer) -> list:
+    """Only the fastest config-5 arrangement (for profiling its kernels alone)."""
+    return [bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
 
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
-          "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack}
+          "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
+          "stackfused": rows_stack_fused}
 
 
-def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False) -> dict:
+def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
     """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
     rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
     nk=False stores every weight [in x out] (reference layout), nk=True [out x in].
     fused_glu=True (output-major only) runs gate, up and SwiGLU as one launch
     and feeds SiLU(gate) * up to the down projection (6 launches per layer).
     graph=True captures one token's launches into a HIP graph (eng_graph_*)
-    and times its replays."""
+    and times its replays. fused_qkv=True (output-major only) stores each layer's
+    q, k and v weights as one [3H x H] matrix, so one GEMV launch (N = 3H) yields
+    q, k and v; same weights, bytes and arithmetic."""
     H, F, L = 4096, 11008, 32
     rng = np.random.default_rng(4)
     if nk:
@@ -545,17 +554,26 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False) -> dic
     layers = []
     for _ in range(L):
         lay = {}
-        for name, key in (("q", "sq"), ("k", "sq"), ("v", "sq"), ("o", "sq"), ("gate", "gu"),
-                          ("up", "gu"), ("down", "dn")):
+        names = (("o", "sq"), ("gate", "gu"), ("up", "gu"), ("down", "dn"))
+        if not fused_qkv:
+            names = (("q", "sq"), ("k", "sq"), ("v", "sq")) + names
+        for name, key in names:
             d = eng.empty(src[key].shape, np.uint16)
             eng.call("eng_memcpy_d2d", d.ptr, src[key].ptr, d.nbytes)
             lay[name] = d
+        if fused_qkv:
+            d = eng.empty((3 * H, H), np.uint16)
+            for part in range(3):
+                eng.call("eng_memcpy_d2d", d.ptr + part * src["sq"].nbytes, src["sq"].ptr,
+                         src["sq"].nbytes)
+            lay["qkv"] = d
         layers.append(lay)
     for d in src.values():
         d.free()
     xh = eng.upload(rng.standard_normal(H, dtype=np.float32))
     g = eng.upload((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
     q, k, v, o = (eng.empty(H, np.float32) for _ in range(4))
+    qkv = eng.empty(3 * H, np.float32)
     gate, up = eng.empty(F, np.float32), eng.empty(F, np.float32)
     if nk:
         gv, rl = eng.lib.eng_gemv_f16w_nk, eng.lib.eng_rmsnorm_linear_f16w_nk
@@ -566,10 +584,15 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False) -> dic
 
     def token(_i, s):
         for lay in layers:
-            gv(lay["q"].ptr, xh.ptr, q.ptr, H, H, s)
-            gv(lay["k"].ptr, xh.ptr, k.ptr, H, H, s)
-            gv(lay["v"].ptr, xh.ptr, v.ptr, H, H, s)
-            gv(lay["o"].ptr, v.ptr, o.ptr, H, H, s)
+            if fused_qkv:
+                gv(lay["qkv"].ptr, xh.ptr, qkv.ptr, 3 * H, H, s)
+                vin = qkv.ptr + 2 * H * 4
+            else:
+                gv(lay["q"].ptr, xh.ptr, q.ptr, H, H, s)
+                gv(lay["k"].ptr, xh.ptr, k.ptr, H, H, s)
+                gv(lay["v"].ptr, xh.ptr, v.ptr, H, H, s)
+                vin = v.ptr
+            gv(lay["o"].ptr, vin, o.ptr, H, H, s)
             if fused_glu:
                 glu(o.ptr, g.ptr, lay["gate"].ptr, lay["up"].ptr, gate.ptr, 1, F, H, 1e-5, s)
             else:
@@ -595,11 +618,13 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False) -> dic
     layout = "output-major W[out x in]" if nk else "reference layout W[in x out]"
     if fused_glu:
         layout += ", gate/up + SwiGLU fused"
+    if fused_qkv:
+        layout += ", q/k/v as one [3H x H] matrix"
     if graph:
         layout += ", replayed as one HIP graph"
     row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
                   st, wbytes + abytes)
-    row["launches_per_token"] = (6 if fused_glu else 7) * L
+    row["launches_per_token"] = (7 - (1 if fused_glu else 0) - (2 if fused_qkv else 0)) * L
     return row
 
 
@@ -611,7 +636,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary rows)")
     ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
-                    + ", ".join(GROUPS) + " (default: all)")
+                    + ", ".join(GROUPS) + " (default: all but stackfused, which repeats a "
+                    "stack row on its own for profiling)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -643,7 +669,7 @@ def main() -> int:
 
     secondary = []
     if not args.quick:
-        groups = [g for g in args.only.split(",") if g] or list(GROUPS)
+        groups = [g for g in args.only.split(",") if g] or [g for g in GROUPS if g != "stackfused"]
         for g in groups:
             if g not in GROUPS:
                 log(f"unknown group {g!r}; choose from {', '.join(GROUPS)}")
