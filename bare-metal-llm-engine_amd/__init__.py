@@ -123,7 +123,20 @@ SIGNATURES = {
     "eng_cast_f32_to_f16": [_p, _p, _i64, _p],
     "eng_cast_f16_to_f32": [_p, _p, _i64, _p],
     "eng_kv_cache_write_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
+    "eng_engref_open": [ctypes.c_char_p, _pp],
+    "eng_engref_close": [_p],
+    "eng_engref_count": [_p, ctypes.POINTER(ctypes.c_int32)],
+    "eng_engref_find": [_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int32)],
+    "eng_engref_tensor": [_p, ctypes.c_int32, ctypes.POINTER(ctypes.c_char_p),
+                          ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(ctypes.c_int32),
+                          ctypes.POINTER(ctypes.POINTER(ctypes.c_int64)),
+                          ctypes.POINTER(ctypes.c_int64), _pp, ctypes.POINTER(ctypes.c_int64)],
+    "eng_engref_slab_bytes": [_p, ctypes.POINTER(ctypes.c_int64)],
+    "eng_engref_upload": [_p, _p, _i64, _p],
 }
+
+# ENGREF01 dtype codes -> numpy element types (f16 as its bit pattern).
+ENGREF_DTYPES = {0: np.dtype("<f4"), 1: np.dtype("<u2"), 2: np.dtype("<f8")}
 STRING_FUNCTIONS = ("eng_last_error", "eng_build_info")
 
 
@@ -235,6 +248,10 @@ class Engine:
 
     def graph(self, stream: "Stream") -> "Graph":
         return Graph(self, stream)
+
+    # -- ENGREF01 files --------------------------------------------------
+    def engref(self, path) -> "EngrefFile":
+        return EngrefFile(self, path)
 
     # -- host fp16 -------------------------------------------------------
     def f32_to_f16(self, a: np.ndarray) -> np.ndarray:
@@ -383,3 +400,98 @@ class Event:
         if self.handle:
             h, self.handle = self.handle, None
             self.eng.call("eng_event_destroy", h)
+
+
+class EngrefTensor:
+    """One tensor of an ENGREF01 file: name, dtype code, shape, byte count,
+    slab offset and a numpy view of the mapped bytes (valid while the file is
+    open; f16 tensors are uint16 bit patterns)."""
+
+    def __init__(self, name, dtype, shape, nbytes, slab_offset, host):
+        self.name = name
+        self.dtype = dtype
+        self.shape = shape
+        self.nbytes = nbytes
+        self.slab_offset = slab_offset
+        self.host = host
+
+
+class EngrefFile:
+    """An ENGREF01 file mapped by the library (eng_engref_*), with the
+    reference reader's interface (tests/golden.hpp:48-72: at / has / names /
+    size) plus the slab layout for uploading every tensor in one allocation."""
+
+    def __init__(self, eng: Engine, path):
+        self.eng = eng
+        h = ctypes.c_void_p(0)
+        eng.call("eng_engref_open", os.fsencode(str(path)), ctypes.byref(h))
+        self.handle = h.value
+        n = ctypes.c_int32(0)
+        eng.call("eng_engref_count", self.handle, ctypes.byref(n))
+        self.tensors = [self._tensor(i) for i in range(n.value)]
+        self._by_name = {t.name: t for t in self.tensors}
+
+    def _tensor(self, index: int) -> EngrefTensor:
+        name = ctypes.c_char_p()
+        dtype = ctypes.c_int32(0)
+        ndim = ctypes.c_int32(0)
+        dims = ctypes.POINTER(ctypes.c_int64)()
+        nbytes = ctypes.c_int64(0)
+        data = ctypes.c_void_p(0)
+        off = ctypes.c_int64(0)
+        self.eng.call("eng_engref_tensor", self.handle, index, ctypes.byref(name),
+                      ctypes.byref(dtype), ctypes.byref(ndim), ctypes.byref(dims),
+                      ctypes.byref(nbytes), ctypes.byref(data), ctypes.byref(off))
+        shape = tuple(int(dims[i]) for i in range(ndim.value))
+        dt = ENGREF_DTYPES[dtype.value]
+        if nbytes.value:
+            raw = (ctypes.c_char * nbytes.value).from_address(data.value)
+            host = np.frombuffer(raw, dtype=dt).reshape(shape)
+        else:
+            host = np.empty(shape, dtype=dt)
+        return EngrefTensor(name.value.decode(), dtype.value, shape, nbytes.value, off.value, host)
+
+    def size(self) -> int:
+        return len(self.tensors)
+
+    def names(self) -> list:
+        return sorted(self._by_name)
+
+    def has(self, name: str) -> bool:
+        return name in self._by_name
+
+    def index(self, name: str) -> int:
+        i = ctypes.c_int32(0)
+        self.eng.call("eng_engref_find", self.handle, name.encode(), ctypes.byref(i))
+        return i.value
+
+    def at(self, name: str) -> EngrefTensor:
+        return self.tensors[self.index(name)]
+
+    def slab_bytes(self) -> int:
+        v = ctypes.c_int64(0)
+        self.eng.call("eng_engref_slab_bytes", self.handle, ctypes.byref(v))
+        return v.value
+
+    def upload(self, slab: DeviceArray, stream: "Stream | None" = None) -> None:
+        self.eng.call("eng_engref_upload", self.handle, slab.ptr, slab.nbytes,
+                      stream.handle if stream else None)
+
+    def close(self) -> None:
+        if self.handle:
+            h, self.handle = self.handle, None
+            self.tensors = []
+            self._by_name = {}
+            self.eng.call("eng_engref_close", h)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

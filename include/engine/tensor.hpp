@@ -139,6 +139,36 @@ class Tensor {
     return t;
   }
 
+  /// Contiguous view of `shape` at `byte_offset` inside an existing Storage,
+  /// sharing (and keeping alive) that Storage: many tensors aliasing one
+  /// allocation, as a weight slab's tensors do.
+  static Tensor view(std::shared_ptr<Storage> storage, std::int64_t byte_offset,
+                     std::vector<std::int64_t> shape, DType dtype) {
+    ENGINE_CHECK(storage != nullptr, "Tensor::view: storage is null");
+    ENGINE_CHECK(!dtype_is_sub_byte(dtype), "Tensor::view: sub-byte dtypes are not supported");
+    for (std::size_t i = 0; i < shape.size(); ++i) {
+      ENGINE_CHECK(shape[i] >= 0, "Tensor::view: dimension " + std::to_string(i) + " is " +
+                                      std::to_string(shape[i]) + ", must be >= 0");
+    }
+    const auto esz = static_cast<std::int64_t>(dtype_size(dtype));
+    ENGINE_CHECK(byte_offset >= 0 && byte_offset % esz == 0,
+                 "Tensor::view: byte offset " + std::to_string(byte_offset) +
+                     " is not a non-negative multiple of the element size");
+    const std::size_t bytes = bytes_for(shape, dtype);
+    ENGINE_CHECK(static_cast<std::size_t>(byte_offset) + bytes <= storage->bytes(),
+                 "Tensor::view: " + std::to_string(bytes) + " bytes at offset " +
+                     std::to_string(byte_offset) + " overrun a storage of " +
+                     std::to_string(storage->bytes()) + " bytes");
+    Tensor t;
+    t.device_ = storage->device();
+    t.storage_ = std::move(storage);
+    t.shape_ = std::move(shape);
+    t.strides_ = contiguous_strides(t.shape_);
+    t.offset_ = byte_offset / esz;
+    t.dtype_ = dtype;
+    return t;
+  }
+
   // -- shape / layout ------------------------------------------------------
   const std::vector<std::int64_t>& shape() const { return shape_; }
   const std::vector<std::int64_t>& strides() const { return strides_; }

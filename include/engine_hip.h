@@ -354,6 +354,57 @@ int eng_kv_cache_write_f16(const eng_half* k_new, const eng_half* v_new, eng_hal
                            eng_half* v_cache, int64_t s_new, int64_t n_kv_heads, int64_t head_dim,
                            int64_t pos_offset, int64_t kv_max_seq_len, eng_stream stream);
 
+/* ------------------------------------------------------------------------
+ * ENGREF01 tensor files and device weight slabs.
+ *
+ * The container is the reference's golden format (tools/gen_reference.py:
+ * 56-83, tests/golden.hpp:21-33): "ENGREF01", int32 count, then per tensor
+ * int32 name length, name, int32 dtype, int32 ndim, int64 dims, int64 byte
+ * count, data. The reference reader (tests/golden.cpp:104-209, which these
+ * functions replace) accepts dtype 0 only; here 1 stores IEEE binary16
+ * weights at native size and 2 float64. A file is memory-mapped and checked
+ * as the reference checks it (messages: "bad magic", "implausible tensor
+ * count", "implausible name length", "truncated tensor name", "has dtype",
+ * "implausible ndim", "negative dimension", "header says ... bytes but its
+ * shape implies", "truncated data", "duplicate tensor name", "unexpected
+ * trailing bytes", "unexpected end of file while reading"); a missing
+ * tensor name reports the names present ("not found. Available:", as
+ * tests/golden.cpp:197-205). The slab is the on-disk-to-HBM step of the
+ * reference's planned mmap weight loader (README.md:247): every tensor at a
+ * 256-byte aligned offset, in file order, in one device allocation.
+ * ---------------------------------------------------------------------- */
+
+#define ENG_ENGREF_F32 0
+#define ENG_ENGREF_F16 1
+#define ENG_ENGREF_F64 2
+
+typedef struct eng_engref_s* eng_engref;
+
+/* Maps and validates `path`; *file is NULL on failure. A handle is
+ * read-only after open and may be shared by threads. */
+int eng_engref_open(const char* path, eng_engref* file);
+/* Unmaps the file; pointers returned for it become invalid. NULL is a no-op. */
+int eng_engref_close(eng_engref file);
+int eng_engref_count(eng_engref file, int32_t* count);
+/* Index of the tensor called `name` (unknown name: ENG_INVALID_ARGUMENT). */
+int eng_engref_find(eng_engref file, const char* name, int32_t* index);
+/* Tensor `index` (0 .. count-1, file order). Any output pointer may be NULL.
+ * name (NUL-terminated), dims[ndim] and host_data (the mapped bytes,
+ * little-endian, not necessarily aligned) live until eng_engref_close;
+ * slab_offset is the tensor's byte offset in the slab. */
+int eng_engref_tensor(eng_engref file, int32_t index, const char** name, int32_t* dtype,
+                      int32_t* ndim, const int64_t** dims, int64_t* nbytes,
+                      const void** host_data, int64_t* slab_offset);
+/* Bytes of device memory the slab needs (a multiple of 256). */
+int eng_engref_slab_bytes(eng_engref file, int64_t* bytes);
+/* Copies every tensor into the caller's device allocation `slab` (256-byte
+ * aligned, `capacity` >= eng_engref_slab_bytes) through pinned staging
+ * buffers on `stream`; returns when the copies are complete. Padding bytes
+ * between tensors are left as they were. Messages: "capacity must be
+ * non-negative", "slab capacity ... bytes needed", "slab is null", "slab must
+ * be 256-byte aligned". */
+int eng_engref_upload(eng_engref file, void* slab, int64_t capacity, eng_stream stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -9,6 +9,7 @@
 #include <engine/allocator.hpp>
 #include <engine/device_buffer.hpp>
 #include <engine/dtype.hpp>
+#include <engine/engref.hpp>
 #include <engine/half.hpp>
 #include <engine/hip_device.hpp>
 #include <engine/hip_stream.hpp>
@@ -20,7 +21,10 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdio>
 #include <random>
+#include <string>
+#include <unistd.h>
 #include <vector>
 
 using engine::Device;
@@ -562,6 +566,133 @@ TEST(gpu_kernels, ffn_sub_block_through_cpp_api) {
   }
   EXPECT_EQ(bad, 0);
   EXPECT_TRUE(got_out == got_sum);
+}
+
+// --------------------------------------------------------------------- engref
+// Writes an ENGREF01 file (the reference's container, tools/gen_reference.py:
+// 64-83) with explicit dtype codes.
+struct EngrefWriter {
+  std::vector<unsigned char> body;
+  int count = 0;
+  template <typename T>
+  void pod(T v) {
+    const auto* p = reinterpret_cast<const unsigned char*>(&v);
+    body.insert(body.end(), p, p + sizeof(T));
+  }
+  void add(const std::string& name, std::int32_t code, std::vector<std::int64_t> dims,
+           const void* data, std::int64_t nbytes) {
+    pod<std::int32_t>(static_cast<std::int32_t>(name.size()));
+    body.insert(body.end(), name.begin(), name.end());
+    pod<std::int32_t>(code);
+    pod<std::int32_t>(static_cast<std::int32_t>(dims.size()));
+    for (auto d : dims) pod<std::int64_t>(d);
+    pod<std::int64_t>(nbytes);
+    const auto* p = static_cast<const unsigned char*>(data);
+    body.insert(body.end(), p, p + nbytes);
+    ++count;
+  }
+  std::string save(const std::string& stem) const {
+    const std::string path = "/tmp/engref_cpp_" + std::to_string(::getpid()) + "_" + stem + ".bin";
+    std::FILE* f = std::fopen(path.c_str(), "wb");
+    std::fwrite("ENGREF01", 1, 8, f);
+    std::fwrite(&count, 4, 1, f);
+    std::fwrite(body.data(), 1, body.size(), f);
+    std::fclose(f);
+    return path;
+  }
+};
+
+TEST(cpu_engref, load_names_dims_and_values) {
+  EngrefWriter w;
+  const float xs[3] = {1.5f, -2.0f, 3.25f};
+  const std::uint16_t hs[4] = {0x3c00, 0xc000, 0x3555, 0x7bff};  // 1, -2, 0.333251953125, 65504
+  const double ds[2] = {0.1, -7.0};
+  w.add("x", ENG_ENGREF_F32, {3}, xs, sizeof(xs));
+  w.add("h", ENG_ENGREF_F16, {2, 2}, hs, sizeof(hs));
+  w.add("d", ENG_ENGREF_F64, {2}, ds, sizeof(ds));
+  const std::string path = w.save("values");
+  engine::EngrefFile f = engine::EngrefFile::load(path);
+  EXPECT_EQ(f.size(), 3u);
+  EXPECT_TRUE(f.names() == (std::vector<std::string>{"d", "h", "x"}));
+  EXPECT_TRUE(f.has("h") && !f.has("y"));
+  EXPECT_EQ(f.at("h").dim(1), 2);
+  EXPECT_EQ(f.at("h").nbytes, 8);
+  EXPECT_THROWS_MSG(f.at("h").dim(2), "out of range");
+  EXPECT_TRUE(f.at("x").floats() == (std::vector<float>{1.5f, -2.0f, 3.25f}));
+  EXPECT_TRUE(f.at("h").floats() == (std::vector<float>{1.0f, -2.0f, 0.333251953125f, 65504.0f}));
+  EXPECT_EQ(f.at("d").floats()[0], 0.1f);
+  EXPECT_TRUE(f.at("h").dtype() == DType::F16);
+  EXPECT_THROWS_MSG(f.at("d").dtype(), "float64");
+  EXPECT_THROWS_MSG(f.at("nope"), "not found. Available: d h x");
+  EXPECT_EQ(f.at("x").slab_offset, 0);
+  EXPECT_EQ(f.at("h").slab_offset, 256);
+  EXPECT_EQ(f.at("d").slab_offset, 512);
+  EXPECT_EQ(f.slab_bytes(), 768);
+  std::remove(path.c_str());
+}
+
+TEST(cpu_engref, errors_follow_the_reference_reader) {
+  engine::EngrefFile f;
+  std::string err;
+  EXPECT_TRUE(!engine::EngrefFile::try_load("/nonexistent/dir/file.bin", f, err));
+  EXPECT_TRUE(err.find("cannot open") != std::string::npos);
+  EngrefWriter w;
+  const float v[2] = {1, 2};
+  w.add("t", ENG_ENGREF_F32, {3}, v, sizeof(v));  // 8 bytes for a shape of 3 floats
+  const std::string path = w.save("mismatch");
+  EXPECT_THROWS_MSG(engine::EngrefFile::load(path), "header says 8 bytes but its shape implies 12");
+  std::remove(path.c_str());
+  EngrefWriter d;
+  d.add("t", ENG_ENGREF_F32, {2}, v, sizeof(v));
+  d.add("t", ENG_ENGREF_F32, {2}, v, sizeof(v));
+  const std::string dup = d.save("dup");
+  EXPECT_THROWS_MSG(engine::EngrefFile::load(dup), "duplicate tensor name 't'");
+  std::remove(dup.c_str());
+}
+
+TEST(gpu_engref, weight_slab_views_feed_the_reference_api) {
+  require_gpu(ctx);
+  const std::int64_t K = 640, N = 384;
+  std::mt19937 rng(11);
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  std::vector<engine::half> A(static_cast<std::size_t>(K * N)), x(static_cast<std::size_t>(K));
+  for (auto& a : A) a = engine::float_to_half(0.05f * nd(rng));
+  for (auto& v : x) v = engine::float_to_half(nd(rng));
+  EngrefWriter w;
+  w.add("x", ENG_ENGREF_F16, {K}, x.data(), K * 2);
+  w.add("A", ENG_ENGREF_F16, {K, N}, A.data(), K * N * 2);
+  const std::string path = w.save("slab");
+  engine::EngrefFile f = engine::EngrefFile::load(path);
+  engine::WeightSlab slab = engine::WeightSlab::upload(f);
+  EXPECT_EQ(static_cast<std::int64_t>(slab.bytes()), f.slab_bytes());
+  Tensor tA = slab.tensor("A");
+  Tensor tx = slab.tensor("x");
+  EXPECT_TRUE(tA.device() == Device::HIP && tA.dtype() == DType::F16);
+  EXPECT_TRUE(tA.shape() == (std::vector<std::int64_t>{K, N}));
+  EXPECT_TRUE(tA.storage() == tx.storage());  // both alias the one slab
+  EXPECT_EQ(tA.data(), slab.data("A"));
+  // the slab's bytes are the file's
+  Tensor back = tA.to(Device::CPU);
+  EXPECT_EQ(std::memcmp(back.data(), A.data(), A.size() * 2), 0);
+  engine::DeviceBuffer<engine::half> out(static_cast<std::size_t>(N));
+  engine::cuda::gemv_fp16(tA.ptr<engine::half>(Device::HIP), tx.ptr<engine::half>(Device::HIP),
+                          out.get(), N, K);
+  HIP_CHECK(hipDeviceSynchronize());
+  const std::vector<engine::half> got = out.download();
+  int bad = 0;
+  for (std::int64_t n = 0; n < N; ++n) {
+    double ref = 0.0, mag = 0.0;
+    for (std::int64_t k = 0; k < K; ++k) {
+      const double p = double(engine::half_to_float(x[k])) * engine::half_to_float(A[k * N + n]);
+      ref += p;
+      mag += std::fabs(p);
+    }
+    // fp32 accumulation (K u sum|p|) plus the half rounding of the output
+    const double bound = K * 0x1p-24 * mag + 0x1p-11 * std::fabs(ref);
+    if (!(std::fabs(engine::half_to_float(got[n]) - ref) <= bound)) ++bad;
+  }
+  EXPECT_EQ(bad, 0);
+  std::remove(path.c_str());
 }
 
 }  // namespace
