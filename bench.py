@@ -1,7 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,ffn,attention,stack,stackfused]
+                    [--only config2,config3,refapi,gemm,ffn,attention,stack,stackfused,gemvsweep]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -524,6 +524,28 @@ def rows_stack(eng, timer) -> list:
             bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
 
 
+def rows_gemv_sweep(eng, timer) -> list:
+    """Output-major fp16 GEMV (eng_gemv_f16w_nk) over a range of sizes, cold
+    weights: time against bytes separates the per-launch fixed cost from the
+    streaming rate inside a launch."""
+    rng = np.random.default_rng(5)
+    rows = []
+    for N, K in ((4096, 512), (4096, 1024), (4096, 2048), (4096, 4096), (1024, 4096),
+                 (2048, 4096), (8192, 4096), (16384, 4096), (32768, 4096), (65536, 4096)):
+        host = rand_f16(rng, (N, K))
+        count = max(2, (1 << 30) // host.nbytes + 1)
+        Ws = rotating(eng, host, count)
+        dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
+        dy = eng.empty(N, np.float32)
+        st = timer.sampled(lambda i, s: eng.lib.eng_gemv_f16w_nk(Ws[i % count].ptr, dx.ptr, dy.ptr,
+                                                                  N, K, s))
+        rows.append(hbm_row(f"gemv_f16w_nk sweep N={N} K={K} cold", st, 2 * N * K + 4 * K + 4 * N,
+                            {"N": N, "K": K}))
+        for d in Ws + [dx, dy]:
+            d.free()
+    return rows
+
+
 def rows_stack_fused(eng, timer) -> list:
     """Only the fastest config-5 arrangement (for profiling its kernels alone)."""
     return [bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
@@ -531,7 +553,7 @@ def rows_stack_fused(eng, timer) -> list:
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
-          "stackfused": rows_stack_fused}
+          "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep}
 
 
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
@@ -637,7 +659,8 @@ def main() -> int:
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary rows)")
     ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
                     + ", ".join(GROUPS) + " (default: all but stackfused, which repeats a "
-                    "stack row on its own for profiling)")
+                    "stack row on its own for profiling, and gemvsweep, a size sweep of the "
+                    "headline GEMV)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -669,7 +692,8 @@ def main() -> int:
 
     secondary = []
     if not args.quick:
-        groups = [g for g in args.only.split(",") if g] or [g for g in GROUPS if g != "stackfused"]
+        groups = [g for g in args.only.split(",") if g] or [g for g in GROUPS
+                                                            if g not in ("stackfused", "gemvsweep")]
         for g in groups:
             if g not in GROUPS:
                 log(f"unknown group {g!r}; choose from {', '.join(GROUPS)}")
