@@ -252,6 +252,63 @@ def test_attention_decode_long_sequence(gpu, orc, L):
             helpers.assert_within(got[h], target, rtol * (1 + np.abs(target)), f"needle {js} h={h}")
 
 
+# ------------------------------------------------------- adversarial softmax
+def adversarial_case(name, D, L, Hq=8, Hkv=2):
+    """The decode cases of the reference's attention_adversarial_softmax
+    (tests/test_kernels.cu, kv_len = 260, 8 / 2 heads): q = 2 on dims 0..3 and
+    k = s on dims 0..3, so with scale 1 / 8 (D = 64) every score is exactly the
+    s below; V is the reference's deterministic code ((17 j + 5 d + 11 g + 3)
+    % 31 - 15) / 16. At D = 128 the same q and k give scores s * 8 / sqrt(128)."""
+    q = np.zeros((Hq, D), np.float32)
+    k = np.zeros((Hkv, L, D), np.float32)
+    j = np.arange(L)
+    if name == "all_equal":
+        for h in range(Hq):
+            q[h, :4] = (25.0, 100.0, -30.0, -100.0)[h % 4]
+        k[:, :, :4] = 2.0
+    else:
+        q[:, :4] = 2.0
+        for g in range(Hkv):
+            if name == "neg_30_100":
+                s = (-30.0 if g == 0 else -100.0) - (j % 4)
+            elif name == "mixed_30":
+                s = np.where(j == 199, 30.0, np.where(j % 2 == 0, 10.0, -30.0))
+            else:  # dominant key
+                s = np.where(j == 197, 30.0, -20.0)
+            k[g, :, :4] = s[:, None]
+    g_, j_, d_ = np.meshgrid(np.arange(Hkv), j, np.arange(D), indexing="ij")
+    v = (((j_ * 17 + d_ * 5 + g_ * 11 + 3) % 31) - 15).astype(np.float32) * 0.0625
+    f16 = lambda a: a.astype(np.float16).view(np.uint16)
+    return f16(q), f16(k), f16(v)
+
+
+@pytest.mark.parametrize("name", ["neg_30_100", "mixed_30", "all_equal", "dominant"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_decode_adversarial_softmax(gpu, orc, name, D):
+    """Scores of -30..-103 (underflow without the max), +10 then +30 in a late
+    tile (the lazy rescale must fire across tiles and splits), equal logits up
+    to +100 (overflow without the max) and one dominant key, for every kernel:
+    automatic splits, one split, 8 splits, one head per workgroup, and the
+    unaligned-cache kernels."""
+    H, Hkv, L = 8, 2, 260
+    q, k, v = adversarial_case(name, D, L, H, Hkv)
+    sc = 1.0 / np.sqrt(D)
+    for split, share in ((0, None), (1, None), (8, None), (8, False)):
+        got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split, share=share)
+        assert np.isfinite(helpers.as_f64(got)).all()
+        check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"{name} D={D} split={split} share={share}")
+    # the same cache one element off 16-byte alignment
+    ku = np.concatenate([np.zeros(1, np.uint16), k.ravel()])
+    vu = np.concatenate([np.zeros(1, np.uint16), v.ravel()])
+    got = gpu_decode(gpu, q, ku, vu, L, H, Hkv, D, L * D, sc, 8, k_offset=1)
+    check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"{name} D={D} unaligned")
+    if name == "dominant" and D == 64:
+        # closed form: every head's output is key 197's value row (weight ratio e^-50)
+        vv = helpers.as_f64(v).reshape(Hkv, L, D)
+        for h in range(H):
+            assert np.array_equal(helpers.as_f64(got[h]), vv[h // 4, 197]), h
+
+
 # ------------------------------------------------------------------- bridge
 def test_cast_kernels_are_exact(gpu, orc):
     rng = np.random.default_rng(42)
