@@ -508,21 +508,27 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
 
 // Tile shape: the largest of 128 x 128, 128 x 64, 64 x 64 whose makespan (rounds
 // of one tile per CU, times the tile's share of the work) is not worse than a
-// smaller shape's. Smaller tiles re-read A and B more, so ties go to the larger.
+// smaller shape's. Smaller tiles re-read A and B more, so ties go to the larger
+// -- except that 64 x 64 wins a tie with 128 x 64 when 128 x 64 leaves at most
+// one workgroup per CU: two co-resident 64 x 64 workgroups hide each other's
+// latency (MI355X: 512 x 4096 x 11008 361 vs 376 us, 512 x 4096 x 4096 138 vs
+// 142 us). The same preference measured slower one step up (1024 x 4096 x 4096:
+// 256 tiles of 128 x 128 258 us, 512 of 128 x 64 272 us) and with more than one
+// workgroup per CU (512 x 11008 x 4096: 128 x 64 411 us, 64 x 64 420 us).
 enum class Tile { T128x128, T128x64, T64x64 };
 
 Tile choose_tile(long long M, long long N) {
   const long long cus = device_cu_count();
+  auto tiles = [&](long long bm, long long bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   auto makespan = [&](long long bm, long long bn) {
-    const long long tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    const long long rounds = (tiles + cus - 1) / cus;
+    const long long rounds = (tiles(bm, bn) + cus - 1) / cus;
     return static_cast<double>(rounds) * static_cast<double>(bm * bn) / (128.0 * 128.0);
   };
   const double t1 = makespan(128, 128);
   const double t2 = makespan(128, 64);
   const double t3 = makespan(64, 64);
   if (t1 <= t2 && t1 <= t3) return Tile::T128x128;
-  if (t2 <= t3) return Tile::T128x64;
+  if (t2 < t3 || (t2 == t3 && tiles(128, 64) > cus)) return Tile::T128x64;
   return Tile::T64x64;
 }
 
