@@ -666,7 +666,9 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus}, WORLD_SIZE {world} requested): "
-              "this engine has no multi-GPU path; see DESIGN.md for how the path would shard.",
+              "this engine has no multi-GPU path (the decode GEMVs would shard W by output rows "
+              "across GPUs, one per rank, with x replicated and no exchange but an optional "
+              "all-gather of y).",
               file=sys.stderr)
         return 2
 
