@@ -123,6 +123,8 @@ SIGNATURES = {
     "eng_cast_f32_to_f16": [_p, _p, _i64, _p],
     "eng_cast_f16_to_f32": [_p, _p, _i64, _p],
     "eng_kv_cache_write_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p],
+    "eng_transpose_f16": [_p, _p, _i64, _i64, _p],
+    "eng_transpose_f32": [_p, _p, _i64, _i64, _p],
     "eng_engref_open": [ctypes.c_char_p, _pp],
     "eng_engref_close": [_p],
     "eng_engref_count": [_p, ctypes.POINTER(ctypes.c_int32)],

@@ -1,7 +1,8 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,ffn,attention,stack,stackfused,gemvsweep]
+                    [--only config2,config3,refapi,gemm,ffn,attention,stack,layout,stackfused,
+                            gemvsweep]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -524,6 +525,24 @@ def rows_stack(eng, timer) -> list:
             bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
 
 
+def rows_layout(eng, timer) -> list:
+    """Weight layout conversion (eng_transpose_f16): reference-layout A [K x N]
+    to output-major W [N x K], once per weight at load time. Bytes: read and
+    write every element (4 bytes per fp16 element)."""
+    rng = np.random.default_rng(6)
+    rows = []
+    for K, N in ((4096, 4096), (4096, 11008), (11008, 4096)):
+        host = rand_f16(rng, (K, N))
+        count = max(2, (1 << 30) // host.nbytes + 1)
+        srcs = rotating(eng, host, count)
+        dst = eng.empty((N, K), np.uint16)
+        st = timer.sampled(lambda i, s: eng.lib.eng_transpose_f16(srcs[i % count].ptr, dst.ptr, K, N, s))
+        rows.append(hbm_row(f"transpose fp16 [{K} x {N}] -> [{N} x {K}] cold source", st, 4 * K * N))
+        for d in srcs + [dst]:
+            d.free()
+    return rows
+
+
 def rows_gemv_sweep(eng, timer) -> list:
     """Output-major fp16 GEMV (eng_gemv_f16w_nk) over a range of sizes, cold
     weights: time against bytes separates the per-launch fixed cost from the
@@ -553,6 +572,7 @@ def rows_stack_fused(eng, timer) -> list:
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
+          "layout": rows_layout,
           "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep}
 
 

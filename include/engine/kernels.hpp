@@ -100,6 +100,18 @@ inline void gemv_nk(const float* W, const float* x, float* y, std::int64_t N, st
   ENGINE_ABI_CHECK(eng_gemv_f32_nk(W, x, y, N, K, stream));
 }
 
+/// Weight layout conversion (additive): dst[cols x rows] = src[rows x cols]^T,
+/// bits unchanged. Converts a reference-layout A [K x N] once into the
+/// output-major W [N x K] of gemv_nk / rmsnorm_linear_nk.
+inline void transpose(const half* src, half* dst, std::int64_t rows, std::int64_t cols,
+                      hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_transpose_f16(detail::bits(src), detail::bits(dst), rows, cols, stream));
+}
+inline void transpose(const float* src, float* dst, std::int64_t rows, std::int64_t cols,
+                      hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_transpose_f32(src, dst, rows, cols, stream));
+}
+
 /// Output-major weights: out[M x N] = RMSNorm(in[M x K], rms_weight, eps) * W[N x K]^T.
 inline void rmsnorm_linear_nk(const float* in, const float* rms_weight, const half* W, float* out,
                               std::int64_t M, std::int64_t N, std::int64_t K, float eps,

@@ -354,6 +354,19 @@ int eng_kv_cache_write_f16(const eng_half* k_new, const eng_half* v_new, eng_hal
                            eng_half* v_cache, int64_t s_new, int64_t n_kv_heads, int64_t head_dim,
                            int64_t pos_offset, int64_t kv_max_seq_len, eng_stream stream);
 
+/* Weight layout conversion: dst [cols x rows] = src [rows x cols] transposed,
+ * bit patterns copied unchanged. Converts reference-layout weights A [K x N]
+ * (out = x . A, reference include/engine/kernels.hpp:83-99) once, at load
+ * time, into the output-major W [N x K] that eng_gemv_f16w_nk /
+ * eng_rmsnorm_linear_f16w_nk (and the _f32 forms) stream fastest. No
+ * reference counterpart (the reference has one weight layout). Messages:
+ * "negative dimension", "null device pointer", "src and dst overlap"; a zero
+ * dimension is a no-op. */
+int eng_transpose_f16(const eng_half* src, eng_half* dst, int64_t rows, int64_t cols,
+                      eng_stream stream);
+int eng_transpose_f32(const float* src, float* dst, int64_t rows, int64_t cols,
+                      eng_stream stream);
+
 /* ------------------------------------------------------------------------
  * ENGREF01 tensor files and device weight slabs.
  *

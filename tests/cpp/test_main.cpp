@@ -677,6 +677,14 @@ TEST(gpu_engref, weight_slab_views_feed_the_reference_api) {
   engine::DeviceBuffer<engine::half> out(static_cast<std::size_t>(N));
   engine::cuda::gemv_fp16(tA.ptr<engine::half>(Device::HIP), tx.ptr<engine::half>(Device::HIP),
                           out.get(), N, K);
+  // the same weights converted to output-major [N x K] on the device
+  engine::DeviceBuffer<engine::half> W(static_cast<std::size_t>(N * K));
+  engine::cuda::transpose(tA.ptr<engine::half>(Device::HIP), W.get(), K, N);
+  const std::vector<engine::half> wt = W.download();
+  int moved_wrong = 0;
+  for (std::int64_t k = 0; k < K; ++k)
+    for (std::int64_t n = 0; n < N; ++n) moved_wrong += wt[n * K + k].u != A[k * N + n].u;
+  EXPECT_EQ(moved_wrong, 0);
   HIP_CHECK(hipDeviceSynchronize());
   const std::vector<engine::half> got = out.download();
   int bad = 0;

@@ -127,6 +127,12 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_graph_capture_end", None, P), 1, "eng_graph_capture_end: stream is null"),
     (("eng_graph_capture_end", P, None), 1, "eng_graph_capture_end: graph is null"),
     (("eng_graph_launch", None, None), 1, "eng_graph_launch: graph is null"),
+    (("eng_transpose_f16", P, P + 4096, -1, 4, None), 1, "transpose: negative dimension"),
+    (("eng_transpose_f16", None, P, 4, 4, None), 1, "transpose: null device pointer"),
+    (("eng_transpose_f32", P, None, 4, 4, None), 1, "transpose: null device pointer"),
+    (("eng_transpose_f16", P, P, 4, 4, None), 1, "src and dst overlap"),
+    (("eng_transpose_f32", P, P + 60, 4, 4, None), 1, "src and dst overlap"),
+    (("eng_transpose_f32", P + 60, P, 4, 4, None), 1, "src and dst overlap"),
 ])
 def test_preconditions_fail_before_launch(eng, call, code, substr):
     name, *args = call
@@ -163,6 +169,8 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_cast_f16_to_f32", None, None, 0, None),
     ("eng_kv_cache_write_f16", None, None, None, None, 0, 2, 64, 3, 3, None),
     ("eng_graph_destroy", None),
+    ("eng_transpose_f16", None, None, 0, 7, None),
+    ("eng_transpose_f32", None, None, 7, 0, None),
 ])
 def test_empty_work_is_a_no_op(eng, call):
     name, *args = call
