@@ -1,0 +1,84 @@
+"""Maximum-size cases: operands of more than 2^31 elements.
+
+Index arithmetic past 32 bits is exercised where it matters for the decode
+path: an output-major fp16 GEMV with W [N x K] of 2^31 + 2^18 elements, the
+transpose of that W into the reference layout, and the reference-layout
+split-K GEMV over it. W repeats every 64 rows (built on the device by
+doubling copies of one 64-row block), so every output equals the output of
+its row modulo 64, bit for bit (the kernels compute each row / column with
+the same arithmetic in the same order); the first 64 outputs are checked
+against the C oracle with the GEMV bound.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import helpers
+
+pytestmark = pytest.mark.gpu
+
+PERIOD = 64
+K = 4096
+N = (1 << 19) + PERIOD  # N * K = 2^31 + 2^18 elements (4 GiB + 512 KiB of fp16)
+
+
+def tiled_rows(eng, block, rows):
+    """Device [rows x K] fp16 matrix repeating `block` ([PERIOD x K]) by rows."""
+    d = eng.empty((rows, block.shape[1]), np.uint16)
+    eng.call("eng_memcpy_h2d", d.ptr, block.ctypes.data, block.nbytes)
+    have = block.shape[0]
+    row_bytes = block.shape[1] * 2
+    while have < rows:
+        n = min(have, rows - have)
+        eng.call("eng_memcpy_d2d", d.ptr + have * row_bytes, d.ptr, n * row_bytes)
+        have += n
+    return d
+
+
+def check_periodic(got, y64_block, what):
+    got = np.asarray(got)
+    blocks = got[: (len(got) // PERIOD) * PERIOD].reshape(-1, PERIOD)
+    bad = np.nonzero(~(blocks == blocks[0]).all(axis=1))[0]
+    assert bad.size == 0, f"{what}: block {bad[:4]} differs from block 0"
+    return blocks[0]
+
+
+def test_gemv_past_2_31_elements_both_layouts(gpu, orc):
+    assert N * K > (1 << 31)
+    rng = np.random.default_rng(31)
+    W0 = (0.02 * rng.standard_normal((PERIOD, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal(K, dtype=np.float32)
+    W = tiled_rows(gpu, W0, N)
+    dx = gpu.upload(x)
+    y = gpu.empty(N, np.float32)
+    print(f"large: output-major gemv N={N} K={K} ({N * K} elements)", flush=True)
+    gpu.call("eng_gemv_f16w_nk", W.ptr, dx.ptr, y.ptr, N, K, None)
+    gpu.sync()
+    y_nk = y.download()
+    block = check_periodic(y_nk, None, "output-major gemv")
+    A0 = np.ascontiguousarray(W0.T)  # [K x PERIOD]
+    y64 = orc.gemv_f16w(A0, x).astype(np.float64)
+    a = helpers.absdot(x, A0) + np.abs(y64)
+    derived, stat = helpers.dot_bounds(a, y64, K)
+    helpers.assert_within(block, y64, derived, "output-major gemv block 0 [derived bound]")
+    helpers.assert_within(block, y64, stat, "output-major gemv block 0 [statistical bound]")
+
+    # reference layout A [K x N] = W^T: columns repeat every 64
+    print("large: transpose to the reference layout", flush=True)
+    A = gpu.empty((K, N), np.uint16)
+    gpu.call("eng_transpose_f16", W.ptr, A.ptr, N, K, None)
+    W.free()
+    row = np.empty(N, np.uint16)
+    for k in (0, 1, K // 2, K - 1):  # spot rows of A: A[k][n] = W0[n % 64][k]
+        gpu.call("eng_memcpy_d2h", row.ctypes.data, A.ptr + 2 * k * N, 2 * N)
+        assert np.array_equal(row, np.tile(W0[:, k], N // PERIOD + 1)[:N]), k
+    print("large: reference-layout split-K gemv", flush=True)
+    gpu.call("eng_gemv_f16w", A.ptr, dx.ptr, y.ptr, N, K, None)
+    gpu.sync()
+    y_kn = y.download()
+    block_kn = check_periodic(y_kn, None, "reference-layout gemv")
+    helpers.assert_within(block_kn, y64, derived, "reference-layout gemv block 0 [derived bound]")
+    helpers.assert_within(block_kn, y64, stat, "reference-layout gemv block 0 [statistical bound]")
+    A.free()
