@@ -406,16 +406,24 @@ class Event:
 
 class EngrefTensor:
     """One tensor of an ENGREF01 file: name, dtype code, shape, byte count,
-    slab offset and a numpy view of the mapped bytes (valid while the file is
-    open; f16 tensors are uint16 bit patterns)."""
+    slab offset and `host`, a read-only numpy view of the mapped bytes (f16
+    tensors as uint16 bit patterns). The view reads the file's mapping, so it
+    is only handed out while the file is open; copy it to keep it longer."""
 
-    def __init__(self, name, dtype, shape, nbytes, slab_offset, host):
+    def __init__(self, file, name, dtype, shape, nbytes, slab_offset, host):
+        self._file = file
         self.name = name
         self.dtype = dtype
         self.shape = shape
         self.nbytes = nbytes
         self.slab_offset = slab_offset
-        self.host = host
+        self._host = host
+
+    @property
+    def host(self) -> np.ndarray:
+        if not self._file.handle:
+            raise ValueError(f"engref tensor '{self.name}': the file is closed")
+        return self._host
 
 
 class EngrefFile:
@@ -451,7 +459,9 @@ class EngrefFile:
             host = np.frombuffer(raw, dtype=dt).reshape(shape)
         else:
             host = np.empty(shape, dtype=dt)
-        return EngrefTensor(name.value.decode(), dtype.value, shape, nbytes.value, off.value, host)
+        host.flags.writeable = False  # the mapping is read-only
+        return EngrefTensor(self, name.value.decode(), dtype.value, shape, nbytes.value, off.value,
+                            host)
 
     def size(self) -> int:
         return len(self.tensors)

@@ -32,7 +32,9 @@ struct EngrefTensor {
   std::int32_t code = ENG_ENGREF_F32;  ///< ENG_ENGREF_F32 / _F16 / _F64
   std::vector<std::int64_t> shape;
   std::int64_t nbytes = 0;
-  const void* host = nullptr;  ///< the mapped bytes (little-endian, maybe unaligned)
+  /// The mapped bytes (little-endian, maybe unaligned); valid while an
+  /// EngrefFile or WeightSlab of this file is alive (they share the mapping).
+  const void* host = nullptr;
   std::int64_t slab_offset = 0;
 
   std::int64_t numel() const {

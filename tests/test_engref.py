@@ -155,6 +155,20 @@ def test_good_file_of_the_malformed_family_parses(eng, tmp_path):
         assert f.names() == ["t"] and f.at("t").nbytes == 8
 
 
+def test_host_views_are_read_only_and_end_with_the_file(eng, tmp_path):
+    path = tmp_path / "v.bin"
+    engref.write(path, {"a": np.arange(5, dtype=np.float32)})
+    f = eng.engref(path)
+    t = f.at("a")
+    with pytest.raises(ValueError):
+        t.host[0] = 1.0
+    kept = t.host.copy()
+    f.close()
+    with pytest.raises(ValueError, match="closed"):
+        t.host
+    assert np.array_equal(kept, np.arange(5, dtype=np.float32))
+
+
 def test_missing_file_and_unknown_name(eng, pkg, tmp_path):
     with pytest.raises(pkg.EngineError) as e:
         eng.engref(tmp_path / "absent.bin")
