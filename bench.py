@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
                     [--only config2,config3,refapi,gemm,ffn,attention,stack,layout,stackfused,
-                            gemvsweep]
+                            gemvsweep,attn32k]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -480,7 +480,11 @@ def rows_ffn(eng, timer) -> list:
     return rows
 
 
-def rows_attention(eng, timer) -> list:
+ATTENTION_CASES = [(512, 32, 4, 64), (2048, 32, 4, 64), (8192, 32, 4, 64), (16384, 32, 4, 64),
+                   (32768, 32, 4, 64), (512, 32, 32, 128), (2048, 32, 32, 128), (8192, 32, 32, 128)]
+
+
+def rows_attention(eng, timer, cases=ATTENTION_CASES, extra_variants=True) -> list:
     """Decode attention at the reference's benchmark shapes (bench_kernels.cu:
     1079-1092): TinyLlama 32/4 heads at D = 64 and Llama-2-7B 32/32 at D = 128,
     cold KV caches (about 1 GiB of rotating copies). Bytes: K and V once plus
@@ -488,8 +492,6 @@ def rows_attention(eng, timer) -> list:
     rows = []
     rng = np.random.default_rng(11)
     f = eng.lib.eng_attention_decode_with_mode_f16
-    cases = [(512, 32, 4, 64), (2048, 32, 4, 64), (8192, 32, 4, 64), (16384, 32, 4, 64),
-             (32768, 32, 4, 64), (512, 32, 32, 128), (2048, 32, 32, 128), (8192, 32, 32, 128)]
     for L, H, Hkv, D in cases:
         elems = 2 * Hkv * L * D
         nslots = max(2, (1 << 30) // (2 * elems) + 1)
@@ -501,9 +503,9 @@ def rows_attention(eng, timer) -> list:
         nbytes = 2 * (2 * Hkv * L * D + 2 * H * D)
         arch = "TinyLlama" if Hkv == 4 else "Llama-2-7B"
         variants = [("auto splits", 0, 1)]
-        if L >= 8192:
+        if extra_variants and L >= 8192:
             variants.append(("split_kv=1", 1, 1))
-        if Hkv == 4 and L == 32768:
+        if extra_variants and Hkv == 4 and L == 32768:
             variants.append(("no GQA sharing", 0, 0))
         for tag, sp, share in variants:
             def launch(i, s, sp=sp, share=share):
@@ -516,6 +518,11 @@ def rows_attention(eng, timer) -> list:
         for d in kv + [dq, do]:
             d.free()
     return rows
+
+
+def rows_attention_tinyllama_32k(eng, timer) -> list:
+    """Only TinyLlama L = 32768 with automatic splits (for profiling its kernels alone)."""
+    return rows_attention(eng, timer, cases=[(32768, 32, 4, 64)], extra_variants=False)
 
 
 def rows_stack(eng, timer) -> list:
@@ -570,10 +577,14 @@ def rows_stack_fused(eng, timer) -> list:
     return [bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
 
 
+# Groups that repeat or sweep a row for profiling; not part of the default run.
+PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k")
+
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
           "layout": rows_layout,
-          "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep}
+          "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep,
+          "attn32k": rows_attention_tinyllama_32k}
 
 
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
@@ -678,9 +689,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary rows)")
     ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
-                    + ", ".join(GROUPS) + " (default: all but stackfused, which repeats a "
-                    "stack row on its own for profiling, and gemvsweep, a size sweep of the "
-                    "headline GEMV)")
+                    + ", ".join(GROUPS) + " (default: all but the profiling groups "
+                    + ", ".join(PROFILING_GROUPS) + ", which repeat or sweep single rows)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -714,8 +724,7 @@ def main() -> int:
 
     secondary = []
     if not args.quick:
-        groups = [g for g in args.only.split(",") if g] or [g for g in GROUPS
-                                                            if g not in ("stackfused", "gemvsweep")]
+        groups = [g for g in args.only.split(",") if g] or [g for g in GROUPS if g not in PROFILING_GROUPS]
         for g in groups:
             if g not in GROUPS:
                 log(f"unknown group {g!r}; choose from {', '.join(GROUPS)}")
