@@ -20,9 +20,9 @@
 //     32-63), so each lane reads a contiguous 16-float run of its A row
 //     (ds_read_b128) and a 16-row column of B (ds_read_b32, conflict-free) --
 //     or, when B is given transposed ([N x K]), a 16-float run of its B row;
-//   * full tiles of fp32 operands take gemm_f32_mfma_dma_kernel, which loads
-//     tiles straight into LDS (below); other shapes and fp16 B take
-//     gemm_f32_mfma_kernel, which stages through registers: A and B tiles are
+//   * full tiles take gemm_f32_mfma_dma_kernel, which loads tiles straight
+//     into LDS (below; fp16 B is converted as fragments are read); ragged
+//     shapes take gemm_f32_mfma_kernel, which stages through registers: A and B tiles are
 //     double-buffered in LDS with 4-float row padding and the next tile's
 //     global loads are issued before the current tile's MFMAs;
 //   * the workgroup -> tile map is XCD-aware: consecutive workgroup ids go to
@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 }
 
-// Full-tile fp32 variant fed by direct global -> LDS loads
+// Full-tile variant fed by direct global -> LDS loads
 // (global_load_lds_dwordx4: lane l of a wave writes 16 bytes at the wave's
 // LDS base + 16 l, from any global address the lane names). No staging
 // registers and no LDS store instructions: the next tile's loads are issued
@@ -290,6 +290,12 @@ __device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
 #endif
 }
 
+__device__ __forceinline__ void lds_dma16(const _Float16* src, _Float16* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
 // Waits until this wave's outstanding memory operations, the direct LDS loads
 // included, have completed.
 __device__ __forceinline__ void wait_all_memory() {
@@ -298,6 +304,13 @@ __device__ __forceinline__ void wait_all_memory() {
 #endif
 }
 __device__ __forceinline__ int swz_kn(int k) { return ((k >> 4) & 1) * 8; }
+// fp16 B tiles (8 halves per 16-byte chunk). [N x K]: a 32-deep row is 4
+// chunks; chunk c of row r sits at c ^ ((r >> 2) & 3), so the 16 rows of a
+// 16-lane slice of ds_read_b128 (row pitch 64 bytes) cover all 64 banks.
+// [K x N]: chunk c of row k sits at c ^ (4 ((k >> 4) & 1)), moving rows k and
+// k + 16 (the two half-waves of a fragment read) 64 bytes apart in the banks.
+__device__ __forceinline__ int swz_rows_h(int r) { return (r >> 2) & 3; }
+__device__ __forceinline__ int swz_kn_h(int k) { return ((k >> 4) & 1) * 4; }
 
 //
 // The two stages of each operand are separate LDS variables and the K loop is
@@ -306,24 +319,31 @@ __device__ __forceinline__ int swz_kn(int k) { return ((k >> 4) & 1) * 8; }
 // prove that a fragment read of the current stage cannot overlap the loads
 // into the other one; it then makes the read wait for the whole next tile.
 // With distinct variables the accesses carry distinct alias scopes.
-template <int BM, int BN, bool BNK>
+//
+// B may also be fp16 (BT = _Float16): its tiles are loaded into LDS as raw
+// halves, half the bytes of an fp32 tile, and converted to fp32 as each lane
+// reads its fragment, so the MFMAs and the accumulation are those of the fp32
+// path (fp16 -> fp32 is exact).
+template <int BM, int BN, bool BNK, typename BT = float>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
-    const float* __restrict__ A, const float* __restrict__ B, float* __restrict__ C, int M, int N,
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
     int K, int tiles_m, int tiles_n) {
+  constexpr bool HB = std::is_same<BT, _Float16>::value;
+  constexpr int BV = 16 / static_cast<int>(sizeof(BT));  // B elements per 16-byte chunk
   constexpr int WM = BM / 2;
   constexpr int WN = BN / 2;
   constexpr int MB = WM / 32;
   constexpr int NB = WN / 32;
   constexpr int A_CH = BM * BK / 4;        // 16-byte chunks of an A tile
-  constexpr int B_CH = BN * BK / 4;
+  constexpr int B_CH = BN * BK / BV;
   constexpr int A_INST = A_CH / kThreads;  // chunk loads per thread (= per wave instruction count)
   constexpr int B_INST = B_CH / kThreads;
-  constexpr int BROW = BN / 4;             // chunks per [K x N] B row
+  constexpr int BROW = BN / BV;            // chunks per [K x N] B row
   static_assert(A_CH % kThreads == 0 && B_CH % kThreads == 0, "tile shape");
   __shared__ __attribute__((aligned(1024))) float As0[BM * BK];
   __shared__ __attribute__((aligned(1024))) float As1[BM * BK];
-  __shared__ __attribute__((aligned(1024))) float Bs0[BN * BK];
-  __shared__ __attribute__((aligned(1024))) float Bs1[BN * BK];
+  __shared__ __attribute__((aligned(1024))) BT Bs0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) BT Bs1[BN * BK];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -340,7 +360,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
 
   // Issue the direct loads of K tile kt into one stage. Wave w's j-th
   // instruction fills chunk slots (4 j + w) * 64 + lane.
-  auto fetch = [&](float* as, float* bs, int kt) {
+  auto fetch = [&](float* as, BT* bs, int kt) {
     const int k0 = kt * BK;
 #pragma unroll
     for (int j = 0; j < A_INST; ++j) {
@@ -355,17 +375,25 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     for (int j = 0; j < B_INST; ++j) {
       const int slot0 = (4 * j + wave) * 64;
       const int slot = slot0 + lane;
-      const float* src;
-      if constexpr (BNK) {
+      const BT* src;
+      if constexpr (BNK && !HB) {
         const int r = slot >> 3;
         const int c = (slot & 7) ^ swz_rows(r);
         src = B + static_cast<long long>(n0 + r) * K + k0 + 4 * c;
-      } else {
+      } else if constexpr (BNK) {
+        const int r = slot >> 2;
+        const int c = (slot & 3) ^ swz_rows_h(r);
+        src = B + static_cast<long long>(n0 + r) * K + k0 + 8 * c;
+      } else if constexpr (!HB) {
         const int k = slot / BROW;
         const int c = (slot % BROW) ^ swz_kn(k);
         src = B + static_cast<long long>(k0 + k) * N + n0 + 4 * c;
+      } else {
+        const int k = slot / BROW;
+        const int c = (slot % BROW) ^ swz_kn_h(k);
+        src = B + static_cast<long long>(k0 + k) * N + n0 + 8 * c;
       }
-      lds_dma16(src, bs + 4 * slot0);
+      lds_dma16(src, bs + BV * slot0);
     }
   };
 
@@ -379,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
 
   // One K step on a resident stage: fragment reads and 16 MFMA k-slices.
   // The A fragment of lane (li, lg) holds k = 16 lg + 4 q + e.
-  auto compute = [&](const float* as, const float* bs) {
+  auto compute = [&](const float* as, const BT* bs) {
     floatx4 af[MB][4];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -393,7 +421,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     float bf[NB][16];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      if constexpr (BNK) {
+      if constexpr (BNK && !HB) {
         const int r = wn * WN + nb * 32 + li;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -402,13 +430,29 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) bf[nb][4 * q + e] = v[e];
         }
+      } else if constexpr (BNK) {
+        // Row r holds k = 0..31 as 4 chunks; this lane's k = 16 lg + s are
+        // chunks 2 lg and 2 lg + 1.
+        const int r = wn * WN + nb * 32 + li;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int c = (lg * 2 + q) ^ swz_rows_h(r);
+          const halfx8 v = *reinterpret_cast<const halfx8*>(bs + 8 * (r * 4 + c));
+#pragma unroll
+          for (int e = 0; e < 8; ++e) bf[nb][8 * q + e] = static_cast<float>(v[e]);
+        }
       } else {
         const int n = wn * WN + nb * 32 + li;
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
           const int k = lg * 16 + s;
-          const int c = (n >> 2) ^ swz_kn(k);
-          bf[nb][s] = bs[4 * (k * BROW + c) + (n & 3)];
+          if constexpr (HB) {
+            const int c = (n >> 3) ^ swz_kn_h(k);
+            bf[nb][s] = static_cast<float>(bs[8 * (k * BROW + c) + (n & 7)]);
+          } else {
+            const int c = (n >> 2) ^ swz_kn(k);
+            bf[nb][s] = bs[4 * (k * BROW + c) + (n & 3)];
+          }
         }
       }
     }
@@ -480,12 +524,14 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
-  if constexpr (std::is_same<BT, float>::value) {
+  {
+    // Whole tiles, 16-byte aligned operands and 16-byte aligned B rows
+    // ([K x N] rows of N elements; [N x K] rows of K, a multiple of BK).
     const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned_to(a.A, 16) &&
-                      aligned_to(a.B, 16) && (BNK || N % 4 == 0);
+                      aligned_to(a.B, 16) && (BNK || N % kBVec == 0);
     if (full && dma_enabled()) {
-      gemm_f32_mfma_dma_kernel<BM, BN, BNK><<<grid, kThreads, 0, stream>>>(a.A, B, a.C, M, N, K,
-                                                                          tiles_m, tiles_n);
+      gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT><<<grid, kThreads, 0, stream>>>(
+          a.A, B, a.C, M, N, K, tiles_m, tiles_n);
       ENG_LAUNCH_CHECK();
       return;
     }

@@ -422,6 +422,20 @@ def rows_gemm(eng, timer) -> list:
     rows.append(gemm_row("rmsnorm_linear_f32 512x4096x4096 (rmsnorm into pooled scratch + MFMA GEMM)",
                         st, M, N, K))
     dA.free(), dg.free(), dW.free(), dC.free()
+
+    # Prefill with fp16 weights (fp32 activations, fp32 accumulate): the gate /
+    # up shape of config 5 at 512 tokens, both weight layouts.
+    M, N, K = 512, 11008, 4096
+    dA = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
+    dg = eng.upload((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    dC = eng.empty((M, N), np.float32)
+    for name, fn, shape in (("reference layout W[KxN]", eng.lib.eng_rmsnorm_linear_f16w, (K, N)),
+                            ("output-major W[NxK]", eng.lib.eng_rmsnorm_linear_f16w_nk, (N, K))):
+        dW = eng.upload(rand_f16(rng, shape))
+        st = timer.sampled(lambda i, s: fn(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
+        rows.append(gemm_row(f"rmsnorm_linear_f16w {M}x{N}x{K} prefill, fp16 W {name}", st, M, N, K))
+        dW.free()
+    dA.free(), dg.free(), dC.free()
     return rows
 
 

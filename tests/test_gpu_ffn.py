@@ -250,6 +250,8 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with arena scratch
     (1, 64, 20000, "f16", True),     # K past the LDS budget: GEMV fallback
     (5, 200, 512, "f16", True),      # prefill: MFMA GEMMs + SwiGLU kernel
+    (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
+    (64, 256, 512, "f16", False),
 ])
 def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma):
     rng = np.random.default_rng(M + N + K)

@@ -558,6 +558,26 @@ def test_rmsnorm_linear_f32_full_tiles_against_oracle(gpu, orc, M, N, K, layout,
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f32 {layout} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (128, 512, 256), (256, 128, 1024),
+                                   (512, 11008, 4096)])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+@pytest.mark.parametrize("with_gamma", [True, False])
+def test_rmsnorm_linear_f16w_full_tiles_against_oracle(gpu, orc, M, N, K, layout, with_gamma):
+    # fp16 weights at M > 1: whole tiles take the direct-to-LDS GEMM with the
+    # B tile loaded as halves and converted while the fragments are read.
+    rng = np.random.default_rng(11 * M + N + K + (layout == "nk"))
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    if layout == "kn":
+        got = gpu_rmsnorm_linear(gpu, x, g, W)
+    else:
+        got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    rows = np.unique(np.linspace(0, M - 1, 16).astype(int))
+    y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
+
+
 def test_nk_k_zero_contract(gpu):
     d1 = gpu.upload(np.zeros(4, np.float32))
     dy = gpu.upload(np.full(12, 7.0, np.float32))
