@@ -20,9 +20,10 @@
 //     32-63), so each lane reads a contiguous 16-float run of its A row
 //     (ds_read_b128) and a 16-row column of B (ds_read_b32, conflict-free) --
 //     or, when B is given transposed ([N x K]), a 16-float run of its B row;
-//   * full tiles take gemm_f32_mfma_dma_kernel, which loads tiles straight
-//     into LDS (below; fp16 B is converted as fragments are read); ragged
-//     shapes take gemm_f32_mfma_kernel, which stages through registers: A and B tiles are
+//   * operands with K % 32 == 0 and 16-byte aligned rows take
+//     gemm_f32_mfma_dma_kernel, which loads tiles straight into LDS (below;
+//     fp16 B is converted as fragments are read; ragged M / N clamp their edge
+//     loads); the rest take gemm_f32_mfma_kernel, which stages through registers: A and B tiles are
 //     double-buffered in LDS with 4-float row padding and the next tile's
 //     global loads are issued before the current tile's MFMAs;
 //   * the workgroup -> tile map is XCD-aware: consecutive workgroup ids go to
@@ -324,7 +325,12 @@ __device__ __forceinline__ int swz_kn_h(int k) { return ((k >> 4) & 1) * 4; }
 // halves, half the bytes of an fp32 tile, and converted to fp32 as each lane
 // reads its fragment, so the MFMAs and the accumulation are those of the fp32
 // path (fp16 -> fp32 is exact).
-template <int BM, int BN, bool BNK, typename BT = float>
+//
+// EDGE: M and N need not be multiples of the tile. Loads of rows (A, [N x K]
+// B) or 16-byte column chunks ([K x N] B) past the matrix read the last valid
+// one instead -- in bounds, and only ever multiplied into accumulators whose
+// C element is outside the matrix -- and those elements are not stored.
+template <int BM, int BN, bool BNK, typename BT = float, bool EDGE = false>
 __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
     int K, int tiles_m, int tiles_n) {
@@ -368,7 +374,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
       const int slot = slot0 + lane;
       const int r = slot >> 3;
       const int c = (slot & 7) ^ swz_rows(r);
-      const float* src = A + static_cast<long long>(m0 + r) * K + k0 + 4 * c;
+      const float* src;
+      if constexpr (EDGE) {
+        src = A + static_cast<long long>(min(m0 + r, M - 1)) * K + k0 + 4 * c;
+      } else {
+        src = A + static_cast<long long>(m0 + r) * K + k0 + 4 * c;
+      }
       lds_dma16(src, as + 4 * slot0);
     }
 #pragma unroll
@@ -376,22 +387,23 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
       const int slot0 = (4 * j + wave) * 64;
       const int slot = slot0 + lane;
       const BT* src;
-      if constexpr (BNK && !HB) {
-        const int r = slot >> 3;
-        const int c = (slot & 7) ^ swz_rows(r);
-        src = B + static_cast<long long>(n0 + r) * K + k0 + 4 * c;
-      } else if constexpr (BNK) {
-        const int r = slot >> 2;
-        const int c = (slot & 3) ^ swz_rows_h(r);
-        src = B + static_cast<long long>(n0 + r) * K + k0 + 8 * c;
-      } else if constexpr (!HB) {
-        const int k = slot / BROW;
-        const int c = (slot % BROW) ^ swz_kn(k);
-        src = B + static_cast<long long>(k0 + k) * N + n0 + 4 * c;
+      if constexpr (BNK) {
+        const int r = HB ? slot >> 2 : slot >> 3;
+        const int c = HB ? (slot & 3) ^ swz_rows_h(r) : (slot & 7) ^ swz_rows(r);
+        if constexpr (EDGE) {
+          src = B + static_cast<long long>(min(n0 + r, N - 1)) * K + k0 + BV * c;
+        } else {
+          src = B + static_cast<long long>(n0 + r) * K + k0 + BV * c;
+        }
       } else {
         const int k = slot / BROW;
-        const int c = (slot % BROW) ^ swz_kn_h(k);
-        src = B + static_cast<long long>(k0 + k) * N + n0 + 8 * c;
+        const int c = (slot % BROW) ^ (HB ? swz_kn_h(k) : swz_kn(k));
+        if constexpr (EDGE) {
+          // N % BV == 0: a chunk is inside the row or wholly past it.
+          src = B + static_cast<long long>(k0 + k) * N + min(n0 + BV * c, N - BV);
+        } else {
+          src = B + static_cast<long long>(k0 + k) * N + n0 + BV * c;
+        }
       }
       lds_dma16(src, bs + BV * slot0);
     }
@@ -493,7 +505,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int row = m0 + wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
-        C[static_cast<long long>(row) * N + col] = acc[mb][nb][v];
+        if (!EDGE || (row < M && col < N)) C[static_cast<long long>(row) * N + col] = acc[mb][nb][v];
       }
     }
   }
@@ -525,13 +537,19 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
   {
-    // Whole tiles, 16-byte aligned operands and 16-byte aligned B rows
-    // ([K x N] rows of N elements; [N x K] rows of K, a multiple of BK).
-    const bool full = M % BM == 0 && N % BN == 0 && K % BK == 0 && aligned_to(a.A, 16) &&
-                      aligned_to(a.B, 16) && (BNK || N % kBVec == 0);
-    if (full && dma_enabled()) {
-      gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT><<<grid, kThreads, 0, stream>>>(
-          a.A, B, a.C, M, N, K, tiles_m, tiles_n);
+    // Direct loads need K % BK == 0, 16-byte aligned operands and 16-byte
+    // aligned B rows ([K x N] rows of N elements; [N x K] rows of K). Whole
+    // tiles take the plain kernel, ragged M / N its EDGE form.
+    const bool direct = K % BK == 0 && aligned_to(a.A, 16) && aligned_to(a.B, 16) &&
+                        (BNK || N % kBVec == 0);
+    if (direct && dma_enabled()) {
+      if (M % BM == 0 && N % BN == 0) {
+        gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, false><<<grid, kThreads, 0, stream>>>(
+            a.A, B, a.C, M, N, K, tiles_m, tiles_n);
+      } else {
+        gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, true><<<grid, kThreads, 0, stream>>>(
+            a.A, B, a.C, M, N, K, tiles_m, tiles_n);
+      }
       ENG_LAUNCH_CHECK();
       return;
     }

@@ -436,6 +436,17 @@ def rows_gemm(eng, timer) -> list:
         rows.append(gemm_row(f"rmsnorm_linear_f16w {M}x{N}x{K} prefill, fp16 W {name}", st, M, N, K))
         dW.free()
     dA.free(), dg.free(), dC.free()
+    # A prompt length that is not a multiple of the tile (1000 tokens).
+    M = 1000
+    dA = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
+    dg = eng.upload((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    dC = eng.empty((M, N), np.float32)
+    dW = eng.upload(rand_f16(rng, (N, K)))
+    fn = eng.lib.eng_rmsnorm_linear_f16w_nk
+    st = timer.sampled(lambda i, s: fn(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
+    rows.append(gemm_row(f"rmsnorm_linear_f16w {M}x{N}x{K} prefill (ragged M), fp16 W output-major W[NxK]",
+                         st, M, N, K))
+    dA.free(), dg.free(), dC.free(), dW.free()
     return rows
 
 

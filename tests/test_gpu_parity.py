@@ -200,6 +200,38 @@ def test_matmul_non_tile_multiples(gpu, orc, M, N, K):
     check_dot(got, y, helpers.absdot(A, B) + np.abs(y), K, f"matmul {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(100, 300, 256), (65, 132, 512), (1, 4096, 64), (200, 64, 96),
+                                   (1000, 11008, 4096), (513, 4100, 128)])
+def test_matmul_ragged_tiles_take_direct_loads(gpu, orc, M, N, K):
+    # K % 32 == 0, aligned, N % 4 == 0: the direct-to-LDS GEMM with clamped
+    # edge loads and masked stores (M / N not multiples of the tile).
+    rng = np.random.default_rng(M + 3 * N + 7 * K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 12).astype(int), [M - 1]]))
+    y = orc.matmul(A[rows], B).astype(np.float64)
+    check_dot(got[rows], y, helpers.absdot(A[rows], B) + np.abs(y), K, f"matmul {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(100, 11008, 4096), (77, 200, 512), (3, 136, 64)])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_rmsnorm_linear_f16w_ragged_tiles(gpu, orc, M, N, K, layout):
+    # fp16 weights with M (and N) not multiples of the tile: the EDGE form of
+    # the direct-load GEMM for both weight layouts.
+    rng = np.random.default_rng(5 * M + N + K + (layout == "nk"))
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    if layout == "kn":
+        got = gpu_rmsnorm_linear(gpu, x, g, W)
+    else:
+        got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    rows = np.unique(np.concatenate([np.linspace(0, M - 1, 12).astype(int), [M - 1]]))
+    y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("N,K,dtype", [(127, 31, "f32"), (73, 125, "f16w"), (4100, 4096, "f16w"),
                                        (11008, 4096, "f32"), (8, 20000, "f16w"), (1, 1, "f32"),
                                        (3000, 7, "f16"), (64, 1, "f16w")])
