@@ -7,9 +7,10 @@
 // up to 16384) runs gemv_rows_glu_kernel: one launch that stages x * gamma in
 // LDS, streams each output's gate and up rows together and applies SiLU in the
 // epilogue, so gate and up never reach memory. Other decode rows compute gate
-// and up with the fused RMSNorm + GEMV kernels; M > 1 normalises the rows
-// once, runs the MFMA GEMM for gate and for up, all into the stream's scratch
-// arena, and finishes with the SwiGLU kernel. Preconditions and
+// and up with the fused RMSNorm + GEMV kernels. A few rows (small-batch
+// decode) compute gate and up with the multi-row GEMV passes; more rows
+// normalise once and run the MFMA GEMM for gate and for up. Gate and up live
+// in the stream's scratch arena; the SwiGLU kernel finishes. Preconditions and
 // messages follow rmsnorm_linear; any zero dimension writes nothing.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
@@ -53,24 +54,28 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
   float* xn = static_cast<float*>(scratch.get());  // first: the GEMM wants it 16-byte aligned
   float* gate = xn + mk;
   float* up = gate + mn;
-  if (M > 1) launch_rmsnorm(in, gamma, xn, M, K, eps, s);
+  bool normed = false;
   for (int half = 0; half < 2; ++half) {
     const void* W = half == 0 ? static_cast<const void*>(Wg) : static_cast<const void*>(Wu);
     float* out = half == 0 ? gate : up;
+    GemvArgs gv;
+    gv.W = W;
+    gv.w = elem;
+    gv.w_nk = true;
+    gv.x = in;
+    gv.gamma = gamma;
+    gv.y = out;
+    gv.N = N;
+    gv.K = K;
+    gv.rms = true;
+    gv.eps = eps;
     if (M == 1) {
-      GemvArgs g;
-      g.W = W;
-      g.w = elem;
-      g.w_nk = true;
-      g.x = in;
-      g.gamma = gamma;
-      g.y = out;
-      g.N = N;
-      g.K = K;
-      g.rms = true;
-      g.eps = eps;
-      launch_gemv(g, s);
-    } else {
+      launch_gemv(gv, s);
+    } else if (!launch_gemv_nk_rows(gv, M, s)) {  // a few rows: passes over W
+      if (!normed) {
+        launch_rmsnorm(in, gamma, xn, M, K, eps, s);
+        normed = true;
+      }
       GemmArgs g;
       g.A = xn;
       g.B = W;

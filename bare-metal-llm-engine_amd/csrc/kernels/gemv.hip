@@ -26,6 +26,7 @@ namespace {
 using gemv::gemv_reduce_kernel;
 using gemv::gemv_rows_kernel;
 using gemv::gemv_rows_lds_kernel;
+using gemv::gemv_rows_lds_multi_kernel;
 using gemv::gemv_stream_kernel;
 
 // Reference-layout configuration: row segments of LPR lanes x 16 bytes.
@@ -214,6 +215,90 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream) {
   ENG_CHECK(a.x_elem == Elem::F16 && a.y_elem == Elem::F16 && !a.rms,
             "gemv: unsupported element types");
   dispatch_kn<_Float16, _Float16, _Float16, false>(a, stream);
+}
+
+namespace {
+
+// One round of resident workgroups (LDS-limited: 160 KiB per CU), each
+// looping over blocks of 4 R rows.
+template <typename WT, int R, int MX, bool RMS>
+void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t stream) {
+  constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
+  const long long blocks = ((a.N + R - 1) / R + 3) / 4;
+  const long long per_cu = std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
+  const long long wgs = std::min(blocks, per_cu * device_cu_count());
+  gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS>
+      <<<static_cast<unsigned>(wgs), 256, lds_bytes, stream>>>(
+          static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
+          static_cast<float*>(a.y), a.N, a.K, a.eps);
+  ENG_LAUNCH_CHECK();
+}
+
+template <typename WT, bool RMS>
+void rows_multi(const GemvArgs& a, int mx, std::size_t lds, bool two, hipStream_t stream) {
+  switch (mx * 2 + (two ? 1 : 0)) {
+    case 4: launch_rows_multi<WT, 1, 2, RMS>(a, lds, stream); break;
+    case 5: launch_rows_multi<WT, 2, 2, RMS>(a, lds, stream); break;
+    case 6: launch_rows_multi<WT, 1, 3, RMS>(a, lds, stream); break;
+    case 7: launch_rows_multi<WT, 2, 3, RMS>(a, lds, stream); break;
+    case 8: launch_rows_multi<WT, 1, 4, RMS>(a, lds, stream); break;
+    default: launch_rows_multi<WT, 2, 4, RMS>(a, lds, stream); break;
+  }
+}
+
+}  // namespace
+
+// Small-batch decode with output-major weights: y[M x N] = rows of x[M x K]
+// times W[N x K]^T, in groups of up to kMultiRows rows that share one pass
+// over W (gemv_rows_lds_multi_kernel; a group of one row is the single-row
+// GEMV). The staged rows share a 64 KiB LDS budget (4 rows at K = 4096, one at
+// K = 11008 with fp16 weights). Taken only when it needs at most kMaxPasses
+// passes over W -- each pass costs about one GEMV, while the MFMA GEMM for a
+// few rows costs about as much as that many passes (the GEMM pads M to its
+// 64-row tile) -- and when the vector path's requirements hold; returns false
+// otherwise and launches nothing.
+bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) {
+  constexpr int kMultiRows = 4;
+  constexpr long long kMaxPasses = 4;
+  constexpr long long kMaxLds = 64 * 1024;
+  if (!a.w_nk || M < 1 || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+  const long long vmax = a.w == Elem::F16 ? 8 : 4;
+  const bool vec_ok = (a.K % vmax == 0) && aligned_to(a.W, 16) && aligned_to(a.x, 16) &&
+                      (a.gamma == nullptr || aligned_to(a.gamma, 16));
+  if (!vec_ok) return false;
+  const long long piece = 64 * vmax;
+  const long long padded = (a.K + piece - 1) / piece * piece;
+  const long long row_bytes = padded * 4;
+  const long long fit = std::min<long long>(kMultiRows, kMaxLds / row_bytes);
+  const long long per_pass = std::max<long long>(1, fit);
+  const long long passes = (M + per_pass - 1) / per_pass;
+  if (passes > kMaxPasses) return false;
+  const bool two = a.N > 16LL * device_cu_count();
+  for (long long m0 = 0; m0 < M; m0 += per_pass) {
+    const int mx = static_cast<int>(std::min<long long>(per_pass, M - m0));
+    GemvArgs g = a;
+    g.x = static_cast<const float*>(a.x) + m0 * a.K;
+    g.y = static_cast<float*>(a.y) + m0 * a.N;
+    if (mx == 1) {
+      launch_gemv(g, stream);
+      continue;
+    }
+    const std::size_t lds = static_cast<std::size_t>(mx * row_bytes);
+    if (a.w == Elem::F16) {
+      if (a.rms) {
+        rows_multi<_Float16, true>(g, mx, lds, two, stream);
+      } else {
+        rows_multi<_Float16, false>(g, mx, lds, two, stream);
+      }
+    } else {
+      if (a.rms) {
+        rows_multi<float, true>(g, mx, lds, two, stream);
+      } else {
+        rows_multi<float, false>(g, mx, lds, two, stream);
+      }
+    }
+  }
+  return true;
 }
 
 }  // namespace eng

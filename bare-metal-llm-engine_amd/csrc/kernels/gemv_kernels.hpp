@@ -469,6 +469,118 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict
   }
 }
 
+// acc[m][j] = sum_k rows[j][k] * xs_m[k] for MX staged activation rows (row m
+// at xs + m * pitch), folded across the wave: the weight pieces are loaded and
+// converted once and used for every activation row. Each (m, j) sum runs over
+// the pieces, then the 4-float LDS groups, in the order dot_rows_lds uses, so
+// row m's result equals the single-row kernel's bit for bit.
+template <typename WT, int VEC, int NR, int U, int MX>
+__device__ __forceinline__ void dot_rows_lds_multi(const WT* const (&rows)[NR], const float* xs,
+                                                   int pitch, long long K, int npieces, int lane,
+                                                   float (&acc)[MX][NR]) {
+  using V = typename RawVec<WT, VEC>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 64 * VEC;
+#pragma unroll
+  for (int m = 0; m < MX; ++m)
+#pragma unroll
+    for (int j = 0; j < NR; ++j) acc[m][j] = 0.0f;
+  for (int p0 = 0; p0 < npieces; p0 += U) {
+    V cur[U][NR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long long k = static_cast<long long>(p0 + u) * PIECE + lane * VEC;
+      const bool ok = k < K;
+#pragma unroll
+      for (int j = 0; j < NR; ++j) {
+        cur[u][j] = ok ? __builtin_nontemporal_load(reinterpret_cast<const V*>(rows[j] + k)) : V{};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (p0 + u >= npieces) break;  // wave-uniform
+#pragma unroll
+      for (int h = 0; h < VEC / 4; ++h) {
+        F4 a[MX];
+#pragma unroll
+        for (int m = 0; m < MX; ++m)
+          a[m] = *reinterpret_cast<const F4*>(xs + m * pitch + (p0 + u) * PIECE + lane * 4 + h * 256);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+#pragma unroll
+          for (int j = 0; j < NR; ++j) {
+            const float w = static_cast<float>(cur[u][j][h * 4 + e]);
+#pragma unroll
+            for (int m = 0; m < MX; ++m) acc[m][j] = fmaf(a[m][e], w, acc[m][j]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+#pragma unroll
+    for (int m = 0; m < MX; ++m)
+#pragma unroll
+      for (int j = 0; j < NR; ++j) acc[m][j] += __shfl_xor(acc[m][j], off);
+  }
+}
+
+// Output-major GEMV over MX activation rows at once (small-batch decode):
+// y[m][n] = s_m * sum_k W[n][k] * x[m][k] * g[k] for m < MX, x and y
+// row-major with row pitches K and N. Each workgroup stages the MX rows of
+// x * gamma in LDS (MX x round_up(K, 64 * VEC) floats, sized by the caller)
+// with their sums of squares, then its waves stream weight rows against all
+// of them -- one pass over W serves MX outputs per row -- taking blocks of
+// 4 R rows in turn (block b, b + gridDim.x, ...), so the staging, MX times a
+// single row's, is paid once per resident workgroup rather than once per
+// block. Per row the arithmetic is gemv_rows_lds_kernel's (same staging, same
+// order), so each y[m] equals a single-row call on x[m] bit for bit. Same
+// requirements as gemv_rows_lds_kernel.
+template <typename WT, int VEC, int R, int U, int MX, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_lds_multi_kernel(const WT* __restrict__ W,
+                                                                  const float* __restrict__ x,
+                                                                  const float* __restrict__ gamma,
+                                                                  float* __restrict__ y,
+                                                                  long long N, long long K,
+                                                                  float eps) {
+  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
+  static_assert(MX >= 2 && MX <= 4, "2 to 4 activation rows");
+  constexpr int PIECE = 64 * VEC;
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[MX][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
+  const int pitch = npieces * PIECE;
+
+  float total_ss[MX];
+#pragma unroll
+  for (int m = 0; m < MX; ++m)
+    stage_xs<VEC, RMS>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m], &total_ss[m]);
+  float scale[MX];
+#pragma unroll
+  for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
+
+  const long long step = static_cast<long long>(gridDim.x) * 4 * R;
+  for (long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R; n0 < N; n0 += step) {
+    const WT* rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = W + (n0 + r < N ? n0 + r : n0) * K;
+    float acc[MX][R];
+    dot_rows_lds_multi<WT, VEC, R, U, MX>(rows, xs, pitch, K, npieces, lane, acc);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (n0 + r < N) y[m * N + n0 + r] = RMS ? acc[m][r] * scale[m] : acc[m][r];
+        }
+      }
+    }
+  }
+}
+
 // SiLU(g) * u with SiLU(g) = g / (1 + e^-g) (reference src/cpu_ref/swiglu_cpu.cpp:
 // 23-25): fp32 exp and a correctly rounded divide; large negative g gives
 // g / inf = -0, large positive g gives g.

@@ -29,6 +29,11 @@ struct GemvArgs {
   float eps = 0.0f;
 };
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
+// Output-major W only: y[M x N] = x[M x K] . W^T for a few rows (x and y
+// row-major, pitches K and N; a.x / a.y point at row 0), in groups that share
+// a pass over W. Returns false, launching nothing, when the shape is better
+// left to the GEMM (or the vector path's alignment requirements fail).
+bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
 
 // C[M x N] = A'[M x K] . B[K x N] on FP32 MFMA, where A' = A with column k
 // scaled by gamma_k when gamma is given; with rms, row r of C is further

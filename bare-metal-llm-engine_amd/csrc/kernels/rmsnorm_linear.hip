@@ -30,21 +30,23 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
   ENG_CHECK(eps >= 0.0f, "rmsnorm_linear: eps must be non-negative");
   if (M == 0 || N == 0 || K == 0) return;
   hipStream_t s = as_stream(stream);
+  GemvArgs g1;
+  g1.W = W;
+  g1.w = w_elem;
+  g1.w_nk = nk;
+  g1.x = in;
+  g1.gamma = rms_weight;
+  g1.y = out;
+  g1.N = N;
+  g1.K = K;
+  g1.rms = true;
+  g1.eps = eps;
   if (M == 1) {
-    GemvArgs g;
-    g.W = W;
-    g.w = w_elem;
-    g.w_nk = nk;
-    g.x = in;
-    g.gamma = rms_weight;
-    g.y = out;
-    g.N = N;
-    g.K = K;
-    g.rms = true;
-    g.eps = eps;
-    launch_gemv(g, s);
+    launch_gemv(g1, s);
     return;
   }
+  // A few rows with output-major weights: the rows share passes over W.
+  if (nk && launch_gemv_nk_rows(g1, M, s)) return;
   StreamScratch normed(s, static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float));
   float* xn = static_cast<float*>(normed.get());
   launch_rmsnorm(in, rms_weight, xn, M, K, eps, s);

@@ -249,7 +249,10 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (1, 257, 1024, "f32", True),     # fp32 weights: fused launch
     (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with arena scratch
     (1, 64, 20000, "f16", True),     # K past the LDS budget: GEMV fallback
-    (5, 200, 512, "f16", True),      # prefill: MFMA GEMMs + SwiGLU kernel
+    (5, 200, 512, "f16", True),      # small batch: multi-row GEMV passes + SwiGLU kernel
+    (4, 11008, 4096, "f16", True),   # small batch at the config 5 gate/up shape
+    (3, 300, 1000, "f32", False),    # small batch, fp32 weights, null gain
+    (40, 200, 512, "f16", True),     # prefill: MFMA GEMMs + SwiGLU kernel
     (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
     (64, 256, 512, "f16", False),
 ])

@@ -610,6 +610,39 @@ def test_rmsnorm_linear_f16w_full_tiles_against_oracle(gpu, orc, M, N, K, layout
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 11008, 4096), (4, 300, 4096), (5, 4096, 4096),
+                                   (8, 11008, 4096), (13, 1000, 2048), (16, 4096, 4096),
+                                   (2, 4096, 11008), (4, 4096, 11008)])
+@pytest.mark.parametrize("with_gamma", [True, False])
+def test_rmsnorm_linear_f16w_nk_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, with_gamma):
+    # Small-batch decode: the rows share passes over W (multi-row kernel), and
+    # each row's result is the single-row call's, bit for bit.
+    rng = np.random.default_rng(M * 100 + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
+    W = (0.02 * rng.standard_normal((N, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
+    for m in sorted({0, M // 2, M - 1}):
+        one = gpu_rmsnorm_linear_nk(gpu, x[m:m + 1], g, W)
+        assert np.array_equal(got[m], one[0]), f"row {m} of {M}"
+    Wt = np.ascontiguousarray(W.T)
+    rows = np.array(sorted({0, M - 1}))
+    y = orc.rmsnorm_linear(x[rows], g, Wt, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, Wt, K, f"small batch f16w nk {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (7, 11008, 4096), (16, 512, 1024)])
+def test_rmsnorm_linear_f32_nk_small_batch_against_oracle(gpu, orc, M, N, K):
+    rng = np.random.default_rng(M * 10 + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
+    Wt = np.ascontiguousarray(W.T)
+    y = orc.rmsnorm_linear(x, g, Wt, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, Wt, K, f"small batch f32 nk {M}x{N}x{K}")
+
+
 def test_nk_k_zero_contract(gpu):
     d1 = gpu.upload(np.zeros(4, np.float32))
     dy = gpu.upload(np.full(12, 7.0, np.float32))
