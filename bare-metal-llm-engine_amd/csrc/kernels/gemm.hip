@@ -655,18 +655,20 @@ int eng_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t 
                            s);
       return;
     }
+    // A single row is a GEMV, out[N] = A[0][K] . B[K x N]; a few rows share
+    // passes over B (the GEMM's 64-row tile would waste most of its work).
+    eng::GemvArgs gv;
+    gv.W = B;
+    gv.w = eng::Elem::F32;
+    gv.x = A;
+    gv.y = C;
+    gv.N = N;
+    gv.K = K;
     if (M == 1) {
-      // A single row is a GEMV: out[N] = A[0][K] . B[K x N].
-      eng::GemvArgs g;
-      g.W = B;
-      g.w = eng::Elem::F32;
-      g.x = A;
-      g.y = C;
-      g.N = N;
-      g.K = K;
-      eng::launch_gemv(g, s);
+      eng::launch_gemv(gv, s);
       return;
     }
+    if (eng::launch_gemv_kn_rows(gv, M, s)) return;
     eng::GemmArgs g;
     g.A = A;
     g.B = B;

@@ -29,8 +29,10 @@ using gemv::gemv_rows_lds_kernel;
 using gemv::gemv_rows_lds_multi_kernel;
 using gemv::gemv_stream_kernel;
 
-// Reference-layout configuration: row segments of LPR lanes x 16 bytes.
-template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool RMS>
+// Reference-layout configuration: row segments of LPR lanes x 16 bytes; MX
+// activation rows per launch (x row pitch K, y row pitch N).
+template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool RMS,
+          int MX = 1>
 void run_kn(const GemvArgs& a, hipStream_t stream) {
   constexpr int RPW = 64 / LPR;
   constexpr int STEP = WAVES * RPW;
@@ -47,6 +49,12 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   // stragglers latency-bound (measured: 18-29% slower at 11008 x 4096 and
   // fp32 4096 x 4096). A chunk never has fewer rows than one unrolled step of
   // all waves.
+  // The split does not depend on MX: a row's K chunks, and so its summation,
+  // are the same in every batch, so each row of a small batch equals the
+  // single-row result bit for bit. (Sizing the grid to the fewer resident
+  // workgroups that 3 or 4 rows' accumulators allow measured 14% faster at
+  // 4 x 11008 x 4096 -- 21.5 vs 24.6 us -- but would make results depend on
+  // the batch.)
   long long nsplit = 1;
   if (ncb < 2 * cus) {
     nsplit = (4 * cus) / ncb;
@@ -62,36 +70,37 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   const XT* x = static_cast<const XT*>(a.x);
   YT* y = static_cast<YT*>(a.y);
   if (nsplit == 1) {
-    gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, false>
+    gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, false, MX>
         <<<static_cast<unsigned>(ncb), WAVES * 64, 0, stream>>>(W, x, a.gamma, y, N, K, K, ncb,
                                                                  nullptr, nullptr, a.eps);
     ENG_LAUNCH_CHECK();
     return;
   }
-  // fp32 partial sums [nsplit x N], then partial sums of squares [nsplit].
-  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * (N + 1) * sizeof(float));
+  // fp32 partial sums [nsplit x MX x N], then partial sums of squares [nsplit x MX].
+  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * MX * (N + 1) * sizeof(float));
   float* partials = static_cast<float*>(ws.get());
-  float* partial_ss = partials + nsplit * N;
-  gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true>
+  float* partial_ss = partials + nsplit * MX * N;
+  gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true, MX>
       <<<static_cast<unsigned>(ncb * nsplit), WAVES * 64, 0, stream>>>(
           W, x, a.gamma, y, N, K, kchunk, ncb, partials, partial_ss, a.eps);
   ENG_LAUNCH_CHECK();
-  gemv_reduce_kernel<YT, RMS><<<static_cast<unsigned>((N + 63) / 64), 256, 0, stream>>>(
-      partials, partial_ss, y, N, K, static_cast<int>(nsplit), a.eps);
+  gemv_reduce_kernel<YT, RMS>
+      <<<dim3(static_cast<unsigned>((N + 63) / 64), MX), 256, 0, stream>>>(
+          partials, partial_ss, y, N, K, static_cast<int>(nsplit), a.eps, MX);
   ENG_LAUNCH_CHECK();
 }
 
 // 512-byte row segments (8 waves, 4 loads in flight per lane) for aligned
 // vector rows; the scalar fallback (unaligned W or N not a multiple of the
 // vector width) uses one lane per column.
-template <typename WT, typename XT, typename YT, bool RMS>
+template <typename WT, typename XT, typename YT, bool RMS, int MX = 1>
 void dispatch_kn(const GemvArgs& a, hipStream_t stream) {
   constexpr int VMAX = 16 / static_cast<int>(sizeof(WT));
   const bool vec_ok = (a.N % VMAX == 0) && aligned_to(a.W, 16);
   if (vec_ok) {
-    run_kn<WT, XT, YT, VMAX, 32, 8, 4, RMS>(a, stream);
+    run_kn<WT, XT, YT, VMAX, 32, 8, 4, RMS, MX>(a, stream);
   } else {
-    run_kn<WT, XT, YT, 1, 64, 4, 8, RMS>(a, stream);
+    run_kn<WT, XT, YT, 1, 64, 4, 8, RMS, MX>(a, stream);
   }
 }
 
@@ -295,6 +304,52 @@ bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) 
         rows_multi<float, true>(g, mx, lds, two, stream);
       } else {
         rows_multi<float, false>(g, mx, lds, two, stream);
+      }
+    }
+  }
+  return true;
+}
+
+namespace {
+
+template <typename WT, bool RMS>
+void kn_rows(const GemvArgs& a, int mx, hipStream_t stream) {
+  switch (mx) {
+    case 2: dispatch_kn<WT, float, float, RMS, 2>(a, stream); break;
+    case 3: dispatch_kn<WT, float, float, RMS, 3>(a, stream); break;
+    default: dispatch_kn<WT, float, float, RMS, 4>(a, stream); break;
+  }
+}
+
+}  // namespace
+
+// Small-batch decode with reference-layout weights A [K x N]: y[M x N] =
+// x[M x K] . A, up to 4 rows per pass over A (the split-K kernel with MX
+// activation rows; one row is the single-row GEMV). Same policy as
+// launch_gemv_nk_rows: at most 4 passes, else false (the GEMM is left to run).
+bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) {
+  constexpr long long kRows = 4;
+  constexpr long long kMaxPasses = 4;
+  if (a.w_nk || M < 1 || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+  if ((M + kRows - 1) / kRows > kMaxPasses) return false;
+  for (long long m0 = 0; m0 < M; m0 += kRows) {
+    const int mx = static_cast<int>(std::min<long long>(kRows, M - m0));
+    GemvArgs g = a;
+    g.x = static_cast<const float*>(a.x) + m0 * a.K;
+    g.y = static_cast<float*>(a.y) + m0 * a.N;
+    if (mx == 1) {
+      launch_gemv(g, stream);
+    } else if (a.w == Elem::F16) {
+      if (a.rms) {
+        kn_rows<_Float16, true>(g, mx, stream);
+      } else {
+        kn_rows<_Float16, false>(g, mx, stream);
+      }
+    } else {
+      if (a.rms) {
+        kn_rows<float, true>(g, mx, stream);
+      } else {
+        kn_rows<float, false>(g, mx, stream);
       }
     }
   }

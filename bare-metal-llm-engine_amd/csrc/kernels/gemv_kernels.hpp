@@ -69,8 +69,13 @@ __device__ __forceinline__ long long xcd_contiguous(long long wg, long long tota
   return xcd * q + (xcd < r ? xcd : r) + wg / kXcds;
 }
 
+// MX > 1: MX activation rows at once (small-batch decode), row m of x at
+// x + m K and of y at y + m N; every weight row read is multiplied into all MX
+// rows, each (m, column) summed in the single-row order, so row m equals a
+// single-row call on x[m] bit for bit. Partial sums are laid out
+// [nsplit][MX][N], sums of squares [nsplit][MX].
 template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool NT,
-          bool RMS, bool PARTIAL>
+          bool RMS, bool PARTIAL, int MX = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
     const WT* __restrict__ W, const XT* __restrict__ x, const float* __restrict__ gamma,
     YT* __restrict__ y, long long N, long long K, long long kchunk, long long ncb,
@@ -81,8 +86,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
   constexpr int THREADS = WAVES * 64;
   using V = typename RawVec<WT, VEC>::type;
 
-  __shared__ float red[WAVES][CW];
-  __shared__ float red_ss[WAVES];
+  __shared__ float red[MX][WAVES][CW];
+  __shared__ float red_ss[MX][WAVES];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -100,10 +105,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
   const long long row_begin = s * kchunk;
   const long long row_end = row_begin + kchunk < K ? row_begin + kchunk : K;
 
-  float acc[VEC];
+  float acc[MX][VEC];
+  float ss[MX];
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-  float ss = 0.0f;
+  for (int m = 0; m < MX; ++m) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[m][e] = 0.0f;
+    ss[m] = 0.0f;
+  }
 
   // Columns past N (whole vectors, as N % VEC == 0 when VEC > 1) read column
   // 0 instead; their sums are never written.
@@ -117,7 +126,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
     // load's register reused as the next address -- waits for every weight
     // load issued before it.)
     V raw[U];
-    float xv[U];
+    float xv[U][MX];
     float gv[U];
     bool okr[U];
 #pragma unroll
@@ -125,7 +134,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
       const long long r = base + static_cast<long long>(u) * STEP;
       okr[u] = r < row_end;
       const long long rr = okr[u] ? r : row_end - 1;
-      xv[u] = to_f32(x[rr]);
+#pragma unroll
+      for (int m = 0; m < MX; ++m) xv[u][m] = to_f32(x[m * K + rr]);
       if constexpr (RMS) gv[u] = gamma != nullptr ? gamma[rr] : 1.0f;
       const V* p = reinterpret_cast<const V*>(wsafe + rr * N);
       if constexpr (NT) {
@@ -136,14 +146,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      float xr = okr[u] ? xv[u] : 0.0f;
-      if constexpr (RMS) {
-        ss = fmaf(xr, xr, ss);
-        xr *= gv[u];
-      }
-      const V w = okr[u] ? raw[u] : V{};
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = fmaf(xr, lane_elem<VEC>(w, e), acc[e]);
+      for (int m = 0; m < MX; ++m) {
+        float xr = okr[u] ? xv[u][m] : 0.0f;
+        if constexpr (RMS) {
+          ss[m] = fmaf(xr, xr, ss[m]);
+          xr *= gv[u];
+        }
+        const V w = okr[u] ? raw[u] : V{};
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[m][e] = fmaf(xr, lane_elem<VEC>(w, e), acc[m][e]);
+      }
     }
   }
 
@@ -151,39 +164,58 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 #pragma unroll
   for (int off = LPR; off < 64; off <<= 1) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], off);
-    if constexpr (RMS) ss += __shfl_xor(ss, off);
+    for (int m = 0; m < MX; ++m) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[m][e] += __shfl_xor(acc[m][e], off);
+      if constexpr (RMS) ss[m] += __shfl_xor(ss[m], off);
+    }
   }
   if (rg == 0) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) red[wave][seg * VEC + e] = acc[e];
+    for (int m = 0; m < MX; ++m)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) red[m][wave][seg * VEC + e] = acc[m][e];
   }
-  if (RMS && lane == 0) red_ss[wave] = ss;
+  if (RMS && lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MX; ++m) red_ss[m][wave] = ss[m];
+  }
   __syncthreads();
 
-  float wg_ss = 0.0f;
-  if constexpr (RMS) {
+  float wg_ss[MX];
+  float scale[MX];
 #pragma unroll
-    for (int w = 0; w < WAVES; ++w) wg_ss += red_ss[w];
+  for (int m = 0; m < MX; ++m) {
+    wg_ss[m] = 0.0f;
+    if constexpr (RMS) {
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) wg_ss[m] += red_ss[m][w];
+    }
+    scale[m] = (RMS && !PARTIAL) ? rms_scale(wg_ss[m], K, eps) : 1.0f;
   }
-  const float scale = (RMS && !PARTIAL) ? rms_scale(wg_ss, K, eps) : 1.0f;
 
   for (int c = t; c < CW; c += THREADS) {
     const long long col = cb * CW + c;
     if (col < N) {
-      float v = red[0][c];
 #pragma unroll
-      for (int w = 1; w < WAVES; ++w) v += red[w][c];
-      if constexpr (PARTIAL) {
-        part[s * N + col] = v;
-      } else {
-        if constexpr (RMS) v *= scale;
-        y[col] = from_f32<YT>(v);
+      for (int m = 0; m < MX; ++m) {
+        float v = red[m][0][c];
+#pragma unroll
+        for (int w = 1; w < WAVES; ++w) v += red[m][w][c];
+        if constexpr (PARTIAL) {
+          part[(s * MX + m) * N + col] = v;
+        } else {
+          if constexpr (RMS) v *= scale[m];
+          y[m * N + col] = from_f32<YT>(v);
+        }
       }
     }
   }
   if constexpr (PARTIAL && RMS) {
-    if (cb == 0 && t == 0) part_ss[s] = wg_ss;
+    if (cb == 0 && t == 0) {
+#pragma unroll
+      for (int m = 0; m < MX; ++m) part_ss[s * MX + m] = wg_ss[m];
+    }
   }
 }
 
@@ -191,29 +223,35 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 // its 4 waves each sum a contiguous quarter of the splits in split order (8
 // independent loads in flight per lane), and the quarters are combined as
 // ((q0 + q1) + q2) + q3, so the association is fixed for a given nsplit.
+// blockIdx.y selects the activation row m of an mx-row launch (partials
+// [nsplit][mx][N], output row m at y + m N).
 template <typename YT, bool RMS>
 __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part,
                                                           const float* __restrict__ part_ss,
                                                           YT* __restrict__ y, long long N,
-                                                          long long K, int nsplit, float eps) {
+                                                          long long K, int nsplit, float eps,
+                                                          int mx) {
   __shared__ float quarter[4][64];
   const int c = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
+  const int m = blockIdx.y;
   const long long col = static_cast<long long>(blockIdx.x) * 64 + c;
   const int per = (nsplit + 3) / 4;
   const int s0 = g * per;
   const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
+  const float* pm = part + static_cast<long long>(m) * N;
+  const long long stride = static_cast<long long>(mx) * N;
   float v = 0.0f;
   if (col < N) {
     int s = s0;
     for (; s + 8 <= s1; s += 8) {
       float t[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) t[i] = part[static_cast<long long>(s + i) * N + col];
+      for (int i = 0; i < 8; ++i) t[i] = pm[static_cast<long long>(s + i) * stride + col];
 #pragma unroll
       for (int i = 0; i < 8; ++i) v += t[i];
     }
-    for (; s < s1; ++s) v += part[static_cast<long long>(s) * N + col];
+    for (; s < s1; ++s) v += pm[static_cast<long long>(s) * stride + col];
   }
   quarter[g][c] = v;
   __syncthreads();
@@ -221,10 +259,10 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restric
   float out = ((quarter[0][c] + quarter[1][c]) + quarter[2][c]) + quarter[3][c];
   if constexpr (RMS) {
     float tot = 0.0f;
-    for (int s = 0; s < nsplit; ++s) tot += part_ss[s];
+    for (int s = 0; s < nsplit; ++s) tot += part_ss[s * mx + m];
     out *= rms_scale(tot, K, eps);
   }
-  y[col] = from_f32<YT>(out);
+  y[static_cast<long long>(m) * N + col] = from_f32<YT>(out);
 }
 
 // Output-major weights: y[n] = sum_k W[n][k] * xs[k] with W row-major [N x K]

@@ -34,6 +34,8 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream);
 // a pass over W. Returns false, launching nothing, when the shape is better
 // left to the GEMM (or the vector path's alignment requirements fail).
 bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
+// Reference-layout W [K x N] counterpart of launch_gemv_nk_rows.
+bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
 
 // C[M x N] = A'[M x K] . B[K x N] on FP32 MFMA, where A' = A with column k
 // scaled by gamma_k when gamma is given; with rms, row r of C is further

@@ -45,8 +45,8 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     launch_gemv(g1, s);
     return;
   }
-  // A few rows with output-major weights: the rows share passes over W.
-  if (nk && launch_gemv_nk_rows(g1, M, s)) return;
+  // A few rows (small-batch decode): the rows share passes over W.
+  if (nk ? launch_gemv_nk_rows(g1, M, s) : launch_gemv_kn_rows(g1, M, s)) return;
   StreamScratch normed(s, static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float));
   float* xn = static_cast<float*>(normed.get());
   launch_rmsnorm(in, rms_weight, xn, M, K, eps, s);

@@ -380,6 +380,17 @@ def rows_config3(eng, timer) -> list:
         dxm.free(), dym.free()
     for w in Ws:
         w.free()
+    Ws = rotating(eng, rand_f16(np.random.default_rng(2), (K, N)), R)
+    f = eng.lib.eng_rmsnorm_linear_f16w
+    M = 4
+    dxm = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
+    dym = eng.empty((M, N), np.float32)
+    st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
+    rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (small-batch decode), "
+                        "reference layout W[KxN]", st, 2 * K * N + 4 * M * K + 4 * K + 4 * M * N))
+    dxm.free(), dym.free()
+    for w in Ws:
+        w.free()
     return rows
 
 

@@ -631,6 +631,42 @@ def test_rmsnorm_linear_f16w_nk_small_batch_rows_match_single_row_calls(gpu, orc
     check_rmsnorm_linear(got[rows], y, x[rows], g, Wt, K, f"small batch f16w nk {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype", [(2, 4096, 4096, "f16"), (3, 11008, 4096, "f16"),
+                                         (4, 300, 1000, "f16"), (6, 4096, 11008, "f16"),
+                                         (16, 4096, 4096, "f16"), (5, 4096, 4096, "f32"),
+                                         (4, 257, 100, "f32")])
+def test_rmsnorm_linear_kn_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, dtype):
+    # Reference-layout weights A [K x N]: the split-K kernel with several
+    # activation rows; each row equals the single-row call bit for bit.
+    rng = np.random.default_rng(M * 77 + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    A = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    if dtype == "f16":
+        A = orc.f32_to_f16(A)
+    got = gpu_rmsnorm_linear(gpu, x, g, A)
+    for m in sorted({0, M // 2, M - 1}):
+        one = gpu_rmsnorm_linear(gpu, x[m:m + 1], g, A)
+        assert np.array_equal(got[m], one[0]), f"row {m} of {M}"
+    rows = np.array(sorted({0, M - 1}))
+    y = orc.rmsnorm_linear(x[rows], g, A, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, A, K, f"small batch kn {dtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 130, 77), (8, 11008, 4096), (16, 64, 1000)])
+def test_matmul_small_m_rows_match_gemv(gpu, orc, M, N, K):
+    # matmul with a few rows shares passes over B; row m equals the M = 1
+    # product of A[m] bit for bit.
+    rng = np.random.default_rng(M + N + K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    for m in sorted({0, M - 1}):
+        assert np.array_equal(got[m], gpu_matmul(gpu, A[m:m + 1], B)[0]), f"row {m} of {M}"
+    y = orc.matmul(A, B).astype(np.float64)
+    check_dot(got, y, helpers.absdot(A, B) + np.abs(y), K, f"matmul small M {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (7, 11008, 4096), (16, 512, 1024)])
 def test_rmsnorm_linear_f32_nk_small_batch_against_oracle(gpu, orc, M, N, K):
     rng = np.random.default_rng(M * 10 + N + K)
