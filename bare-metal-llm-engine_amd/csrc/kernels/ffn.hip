@@ -8,13 +8,16 @@
 // LDS, streams each output's gate and up rows together and applies SiLU in the
 // epilogue, so gate and up never reach memory. Other decode rows compute gate
 // and up with the fused RMSNorm + GEMV kernels. A few rows (small-batch
-// decode) compute gate and up with the multi-row GEMV passes; more rows
-// normalise once and run the MFMA GEMM for gate and for up. Gate and up live
-// in the stream's scratch arena; the SwiGLU kernel finishes. Preconditions and
+// decode) run gemv_rows_glu_multi_kernel: up to 4 rows per pass over Wg and
+// Wu, SwiGLU applied in the epilogue, each row equal to its M = 1 result;
+// otherwise a few rows compute gate and up with the multi-row GEMV passes,
+// and more rows normalise once and run the MFMA GEMM for gate and for up, in
+// the stream's scratch arena, and the SwiGLU kernel finishes. Preconditions and
 // messages follow rmsnorm_linear; any zero dimension writes nothing.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
+#include <algorithm>
 #include <cstddef>
 
 namespace eng {
@@ -45,6 +48,42 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
         <<<static_cast<unsigned>(wgs), 256, static_cast<std::size_t>(padded) * 4, s>>>(
             Wg, Wu, in, gamma, act, N, K, eps);
     ENG_LAUNCH_CHECK();
+    return;
+  }
+  // Small batch: up to 4 rows per pass over Wg and Wu, at most 4 passes.
+  const long long fit = std::min<long long>(4, kMaxLds / (padded * 4));
+  const bool multi = M > 1 && fit >= 2 && (M + fit - 1) / fit <= 4 && K % VEC == 0 &&
+                     aligned_to(Wg, 16) && aligned_to(Wu, 16) && aligned_to(in, 16) &&
+                     (gamma == nullptr || aligned_to(gamma, 16));
+  if (multi) {
+    const long long blocks = (N + 3) / 4;
+    for (long long m0 = 0; m0 < M; m0 += fit) {
+      const int mx = static_cast<int>(std::min<long long>(fit, M - m0));
+      const float* xm = in + m0 * K;
+      float* am = act + m0 * N;
+      const std::size_t lds = static_cast<std::size_t>(mx * padded * 4);
+      const long long per_cu = std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds + 64)));
+      const unsigned grid = static_cast<unsigned>(std::min(blocks, per_cu * device_cu_count()));
+      switch (mx) {
+        case 1:
+          gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true>
+              <<<static_cast<unsigned>(blocks), 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          break;
+        case 2:
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 2, true>
+              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          break;
+        case 3:
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 3, true>
+              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          break;
+        default:
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 4, true>
+              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          break;
+      }
+      ENG_LAUNCH_CHECK();
+    }
     return;
   }
 

@@ -671,5 +671,46 @@ __global__ __launch_bounds__(256) void gemv_rows_glu_kernel(const WT* __restrict
   }
 }
 
+// Small-batch form of gemv_rows_glu_kernel: MX activation rows (x pitch K,
+// act pitch N) share each pass over Wg and Wu. The rows are staged once per
+// workgroup and the workgroups (one round of residents) loop over blocks of
+// 4 outputs, as in gemv_rows_lds_multi_kernel; each wave streams one
+// output's gate and up rows. Per row the arithmetic is the single-row fused
+// kernel's, so act[m] equals an M = 1 call bit for bit.
+template <typename WT, int VEC, int U, int MX, bool RMS>
+__global__ __launch_bounds__(256) void gemv_rows_glu_multi_kernel(
+    const WT* __restrict__ Wg, const WT* __restrict__ Wu, const float* __restrict__ x,
+    const float* __restrict__ gamma, float* __restrict__ act, long long N, long long K,
+    float eps) {
+  static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
+  static_assert(MX >= 2 && MX <= 4, "2 to 4 activation rows");
+  constexpr int PIECE = 64 * VEC;
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[MX][4];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
+  const int pitch = npieces * PIECE;
+
+  float total_ss[MX];
+#pragma unroll
+  for (int m = 0; m < MX; ++m)
+    stage_xs<VEC, RMS>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m], &total_ss[m]);
+  float scale[MX];
+#pragma unroll
+  for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
+
+  const long long step = static_cast<long long>(gridDim.x) * 4;
+  for (long long n = static_cast<long long>(blockIdx.x) * 4 + wave; n < N; n += step) {
+    const WT* rows[2] = {Wg + n * K, Wu + n * K};
+    float acc[MX][2];
+    dot_rows_lds_multi<WT, VEC, 2, U, MX>(rows, xs, pitch, K, npieces, lane, acc);
+    if (lane == 0) {
+#pragma unroll
+      for (int m = 0; m < MX; ++m) act[m * N + n] = swiglu_f32(acc[m][0] * scale[m], acc[m][1] * scale[m]);
+    }
+  }
+}
+
 }  // namespace gemv
 }  // namespace eng

@@ -523,7 +523,15 @@ def rows_ffn(eng, timer) -> list:
 
     st = timer.sampled(unfused)
     rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, unfused (3 launches)", st, nbytes))
-    for d in Wg + Wu + [dx, dgm, dgate, dup, dact]:
+    # Small-batch decode: 4 rows share each pass over the gate / up weights.
+    M = 4
+    dxm = eng.upload(rng.standard_normal((M, H), dtype=np.float32))
+    dam = eng.empty((M, F), np.float32)
+    st = timer.sampled(lambda i, s: glu(dxm.ptr, dgm.ptr, Wg[i % RW].ptr, Wu[i % RW].ptr, dam.ptr,
+                                        M, F, H, 1e-5, s))
+    rows.append(hbm_row(f"FFN gate/up + SwiGLU {M}x11008x4096 fp16-W cold (small-batch decode, 1 launch)",
+                        st, 2 * 2 * H * F + 4 * M * H + 4 * H + 4 * M * F))
+    for d in Wg + Wu + [dx, dgm, dgate, dup, dact, dxm, dam]:
         d.free()
     return rows
 

@@ -271,6 +271,28 @@ def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma
               f"rmsnorm_linear_swiglu nk {M}x{N}x{K} {dtype}")
 
 
+@pytest.mark.parametrize("M,N,K,dtype", [(2, 11008, 4096, "f16"), (3, 1000, 2048, "f16"),
+                                         (5, 4096, 4096, "f16"), (16, 11008, 4096, "f16"),
+                                         (4, 512, 1024, "f32")])
+def test_rmsnorm_linear_swiglu_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, dtype):
+    # A few rows share each pass over Wg and Wu (fused SwiGLU epilogue); each
+    # row's act equals the M = 1 fused call bit for bit.
+    rng = np.random.default_rng(M * 13 + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Wgf = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    Wuf = (rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    Wg, Wu = (orc.f32_to_f16(W) if dtype == "f16" else W for W in (Wgf, Wuf))
+    got = gpu_glu_nk(gpu, x, g, Wg, Wu)
+    for m in sorted({0, M // 2, M - 1}):
+        assert np.array_equal(got[m], gpu_glu_nk(gpu, x[m:m + 1], g, Wg, Wu)[0]), f"row {m} of {M}"
+    rows = np.array(sorted({0, M - 1}))
+    Wg_kn, Wu_kn = np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T)
+    act64, bd, bs = glu_reference(x[rows], g, Wg_kn, Wu_kn)
+    check_glu(got[rows], orc.rmsnorm_linear_swiglu(x[rows], g, Wg_kn, Wu_kn, EPS), act64, bd, bs,
+              f"small batch glu {M}x{N}x{K} {dtype}")
+
+
 def test_rmsnorm_linear_swiglu_equals_separate_calls(gpu):
     """Fused act == SwiGLU of the two RMSNorm+linear outputs, within rounding."""
     rng = np.random.default_rng(35)
