@@ -58,11 +58,7 @@ __device__ __forceinline__ float merge_weight(float a, float b) {
 // Sum over the LPK (8 or 16) consecutive lanes that hold one key, left in
 // every one of them: DPP quad_perm xor-1 and xor-2, then row_half_mirror
 // (lane i <- 7 - i within 8 lanes) and, for 16 lanes, row_mirror (i <- 15 - i).
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float x) {
-  const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false);
-  return x + __builtin_bit_cast(float, y);
-}
+using gemv::dpp_add;
 template <int LPK>
 __device__ __forceinline__ float sum_key_lanes(float x) {
   static_assert(LPK == 8 || LPK == 16, "8 or 16 lanes per key");

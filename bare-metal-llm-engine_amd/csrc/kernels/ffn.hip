@@ -42,10 +42,13 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
                      aligned_to(Wu, 16) && aligned_to(in, 16) &&
                      (gamma == nullptr || aligned_to(gamma, 16));
   if (fused) {
-    const long long wgs = (N + 3) / 4;  // one output (its gate and up rows) per wave
+    // One output (its gate and up rows) per wave; fp16 weights in workgroups of
+    // 16 waves (x staged once per 16 outputs).
+    constexpr int WAVES = sizeof(WT) == 2 ? 16 : 4;
+    const long long wgs = (N + WAVES - 1) / WAVES;
     ENG_CHECK(wgs <= 0x7fffffffLL, "rmsnorm_linear_swiglu: N too large for one launch");
-    gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true>
-        <<<static_cast<unsigned>(wgs), 256, static_cast<std::size_t>(padded) * 4, s>>>(
+    gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>
+        <<<static_cast<unsigned>(wgs), WAVES * 64, static_cast<std::size_t>(padded) * 4, s>>>(
             Wg, Wu, in, gamma, act, N, K, eps);
     ENG_LAUNCH_CHECK();
     return;
@@ -56,30 +59,36 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
                      aligned_to(Wg, 16) && aligned_to(Wu, 16) && aligned_to(in, 16) &&
                      (gamma == nullptr || aligned_to(gamma, 16));
   if (multi) {
-    const long long blocks = (N + 3) / 4;
+    // fp16 weights: workgroups of 16 waves, one per CU (4 rows at 11008 x
+    // 4096: 36.4 us against 37.8 us for 4-wave workgroups, two per CU); fp32
+    // weights: 4-wave workgroups, as many per CU as the LDS holds.
+    constexpr int WAVES = sizeof(WT) == 2 ? 16 : 4;
+    const long long blocks = (N + WAVES - 1) / WAVES;
     for (long long m0 = 0; m0 < M; m0 += fit) {
       const int mx = static_cast<int>(std::min<long long>(fit, M - m0));
       const float* xm = in + m0 * K;
       float* am = act + m0 * N;
       const std::size_t lds = static_cast<std::size_t>(mx * padded * 4);
-      const long long per_cu = std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds + 64)));
+      const long long per_cu =
+          WAVES == 16 ? 1
+                      : std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds + 64)));
       const unsigned grid = static_cast<unsigned>(std::min(blocks, per_cu * device_cu_count()));
       switch (mx) {
         case 1:
-          gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true>
-              <<<static_cast<unsigned>(blocks), 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>
+              <<<static_cast<unsigned>(blocks), WAVES * 64, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
           break;
         case 2:
-          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 2, true>
-              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 2, true, WAVES>
+              <<<grid, WAVES * 64, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
           break;
         case 3:
-          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 3, true>
-              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 3, true, WAVES>
+              <<<grid, WAVES * 64, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
           break;
         default:
-          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 4, true>
-              <<<grid, 256, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
+          gemv::gemv_rows_glu_multi_kernel<WT, VEC, 4, 4, true, WAVES>
+              <<<grid, WAVES * 64, lds, s>>>(Wg, Wu, xm, gamma, am, N, K, eps);
           break;
       }
       ENG_LAUNCH_CHECK();

@@ -104,7 +104,8 @@ void dispatch_kn(const GemvArgs& a, hipStream_t stream) {
   }
 }
 
-// Output-major launches: 256-thread workgroups of 4 waves, R rows per wave.
+// Output-major register-kernel launches: 256-thread workgroups of 4 waves, R
+// rows per wave.
 template <typename WT, int VEC, int R, int U, bool RMS>
 void launch_rows(const GemvArgs& a, hipStream_t stream) {
   const long long wgs = ((a.N + R - 1) / R + 3) / 4;
@@ -115,13 +116,15 @@ void launch_rows(const GemvArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
-template <typename WT, int R, bool RMS>
+// LDS-staged output-major launches: workgroups of WAVES waves, R rows per
+// wave, U loads per row in flight.
+template <typename WT, int R, int U, bool RMS, int WAVES>
 void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t stream) {
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
-  const long long wgs = ((a.N + R - 1) / R + 3) / 4;
+  const long long wgs = ((a.N + R - 1) / R + WAVES - 1) / WAVES;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
-  gemv_rows_lds_kernel<WT, VEC, R, 4, RMS>
-      <<<static_cast<unsigned>(wgs), 256, lds_bytes, stream>>>(
+  gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>
+      <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
           static_cast<float*>(a.y), a.N, a.K, a.eps);
   ENG_LAUNCH_CHECK();
@@ -133,10 +136,12 @@ void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t strea
 // beyond that 8 in flight. For fp16 weights the x (and gamma) stream is
 // larger than the weight row it meets, and once it no longer stays in the
 // vector L1 (RMSNorm's x and gamma, or K > 4096) or rows outnumber resident
-// waves, staging x * gamma in LDS per workgroup wins 3-8%: one row per wave
-// unless N > 16 x CUs with RMSNorm or K > 4096 without (2 rows share each LDS
-// read). fp32 weights stay on the register kernel (2 rows per wave with
-// RMSNorm), where the LDS variant measured slower.
+// waves, staging x * gamma in LDS wins: one row per wave, workgroups of 16
+// waves (x staged once per 16 rows; 6-16% faster than 4-wave workgroups at
+// 4096 x 4096 with RMSNorm, 11008 x 4096, 12288 x 4096 and 4096 x 11008),
+// 4 loads per row in flight, 16 when K > 4096. fp32 weights stay on the
+// register kernel (2 rows per wave with RMSNorm), where the LDS variant
+// measured slower.
 template <typename WT, bool RMS>
 void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
   constexpr int VMAX = 16 / static_cast<int>(sizeof(WT));
@@ -153,12 +158,11 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     const long long padded = (a.K + kPiece - 1) / kPiece * kPiece;
     const bool fits = padded * 4 <= kMaxLds;
     if (fits && (RMS || a.N > one_round || a.K > 4096)) {
-      const bool two = RMS ? a.N > one_round : a.K > 4096;
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
-      if (two) {
-        launch_rows_lds<WT, 2, RMS>(a, lds, stream);
+      if (a.K > 4096) {
+        launch_rows_lds<WT, 1, 16, RMS, 16>(a, lds, stream);
       } else {
-        launch_rows_lds<WT, 1, RMS>(a, lds, stream);
+        launch_rows_lds<WT, 1, 4, RMS, 16>(a, lds, stream);
       }
       return;
     }
@@ -228,16 +232,22 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream) {
 
 namespace {
 
-// One round of resident workgroups (LDS-limited: 160 KiB per CU), each
-// looping over blocks of 4 R rows.
-template <typename WT, int R, int MX, bool RMS>
+// One round of resident workgroups, each looping over blocks of WAVES x R
+// rows. fp16 weights: workgroups of 16 waves, one row per wave, one
+// workgroup per CU when the staged rows take more than 32 KiB of LDS, else
+// two (4 rows at 11008 x 4096: 20.6 us against 28.1 us for 4-wave
+// workgroups, two per CU). fp32 weights: 4-wave workgroups, as many per CU as
+// the LDS holds (up to 4).
+template <typename WT, int R, int MX, bool RMS, int WAVES>
 void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t stream) {
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
-  const long long blocks = ((a.N + R - 1) / R + 3) / 4;
-  const long long per_cu = std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
+  const long long blocks = ((a.N + R - 1) / R + WAVES - 1) / WAVES;
+  const long long per_cu =
+      WAVES == 16 ? (lds_bytes <= 32 * 1024 ? 2 : 1)
+                  : std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
   const long long wgs = std::min(blocks, per_cu * device_cu_count());
-  gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS>
-      <<<static_cast<unsigned>(wgs), 256, lds_bytes, stream>>>(
+  gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>
+      <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
           static_cast<float*>(a.y), a.N, a.K, a.eps);
   ENG_LAUNCH_CHECK();
@@ -245,13 +255,21 @@ void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t str
 
 template <typename WT, bool RMS>
 void rows_multi(const GemvArgs& a, int mx, std::size_t lds, bool two, hipStream_t stream) {
+  if constexpr (sizeof(WT) == 2) {
+    switch (mx) {
+      case 2: launch_rows_multi<WT, 1, 2, RMS, 16>(a, lds, stream); break;
+      case 3: launch_rows_multi<WT, 1, 3, RMS, 16>(a, lds, stream); break;
+      default: launch_rows_multi<WT, 1, 4, RMS, 16>(a, lds, stream); break;
+    }
+    return;
+  }
   switch (mx * 2 + (two ? 1 : 0)) {
-    case 4: launch_rows_multi<WT, 1, 2, RMS>(a, lds, stream); break;
-    case 5: launch_rows_multi<WT, 2, 2, RMS>(a, lds, stream); break;
-    case 6: launch_rows_multi<WT, 1, 3, RMS>(a, lds, stream); break;
-    case 7: launch_rows_multi<WT, 2, 3, RMS>(a, lds, stream); break;
-    case 8: launch_rows_multi<WT, 1, 4, RMS>(a, lds, stream); break;
-    default: launch_rows_multi<WT, 2, 4, RMS>(a, lds, stream); break;
+    case 4: launch_rows_multi<WT, 1, 2, RMS, 4>(a, lds, stream); break;
+    case 5: launch_rows_multi<WT, 2, 2, RMS, 4>(a, lds, stream); break;
+    case 6: launch_rows_multi<WT, 1, 3, RMS, 4>(a, lds, stream); break;
+    case 7: launch_rows_multi<WT, 2, 3, RMS, 4>(a, lds, stream); break;
+    case 8: launch_rows_multi<WT, 1, 4, RMS, 4>(a, lds, stream); break;
+    default: launch_rows_multi<WT, 2, 4, RMS, 4>(a, lds, stream); break;
   }
 }
 

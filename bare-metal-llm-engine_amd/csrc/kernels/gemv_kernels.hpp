@@ -13,7 +13,8 @@
 //     renumbered so each XCD walks a contiguous band of slabs, and slabs narrower
 //     than a 128-byte line share their lines inside one XCD's L2.
 // Sums are folded across lane groups with cross-lane shuffles and across waves
-// through LDS, always in the same order. Partial mode writes fp32 partial
+// through LDS, always in the same order (the output-major kernels below fold
+// whole waves with wave_sum). Partial mode writes fp32 partial
 // sums (and per-chunk sums of squares) that gemv_reduce_kernel combines in
 // chunk order, so results never depend on scheduling and no workgroup waits
 // on another.
@@ -53,6 +54,33 @@ __device__ __forceinline__ float lane_elem(const V& v, int e) {
   } else {
     return static_cast<float>(v[e]);
   }
+}
+
+// x + (x of the lane that DPP control CTRL selects).
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false);
+  return x + __builtin_bit_cast(float, y);
+}
+
+// Sum over the 64 lanes of a wave, in one fixed order, returned in every
+// lane: DPP quad_perm xor-1 and xor-2, row_half_mirror (lane i <- 7 - i within
+// 8 lanes) and row_mirror (i <- 15 - i) leave each 16-lane row's sum in all of
+// its lanes (a + b == b + a, so both lanes of a pair hold the same bits); the
+// four row sums, read from lanes 0, 16, 32 and 48, are added as
+// (r0 + r1) + (r2 + r3). Four VALU adds and four lane reads, where a shuffle
+// tree costs six LDS-crossbar round trips.
+__device__ __forceinline__ float wave_sum(float x) {
+  x = dpp_add<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = dpp_add<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = dpp_add<0x141>(x);  // row_half_mirror
+  x = dpp_add<0x140>(x);  // row_mirror
+  const int b = __builtin_bit_cast(int, x);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ float rms_scale(float sumsq, long long K, float eps) {
@@ -270,7 +298,7 @@ __global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restric
 // consecutive output rows; lane l reads 16-byte pieces l, l + 64, ... of each
 // row (a wave load instruction is 1 KiB contiguous per row) together with the
 // matching x values, keeps U steps of loads in flight, and folds its lanes
-// with shuffles at the end. No partial sums leave the wave. With RMS the wave
+// with wave_sum at the end. No partial sums leave the wave. With RMS the wave
 // also sums x^2 over the x values it reads anyway.
 template <typename WT, int VEC, int R, int U, bool RMS>
 __global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W,
@@ -349,11 +377,8 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(const WT* __restrict__ W
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] += __shfl_xor(acc[r], off);
-    if constexpr (RMS) ss += __shfl_xor(ss, off);
-  }
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+  if constexpr (RMS) ss = wave_sum(ss);
   if (lane == 0) {
     const float scale = RMS ? rms_scale(ss, K, eps) : 1.0f;
 #pragma unroll
@@ -379,48 +404,75 @@ __device__ __forceinline__ int lds_slot(int k) {
   return p * PIECE + (e >> 2) * 256 + l * 4 + (e & 3);
 }
 
-// Workgroup-cooperative staging for the LDS kernels (256 threads): writes
-// xs = x * gamma (gamma optional, applied only with RMS) into LDS slots,
-// zero-padded to whole pieces, sums x^2 across the workgroup (RMS) into
-// *total_ss, and ends with a barrier. K % 4 == 0 and 16-byte aligned x /
-// gamma are required. The sum is folded in a fixed order (lanes by shuffle,
-// then waves 0..3), so every workgroup computes the same value.
-template <int VEC, bool RMS>
+// Workgroup-cooperative staging for the LDS kernels (THREADS threads):
+// writes xs = x * gamma (gamma optional, applied only with RMS) into LDS
+// slots, zero-padded to whole pieces, sums x^2 (RMS) into *total_ss, and ends
+// with a barrier. K % 4 == 0 and 16-byte aligned x / gamma are required.
+// The sum has one fixed order for every workgroup size: 1024 virtual threads,
+// v taking the 16-byte chunks v, v + 1024, v + 2048, ... in turn; each virtual
+// wave (64 consecutive v) folded by shuffles; the 16 virtual-wave sums added
+// in order. A workgroup of THREADS threads plays virtual threads tid,
+// tid + THREADS, ..., so kernels with different workgroup sizes (and the
+// small-batch kernels, which stage row by row) compute the same bits.
+// wave_ss holds kStageWaves floats of shared memory.
+constexpr int kStageWaves = 16;
+
+template <int VEC, bool RMS, int THREADS = 256>
 __device__ __forceinline__ void stage_xs(const float* __restrict__ x,
                                          const float* __restrict__ gamma, long long K,
                                          int npieces, float* xs, float* wave_ss,
                                          float* total_ss) {
+  static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "4, 8 or 16 waves");
   using F4 = typename RawVec<float, 4>::type;
   constexpr int PIECE = 64 * VEC;
+  constexpr int VT = kStageWaves * 64;  // virtual threads
+  constexpr int JV = VT / THREADS;      // virtual threads per thread
   const int tid = threadIdx.x;
-  float ss = 0.0f;
+  float ss[JV];
+#pragma unroll
+  for (int j = 0; j < JV; ++j) ss[j] = 0.0f;
   const int padded = npieces * PIECE;
-  for (int k = tid * 4; k < padded; k += 1024) {
-    F4 v = F4{};
-    if (k < K) {
-      v = *reinterpret_cast<const F4*>(x + k);
-      if constexpr (RMS) {
-        ss = fmaf(v[0], v[0], ss);
-        ss = fmaf(v[1], v[1], ss);
-        ss = fmaf(v[2], v[2], ss);
-        ss = fmaf(v[3], v[3], ss);
-        if (gamma != nullptr) v *= *reinterpret_cast<const F4*>(gamma + k);
+  for (int base = 0; base < padded; base += VT * 4) {
+#pragma unroll
+    for (int j = 0; j < JV; ++j) {
+      const int k = base + (tid + j * THREADS) * 4;
+      if (k < padded) {
+        F4 v = F4{};
+        if (k < K) {
+          v = *reinterpret_cast<const F4*>(x + k);
+          if constexpr (RMS) {
+            ss[j] = fmaf(v[0], v[0], ss[j]);
+            ss[j] = fmaf(v[1], v[1], ss[j]);
+            ss[j] = fmaf(v[2], v[2], ss[j]);
+            ss[j] = fmaf(v[3], v[3], ss[j]);
+            if (gamma != nullptr) v *= *reinterpret_cast<const F4*>(gamma + k);
+          }
+        }
+        *reinterpret_cast<F4*>(xs + lds_slot<VEC>(k)) = v;
       }
     }
-    *reinterpret_cast<F4*>(xs + lds_slot<VEC>(k)) = v;
   }
   if constexpr (RMS) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((tid & 63) == 0) wave_ss[tid >> 6] = ss;
+    for (int j = 0; j < JV; ++j) {
+      const float w = wave_sum(ss[j]);
+      if ((tid & 63) == 0) wave_ss[(tid >> 6) + j * (THREADS / 64)] = w;
+    }
   }
   __syncthreads();
-  if constexpr (RMS) *total_ss = ((wave_ss[0] + wave_ss[1]) + wave_ss[2]) + wave_ss[3];
+  if constexpr (RMS) {
+    float t = wave_ss[0];
+#pragma unroll
+    for (int w = 1; w < kStageWaves; ++w) t += wave_ss[w];
+    *total_ss = t;
+  }
 }
 
-// acc[j] = sum_k rows[j][k] * xs[k] over this lane's elements (the caller
-// folds the lanes): NR weight rows streamed with 16-byte nontemporal loads,
-// U loads per row in flight, against the staged vector in LDS.
+// acc[j] = sum_k rows[j][k] * xs[k]: each lane sums its elements, then
+// wave_sum folds the lanes (the result is in every lane). NR weight rows
+// streamed with 16-byte nontemporal loads, U loads per row in flight, against
+// the staged vector in LDS. Each lane's order is gemv_rows_kernel's, so the
+// register and LDS kernels agree bit for bit without RMSNorm.
 template <typename WT, int VEC, int NR, int U>
 __device__ __forceinline__ void dot_rows_lds(const WT* const (&rows)[NR], const float* xs,
                                              long long K, int npieces, int lane,
@@ -459,10 +511,7 @@ __device__ __forceinline__ void dot_rows_lds(const WT* const (&rows)[NR], const 
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-#pragma unroll
-    for (int j = 0; j < NR; ++j) acc[j] += __shfl_xor(acc[j], off);
-  }
+  for (int j = 0; j < NR; ++j) acc[j] = wave_sum(acc[j]);
 }
 
 // Output-major GEMV with the activation vector staged once per workgroup.
@@ -472,10 +521,13 @@ __device__ __forceinline__ void dot_rows_lds(const WT* const (&rows)[NR], const 
 // (stage_xs), then each wave streams its R rows against LDS, U loads per row
 // in flight (dot_rows_lds). (Issuing weight loads ahead of the staging
 // measured slower: vector loads complete in order, so the staging then waits
-// for HBM.) Requires K % VEC == 0 and 16-byte aligned W, x and gamma; the
-// caller sizes dynamic LDS as round_up(K, 64 * VEC) floats.
-template <typename WT, int VEC, int R, int U, bool RMS>
-__global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict__ W,
+// for HBM.) Workgroups of WAVES waves: 16 (one workgroup of 1024 threads per
+// 16 rows) stages x once per 16 rows instead of once per 4 and lets the LDS
+// budget hold twice the resident waves. Requires K % VEC == 0 and 16-byte
+// aligned W, x and gamma; the caller sizes dynamic LDS as round_up(K, 64 *
+// VEC) floats.
+template <typename WT, int VEC, int R, int U, bool RMS, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __restrict__ W,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ gamma,
                                                             float* __restrict__ y, long long N,
@@ -483,14 +535,14 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_kernel(const WT* __restrict
   static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
   constexpr int PIECE = 64 * VEC;
   extern __shared__ float xs[];
-  __shared__ float wave_ss[4];
+  __shared__ float wave_ss[kStageWaves];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
+  const long long n0 = (static_cast<long long>(blockIdx.x) * WAVES + wave) * R;
   const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
 
   float total_ss = 0.0f;
-  stage_xs<VEC, RMS>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
+  stage_xs<VEC, RMS, WAVES * 64>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
   if (n0 >= N) return;
 
   const WT* rows[R];
@@ -556,12 +608,9 @@ __device__ __forceinline__ void dot_rows_lds_multi(const WT* const (&rows)[NR], 
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
+  for (int m = 0; m < MX; ++m)
 #pragma unroll
-    for (int m = 0; m < MX; ++m)
-#pragma unroll
-      for (int j = 0; j < NR; ++j) acc[m][j] += __shfl_xor(acc[m][j], off);
-  }
+    for (int j = 0; j < NR; ++j) acc[m][j] = wave_sum(acc[m][j]);
 }
 
 // Output-major GEMV over MX activation rows at once (small-batch decode):
@@ -570,13 +619,13 @@ __device__ __forceinline__ void dot_rows_lds_multi(const WT* const (&rows)[NR], 
 // x * gamma in LDS (MX x round_up(K, 64 * VEC) floats, sized by the caller)
 // with their sums of squares, then its waves stream weight rows against all
 // of them -- one pass over W serves MX outputs per row -- taking blocks of
-// 4 R rows in turn (block b, b + gridDim.x, ...), so the staging, MX times a
+// WAVES x R rows in turn (block b, b + gridDim.x, ...), so the staging, MX times a
 // single row's, is paid once per resident workgroup rather than once per
 // block. Per row the arithmetic is gemv_rows_lds_kernel's (same staging, same
 // order), so each y[m] equals a single-row call on x[m] bit for bit. Same
 // requirements as gemv_rows_lds_kernel.
-template <typename WT, int VEC, int R, int U, int MX, bool RMS>
-__global__ __launch_bounds__(256) void gemv_rows_lds_multi_kernel(const WT* __restrict__ W,
+template <typename WT, int VEC, int R, int U, int MX, bool RMS, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_multi_kernel(const WT* __restrict__ W,
                                                                   const float* __restrict__ x,
                                                                   const float* __restrict__ gamma,
                                                                   float* __restrict__ y,
@@ -586,7 +635,7 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_multi_kernel(const WT* __re
   static_assert(MX >= 2 && MX <= 4, "2 to 4 activation rows");
   constexpr int PIECE = 64 * VEC;
   extern __shared__ float xs[];
-  __shared__ float wave_ss[MX][4];
+  __shared__ float wave_ss[MX][kStageWaves];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
@@ -595,13 +644,14 @@ __global__ __launch_bounds__(256) void gemv_rows_lds_multi_kernel(const WT* __re
   float total_ss[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m)
-    stage_xs<VEC, RMS>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m], &total_ss[m]);
+    stage_xs<VEC, RMS, WAVES * 64>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m],
+                                   &total_ss[m]);
   float scale[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
 
-  const long long step = static_cast<long long>(gridDim.x) * 4 * R;
-  for (long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R; n0 < N; n0 += step) {
+  const long long step = static_cast<long long>(gridDim.x) * WAVES * R;
+  for (long long n0 = (static_cast<long long>(blockIdx.x) * WAVES + wave) * R; n0 < N; n0 += step) {
     const WT* rows[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) rows[r] = W + (n0 + r < N ? n0 + r : n0) * K;
@@ -632,9 +682,10 @@ __device__ __forceinline__ float swiglu_f32(float g, float u) {
 // The staged vector is shared by both projections; each wave streams the
 // gate and up rows of its R outputs together (2R weight streams), so the
 // intermediate gate / up vectors never reach memory and the FFN saves a
-// launch. Same requirements as gemv_rows_lds_kernel.
-template <typename WT, int VEC, int R, int U, bool RMS>
-__global__ __launch_bounds__(256) void gemv_rows_glu_kernel(const WT* __restrict__ Wg,
+// launch. Workgroups of WAVES waves, as in gemv_rows_lds_kernel. Same
+// requirements as gemv_rows_lds_kernel.
+template <typename WT, int VEC, int R, int U, bool RMS, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_glu_kernel(const WT* __restrict__ Wg,
                                                             const WT* __restrict__ Wu,
                                                             const float* __restrict__ x,
                                                             const float* __restrict__ gamma,
@@ -643,14 +694,14 @@ __global__ __launch_bounds__(256) void gemv_rows_glu_kernel(const WT* __restrict
   static_assert(VEC == 4 || VEC == 8, "16-byte weight loads");
   constexpr int PIECE = 64 * VEC;
   extern __shared__ float xs[];
-  __shared__ float wave_ss[4];
+  __shared__ float wave_ss[kStageWaves];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const long long n0 = (static_cast<long long>(blockIdx.x) * 4 + wave) * R;
+  const long long n0 = (static_cast<long long>(blockIdx.x) * WAVES + wave) * R;
   const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
 
   float total_ss = 0.0f;
-  stage_xs<VEC, RMS>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
+  stage_xs<VEC, RMS, WAVES * 64>(x, gamma, K, npieces, xs, wave_ss, &total_ss);
   if (n0 >= N) return;
 
   const WT* rows[2 * R];
@@ -674,11 +725,11 @@ __global__ __launch_bounds__(256) void gemv_rows_glu_kernel(const WT* __restrict
 // Small-batch form of gemv_rows_glu_kernel: MX activation rows (x pitch K,
 // act pitch N) share each pass over Wg and Wu. The rows are staged once per
 // workgroup and the workgroups (one round of residents) loop over blocks of
-// 4 outputs, as in gemv_rows_lds_multi_kernel; each wave streams one
+// WAVES outputs, as in gemv_rows_lds_multi_kernel; each wave streams one
 // output's gate and up rows. Per row the arithmetic is the single-row fused
 // kernel's, so act[m] equals an M = 1 call bit for bit.
-template <typename WT, int VEC, int U, int MX, bool RMS>
-__global__ __launch_bounds__(256) void gemv_rows_glu_multi_kernel(
+template <typename WT, int VEC, int U, int MX, bool RMS, int WAVES = 4>
+__global__ __launch_bounds__(WAVES * 64) void gemv_rows_glu_multi_kernel(
     const WT* __restrict__ Wg, const WT* __restrict__ Wu, const float* __restrict__ x,
     const float* __restrict__ gamma, float* __restrict__ act, long long N, long long K,
     float eps) {
@@ -686,7 +737,7 @@ __global__ __launch_bounds__(256) void gemv_rows_glu_multi_kernel(
   static_assert(MX >= 2 && MX <= 4, "2 to 4 activation rows");
   constexpr int PIECE = 64 * VEC;
   extern __shared__ float xs[];
-  __shared__ float wave_ss[MX][4];
+  __shared__ float wave_ss[MX][kStageWaves];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int npieces = static_cast<int>((K + PIECE - 1) / PIECE);
@@ -695,13 +746,14 @@ __global__ __launch_bounds__(256) void gemv_rows_glu_multi_kernel(
   float total_ss[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m)
-    stage_xs<VEC, RMS>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m], &total_ss[m]);
+    stage_xs<VEC, RMS, WAVES * 64>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m],
+                                   &total_ss[m]);
   float scale[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
 
-  const long long step = static_cast<long long>(gridDim.x) * 4;
-  for (long long n = static_cast<long long>(blockIdx.x) * 4 + wave; n < N; n += step) {
+  const long long step = static_cast<long long>(gridDim.x) * WAVES;
+  for (long long n = static_cast<long long>(blockIdx.x) * WAVES + wave; n < N; n += step) {
     const WT* rows[2] = {Wg + n * K, Wu + n * K};
     float acc[MX][2];
     dot_rows_lds_multi<WT, VEC, 2, U, MX>(rows, xs, pitch, K, npieces, lane, acc);
