@@ -515,11 +515,11 @@ def test_gemv_nk_shapes_against_oracle(gpu, orc, N, K, dtype):
     (5, 8, True, True),          # K below one 512-element piece
     (333, 1000, True, True),     # ragged last piece, N not a multiple of 4 rows
     (333, 1000, True, False),    # null gain
-    (4099, 520, True, True),     # N beyond one resident round: 2 rows per wave, odd N
+    (4099, 520, True, True),     # N beyond one resident round, odd N: last 16-wave workgroup partly idle
     (64, 16384, True, True),     # largest K whose staged vector fits 64 KiB of LDS
     (64, 16392, True, True),     # just past it: register kernel fallback
-    (300, 8200, False, False),   # K > 4096 without RMSNorm: 2 rows per wave
-    (5000, 1000, False, False),  # many rows, small K: 1 row per wave
+    (300, 8200, False, False),   # K > 4096 without RMSNorm: LDS-staged, 16 loads per row in flight
+    (5000, 1000, False, False),  # many rows, small K: LDS-staged, 4 loads per row in flight
     (64, 20000, False, False),   # LDS does not fit: register kernel, 4 loads in flight
 ])
 def test_nk_fp16_kernel_selection_against_oracle(gpu, orc, N, K, rms, gamma):
