@@ -85,7 +85,7 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
           W, x, a.gamma, y, N, K, kchunk, ncb, partials, partial_ss, a.eps);
   ENG_LAUNCH_CHECK();
   gemv_reduce_kernel<YT, RMS>
-      <<<dim3(static_cast<unsigned>((N + 63) / 64), MX), 256, 0, stream>>>(
+      <<<dim3(static_cast<unsigned>((N + 63) / 64), MX), gemv::kReduceWaves * 64, 0, stream>>>(
           partials, partial_ss, y, N, K, static_cast<int>(nsplit), a.eps, MX);
   ENG_LAUNCH_CHECK();
 }

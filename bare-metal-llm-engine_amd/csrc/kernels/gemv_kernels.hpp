@@ -247,49 +247,59 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
   }
 }
 
-// y[col] = scale * sum_{s < nsplit} part[s][col]. A workgroup owns 64 columns;
-// its 4 waves each sum a contiguous quarter of the splits in split order (8
-// independent loads in flight per lane), and the quarters are combined as
-// ((q0 + q1) + q2) + q3, so the association is fixed for a given nsplit.
-// blockIdx.y selects the activation row m of an mx-row launch (partials
-// [nsplit][mx][N], output row m at y + m N).
-template <typename YT, bool RMS>
-__global__ __launch_bounds__(256) void gemv_reduce_kernel(const float* __restrict__ part,
-                                                          const float* __restrict__ part_ss,
-                                                          YT* __restrict__ y, long long N,
-                                                          long long K, int nsplit, float eps,
-                                                          int mx) {
-  __shared__ float quarter[4][64];
+// y[col] = scale * sum_{s < nsplit} part[s][col]. A workgroup of
+// kReduceWaves waves owns 64 columns; wave g sums the contiguous group of
+// splits [g * per, (g + 1) * per) in split order with 8 loads in flight per
+// lane (loads past the group re-read its last partial and add 0), and the
+// group sums are added in group order, so the association is fixed for a
+// given nsplit. Up to 64 splits take one round trip per lane (8 waves
+// measured best: 4 or 16 were up to 0.4 us slower at 4096 x 4096 and
+// 11008 x 4096). blockIdx.y selects the activation row m of an mx-row launch
+// (partials [nsplit][mx][N], output row m at y + m N).
+constexpr int kReduceWaves = 8;
+
+template <typename YT, bool RMS, int WAVES = kReduceWaves>
+__global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
+    const float* __restrict__ part, const float* __restrict__ part_ss, YT* __restrict__ y,
+    long long N, long long K, int nsplit, float eps, int mx) {
+  __shared__ float group_sum[WAVES][64];
   const int c = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
   const int m = blockIdx.y;
   const long long col = static_cast<long long>(blockIdx.x) * 64 + c;
-  const int per = (nsplit + 3) / 4;
-  const int s0 = g * per;
+  const long long cc = col < N ? col : N - 1;  // columns past N read column N - 1, never stored
+  const int per = (nsplit + WAVES - 1) / WAVES;
+  const int s0 = g * per < nsplit ? g * per : nsplit;
   const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
-  const float* pm = part + static_cast<long long>(m) * N;
+  const float* pm = part + static_cast<long long>(m) * N + cc;
   const long long stride = static_cast<long long>(mx) * N;
   float v = 0.0f;
-  if (col < N) {
-    int s = s0;
-    for (; s + 8 <= s1; s += 8) {
-      float t[8];
+  for (int s = s0; s < s1; s += 8) {
+    float t[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) t[i] = pm[static_cast<long long>(s + i) * stride + col];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) v += t[i];
+    for (int i = 0; i < 8; ++i) {
+      const int si = s + i < s1 ? s + i : s1 - 1;
+      t[i] = pm[static_cast<long long>(si) * stride];
     }
-    for (; s < s1; ++s) v += pm[static_cast<long long>(s) * stride + col];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v += s + i < s1 ? t[i] : 0.0f;
   }
-  quarter[g][c] = v;
+  group_sum[g][c] = v;
+  // Sum of squares over the splits: lane c of wave 0 takes splits c, c + 64,
+  // ... in turn, then the lanes are folded (one fixed order per nsplit).
+  float tot = 0.0f;
+  if constexpr (RMS) {
+    if (g == 0) {
+      for (int s = c; s < nsplit; s += 64) tot += part_ss[s * mx + m];
+      tot = wave_sum(tot);
+    }
+  }
   __syncthreads();
   if (g != 0 || col >= N) return;
-  float out = ((quarter[0][c] + quarter[1][c]) + quarter[2][c]) + quarter[3][c];
-  if constexpr (RMS) {
-    float tot = 0.0f;
-    for (int s = 0; s < nsplit; ++s) tot += part_ss[s * mx + m];
-    out *= rms_scale(tot, K, eps);
-  }
+  float out = group_sum[0][c];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) out += group_sum[w][c];
+  if constexpr (RMS) out *= rms_scale(tot, K, eps);
   y[static_cast<long long>(m) * N + col] = from_f32<YT>(out);
 }
 
