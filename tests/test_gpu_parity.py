@@ -254,6 +254,27 @@ def test_gemv_shapes_against_oracle(gpu, orc, N, K, dtype):
         helpers.assert_within(got, y, derived + helpers.U16 * np.abs(y) + 2.0**-25, f"gemv_fp16 {N}x{K}")
 
 
+@pytest.mark.parametrize("N,K,dtype", [(64, 16384, "f16w"), (300, 16384, "f32"), (4100, 4096, "f16w"),
+                                       (11008, 96, "f16w")])
+def test_rmsnorm_linear_split_k_reduce_regimes(gpu, orc, N, K, dtype):
+    # Reference-layout decode: the split count ranges from 256 (N = 64: every
+    # reduce wave sums four groups of 8 partials, wave 0 folds four sums of
+    # squares per lane) down to 2 (K = 96); rows of a 3-row batch equal the
+    # single-row calls bit for bit whatever the split count.
+    rng = np.random.default_rng(N + 5 * K)
+    x = rng.standard_normal((3, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    if dtype == "f16w":
+        W = orc.f32_to_f16(W)
+    one = gpu_rmsnorm_linear(gpu, x[:1], g, W)
+    y = orc.rmsnorm_linear(x[:1], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(one, y, x[:1], g, W, K, f"rmsnorm_linear kn {N}x{K} {dtype}")
+    three = gpu_rmsnorm_linear(gpu, x, g, W)
+    for m in range(3):
+        assert np.array_equal(three[m], gpu_rmsnorm_linear(gpu, x[m:m + 1], g, W)[0]), f"row {m}"
+
+
 def test_misaligned_pointers_take_the_scalar_path(gpu, orc):
     """A weight pointer off 16-byte alignment must still give the right answer."""
     rng = np.random.default_rng(12)
