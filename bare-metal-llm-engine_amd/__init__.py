@@ -117,6 +117,8 @@ SIGNATURES = {
     "eng_swiglu_f16": [_p, _p, _p, _i64, _p],
     "eng_rmsnorm_linear_swiglu_f16w_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_swiglu_f32_nk": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_rmsnorm_linear_swiglu_f16w": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_rmsnorm_linear_swiglu_f32": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_attention_decode_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, ctypes.c_int, _p],
     "eng_attention_decode_with_mode_f16": [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f,
                                            ctypes.c_int, ctypes.c_int, _p],

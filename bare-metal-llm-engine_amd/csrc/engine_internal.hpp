@@ -78,11 +78,15 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 // kernel pairs on it; take it before the first launch that writes the arena
 // and keep it past the last one that reads it. The arena grows to the largest
 // request (growth waits for the stream, then reallocates) and is freed when
-// the stream is destroyed through eng_stream_destroy, or at exit. A launcher
-// takes at most one lease at a time.
+// the stream is destroyed through eng_stream_destroy, or at exit. Each
+// (device, stream) has one arena per level: a launcher takes at most one lease
+// per level, and a composite launcher that keeps a lease while it calls other
+// launchers (the FFN's gate / up buffers around the GEMV launches, which may
+// lease split-K partials) takes level 1, so the inner lease (level 0) never
+// waits on its own caller's lock.
 class StreamScratch {
  public:
-  StreamScratch(hipStream_t stream, std::size_t bytes);
+  StreamScratch(hipStream_t stream, std::size_t bytes, int level = 0);
   ~StreamScratch();
   StreamScratch(const StreamScratch&) = delete;
   StreamScratch& operator=(const StreamScratch&) = delete;

@@ -27,10 +27,15 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(unsigned char* __restric
 struct Key {
   int device;
   hipStream_t stream;
+  int level;
   bool operator<(const Key& o) const {
-    return device != o.device ? device < o.device : stream < o.stream;
+    if (device != o.device) return device < o.device;
+    if (stream != o.stream) return stream < o.stream;
+    return level < o.level;
   }
 };
+
+constexpr int kScratchLevels = 2;
 
 struct Arena {
   std::mutex mu;  // held by the live lease
@@ -58,13 +63,14 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
-StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes) {
+StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes, int level) {
+  ENG_CHECK(level >= 0 && level < kScratchLevels, "stream scratch: no such level");
   int dev = 0;
   ENG_HIP_CHECK(hipGetDevice(&dev));
   Arena* arena = nullptr;
   {
     std::lock_guard<std::mutex> lock(g_arenas_mu);
-    auto& slot = arenas()[Key{dev, stream}];
+    auto& slot = arenas()[Key{dev, stream, level}];
     if (!slot) slot = std::make_unique<Arena>();
     arena = slot.get();
   }
@@ -95,17 +101,19 @@ void release_stream_scratch(hipStream_t stream) {
     (void)hipGetLastError();
     return;
   }
-  std::unique_ptr<Arena> arena;
-  {
-    std::lock_guard<std::mutex> lock(g_arenas_mu);
-    auto& m = arenas();
-    auto it = m.find(Key{dev, stream});
-    if (it == m.end()) return;
-    arena = std::move(it->second);
-    m.erase(it);
+  for (int level = 0; level < kScratchLevels; ++level) {
+    std::unique_ptr<Arena> arena;
+    {
+      std::lock_guard<std::mutex> lock(g_arenas_mu);
+      auto& m = arenas();
+      auto it = m.find(Key{dev, stream, level});
+      if (it == m.end()) continue;
+      arena = std::move(it->second);
+      m.erase(it);
+    }
+    std::lock_guard<std::mutex> lock(arena->mu);  // no lease may be live
+    if (arena->base != nullptr) (void)hipFree(arena->base);
   }
-  std::lock_guard<std::mutex> lock(arena->mu);  // no lease may be live
-  if (arena->base != nullptr) (void)hipFree(arena->base);
 }
 
 }  // namespace eng

@@ -1,19 +1,25 @@
 // ffn.hip -- fused RMSNorm + gate / up projections + SwiGLU, the first half of
-// a Llama FFN, with output-major weights Wg, Wu [N x K]:
-//   act[r][n] = SiLU(xn[r] . Wg[n]) * (xn[r] . Wu[n]),  xn = RMSNorm(in) * gamma.
+// a Llama FFN:
+//   act[r][n] = SiLU(xn[r] . Wg[:, n]) * (xn[r] . Wu[:, n]),  xn = RMSNorm(in) * gamma,
+// with weights in the reference layout Wg, Wu [K x N] or output-major [N x K].
 // The reference composes this from rmsnorm, two GEMVs / GEMMs and swiglu
 // (tests/test_kernels.cu:2867-2898; its ADR 0006 defers fusing gate / up /
-// SwiGLU on one weight stream). Decode (M == 1, 16-byte aligned operands, K
-// up to 16384) runs gemv_rows_glu_kernel: one launch that stages x * gamma in
-// LDS, streams each output's gate and up rows together and applies SiLU in the
-// epilogue, so gate and up never reach memory. Other decode rows compute gate
-// and up with the fused RMSNorm + GEMV kernels. A few rows (small-batch
-// decode) run gemv_rows_glu_multi_kernel: up to 4 rows per pass over Wg and
-// Wu, SwiGLU applied in the epilogue, each row equal to its M = 1 result;
-// otherwise a few rows compute gate and up with the multi-row GEMV passes,
-// and more rows normalise once and run the MFMA GEMM for gate and for up, in
-// the stream's scratch arena, and the SwiGLU kernel finishes. Preconditions and
-// messages follow rmsnorm_linear; any zero dimension writes nothing.
+// SwiGLU on one weight stream).
+//   * Output-major decode (M == 1, 16-byte aligned operands, K up to 16384)
+//     runs gemv_rows_glu_kernel: one launch that stages x * gamma in LDS,
+//     streams each output's gate and up rows together and applies SiLU in the
+//     epilogue, so gate and up never reach memory. A few rows (small-batch
+//     decode) run gemv_rows_glu_multi_kernel: up to 4 rows per pass over Wg
+//     and Wu, each row equal to its M = 1 result.
+//   * Reference-layout decode (M == 1, N a multiple of the 16-byte vector,
+//     aligned weights) runs the split-K stream kernel over both matrices in
+//     one launch and the reduce with the SwiGLU epilogue (launch_gemv_kn_glu):
+//     two launches where the composition takes five, and the same bits.
+//   * Otherwise gate and up are computed separately into the stream's scratch
+//     arena -- single-row GEMVs, small-batch passes over W, or (more rows)
+//     RMSNorm once and the MFMA GEMM -- and the SwiGLU kernel finishes.
+// Preconditions and messages follow rmsnorm_linear; any zero dimension
+// writes nothing.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
@@ -24,9 +30,9 @@ namespace eng {
 namespace {
 
 template <typename WT>
-void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg, const WT* Wu,
-                              float* act, int64_t M, int64_t N, int64_t K, float eps,
-                              Elem elem, eng_stream stream) {
+void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, const WT* Wu,
+                           float* act, int64_t M, int64_t N, int64_t K, float eps, Elem elem,
+                           bool nk, eng_stream stream) {
   ENG_CHECK(M >= 0 && N >= 0 && K >= 0, "rmsnorm_linear_swiglu: negative dimension");
   ENG_CHECK(in != nullptr && Wg != nullptr && Wu != nullptr && act != nullptr,
             "rmsnorm_linear_swiglu: null device pointer");
@@ -38,7 +44,21 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
   constexpr long long kPiece = 64 * VEC;
   constexpr long long kMaxLds = 64 * 1024;
   const long long padded = (K + kPiece - 1) / kPiece * kPiece;
-  const bool fused = M == 1 && K % VEC == 0 && padded * 4 <= kMaxLds && aligned_to(Wg, 16) &&
+  if (!nk && M == 1) {
+    // Reference layout: one stream launch over Wg and Wu, SwiGLU in the reduce.
+    GemvArgs gv;
+    gv.W = Wg;
+    gv.w = elem;
+    gv.x = in;
+    gv.gamma = gamma;
+    gv.y = act;
+    gv.N = N;
+    gv.K = K;
+    gv.rms = true;
+    gv.eps = eps;
+    if (launch_gemv_kn_glu(gv, Wu, s)) return;
+  }
+  const bool fused = nk && M == 1 && K % VEC == 0 && padded * 4 <= kMaxLds && aligned_to(Wg, 16) &&
                      aligned_to(Wu, 16) && aligned_to(in, 16) &&
                      (gamma == nullptr || aligned_to(gamma, 16));
   if (fused) {
@@ -55,7 +75,7 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
   }
   // Small batch: up to 4 rows per pass over Wg and Wu, at most 4 passes.
   const long long fit = std::min<long long>(4, kMaxLds / (padded * 4));
-  const bool multi = M > 1 && fit >= 2 && (M + fit - 1) / fit <= 4 && K % VEC == 0 &&
+  const bool multi = nk && M > 1 && fit >= 2 && (M + fit - 1) / fit <= 4 && K % VEC == 0 &&
                      aligned_to(Wg, 16) && aligned_to(Wu, 16) && aligned_to(in, 16) &&
                      (gamma == nullptr || aligned_to(gamma, 16));
   if (multi) {
@@ -98,7 +118,8 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
   const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
-  StreamScratch scratch(s, (mk + 2 * mn) * sizeof(float));
+  // Level 1: the GEMV launches below may lease split-K partials (level 0).
+  StreamScratch scratch(s, (mk + 2 * mn) * sizeof(float), 1);
   float* xn = static_cast<float*>(scratch.get());  // first: the GEMM wants it 16-byte aligned
   float* gate = xn + mk;
   float* up = gate + mn;
@@ -109,7 +130,7 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
     GemvArgs gv;
     gv.W = W;
     gv.w = elem;
-    gv.w_nk = true;
+    gv.w_nk = nk;
     gv.x = in;
     gv.gamma = gamma;
     gv.y = out;
@@ -119,7 +140,8 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
     gv.eps = eps;
     if (M == 1) {
       launch_gemv(gv, s);
-    } else if (!launch_gemv_nk_rows(gv, M, s)) {  // a few rows: passes over W
+    } else if (!(nk ? launch_gemv_nk_rows(gv, M, s) : launch_gemv_kn_rows(gv, M, s))) {
+      // more than a few rows: normalise once, then the MFMA GEMM
       if (!normed) {
         launch_rmsnorm(in, gamma, xn, M, K, eps, s);
         normed = true;
@@ -128,7 +150,7 @@ void rmsnorm_linear_swiglu_nk(const float* in, const float* gamma, const WT* Wg,
       g.A = xn;
       g.B = W;
       g.b = elem;
-      g.b_nk = true;
+      g.b_nk = nk;
       g.C = out;
       g.M = M;
       g.N = N;
@@ -149,9 +171,9 @@ int eng_rmsnorm_linear_swiglu_f16w_nk(const float* in, const float* rms_weight,
                                       int64_t M, int64_t N, int64_t K, float eps,
                                       eng_stream stream) {
   return eng::guarded([&] {
-    eng::rmsnorm_linear_swiglu_nk(in, rms_weight, reinterpret_cast<const _Float16*>(W_gate),
-                                  reinterpret_cast<const _Float16*>(W_up), act, M, N, K, eps,
-                                  eng::Elem::F16, stream);
+    eng::rmsnorm_linear_swiglu(in, rms_weight, reinterpret_cast<const _Float16*>(W_gate),
+                               reinterpret_cast<const _Float16*>(W_up), act, M, N, K, eps,
+                               eng::Elem::F16, true, stream);
   });
 }
 
@@ -160,8 +182,28 @@ int eng_rmsnorm_linear_swiglu_f32_nk(const float* in, const float* rms_weight,
                                      int64_t M, int64_t N, int64_t K, float eps,
                                      eng_stream stream) {
   return eng::guarded([&] {
-    eng::rmsnorm_linear_swiglu_nk(in, rms_weight, W_gate, W_up, act, M, N, K, eps,
-                                  eng::Elem::F32, stream);
+    eng::rmsnorm_linear_swiglu(in, rms_weight, W_gate, W_up, act, M, N, K, eps, eng::Elem::F32,
+                               true, stream);
+  });
+}
+
+int eng_rmsnorm_linear_swiglu_f16w(const float* in, const float* rms_weight,
+                                   const eng_half* W_gate, const eng_half* W_up, float* act,
+                                   int64_t M, int64_t N, int64_t K, float eps,
+                                   eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_swiglu(in, rms_weight, reinterpret_cast<const _Float16*>(W_gate),
+                               reinterpret_cast<const _Float16*>(W_up), act, M, N, K, eps,
+                               eng::Elem::F16, false, stream);
+  });
+}
+
+int eng_rmsnorm_linear_swiglu_f32(const float* in, const float* rms_weight,
+                                  const float* W_gate, const float* W_up, float* act, int64_t M,
+                                  int64_t N, int64_t K, float eps, eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_swiglu(in, rms_weight, W_gate, W_up, act, M, N, K, eps, eng::Elem::F32,
+                               false, stream);
   });
 }
 

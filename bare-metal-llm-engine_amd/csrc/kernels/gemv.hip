@@ -29,6 +29,23 @@ using gemv::gemv_rows_lds_kernel;
 using gemv::gemv_rows_lds_multi_kernel;
 using gemv::gemv_stream_kernel;
 
+// K split of the reference-layout kernel for ncb column blocks: the grid is
+// one round of resident workgroups (4 of the 512-thread workgroups per CU),
+// every chunk a whole number of STEP-row loads and at least one unrolled step
+// of all waves.
+void kn_split(long long ncb, long long K, long long STEP, long long U, long long cus,
+              long long& nsplit, long long& kchunk) {
+  nsplit = 1;
+  if (ncb < 2 * cus) {
+    nsplit = (4 * cus) / ncb;
+    nsplit = std::min(nsplit, (K + STEP * U - 1) / (STEP * U));
+    nsplit = std::max(nsplit, 1LL);
+  }
+  kchunk = (K + nsplit - 1) / nsplit;
+  kchunk = (kchunk + STEP - 1) / STEP * STEP;
+  nsplit = (K + kchunk - 1) / kchunk;
+}
+
 // Reference-layout configuration: row segments of LPR lanes x 16 bytes; MX
 // activation rows per launch (x row pitch K, y row pitch N).
 template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool RMS,
@@ -55,15 +72,9 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   // workgroups that 3 or 4 rows' accumulators allow measured 14% faster at
   // 4 x 11008 x 4096 -- 21.5 vs 24.6 us -- but would make results depend on
   // the batch.)
-  long long nsplit = 1;
-  if (ncb < 2 * cus) {
-    nsplit = (4 * cus) / ncb;
-    nsplit = std::min(nsplit, (K + STEP * U - 1) / (STEP * U));
-    nsplit = std::max(nsplit, 1LL);
-  }
-  long long kchunk = (K + nsplit - 1) / nsplit;
-  kchunk = (kchunk + STEP - 1) / STEP * STEP;
-  nsplit = (K + kchunk - 1) / kchunk;
+  long long nsplit = 0;
+  long long kchunk = 0;
+  kn_split(ncb, K, STEP, U, cus, nsplit, kchunk);
   ENG_CHECK(ncb * nsplit <= 0x7fffffffLL, "gemv: grid too large for one launch");
 
   const WT* W = static_cast<const WT*>(a.W);
@@ -72,7 +83,7 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   if (nsplit == 1) {
     gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, false, MX>
         <<<static_cast<unsigned>(ncb), WAVES * 64, 0, stream>>>(W, x, a.gamma, y, N, K, K, ncb,
-                                                                 nullptr, nullptr, a.eps);
+                                                                 nullptr, nullptr, a.eps, nullptr);
     ENG_LAUNCH_CHECK();
     return;
   }
@@ -82,7 +93,7 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
   float* partial_ss = partials + nsplit * MX * N;
   gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true, MX>
       <<<static_cast<unsigned>(ncb * nsplit), WAVES * 64, 0, stream>>>(
-          W, x, a.gamma, y, N, K, kchunk, ncb, partials, partial_ss, a.eps);
+          W, x, a.gamma, y, N, K, kchunk, ncb, partials, partial_ss, a.eps, nullptr);
   ENG_LAUNCH_CHECK();
   gemv_reduce_kernel<YT, RMS>
       <<<dim3(static_cast<unsigned>((N + 63) / 64), MX), gemv::kReduceWaves * 64, 0, stream>>>(
@@ -370,6 +381,59 @@ bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) 
         kn_rows<float, false>(g, mx, stream);
       }
     }
+  }
+  return true;
+}
+
+namespace {
+
+// act[N] = SiLU(s xg . Wg) * (s xg . Wu), reference-layout Wg = a.W and Wu
+// [K x N]: one stream launch over both matrices (DUAL, two column blocks per
+// block of columns, with a single matrix's K split, so each plane's partial
+// sums are those of the single-matrix kernel) and one reduce launch with the
+// SwiGLU epilogue.
+template <typename WT>
+void run_kn_glu(const GemvArgs& a, const WT* Wu, hipStream_t stream) {
+  constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
+  constexpr int LPR = 32;
+  constexpr int WAVES = 8;
+  constexpr int U = 4;
+  constexpr int STEP = WAVES * (64 / LPR);
+  constexpr int CW = LPR * VEC;
+  const long long N = a.N;
+  const long long K = a.K;
+  const long long ncb = (N + CW - 1) / CW;
+  long long nsplit = 0;
+  long long kchunk = 0;
+  kn_split(ncb, K, STEP, U, device_cu_count(), nsplit, kchunk);
+  ENG_CHECK(2 * ncb * nsplit <= 0x7fffffffLL, "rmsnorm_linear_swiglu: grid too large for one launch");
+  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * (2 * N + 1) * sizeof(float));
+  float* partials = static_cast<float*>(ws.get());
+  float* partial_ss = partials + nsplit * 2 * N;
+  gemv_stream_kernel<WT, float, float, VEC, LPR, WAVES, U, true, true, true, 1, true>
+      <<<static_cast<unsigned>(2 * ncb * nsplit), WAVES * 64, 0, stream>>>(
+          static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma, nullptr, N, K,
+          kchunk, 2 * ncb, partials, partial_ss, a.eps, Wu);
+  ENG_LAUNCH_CHECK();
+  gemv_reduce_kernel<float, true, gemv::kReduceWaves, true>
+      <<<dim3(static_cast<unsigned>((N + 63) / 64), 1), gemv::kReduceWaves * 64, 0, stream>>>(
+          partials, partial_ss, static_cast<float*>(a.y), N, K, static_cast<int>(nsplit), a.eps, 1);
+  ENG_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+// Reference-layout decode FFN half (one row, a.rms, fp32 x and act): see
+// run_kn_glu. Returns false, launching nothing, unless both weight matrices
+// take the vector path (N a multiple of the 16-byte vector, 16-byte aligned).
+bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, hipStream_t stream) {
+  if (a.w_nk || !a.rms || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+  const long long vmax = a.w == Elem::F16 ? 8 : 4;
+  if (a.N % vmax != 0 || !aligned_to(a.W, 16) || !aligned_to(Wu, 16)) return false;
+  if (a.w == Elem::F16) {
+    run_kn_glu<_Float16>(a, static_cast<const _Float16*>(Wu), stream);
+  } else {
+    run_kn_glu<float>(a, static_cast<const float*>(Wu), stream);
   }
   return true;
 }

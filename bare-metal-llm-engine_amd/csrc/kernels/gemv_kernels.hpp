@@ -87,6 +87,13 @@ __device__ __forceinline__ float rms_scale(float sumsq, long long K, float eps) 
   return 1.0f / sqrtf(sumsq / static_cast<float>(K) + eps);
 }
 
+// SiLU(g) * u with SiLU(g) = g / (1 + e^-g) (reference src/cpu_ref/swiglu_cpu.cpp:
+// 23-25): fp32 exp and a correctly rounded divide; large negative g gives
+// g / inf = -0, large positive g gives g.
+__device__ __forceinline__ float swiglu_f32(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
 // Workgroup id -> logical index so that XCD x (ids x, x + 8, ...) gets a
 // contiguous range of logical indices. A bijection on [0, total).
 __device__ __forceinline__ long long xcd_contiguous(long long wg, long long total) {
@@ -102,12 +109,19 @@ __device__ __forceinline__ long long xcd_contiguous(long long wg, long long tota
 // rows, each (m, column) summed in the single-row order, so row m equals a
 // single-row call on x[m] bit for bit. Partial sums are laid out
 // [nsplit][MX][N], sums of squares [nsplit][MX].
+// DUAL (partial mode only): two matrices W and W2 of the same shape against
+// the same x (an FFN's gate and up projections); ncb counts the column blocks
+// of both -- blocks [0, ncb / 2) stream W, the rest the same columns of W2 --
+// and partial sums are laid out [nsplit][MX][2][N]. Each block's arithmetic
+// is the single-matrix kernel's.
 template <typename WT, typename XT, typename YT, int VEC, int LPR, int WAVES, int U, bool NT,
-          bool RMS, bool PARTIAL, int MX = 1>
+          bool RMS, bool PARTIAL, int MX = 1, bool DUAL = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
     const WT* __restrict__ W, const XT* __restrict__ x, const float* __restrict__ gamma,
     YT* __restrict__ y, long long N, long long K, long long kchunk, long long ncb,
-    float* __restrict__ part, float* __restrict__ part_ss, float eps) {
+    float* __restrict__ part, float* __restrict__ part_ss, float eps,
+    const WT* __restrict__ W2) {
+  static_assert(!DUAL || PARTIAL, "two matrices need the partial-sum reduce");
   constexpr int RPW = 64 / LPR;       // rows per wave load
   constexpr int STEP = WAVES * RPW;   // rows per load of all waves
   constexpr int CW = LPR * VEC;       // columns per workgroup
@@ -125,8 +139,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 
   const long long total = static_cast<long long>(gridDim.x);
   const long long logical = xcd_contiguous(blockIdx.x, total);
-  const long long cb = logical % ncb;
+  const long long cb_all = logical % ncb;
   const long long s = logical / ncb;
+  const long long blocks_per_matrix = DUAL ? ncb / 2 : ncb;
+  const bool upper = DUAL && cb_all >= blocks_per_matrix;  // streams W2
+  const long long cb = upper ? cb_all - blocks_per_matrix : cb_all;
 
   const long long col0 = cb * CW + static_cast<long long>(seg) * VEC;
   const bool col_ok = col0 < N;  // VEC > 1 implies N % VEC == 0
@@ -144,7 +161,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 
   // Columns past N (whole vectors, as N % VEC == 0 when VEC > 1) read column
   // 0 instead; their sums are never written.
-  const WT* wsafe = W + (col_ok ? col0 : 0);
+  const WT* wsafe = (upper ? W2 : W) + (col_ok ? col0 : 0);
   for (long long base = row_begin + wave * RPW + rg; base < row_end;
        base += static_cast<long long>(STEP) * U) {
     // All of a step's loads (W, x, gamma) are issued before any is used, and
@@ -231,7 +248,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 #pragma unroll
         for (int w = 1; w < WAVES; ++w) v += red[m][w][c];
         if constexpr (PARTIAL) {
-          part[(s * MX + m) * N + col] = v;
+          if constexpr (DUAL) {
+            part[((s * MX + m) * 2 + (upper ? 1 : 0)) * N + col] = v;
+          } else {
+            part[(s * MX + m) * N + col] = v;
+          }
         } else {
           if constexpr (RMS) v *= scale[m];
           y[m * N + col] = from_f32<YT>(v);
@@ -240,7 +261,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
     }
   }
   if constexpr (PARTIAL && RMS) {
-    if (cb == 0 && t == 0) {
+    if (cb_all == 0 && t == 0) {
 #pragma unroll
       for (int m = 0; m < MX; ++m) part_ss[s * MX + m] = wg_ss[m];
     }
@@ -255,14 +276,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_stream_kernel(
 // given nsplit. Up to 64 splits take one round trip per lane (8 waves
 // measured best: 4 or 16 were up to 0.4 us slower at 4096 x 4096 and
 // 11008 x 4096). blockIdx.y selects the activation row m of an mx-row launch
-// (partials [nsplit][mx][N], output row m at y + m N).
+// (partials [nsplit][mx][N], output row m at y + m N). GLU: partials
+// [nsplit][mx][2][N] from the DUAL stream kernel (gate plane, then up), each
+// plane summed exactly as a single matrix's, and y = SiLU(s g) * (s u).
 constexpr int kReduceWaves = 8;
 
-template <typename YT, bool RMS, int WAVES = kReduceWaves>
+template <typename YT, bool RMS, int WAVES = kReduceWaves, bool GLU = false>
 __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
     const float* __restrict__ part, const float* __restrict__ part_ss, YT* __restrict__ y,
     long long N, long long K, int nsplit, float eps, int mx) {
-  __shared__ float group_sum[WAVES][64];
+  constexpr int PLANES = GLU ? 2 : 1;
+  __shared__ float group_sum[PLANES][WAVES][64];
   const int c = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
   const int m = blockIdx.y;
@@ -271,20 +295,27 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
   const int per = (nsplit + WAVES - 1) / WAVES;
   const int s0 = g * per < nsplit ? g * per : nsplit;
   const int s1 = s0 + per < nsplit ? s0 + per : nsplit;
-  const float* pm = part + static_cast<long long>(m) * N + cc;
-  const long long stride = static_cast<long long>(mx) * N;
-  float v = 0.0f;
+  const float* pm = part + static_cast<long long>(m) * PLANES * N + cc;
+  const long long stride = static_cast<long long>(mx) * PLANES * N;
+  float v[PLANES];
+#pragma unroll
+  for (int q = 0; q < PLANES; ++q) v[q] = 0.0f;
   for (int s = s0; s < s1; s += 8) {
-    float t[8];
+    float t[PLANES][8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int si = s + i < s1 ? s + i : s1 - 1;
-      t[i] = pm[static_cast<long long>(si) * stride];
+#pragma unroll
+      for (int q = 0; q < PLANES; ++q) t[q][i] = pm[static_cast<long long>(si) * stride + q * N];
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) v += s + i < s1 ? t[i] : 0.0f;
+    for (int i = 0; i < 8; ++i) {
+#pragma unroll
+      for (int q = 0; q < PLANES; ++q) v[q] += s + i < s1 ? t[q][i] : 0.0f;
+    }
   }
-  group_sum[g][c] = v;
+#pragma unroll
+  for (int q = 0; q < PLANES; ++q) group_sum[q][g][c] = v[q];
   // Sum of squares over the splits: lane c of wave 0 takes splits c, c + 64,
   // ... in turn, then the lanes are folded (one fixed order per nsplit).
   float tot = 0.0f;
@@ -296,11 +327,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
   }
   __syncthreads();
   if (g != 0 || col >= N) return;
-  float out = group_sum[0][c];
+  float out[PLANES];
 #pragma unroll
-  for (int w = 1; w < WAVES; ++w) out += group_sum[w][c];
-  if constexpr (RMS) out *= rms_scale(tot, K, eps);
-  y[static_cast<long long>(m) * N + col] = from_f32<YT>(out);
+  for (int q = 0; q < PLANES; ++q) {
+    out[q] = group_sum[q][0][c];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) out[q] += group_sum[q][w][c];
+    if constexpr (RMS) out[q] *= rms_scale(tot, K, eps);
+  }
+  if constexpr (GLU) {
+    y[static_cast<long long>(m) * N + col] = from_f32<YT>(swiglu_f32(out[0], out[1]));
+  } else {
+    y[static_cast<long long>(m) * N + col] = from_f32<YT>(out[0]);
+  }
 }
 
 // Output-major weights: y[n] = sum_k W[n][k] * xs[k] with W row-major [N x K]
@@ -677,13 +716,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_multi_kernel(const W
       }
     }
   }
-}
-
-// SiLU(g) * u with SiLU(g) = g / (1 + e^-g) (reference src/cpu_ref/swiglu_cpu.cpp:
-// 23-25): fp32 exp and a correctly rounded divide; large negative g gives
-// g / inf = -0, large positive g gives g.
-__device__ __forceinline__ float swiglu_f32(float g, float u) {
-  return g / (1.0f + expf(-g)) * u;
 }
 
 // Fused RMSNorm + gate / up projections + SwiGLU for decode (M = 1),

@@ -523,6 +523,23 @@ def rows_ffn(eng, timer) -> list:
 
     st = timer.sampled(unfused)
     rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, unfused (3 launches)", st, nbytes))
+    # Reference layout [K x N] (the same buffers read as 4096 x 11008): one
+    # split-K launch over both matrices and a reduce with the SwiGLU epilogue,
+    # vs the reference's composition (two rmsnorm_linear calls and swiglu).
+    glu_kn, rlk = eng.lib.eng_rmsnorm_linear_swiglu_f16w, eng.lib.eng_rmsnorm_linear_f16w
+    st = timer.sampled(lambda i, s: glu_kn(dx.ptr, dgm.ptr, Wg[i % RW].ptr, Wu[i % RW].ptr, dact.ptr,
+                                           1, F, H, 1e-5, s))
+    rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, reference layout W[KxN], "
+                        "fused (2 launches)", st, nbytes))
+
+    def unfused_kn(i, s):
+        rlk(dx.ptr, dgm.ptr, Wg[i % RW].ptr, dgate.ptr, 1, F, H, 1e-5, s)
+        rlk(dx.ptr, dgm.ptr, Wu[i % RW].ptr, dup.ptr, 1, F, H, 1e-5, s)
+        sw(dgate.ptr, dup.ptr, dact.ptr, F, s)
+
+    st = timer.sampled(unfused_kn)
+    rows.append(hbm_row("FFN gate/up + SwiGLU 1x11008x4096 fp16-W cold, reference layout W[KxN], "
+                        "unfused (5 launches)", st, nbytes))
     # Small-batch decode: 4 rows share each pass over the gate / up weights.
     M = 4
     dxm = eng.upload(rng.standard_normal((M, H), dtype=np.float32))
@@ -582,7 +599,9 @@ def rows_attention_tinyllama_32k(eng, timer) -> list:
 
 
 def rows_stack(eng, timer) -> list:
-    return [bench_llama_stack(eng, timer, nk=False), bench_llama_stack(eng, timer, nk=True),
+    return [bench_llama_stack(eng, timer, nk=False),
+            bench_llama_stack(eng, timer, nk=False, fused_glu=True, graph=True, fused_qkv=True),
+            bench_llama_stack(eng, timer, nk=True),
             bench_llama_stack(eng, timer, nk=True, fused_glu=True),
             bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True),
             bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
@@ -646,13 +665,15 @@ GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_refer
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
     """Config 5: 32 layers of q,k,v,o (4096 -> 4096), gate/up (4096 -> 11008) via
     rmsnorm_linear, down (11008 -> 4096); fp16 weights, fp32 activations.
-    nk=False stores every weight [in x out] (reference layout), nk=True [out x in].
-    fused_glu=True (output-major only) runs gate, up and SwiGLU as one launch
-    and feeds SiLU(gate) * up to the down projection (6 launches per layer).
-    graph=True captures one token's launches into a HIP graph (eng_graph_*)
-    and times its replays. fused_qkv=True (output-major only) stores each layer's
-    q, k and v weights as one [3H x H] matrix, so one GEMV launch (N = 3H) yields
-    q, k and v; same weights, bytes and arithmetic."""
+    nk=False stores every weight [in x out] (reference layout: each GEMV is a
+    split-K launch and a reduce launch), nk=True [out x in].
+    fused_glu=True runs gate, up and SwiGLU as one call
+    (eng_rmsnorm_linear_swiglu_f16w[_nk]) and feeds SiLU(gate) * up to the down
+    projection. graph=True captures one token's launches into a HIP graph
+    (eng_graph_*) and times its replays. fused_qkv=True stores each layer's q, k
+    and v weights as one matrix ([3H x H] output-major, [H x 3H] reference
+    layout), so one GEMV call (N = 3H) yields q, k and v; same weights, bytes and
+    arithmetic."""
     H, F, L = 4096, 11008, 32
     rng = np.random.default_rng(4)
     if nk:
@@ -660,6 +681,9 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
     else:
         sq, gu, dn = rand_f16(rng, (H, H)), rand_f16(rng, (H, F)), rand_f16(rng, (F, H))
     src = {"sq": eng.upload(sq), "gu": eng.upload(gu), "dn": eng.upload(dn)}
+    if fused_qkv:
+        # q, k, v stacked: output-major by rows, reference layout by columns
+        src["qkv"] = eng.upload(np.concatenate([sq] * 3, axis=0 if nk else 1))
     layers = []
     for _ in range(L):
         lay = {}
@@ -671,10 +695,8 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
             eng.call("eng_memcpy_d2d", d.ptr, src[key].ptr, d.nbytes)
             lay[name] = d
         if fused_qkv:
-            d = eng.empty((3 * H, H), np.uint16)
-            for part in range(3):
-                eng.call("eng_memcpy_d2d", d.ptr + part * src["sq"].nbytes, src["sq"].ptr,
-                         src["sq"].nbytes)
+            d = eng.empty(src["qkv"].shape, np.uint16)
+            eng.call("eng_memcpy_d2d", d.ptr, src["qkv"].ptr, d.nbytes)
             lay["qkv"] = d
         layers.append(lay)
     for d in src.values():
@@ -689,7 +711,7 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
     else:
         gv, rl = eng.lib.eng_gemv_f16w, eng.lib.eng_rmsnorm_linear_f16w
 
-    glu = eng.lib.eng_rmsnorm_linear_swiglu_f16w_nk
+    glu = eng.lib.eng_rmsnorm_linear_swiglu_f16w_nk if nk else eng.lib.eng_rmsnorm_linear_swiglu_f16w
 
     def token(_i, s):
         for lay in layers:
@@ -728,12 +750,13 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
     if fused_glu:
         layout += ", gate/up + SwiGLU fused"
     if fused_qkv:
-        layout += ", q/k/v as one [3H x H] matrix"
+        layout += ", q/k/v as one [3H x H] matrix" if nk else ", q/k/v as one [H x 3H] matrix"
     if graph:
         layout += ", replayed as one HIP graph"
     row = hbm_row(f"config 5 llama7b-shape decode linear stack, 32 layers, per token, {layout}",
                   st, wbytes + abytes)
-    row["launches_per_token"] = (7 - (1 if fused_glu else 0) - (2 if fused_qkv else 0)) * L
+    calls = 7 - (1 if fused_glu else 0) - (2 if fused_qkv else 0)
+    row["launches_per_token"] = calls * L * (1 if nk else 2)  # reference layout: split-K + reduce
     return row
 
 

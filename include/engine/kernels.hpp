@@ -168,6 +168,21 @@ inline void rmsnorm_linear_swiglu_nk(const float* in, const float* rms_weight, c
       eng_rmsnorm_linear_swiglu_f32_nk(in, rms_weight, W_gate, W_up, act, M, N, K, eps, stream));
 }
 
+/// The same with reference-layout weights [K x N] (rmsnorm_linear's layout):
+/// two launches at M == 1 instead of the composition's five, same result.
+inline void rmsnorm_linear_swiglu(const float* in, const float* rms_weight, const half* W_gate,
+                                  const half* W_up, float* act, std::int64_t M, std::int64_t N,
+                                  std::int64_t K, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(eng_rmsnorm_linear_swiglu_f16w(in, rms_weight, detail::bits(W_gate),
+                                                  detail::bits(W_up), act, M, N, K, eps, stream));
+}
+inline void rmsnorm_linear_swiglu(const float* in, const float* rms_weight, const float* W_gate,
+                                  const float* W_up, float* act, std::int64_t M, std::int64_t N,
+                                  std::int64_t K, float eps, hipStream_t stream = nullptr) {
+  ENGINE_ABI_CHECK(
+      eng_rmsnorm_linear_swiglu_f32(in, rms_weight, W_gate, W_up, act, M, N, K, eps, stream));
+}
+
 namespace detail {
 
 /// FlashDecoding with GQA K / V sharing switched explicitly (reference

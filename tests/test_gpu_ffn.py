@@ -85,6 +85,34 @@ def gpu_glu_nk(eng, x, g, Wg_nk, Wu_nk):
     return da.download()
 
 
+def gpu_glu_kn(eng, x, g, Wg, Wu):
+    """Reference-layout fused gate / up + SwiGLU (Wg, Wu [K x N])."""
+    M, K = x.shape
+    N = Wg.shape[1]
+    fn = "eng_rmsnorm_linear_swiglu_f16w" if Wg.dtype == np.uint16 else "eng_rmsnorm_linear_swiglu_f32"
+    dx, dWg, dWu = eng.upload(x), eng.upload(Wg), eng.upload(Wu)
+    dg = eng.upload(g) if g is not None else None
+    da = eng.empty((M, N), np.float32)
+    eng.call(fn, dx.ptr, dg.ptr if dg else None, dWg.ptr, dWu.ptr, da.ptr, M, N, K, EPS, None)
+    eng.sync()
+    return da.download()
+
+
+def gpu_glu_kn_composed(eng, x, g, Wg, Wu):
+    """The reference's composition: rmsnorm_linear for gate and for up, then swiglu."""
+    M, K = x.shape
+    N = Wg.shape[1]
+    fn = "eng_rmsnorm_linear_f16w" if Wg.dtype == np.uint16 else "eng_rmsnorm_linear_f32"
+    outs = []
+    for W in (Wg, Wu):
+        dx, dW, dy = eng.upload(x), eng.upload(W), eng.empty((M, N), np.float32)
+        dg = eng.upload(g) if g is not None else None
+        eng.call(fn, dx.ptr, dg.ptr if dg else None, dW.ptr, dy.ptr, M, N, K, EPS, None)
+        eng.sync()
+        outs.append(dy.download())
+    return gpu_swiglu(eng, outs[0], outs[1])
+
+
 def rmsnorm_bound(y64, cols):
     return ((cols / 2.0 + 4.0) * U + 3 * U) * np.abs(y64) + 1e-30
 
@@ -312,6 +340,64 @@ def test_rmsnorm_linear_swiglu_equals_separate_calls(gpu):
     act64, bd, _ = glu_reference(x, g, np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T))
     helpers.assert_within(fused, sep, 2 * bd, "fused vs separate")
     assert np.array_equal(fused, gpu_glu_nk(gpu, x, g, Wg, Wu)), "fused launch is deterministic"
+
+
+# ---------------------------------- fused gate/up + SwiGLU (reference layout)
+@pytest.mark.parametrize("stem", [c["stem"] for c in helpers.cases("rmsnorm_linear_swiglu")
+                                  + helpers.cases("rmsnorm_linear_swiglu_f16w")])
+def test_rmsnorm_linear_swiglu_kn_matches_golden(gpu, orc, stem):
+    c = helpers.case(stem)
+    x = helpers.inputs(c)
+    g = x.get("weight")
+    got = gpu_glu_kn(gpu, x["input"], g, x["Wg"], x["Wu"])
+    act64, bd, bs = glu_reference(x["input"], g, x["Wg"], x["Wu"])
+    check_glu(got, orc.rmsnorm_linear_swiglu(x["input"], g, x["Wg"], x["Wu"], EPS), act64, bd, bs,
+              stem + " (kn)")
+
+
+@pytest.mark.parametrize("M,N,K,dtype,gamma", [
+    (1, 11008, 4096, "f16", True),   # config 5 gate/up shape: one launch over both matrices + reduce
+    (1, 1376, 4096, "f16", False),   # null gain
+    (1, 4096, 16384, "f16", True),   # long K: 64 splits
+    (1, 64, 300, "f16", True),       # one column block per matrix
+    (1, 257, 1024, "f32", True),     # N % 4 != 0: composition (scalar split-K kernel)
+    (1, 1000, 1024, "f32", True),    # fp32 weights: fused
+    (1, 36, 20, "f16", True),        # N % 8 != 0 for fp16: composition
+    (3, 300, 1000, "f16", True),     # small batch: split-K passes with 3 rows + SwiGLU kernel
+    (40, 200, 512, "f16", True),     # prefill: MFMA GEMMs + SwiGLU kernel
+])
+def test_rmsnorm_linear_swiglu_kn_against_oracle_and_composition(gpu, orc, M, N, K, dtype, gamma):
+    # Against the oracle, and bit for bit against the reference's composition
+    # (two rmsnorm_linear calls and swiglu): the fused decode path sums each
+    # plane exactly as rmsnorm_linear does.
+    rng = np.random.default_rng(3 * M + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if gamma else None
+    Wgf = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    Wuf = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    Wg, Wu = (orc.f32_to_f16(W) if dtype == "f16" else W for W in (Wgf, Wuf))
+    got = gpu_glu_kn(gpu, x, g, Wg, Wu)
+    rows = np.array(sorted({0, M // 2, M - 1}))
+    act64, bd, bs = glu_reference(x[rows], g, Wg, Wu)
+    check_glu(got[rows], orc.rmsnorm_linear_swiglu(x[rows], g, Wg, Wu, EPS), act64, bd, bs,
+              f"rmsnorm_linear_swiglu kn {M}x{N}x{K} {dtype}")
+    assert np.array_equal(got, gpu_glu_kn_composed(gpu, x, g, Wg, Wu)), "fused == composition"
+
+
+def test_rmsnorm_linear_swiglu_kn_zero_sizes_and_contracts(gpu):
+    dx = gpu.upload(np.ones((1, 64), np.float32))
+    dW = gpu.upload(np.zeros((64, 64), np.uint16))
+    da = gpu.empty((1, 64), np.float32)
+    fn = "eng_rmsnorm_linear_swiglu_f16w"
+    for M, N, K in ((0, 64, 64), (1, 0, 64), (1, 64, 0)):
+        gpu.call(fn, dx.ptr, None, dW.ptr, dW.ptr, da.ptr, M, N, K, EPS, None)
+    gpu.sync()
+    with pytest.raises(RuntimeError, match="negative dimension"):
+        gpu.call(fn, dx.ptr, None, dW.ptr, dW.ptr, da.ptr, -1, 64, 64, EPS, None)
+    with pytest.raises(RuntimeError, match="null device pointer"):
+        gpu.call(fn, dx.ptr, None, None, dW.ptr, da.ptr, 1, 64, 64, EPS, None)
+    with pytest.raises(RuntimeError, match="eps must be non-negative"):
+        gpu.call(fn, dx.ptr, None, dW.ptr, dW.ptr, da.ptr, 1, 64, 64, -1.0, None)
 
 
 # ------------------------------------------------------------ FFN sub-block
