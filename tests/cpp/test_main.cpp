@@ -126,6 +126,9 @@ TEST(cpu_contract, ffn_side_launchers_keep_the_reference_contract) {
   EXPECT_THROWS_MSG(engine::cuda::rmsnorm_linear_swiglu_nk(p, p, ph, ph, p, 1, -1, 4, 1e-5f),
                     "negative");
   EXPECT_NO_THROW(engine::cuda::rmsnorm_linear_swiglu_nk(p, nullptr, p, p, p, 1, 8, 0, 1e-5f));
+  EXPECT_THROWS_MSG(engine::cuda::rmsnorm_linear_swiglu(p, p, ph, nullptr, p, 1, 4, 4, 1e-5f),
+                    "null");
+  EXPECT_NO_THROW(engine::cuda::rmsnorm_linear_swiglu(p, nullptr, p, p, p, 0, 8, 8, 1e-5f));
   for (float v : g_dummy_f) EXPECT_EQ(v, 0.0f);
 }
 

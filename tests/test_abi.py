@@ -28,7 +28,8 @@ def test_header_declares_the_hot_path_entry_points():
                "eng_rmsnorm_f32", "eng_rmsnorm_linear_f32", "eng_rmsnorm_linear_f16w",
                "eng_rmsnorm_linear_fused_direct_f32", "eng_last_error", "eng_vector_add_f32",
                "eng_residual_rmsnorm_f32", "eng_swiglu_f32", "eng_swiglu_f16",
-               "eng_rmsnorm_linear_swiglu_f16w_nk", "eng_rmsnorm_linear_swiglu_f32_nk"):
+               "eng_rmsnorm_linear_swiglu_f16w_nk", "eng_rmsnorm_linear_swiglu_f32_nk",
+               "eng_rmsnorm_linear_swiglu_f16w", "eng_rmsnorm_linear_swiglu_f32"):
         assert fn in names
 
 
@@ -100,6 +101,9 @@ P = 0x1000  # dummy non-null "device" pointer; never dereferenced on these paths
     (("eng_rmsnorm_linear_swiglu_f16w_nk", P, P, P, None, P, 1, 4, 4, 1e-5, None), 1, "null"),
     (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, -4, 4, 1e-5, None), 1, "negative dimension"),
     (("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 4, 4, -1.0, None), 1, "eps"),
+    (("eng_rmsnorm_linear_swiglu_f16w", P, P, None, P, P, 1, 4, 4, 1e-5, None), 1, "null device pointer"),
+    (("eng_rmsnorm_linear_swiglu_f32", P, P, P, P, P, 1, -4, 4, 1e-5, None), 1, "negative dimension"),
+    (("eng_rmsnorm_linear_swiglu_f32", P, P, P, P, P, 1, 4, 4, -1.0, None), 1, "eps"),
     (("eng_attention_decode_f16", None, P, P, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "attention_decode: q is null"),
     (("eng_attention_decode_f16", P, None, P, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "k is null"),
     (("eng_attention_decode_f16", P, P, None, P, 4, 8, 2, 64, 256, 0.125, 0, None), 1, "v is null"),
@@ -165,6 +169,8 @@ def test_preconditions_fail_before_launch(eng, call, code, substr):
     ("eng_swiglu_f16", P, P, P, 0, None),
     ("eng_rmsnorm_linear_swiglu_f16w_nk", P, None, P, P, P, 1, 0, 8, 1e-5, None),
     ("eng_rmsnorm_linear_swiglu_f32_nk", P, P, P, P, P, 1, 8, 0, 1e-5, None),
+    ("eng_rmsnorm_linear_swiglu_f16w", P, None, P, P, P, 0, 8, 8, 1e-5, None),
+    ("eng_rmsnorm_linear_swiglu_f32", P, P, P, P, P, 1, 8, 0, 1e-5, None),
     ("eng_cast_f32_to_f16", None, None, 0, None),
     ("eng_cast_f16_to_f32", None, None, 0, None),
     ("eng_kv_cache_write_f16", None, None, None, None, 0, 2, 64, 3, 3, None),
