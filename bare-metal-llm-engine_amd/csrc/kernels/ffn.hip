@@ -11,10 +11,11 @@
 //     epilogue, so gate and up never reach memory. A few rows (small-batch
 //     decode) run gemv_rows_glu_multi_kernel: up to 4 rows per pass over Wg
 //     and Wu, each row equal to its M = 1 result.
-//   * Reference-layout decode (M == 1, N a multiple of the 16-byte vector,
-//     aligned weights) runs the split-K stream kernel over both matrices in
-//     one launch and the reduce with the SwiGLU epilogue (launch_gemv_kn_glu):
-//     two launches where the composition takes five, and the same bits.
+//   * Reference-layout decode (up to 16 rows, N a multiple of the 16-byte
+//     vector, aligned weights) runs, per pass of up to 4 rows, the split-K
+//     stream kernel over both matrices in one launch and the reduce with the
+//     SwiGLU epilogue (launch_gemv_kn_glu): two launches where the composition
+//     takes five, and the same bits.
 //   * Otherwise gate and up are computed separately into the stream's scratch
 //     arena -- single-row GEMVs, small-batch passes over W, or (more rows)
 //     RMSNorm once and the MFMA GEMM -- and the SwiGLU kernel finishes.
@@ -44,8 +45,9 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
   constexpr long long kPiece = 64 * VEC;
   constexpr long long kMaxLds = 64 * 1024;
   const long long padded = (K + kPiece - 1) / kPiece * kPiece;
-  if (!nk && M == 1) {
-    // Reference layout: one stream launch over Wg and Wu, SwiGLU in the reduce.
+  if (!nk) {
+    // Reference layout, up to 16 rows: per pass of up to 4 rows, one stream
+    // launch over Wg and Wu and the reduce with the SwiGLU epilogue.
     GemvArgs gv;
     gv.W = Wg;
     gv.w = elem;
@@ -56,7 +58,7 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
     gv.K = K;
     gv.rms = true;
     gv.eps = eps;
-    if (launch_gemv_kn_glu(gv, Wu, s)) return;
+    if (launch_gemv_kn_glu(gv, Wu, M, s)) return;
   }
   const bool fused = nk && M == 1 && K % VEC == 0 && padded * 4 <= kMaxLds && aligned_to(Wg, 16) &&
                      aligned_to(Wu, 16) && aligned_to(in, 16) &&

@@ -387,12 +387,12 @@ bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) 
 
 namespace {
 
-// act[N] = SiLU(s xg . Wg) * (s xg . Wu), reference-layout Wg = a.W and Wu
-// [K x N]: one stream launch over both matrices (DUAL, two column blocks per
-// block of columns, with a single matrix's K split, so each plane's partial
-// sums are those of the single-matrix kernel) and one reduce launch with the
-// SwiGLU epilogue.
-template <typename WT>
+// act[MX x N] = SiLU(s xg . Wg) * (s xg . Wu) for MX rows, reference-layout
+// Wg = a.W and Wu [K x N]: one stream launch over both matrices (DUAL, two
+// column blocks per block of columns, with a single matrix's K split, so each
+// plane's partial sums are those of the single-matrix kernel) and one reduce
+// launch with the SwiGLU epilogue.
+template <typename WT, int MX>
 void run_kn_glu(const GemvArgs& a, const WT* Wu, hipStream_t stream) {
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
   constexpr int LPR = 32;
@@ -407,33 +407,56 @@ void run_kn_glu(const GemvArgs& a, const WT* Wu, hipStream_t stream) {
   long long kchunk = 0;
   kn_split(ncb, K, STEP, U, device_cu_count(), nsplit, kchunk);
   ENG_CHECK(2 * ncb * nsplit <= 0x7fffffffLL, "rmsnorm_linear_swiglu: grid too large for one launch");
-  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * (2 * N + 1) * sizeof(float));
+  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * MX * (2 * N + 1) * sizeof(float));
   float* partials = static_cast<float*>(ws.get());
-  float* partial_ss = partials + nsplit * 2 * N;
-  gemv_stream_kernel<WT, float, float, VEC, LPR, WAVES, U, true, true, true, 1, true>
+  float* partial_ss = partials + nsplit * MX * 2 * N;
+  gemv_stream_kernel<WT, float, float, VEC, LPR, WAVES, U, true, true, true, MX, true>
       <<<static_cast<unsigned>(2 * ncb * nsplit), WAVES * 64, 0, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma, nullptr, N, K,
           kchunk, 2 * ncb, partials, partial_ss, a.eps, Wu);
   ENG_LAUNCH_CHECK();
   gemv_reduce_kernel<float, true, gemv::kReduceWaves, true>
-      <<<dim3(static_cast<unsigned>((N + 63) / 64), 1), gemv::kReduceWaves * 64, 0, stream>>>(
-          partials, partial_ss, static_cast<float*>(a.y), N, K, static_cast<int>(nsplit), a.eps, 1);
+      <<<dim3(static_cast<unsigned>((N + 63) / 64), MX), gemv::kReduceWaves * 64, 0, stream>>>(
+          partials, partial_ss, static_cast<float*>(a.y), N, K, static_cast<int>(nsplit), a.eps, MX);
   ENG_LAUNCH_CHECK();
+}
+
+template <typename WT>
+void kn_glu_rows(const GemvArgs& a, const void* Wu, int mx, hipStream_t stream) {
+  const WT* u = static_cast<const WT*>(Wu);
+  switch (mx) {
+    case 1: run_kn_glu<WT, 1>(a, u, stream); break;
+    case 2: run_kn_glu<WT, 2>(a, u, stream); break;
+    case 3: run_kn_glu<WT, 3>(a, u, stream); break;
+    default: run_kn_glu<WT, 4>(a, u, stream); break;
+  }
 }
 
 }  // namespace
 
-// Reference-layout decode FFN half (one row, a.rms, fp32 x and act): see
-// run_kn_glu. Returns false, launching nothing, unless both weight matrices
-// take the vector path (N a multiple of the 16-byte vector, 16-byte aligned).
-bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, hipStream_t stream) {
-  if (a.w_nk || !a.rms || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+// Reference-layout FFN half for decode rows (a.rms, fp32 x and act, M rows
+// of pitches K and N): passes of up to 4 rows, each one DUAL stream launch and
+// one SwiGLU reduce (see run_kn_glu); every row equals its single-row result.
+// Returns false, launching nothing, for more than 4 passes or unless both
+// weight matrices take the vector path (N a multiple of the 16-byte vector,
+// 16-byte aligned).
+bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, std::int64_t M, hipStream_t stream) {
+  constexpr long long kRows = 4;
+  constexpr long long kMaxPasses = 4;
+  if (a.w_nk || !a.rms || M < 1 || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+  if ((M + kRows - 1) / kRows > kMaxPasses) return false;
   const long long vmax = a.w == Elem::F16 ? 8 : 4;
   if (a.N % vmax != 0 || !aligned_to(a.W, 16) || !aligned_to(Wu, 16)) return false;
-  if (a.w == Elem::F16) {
-    run_kn_glu<_Float16>(a, static_cast<const _Float16*>(Wu), stream);
-  } else {
-    run_kn_glu<float>(a, static_cast<const float*>(Wu), stream);
+  for (long long m0 = 0; m0 < M; m0 += kRows) {
+    const int mx = static_cast<int>(std::min<long long>(kRows, M - m0));
+    GemvArgs g = a;
+    g.x = static_cast<const float*>(a.x) + m0 * a.K;
+    g.y = static_cast<float*>(a.y) + m0 * a.N;
+    if (a.w == Elem::F16) {
+      kn_glu_rows<_Float16>(g, Wu, mx, stream);
+    } else {
+      kn_glu_rows<float>(g, Wu, mx, stream);
+    }
   }
   return true;
 }

@@ -36,11 +36,11 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream);
 bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
 // Reference-layout W [K x N] counterpart of launch_gemv_nk_rows.
 bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
-// Reference-layout gate / up + SwiGLU for one row: a.y = SiLU(RMSNorm(a.x) . a.W)
-// * (RMSNorm(a.x) . Wu), equal bit for bit to the two RMSNorm + linear calls
-// and swiglu. Returns false, launching nothing, when the vector path's
-// requirements fail.
-bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, hipStream_t stream);
+// Reference-layout gate / up + SwiGLU for M decode rows: a.y = SiLU(RMSNorm(a.x)
+// . a.W) * (RMSNorm(a.x) . Wu), equal bit for bit to the two RMSNorm + linear
+// calls and swiglu. Returns false, launching nothing, for more than 16 rows or
+// when the vector path's requirements fail.
+bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, std::int64_t M, hipStream_t stream);
 
 // C[M x N] = A'[M x K] . B[K x N] on FP32 MFMA, where A' = A with column k
 // scaled by gamma_k when gamma is given; with rms, row r of C is further

@@ -314,10 +314,11 @@ int eng_rmsnorm_linear_swiglu_f32_nk(const float* in, const float* rms_weight,
 /* The same with reference-layout W_gate, W_up [K x N] (the layout of
  * rmsnorm_linear, include/engine/kernels.hpp:92-99; no reference counterpart:
  * the reference composes two rmsnorm_linear calls and swiglu,
- * tests/test_kernels.cu:2867-2898). Decode (M == 1, N a multiple of 8 fp16 /
- * 4 fp32 elements, 16-byte aligned weights) is one split-K launch over both
- * matrices and one reduce launch with the SwiGLU epilogue; its result equals
- * that composition bit for bit. Same messages as the _nk form. */
+ * tests/test_kernels.cu:2867-2898). Decode (up to 16 rows, N a multiple of 8
+ * fp16 / 4 fp32 elements, 16-byte aligned weights) is, per pass of up to 4
+ * rows, one split-K launch over both matrices and one reduce launch with the
+ * SwiGLU epilogue; its result equals that composition bit for bit. Same
+ * messages as the _nk form. */
 int eng_rmsnorm_linear_swiglu_f16w(const float* in, const float* rms_weight,
                                    const eng_half* W_gate, const eng_half* W_up, float* act,
                                    int64_t M, int64_t N, int64_t K, float eps,

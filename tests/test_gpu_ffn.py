@@ -363,7 +363,10 @@ def test_rmsnorm_linear_swiglu_kn_matches_golden(gpu, orc, stem):
     (1, 257, 1024, "f32", True),     # N % 4 != 0: composition (scalar split-K kernel)
     (1, 1000, 1024, "f32", True),    # fp32 weights: fused
     (1, 36, 20, "f16", True),        # N % 8 != 0 for fp16: composition
-    (3, 300, 1000, "f16", True),     # small batch: split-K passes with 3 rows + SwiGLU kernel
+    (3, 300, 1000, "f16", True),     # small batch: one fused pass of 3 rows
+    (16, 1024, 512, "f16", False),   # 4 fused passes of 4 rows
+    (6, 400, 256, "f32", True),      # passes of 4 and 2 rows, fp32 weights
+    (17, 256, 512, "f32", True),     # past 4 passes: MFMA GEMMs + SwiGLU kernel
     (40, 200, 512, "f16", True),     # prefill: MFMA GEMMs + SwiGLU kernel
 ])
 def test_rmsnorm_linear_swiglu_kn_against_oracle_and_composition(gpu, orc, M, N, K, dtype, gamma):
