@@ -77,8 +77,9 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 // scope, so two host threads that share a stream cannot interleave their
 // kernel pairs on it; take it before the first launch that writes the arena
 // and keep it past the last one that reads it. The arena grows to the largest
-// request (growth waits for the stream, then reallocates) and is freed when
-// the stream is destroyed through eng_stream_destroy, or at exit. Each
+// request (a new block; the outgrown one stays allocated for queued kernels
+// and captured graphs) and its blocks are freed when the stream is destroyed
+// through eng_stream_destroy, or at exit. Each
 // (device, stream) has one arena per level: a launcher takes at most one lease
 // per level, and a composite launcher that keeps a lease while it calls other
 // launchers (the FFN's gate / up buffers around the GEMV launches, which may

@@ -6,6 +6,7 @@
 #include <memory>
 #include <mutex>
 #include <utility>
+#include <vector>
 
 namespace eng {
 namespace {
@@ -41,6 +42,7 @@ struct Arena {
   std::mutex mu;  // held by the live lease
   void* base = nullptr;
   std::size_t capacity = 0;
+  std::vector<void*> retired;  // outgrown blocks, kept for graphs captured on them
 };
 
 constexpr std::size_t kMinArena = std::size_t{1} << 20;
@@ -76,15 +78,15 @@ StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes, int level) {
   }
   std::unique_lock<std::mutex> lock(arena->mu);
   if (bytes > arena->capacity) {
-    // Queued kernels of this stream may still use the old block.
-    if (arena->base != nullptr) {
-      ENG_HIP_CHECK(hipStreamSynchronize(stream));
-      ENG_HIP_CHECK(hipFree(arena->base));
-      arena->base = nullptr;
-      arena->capacity = 0;
-    }
+    // The outgrown block stays allocated until the stream's arenas are
+    // released: queued kernels, and HIP graphs captured while it was current,
+    // still address it. (Doubling keeps the retired blocks below the current
+    // one's size in total.)
     const std::size_t want = std::max({bytes, kMinArena, 2 * arena->capacity});
-    ENG_HIP_CHECK(hipMalloc(&arena->base, want));
+    void* grown = nullptr;
+    ENG_HIP_CHECK(hipMalloc(&grown, want));
+    if (arena->base != nullptr) arena->retired.push_back(arena->base);
+    arena->base = grown;
     arena->capacity = want;
   }
   ptr_ = arena->base;
@@ -113,6 +115,7 @@ void release_stream_scratch(hipStream_t stream) {
     }
     std::lock_guard<std::mutex> lock(arena->mu);  // no lease may be live
     if (arena->base != nullptr) (void)hipFree(arena->base);
+    for (void* p : arena->retired) (void)hipFree(p);
   }
 }
 

@@ -101,6 +101,44 @@ def test_captured_decode_step_replays_match_eager(gpu):
         s.destroy()
 
 
+def test_graph_replays_after_the_stream_arena_grows(gpu):
+    # A graph captured on a small split-K call keeps addressing the arena block
+    # it was captured on after a larger call on the same stream outgrows that
+    # block: the outgrown block stays allocated until the stream is destroyed.
+    rng = np.random.default_rng(8)
+    K, N = 512, 1024
+    W = gpu.upload(f16(gpu, 0.03 * rng.standard_normal((K, N))))      # [in x out]: split-K
+    x = gpu.upload(rng.standard_normal(K).astype(np.float32))
+    y = gpu.empty(N, np.float32)
+    # 4 rows of a reference-layout rmsnorm_linear: split-K partials for 4 rows,
+    # about 4 MiB, past the 1 MiB the first call sizes the arena to
+    Mb, Kb, Nb = 4, 4096, 8192
+    Wb = gpu.upload(f16(gpu, 0.01 * rng.standard_normal((Kb, Nb))))
+    xb = gpu.upload(rng.standard_normal((Mb, Kb)).astype(np.float32))
+    yb = gpu.empty((Mb, Nb), np.float32)
+    s = gpu.stream()
+    h = s.handle
+    graph = None
+    try:
+        gpu.call("eng_gemv_f16w", W.ptr, x.ptr, y.ptr, N, K, h)       # eager; sizes the arena
+        s.sync()
+        eager = y.download().copy()
+        graph = gpu.graph(s)
+        with graph:
+            gpu.call("eng_gemv_f16w", W.ptr, x.ptr, y.ptr, N, K, h)
+        for rep in range(3):
+            gpu.call("eng_rmsnorm_linear_f16w", xb.ptr, None, Wb.ptr, yb.ptr, Mb, Nb, Kb, EPS, h)
+            gpu.call("eng_memset", y.ptr, 0xFF, y.nbytes)
+            s.sync()
+            graph.launch()
+            s.sync()
+            assert np.array_equal(y.download(), eager), f"replay {rep} after growth"
+    finally:
+        if graph is not None:
+            graph.destroy()
+        s.destroy()
+
+
 def test_capture_on_the_null_stream_is_refused(gpu):
     assert gpu.status("eng_graph_capture_begin", None) == 1
     assert "capture needs a created stream" in gpu.last_error()
