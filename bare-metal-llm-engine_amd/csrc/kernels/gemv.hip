@@ -243,6 +243,10 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream) {
 
 namespace {
 
+// Largest staged-rows LDS of a small-batch pass: fp16 weights take up to
+// 128 KiB (two rows at K = 11008, one 16-wave workgroup per CU), fp32 64 KiB.
+constexpr long long kMultiLdsMax = 128 * 1024;
+
 // One round of resident workgroups, each looping over blocks of WAVES x R
 // rows. fp16 weights: workgroups of 16 waves, one row per wave, one
 // workgroup per CU when the staged rows take more than 32 KiB of LDS, else
@@ -257,6 +261,18 @@ void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t str
       WAVES == 16 ? (lds_bytes <= 32 * 1024 ? 2 : 1)
                   : std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
   const long long wgs = std::min(blocks, per_cu * device_cu_count());
+  if (lds_bytes > 64 * 1024) {
+    // Past 64 KiB a kernel's dynamic LDS must be allowed explicitly (once per device).
+    static bool allowed[64] = {false};
+    int dev = 0;
+    ENG_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64 || !allowed[dev]) {
+      ENG_HIP_CHECK(hipFuncSetAttribute(
+          reinterpret_cast<const void*>(&gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>),
+          hipFuncAttributeMaxDynamicSharedMemorySize, kMultiLdsMax));
+      if (dev >= 0 && dev < 64) allowed[dev] = true;
+    }
+  }
   gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>
       <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
@@ -289,8 +305,9 @@ void rows_multi(const GemvArgs& a, int mx, std::size_t lds, bool two, hipStream_
 // Small-batch decode with output-major weights: y[M x N] = rows of x[M x K]
 // times W[N x K]^T, in groups of up to kMultiRows rows that share one pass
 // over W (gemv_rows_lds_multi_kernel; a group of one row is the single-row
-// GEMV). The staged rows share a 64 KiB LDS budget (4 rows at K = 4096, one at
-// K = 11008 with fp16 weights). Taken only when it needs at most kMaxPasses
+// GEMV). The staged rows share an LDS budget of 128 KiB with fp16 weights (4
+// rows at K = 4096, 2 at K = 11008) and 64 KiB with fp32 weights. Taken only
+// when it needs at most kMaxPasses
 // passes over W -- each pass costs about one GEMV, while the MFMA GEMM for a
 // few rows costs about as much as that many passes (the GEMM pads M to its
 // 64-row tile) -- and when the vector path's requirements hold; returns false
@@ -298,8 +315,8 @@ void rows_multi(const GemvArgs& a, int mx, std::size_t lds, bool two, hipStream_
 bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) {
   constexpr int kMultiRows = 4;
   constexpr long long kMaxPasses = 4;
-  constexpr long long kMaxLds = 64 * 1024;
   if (!a.w_nk || M < 1 || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
+  const long long kMaxLds = a.w == Elem::F16 ? kMultiLdsMax : 64 * 1024;
   const long long vmax = a.w == Elem::F16 ? 8 : 4;
   const bool vec_ok = (a.K % vmax == 0) && aligned_to(a.W, 16) && aligned_to(a.x, 16) &&
                       (a.gamma == nullptr || aligned_to(a.gamma, 16));

@@ -388,6 +388,16 @@ def rows_config3(eng, timer) -> list:
     st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
     rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (small-batch decode), "
                         "reference layout W[KxN]", st, 2 * K * N + 4 * M * K + 4 * K + 4 * M * N))
+    # The down-projection shape (K = 11008): the same buffers read as output-major
+    # [4096 x 11008]; 2 rows per pass (90 KiB of staged rows).
+    Kd, Nd = N, K
+    dxd = eng.upload(rng.standard_normal((M, Kd), dtype=np.float32))
+    dyd = eng.empty((M, Nd), np.float32)
+    fd = eng.lib.eng_rmsnorm_linear_f16w_nk
+    st = timer.sampled(lambda i, s: fd(dxd.ptr, None, Ws[i % R].ptr, dyd.ptr, M, Nd, Kd, 1e-5, s))
+    rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold (small-batch decode, down-projection "
+                        "shape), output-major W[NxK]", st, 2 * Kd * Nd + 4 * M * Kd + 4 * M * Nd))
+    dxd.free(), dyd.free()
     dxm.free(), dym.free()
     for w in Ws:
         w.free()
