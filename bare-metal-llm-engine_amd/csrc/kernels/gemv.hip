@@ -127,6 +127,23 @@ void launch_rows(const GemvArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
+// Largest dynamic LDS of the staged-activation kernels with fp16 weights:
+// 128 KiB (x of up to K = 32768 for one row, two rows at K = 11008 for a
+// small-batch pass; one 16-wave workgroup per CU past 64 KiB).
+constexpr long long kStagedLdsMax = 128 * 1024;
+
+// Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
+// device per kernel (`done` is that kernel's flag array).
+void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes) {
+  if (bytes <= 64 * 1024) return;
+  int dev = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && done[dev]) return;
+  ENG_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(kStagedLdsMax)));
+  if (dev >= 0 && dev < 64) done[dev] = true;
+}
+
 // LDS-staged output-major launches: workgroups of WAVES waves, R rows per
 // wave, U loads per row in flight.
 template <typename WT, int R, int U, bool RMS, int WAVES>
@@ -134,6 +151,9 @@ void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t strea
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
   const long long wgs = ((a.N + R - 1) / R + WAVES - 1) / WAVES;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
+  static bool allowed[64] = {false};
+  allow_staged_lds(reinterpret_cast<const void*>(&gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>),
+                   allowed, lds_bytes);
   gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>
       <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
@@ -150,7 +170,9 @@ void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t strea
 // waves, staging x * gamma in LDS wins: one row per wave, workgroups of 16
 // waves (x staged once per 16 rows; 6-16% faster than 4-wave workgroups at
 // 4096 x 4096 with RMSNorm, 11008 x 4096, 12288 x 4096 and 4096 x 11008),
-// 4 loads per row in flight, 16 when K > 4096. fp32 weights stay on the
+// 4 loads per row in flight, 16 when K > 4096. x is staged for K up to 32768
+// (128 KiB of LDS: at 8192 x 28672, 75 us against 95 us on the register
+// kernel, whose x no longer stays in the caches). fp32 weights stay on the
 // register kernel (2 rows per wave with RMSNorm), where the LDS variant
 // measured slower.
 template <typename WT, bool RMS>
@@ -165,9 +187,8 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
   const long long one_round = 16LL * device_cu_count();
   if constexpr (sizeof(WT) == 2) {
     constexpr long long kPiece = 64 * VMAX;
-    constexpr long long kMaxLds = 64 * 1024;
     const long long padded = (a.K + kPiece - 1) / kPiece * kPiece;
-    const bool fits = padded * 4 <= kMaxLds;
+    const bool fits = padded * 4 <= kStagedLdsMax;
     if (fits && (RMS || a.N > one_round || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       if (a.K > 4096) {
@@ -243,10 +264,6 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream) {
 
 namespace {
 
-// Largest staged-rows LDS of a small-batch pass: fp16 weights take up to
-// 128 KiB (two rows at K = 11008, one 16-wave workgroup per CU), fp32 64 KiB.
-constexpr long long kMultiLdsMax = 128 * 1024;
-
 // One round of resident workgroups, each looping over blocks of WAVES x R
 // rows. fp16 weights: workgroups of 16 waves, one row per wave, one
 // workgroup per CU when the staged rows take more than 32 KiB of LDS, else
@@ -261,18 +278,10 @@ void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t str
       WAVES == 16 ? (lds_bytes <= 32 * 1024 ? 2 : 1)
                   : std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
   const long long wgs = std::min(blocks, per_cu * device_cu_count());
-  if (lds_bytes > 64 * 1024) {
-    // Past 64 KiB a kernel's dynamic LDS must be allowed explicitly (once per device).
-    static bool allowed[64] = {false};
-    int dev = 0;
-    ENG_HIP_CHECK(hipGetDevice(&dev));
-    if (dev < 0 || dev >= 64 || !allowed[dev]) {
-      ENG_HIP_CHECK(hipFuncSetAttribute(
-          reinterpret_cast<const void*>(&gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>),
-          hipFuncAttributeMaxDynamicSharedMemorySize, kMultiLdsMax));
-      if (dev >= 0 && dev < 64) allowed[dev] = true;
-    }
-  }
+  static bool allowed[64] = {false};
+  allow_staged_lds(
+      reinterpret_cast<const void*>(&gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>),
+      allowed, lds_bytes);
   gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>
       <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
@@ -316,7 +325,7 @@ bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream) 
   constexpr int kMultiRows = 4;
   constexpr long long kMaxPasses = 4;
   if (!a.w_nk || M < 1 || a.x_elem != Elem::F32 || a.y_elem != Elem::F32) return false;
-  const long long kMaxLds = a.w == Elem::F16 ? kMultiLdsMax : 64 * 1024;
+  const long long kMaxLds = a.w == Elem::F16 ? kStagedLdsMax : 64 * 1024;
   const long long vmax = a.w == Elem::F16 ? 8 : 4;
   const bool vec_ok = (a.K % vmax == 0) && aligned_to(a.W, 16) && aligned_to(a.x, 16) &&
                       (a.gamma == nullptr || aligned_to(a.gamma, 16));

@@ -537,11 +537,14 @@ def test_gemv_nk_shapes_against_oracle(gpu, orc, N, K, dtype):
     (333, 1000, True, True),     # ragged last piece, N not a multiple of 4 rows
     (333, 1000, True, False),    # null gain
     (4099, 520, True, True),     # N beyond one resident round, odd N: last 16-wave workgroup partly idle
-    (64, 16384, True, True),     # largest K whose staged vector fits 64 KiB of LDS
-    (64, 16392, True, True),     # just past it: register kernel fallback
+    (64, 16384, True, True),     # largest K whose staged vector fits the default 64 KiB of LDS
+    (64, 16392, True, True),     # just past it: LDS allowed up to 128 KiB
     (300, 8200, False, False),   # K > 4096 without RMSNorm: LDS-staged, 16 loads per row in flight
     (5000, 1000, False, False),  # many rows, small K: LDS-staged, 4 loads per row in flight
-    (64, 20000, False, False),   # LDS does not fit: register kernel, 4 loads in flight
+    (64, 20000, False, False),   # 80 KiB of staged x
+    (96, 32768, True, True),     # largest K whose staged vector fits 128 KiB
+    (64, 32776, True, False),    # just past it: register kernel fallback
+    (64, 40000, False, False),   # register kernel, 4 loads in flight
 ])
 def test_nk_fp16_kernel_selection_against_oracle(gpu, orc, N, K, rms, gamma):
     """Every output-major fp16 launch variant (LDS-staged x, register x,
