@@ -5,8 +5,9 @@
 // The reference composes this from rmsnorm, two GEMVs / GEMMs and swiglu
 // (tests/test_kernels.cu:2867-2898; its ADR 0006 defers fusing gate / up /
 // SwiGLU on one weight stream).
-//   * Output-major decode (M == 1, 16-byte aligned operands, K up to 16384)
-//     runs gemv_rows_glu_kernel: one launch that stages x * gamma in LDS,
+//   * Output-major decode (M == 1, 16-byte aligned operands, K up to 32768
+//     with fp16 weights, 16384 with fp32) runs gemv_rows_glu_kernel: one
+//     launch that stages x * gamma in LDS,
 //     streams each output's gate and up rows together and applies SiLU in the
 //     epilogue, so gate and up never reach memory. A few rows (small-batch
 //     decode) run gemv_rows_glu_multi_kernel: up to 4 rows per pass over Wg
@@ -43,7 +44,7 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
 
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
   constexpr long long kPiece = 64 * VEC;
-  constexpr long long kMaxLds = 64 * 1024;
+  constexpr long long kMaxLds = sizeof(WT) == 2 ? kStagedLdsMax : 64 * 1024;
   const long long padded = (K + kPiece - 1) / kPiece * kPiece;
   if (!nk) {
     // Reference layout, up to 16 rows: per pass of up to 4 rows, one stream
@@ -69,6 +70,9 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
     constexpr int WAVES = sizeof(WT) == 2 ? 16 : 4;
     const long long wgs = (N + WAVES - 1) / WAVES;
     ENG_CHECK(wgs <= 0x7fffffffLL, "rmsnorm_linear_swiglu: N too large for one launch");
+    static bool allowed[64] = {false};
+    allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>),
+                     allowed, static_cast<std::size_t>(padded) * 4);
     gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>
         <<<static_cast<unsigned>(wgs), WAVES * 64, static_cast<std::size_t>(padded) * 4, s>>>(
             Wg, Wu, in, gamma, act, N, K, eps);
@@ -76,7 +80,7 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
     return;
   }
   // Small batch: up to 4 rows per pass over Wg and Wu, at most 4 passes.
-  const long long fit = std::min<long long>(4, kMaxLds / (padded * 4));
+  const long long fit = std::min<long long>(4, (64 * 1024) / (padded * 4));  // 64 KiB of staged rows
   const bool multi = nk && M > 1 && fit >= 2 && (M + fit - 1) / fit <= 4 && K % VEC == 0 &&
                      aligned_to(Wg, 16) && aligned_to(Wu, 16) && aligned_to(in, 16) &&
                      (gamma == nullptr || aligned_to(gamma, 16));

@@ -127,23 +127,6 @@ void launch_rows(const GemvArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
 }
 
-// Largest dynamic LDS of the staged-activation kernels with fp16 weights:
-// 128 KiB (x of up to K = 32768 for one row, two rows at K = 11008 for a
-// small-batch pass; one 16-wave workgroup per CU past 64 KiB).
-constexpr long long kStagedLdsMax = 128 * 1024;
-
-// Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
-// device per kernel (`done` is that kernel's flag array).
-void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes) {
-  if (bytes <= 64 * 1024) return;
-  int dev = 0;
-  ENG_HIP_CHECK(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && done[dev]) return;
-  ENG_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    static_cast<int>(kStagedLdsMax)));
-  if (dev >= 0 && dev < 64) done[dev] = true;
-}
-
 // LDS-staged output-major launches: workgroups of WAVES waves, R rows per
 // wave, U loads per row in flight.
 template <typename WT, int R, int U, bool RMS, int WAVES>
@@ -209,6 +192,16 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes) {
+  if (bytes <= 64 * 1024) return;
+  int dev = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  if (dev >= 0 && dev < 64 && done[dev]) return;
+  ENG_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    static_cast<int>(kStagedLdsMax)));
+  if (dev >= 0 && dev < 64) done[dev] = true;
+}
 
 int device_cu_count() {
   static int cached[64] = {0};

@@ -29,6 +29,13 @@ struct GemvArgs {
   float eps = 0.0f;
 };
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
+// Largest dynamic LDS of the staged-activation kernels with fp16 weights:
+// 128 KiB (x of up to K = 32768 for one row, two rows at K = 11008 for a
+// small-batch pass; one 16-wave workgroup per CU past 64 KiB).
+constexpr long long kStagedLdsMax = 128 * 1024;
+// Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
+// device per kernel (`done` is that kernel's flag array); a no-op below.
+void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes);
 // Output-major W only: y[M x N] = x[M x K] . W^T for a few rows (x and y
 // row-major, pitches K and N; a.x / a.y point at row 0), in groups that share
 // a pass over W. Returns false, launching nothing, when the shape is better

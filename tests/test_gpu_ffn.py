@@ -276,7 +276,8 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (1, 300, 1000, "f16", True),     # ragged last piece
     (1, 257, 1024, "f32", True),     # fp32 weights: fused launch
     (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with arena scratch
-    (1, 64, 20000, "f16", True),     # K past the LDS budget: GEMV fallback
+    (1, 64, 20000, "f16", True),     # 80 KiB of staged x: fused launch past the default LDS size
+    (1, 64, 33000, "f16", True),     # K past the 128 KiB budget: GEMV fallback
     (5, 200, 512, "f16", True),      # small batch: multi-row GEMV passes + SwiGLU kernel
     (4, 11008, 4096, "f16", True),   # small batch at the config 5 gate/up shape
     (3, 300, 1000, "f32", False),    # small batch, fp32 weights, null gain
