@@ -60,6 +60,7 @@ SIGNATURES = {
     "eng_clock_rate_khz": [_pint],
     "eng_live_sm_clock_mhz": [_pint],
     "eng_live_mem_clock_mhz": [_pint],
+    "eng_live_clock_source": [ctypes.c_char_p, _sz],
     "eng_device_arch": [ctypes.c_char_p, _sz],
     "eng_device_cu_count": [_pint],
     "eng_malloc": [_pp, _sz],
@@ -221,6 +222,23 @@ class Engine:
         v = ctypes.c_int(0)
         self.call("eng_clock_rate_khz", ctypes.byref(v))
         return v.value
+
+    def live_clocks_mhz(self) -> tuple:
+        """(engine clock, memory clock) in MHz as the driver reports them now
+        (see eng_live_sm_clock_mhz; the memory clock is 0 when unreadable)."""
+        sm, mem = ctypes.c_int(0), ctypes.c_int(0)
+        self.call("eng_live_sm_clock_mhz", ctypes.byref(sm))
+        self.call("eng_live_mem_clock_mhz", ctypes.byref(mem))
+        return sm.value, mem.value
+
+    def live_clock_source(self) -> str:
+        return self._string("eng_live_clock_source")
+
+    def driver_version(self) -> str:
+        return self._string("eng_driver_version")
+
+    def build_info(self) -> str:
+        return self.lib.eng_build_info().decode()
 
     def sync(self) -> None:
         self.call("eng_device_sync")

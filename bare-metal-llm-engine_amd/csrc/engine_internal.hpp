@@ -17,6 +17,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace eng {
 
@@ -78,8 +79,12 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 // kernel pairs on it; take it before the first launch that writes the arena
 // and keep it past the last one that reads it. The arena grows to the largest
 // request (a new block; the outgrown one stays allocated for queued kernels
-// and captured graphs) and its blocks are freed when the stream is destroyed
-// through eng_stream_destroy, or at exit. Each
+// and HIP graphs captured on it) and its blocks are freed when the stream is
+// destroyed through eng_stream_destroy, or at exit. A graph captured on the
+// stream takes its blocks over at the end of the capture (adopt_stream_scratch)
+// and the stream continues on fresh blocks, so a replay never shares scratch
+// with eager calls or with another graph. Growing is refused while the stream
+// is capturing (allocation is not capturable). Each
 // (device, stream) has one arena per level: a launcher takes at most one lease
 // per level, and a composite launcher that keeps a lease while it calls other
 // launchers (the FFN's gate / up buffers around the GEMV launches, which may
@@ -98,6 +103,10 @@ class StreamScratch {
   void* ptr_ = nullptr;
 };
 void release_stream_scratch(hipStream_t stream);
+// Moves every block of `stream`'s scratch arenas (all levels, current and
+// outgrown) into `owned` and gives each arena a fresh block of its current
+// size. The caller (a captured graph) frees the moved blocks.
+void adopt_stream_scratch(hipStream_t stream, std::vector<void*>& owned);
 
 }  // namespace eng
 

@@ -78,10 +78,16 @@ StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes, int level) {
   }
   std::unique_lock<std::mutex> lock(arena->mu);
   if (bytes > arena->capacity) {
+    // Growing allocates, which a stream under HIP graph capture may not do:
+    // the capture needs an arena already sized by the same work run eagerly.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    ENG_HIP_CHECK(hipStreamIsCapturing(stream, &cap));
+    ENG_CHECK(cap == hipStreamCaptureStatusNone,
+              "stream scratch: this call needs a larger scratch arena than the capturing "
+              "stream has; run the same work once eagerly on this stream before capturing it");
     // The outgrown block stays allocated until the stream's arenas are
-    // released: queued kernels, and HIP graphs captured while it was current,
-    // still address it. (Doubling keeps the retired blocks below the current
-    // one's size in total.)
+    // released: queued kernels still address it. (Doubling keeps the retired
+    // blocks below the current one's size in total.)
     const std::size_t want = std::max({bytes, kMinArena, 2 * arena->capacity});
     void* grown = nullptr;
     ENG_HIP_CHECK(hipMalloc(&grown, want));
@@ -95,6 +101,30 @@ StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes, int level) {
 
 StreamScratch::~StreamScratch() {
   if (held_ != nullptr) held_->unlock();
+}
+
+void adopt_stream_scratch(hipStream_t stream, std::vector<void*>& owned) {
+  int dev = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  for (int level = 0; level < kScratchLevels; ++level) {
+    Arena* arena = nullptr;
+    {
+      std::lock_guard<std::mutex> lock(g_arenas_mu);
+      auto& m = arenas();
+      auto it = m.find(Key{dev, stream, level});
+      if (it == m.end()) continue;
+      arena = it->second.get();
+    }
+    std::lock_guard<std::mutex> lock(arena->mu);
+    if (arena->base == nullptr) continue;
+    // Fresh block first: if it cannot be allocated, the arena is unchanged.
+    void* fresh = nullptr;
+    ENG_HIP_CHECK(hipMalloc(&fresh, arena->capacity));
+    owned.push_back(arena->base);
+    owned.insert(owned.end(), arena->retired.begin(), arena->retired.end());
+    arena->retired.clear();
+    arena->base = fresh;
+  }
 }
 
 void release_stream_scratch(hipStream_t stream) {

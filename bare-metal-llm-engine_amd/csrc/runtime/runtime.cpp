@@ -6,8 +6,14 @@
 // (33-92), exposed as plain C functions.
 #include "../engine_internal.hpp"
 
+#include <dirent.h>
+
+#include <cctype>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <fstream>
+#include <memory>
 #include <sstream>
 #include <string>
 
@@ -68,6 +74,80 @@ double spec_peak_gbs(const hipDeviceProp_t& prop) {
   const double clock_hz = static_cast<double>(prop.memoryClockRate) * 1.0e3;
   const double bus_bytes = static_cast<double>(prop.memoryBusWidth) / 8.0;
   return clock_hz * bus_bytes * 2.0 / 1.0e9;
+}
+
+// sysfs directory of the current device's PCI function, e.g.
+// "/sys/bus/pci/devices/0000:75:00.0"; empty when the bus id is unknown.
+std::string pci_sysfs_dir() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return {};
+  }
+  char bus[64] = {0};
+  if (hipDeviceGetPCIBusId(bus, sizeof(bus), dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return {};
+  }
+  std::string id(bus);
+  for (char& c : id) c = static_cast<char>(std::tolower(static_cast<unsigned char>(c)));
+  return id.empty() ? std::string() : "/sys/bus/pci/devices/" + id;
+}
+
+// Current level of an amdgpu DPM table (pp_dpm_sclk / pp_dpm_mclk): lines
+// "<index>: <value>Mhz", the current one marked with '*'. Returns MHz, or 0
+// when the file is missing or has no marked line.
+int dpm_current_mhz(const std::string& path) {
+  std::ifstream f(path);
+  std::string line;
+  while (std::getline(f, line)) {
+    if (line.find('*') == std::string::npos) continue;
+    const std::size_t colon = line.find(':');
+    if (colon == std::string::npos) continue;
+    const long v = std::strtol(line.c_str() + colon + 1, nullptr, 10);
+    if (v > 0) return static_cast<int>(v);
+  }
+  return 0;
+}
+
+// hwmon frequency input of the device (freq1_input = engine clock, freq2_input
+// = memory clock, in Hz). Returns MHz or 0.
+int hwmon_mhz(const std::string& dir, const char* file) {
+  DIR* d = opendir((dir + "/hwmon").c_str());
+  if (d == nullptr) return 0;
+  int mhz = 0;
+  while (dirent* e = readdir(d)) {
+    if (std::strncmp(e->d_name, "hwmon", 5) != 0) continue;
+    std::ifstream f(dir + "/hwmon/" + e->d_name + "/" + file);
+    long long hz = 0;
+    if (f >> hz && hz > 0) {
+      mhz = static_cast<int>(hz / 1000000);
+      break;
+    }
+  }
+  closedir(d);
+  return mhz;
+}
+
+// Live clock in MHz and where it came from: the DPM table's current level,
+// else the hwmon input, else 0 ("unavailable").
+int live_clock_mhz(bool engine_clock, std::string* source) {
+  const std::string dir = pci_sysfs_dir();
+  if (!dir.empty()) {
+    const std::string dpm = dir + (engine_clock ? "/pp_dpm_sclk" : "/pp_dpm_mclk");
+    int mhz = dpm_current_mhz(dpm);
+    if (mhz > 0) {
+      if (source) *source = dpm;
+      return mhz;
+    }
+    mhz = hwmon_mhz(dir, engine_clock ? "freq1_input" : "freq2_input");
+    if (mhz > 0) {
+      if (source) *source = dir + "/hwmon/*/" + (engine_clock ? "freq1_input" : "freq2_input");
+      return mhz;
+    }
+  }
+  if (source) *source = "unavailable";
+  return 0;
 }
 
 }  // namespace
@@ -154,7 +234,9 @@ int eng_live_sm_clock_mhz(int* mhz) {
     ENG_CHECK(mhz != nullptr, "eng_live_sm_clock_mhz: mhz is null");
     *mhz = 0;
     if (eng::device_count_or_zero() == 0) return;
-    hipDeviceProp_t prop{};
+    *mhz = eng::live_clock_mhz(true, nullptr);
+    if (*mhz > 0) return;
+    hipDeviceProp_t prop{};  // no live source: the nominal clock, as the reference falls back
     eng::current_props(prop);
     *mhz = prop.clockRate / 1000;
   });
@@ -165,9 +247,21 @@ int eng_live_mem_clock_mhz(int* mhz) {
     ENG_CHECK(mhz != nullptr, "eng_live_mem_clock_mhz: mhz is null");
     *mhz = 0;
     if (eng::device_count_or_zero() == 0) return;
-    hipDeviceProp_t prop{};
-    eng::current_props(prop);
-    *mhz = prop.memoryClockRate / 1000;
+    *mhz = eng::live_clock_mhz(false, nullptr);
+  });
+}
+
+int eng_live_clock_source(char* buf, size_t len) {
+  return guarded([&] {
+    if (eng::device_count_or_zero() == 0) {
+      eng::copy_out("no HIP device", buf, len);
+      return;
+    }
+    std::string sclk;
+    std::string mclk;
+    (void)eng::live_clock_mhz(true, &sclk);
+    (void)eng::live_clock_mhz(false, &mclk);
+    eng::copy_out("engine clock: " + sclk + "; memory clock: " + mclk, buf, len);
   });
 }
 
@@ -328,9 +422,12 @@ int eng_event_destroy(eng_event event) {
 }
 
 namespace {
+// A captured graph with the scratch blocks its kernels address: taken over
+// from the capture stream's arenas when the capture ends, freed with the graph.
 struct GraphHandle {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  std::vector<void*> scratch;
 };
 }  // namespace
 
@@ -355,7 +452,18 @@ int eng_graph_capture_end(eng_stream stream, eng_graph* graph) {
       (void)hipGraphDestroy(g);
       ENG_HIP_CHECK(err);
     }
-    *graph = reinterpret_cast<eng_graph>(new GraphHandle{g, exec});
+    auto h = std::make_unique<GraphHandle>();
+    h->graph = g;
+    h->exec = exec;
+    try {
+      eng::adopt_stream_scratch(eng::as_stream(stream), h->scratch);
+    } catch (...) {
+      (void)hipGraphExecDestroy(exec);
+      (void)hipGraphDestroy(g);
+      for (void* p : h->scratch) (void)hipFree(p);
+      throw;
+    }
+    *graph = reinterpret_cast<eng_graph>(h.release());
   });
 }
 
@@ -371,9 +479,14 @@ int eng_graph_destroy(eng_graph graph) {
   return guarded([&] {
     if (graph == nullptr) return;
     auto* h = reinterpret_cast<GraphHandle*>(graph);
+    // Replays may still be queued on any stream: wait for the device before
+    // freeing the scratch they address.
+    const hipError_t e0 = h->scratch.empty() ? hipSuccess : hipDeviceSynchronize();
     const hipError_t e1 = hipGraphExecDestroy(h->exec);
     const hipError_t e2 = hipGraphDestroy(h->graph);
+    for (void* p : h->scratch) (void)hipFree(p);
     delete h;
+    ENG_HIP_CHECK(e0);
     ENG_HIP_CHECK(e1);
     ENG_HIP_CHECK(e2);
   });

@@ -6,7 +6,10 @@
 //   * engine::EngineError (a std::runtime_error) for every failure, with the
 //     message "[engine] <file>:<line>\n  check failed: <expr>\n  <message>";
 //   * ENGINE_CHECK: always-on precondition; ENGINE_ASSERT: debug-only;
-//   * HIP_CHECK wraps HIP runtime calls made by user code;
+//   * HIP_CHECK wraps HIP runtime calls made by user code; HIP_CHECK_KERNEL,
+//     placed after a kernel launch, reports launch errors and -- in debug
+//     builds or with ENGINE_ALWAYS_SYNC_CHECK -- synchronises so an in-kernel
+//     fault is attributed to that line (CUDA_CHECK_KERNEL, :94-107);
 //   * ENGINE_ABI_CHECK turns a non-zero status of the engine's C-ABI into an
 //     EngineError carrying the library's own message (eng_last_error()).
 //===----------------------------------------------------------------------===//
@@ -67,5 +70,18 @@ inline void check_status(int status) {
 #endif
 
 #define HIP_CHECK(call) ::engine::detail::check_hip((call), __FILE__, __LINE__, #call)
+
+// After a kernel launch in user code: the launch-configuration error always;
+// in debug builds (or with ENGINE_ALWAYS_SYNC_CHECK) also a device
+// synchronisation, so execution faults surface at this line.
+#if !defined(NDEBUG) || defined(ENGINE_ALWAYS_SYNC_CHECK)
+#define HIP_CHECK_KERNEL()                  \
+  do {                                      \
+    HIP_CHECK(hipGetLastError());           \
+    HIP_CHECK(hipDeviceSynchronize());      \
+  } while (0)
+#else
+#define HIP_CHECK_KERNEL() HIP_CHECK(hipGetLastError())
+#endif
 
 #define ENGINE_ABI_CHECK(call) ::engine::detail::check_status(call)

@@ -78,11 +78,15 @@ int eng_device_summary(char* buf, size_t len);
 int eng_peak_bandwidth_gbs(double* gbs);
 int eng_driver_version(char* buf, size_t len);
 int eng_clock_rate_khz(int* khz);
-/* Live clocks are not readable without an SMI library; these report the
- * nominal clocks (the reference falls back the same way when NVML is
- * absent, src/cuda_device.cpp:196-222). */
+/* Live clocks in MHz, read on each call from the amdgpu driver's sysfs node
+ * of the device's PCI function: the current level of pp_dpm_sclk /
+ * pp_dpm_mclk, else the hwmon freq1_input / freq2_input. Without either, the
+ * engine clock falls back to the nominal clock and the memory clock reports 0,
+ * as the reference does without NVML (src/cuda_device.cpp:196-222).
+ * eng_live_clock_source names the files read ("unavailable" for a fallback). */
 int eng_live_sm_clock_mhz(int* mhz);
 int eng_live_mem_clock_mhz(int* mhz);
+int eng_live_clock_source(char* buf, size_t len);
 /* Architecture the device reports (e.g. "gfx950:sramecc+:xnack-"). */
 int eng_device_arch(char* buf, size_t len);
 int eng_device_cu_count(int* cus);
@@ -134,8 +138,18 @@ int eng_event_elapsed_ms(float* ms, eng_event start, eng_event end);
  * eng_graph_launch replays it on any stream. Every launcher here is
  * capture-safe once it has run eagerly on that stream at least once with
  * shapes at least as large (the stream's scratch arena is sized outside the
- * capture; zero fills are kernels, not memsets). A failed capture returns an
- * error and leaves no graph; the stream is no longer capturing either way.
+ * capture -- a call that would have to grow it during capture fails with a
+ * message saying so; zero fills are kernels, not memsets). A failed capture
+ * returns an error and leaves no graph; the stream is no longer capturing
+ * either way.
+ * Scratch: at capture end the graph takes over the blocks of the capture
+ * stream's scratch arenas that its kernels address, and the stream continues
+ * on fresh blocks of the same sizes. A replay therefore shares no scratch with
+ * eager calls on the capture stream or with any other graph, may run on any
+ * stream, and stays valid after the capture stream is destroyed. Replays of
+ * one graph share its blocks: they must not overlap (issue them on one
+ * stream, or order them with events). eng_graph_destroy waits for the device
+ * before freeing the graph's blocks.
  * ---------------------------------------------------------------------- */
 typedef void* eng_graph;
 int eng_graph_capture_begin(eng_stream stream);

@@ -367,6 +367,27 @@ TEST(gpu_runtime, device_summary_and_buffer_round_trip) {
   Tensor back = g.clone().to(Device::CPU);
   EXPECT_EQ(back.ptr<float>(Device::CPU)[19], 19.0f);
   EXPECT_THROWS_MSG(g.transpose(0, 1).contiguous(), "not supported");
+  // live clocks: the engine clock is positive (live, or the nominal fallback);
+  // the source names what was read
+  EXPECT_TRUE(engine::hip_live_sm_clock_mhz() > 0);
+  EXPECT_TRUE(engine::hip_live_mem_clock_mhz() >= 0);
+  char src[512];
+  ENGINE_ABI_CHECK(eng_live_clock_source(src, sizeof(src)));
+  EXPECT_TRUE(std::string(src).find("engine clock: ") == 0);
+  std::printf("  live clocks: %d / %d MHz (%s)\n", engine::hip_live_sm_clock_mhz(),
+              engine::hip_live_mem_clock_mhz(), src);
+}
+
+TEST(gpu_runtime, hip_check_kernel_after_a_launch) {
+  require_gpu(ctx);
+  std::vector<float> A(64 * 32, 0.5f), x(64, 2.0f);
+  engine::DeviceBuffer<float> dA(A), dx(x), dy(32);
+  engine::cuda::gemv(dA.get(), dx.get(), dy.get(), 32, 64);
+  EXPECT_NO_THROW([] { HIP_CHECK_KERNEL(); }());
+  HIP_CHECK(hipDeviceSynchronize());
+  EXPECT_EQ(dy.download()[31], 64.0f);
+  // a HIP error reported through HIP_CHECK carries the runtime's name for it
+  EXPECT_THROWS_MSG(HIP_CHECK(hipErrorInvalidValue), "hipErrorInvalidValue");
 }
 
 TEST(gpu_allocator, pool_allocates_and_recycles_device_memory) {

@@ -3,7 +3,9 @@
 The launchers are meant to be capturable: zero fills are kernels, and the
 scratch they pass between their kernels (split-K GEMV and split-KV attention
 partials, rmsnorm_linear's normalised rows at M > 1, the FFN's gate / up) is
-the stream's arena, sized by an eager call before the capture. The graph is
+the stream's arena, sized by an eager call before the capture; the graph takes
+those blocks over when the capture ends, so replays on other streams never
+share scratch with eager calls (checked against the oracle below). The graph is
 replayed several times with the program's own eager work and synchronisations
 in between -- outputs clobbered, other launches on the same stream, an input
 changed in place -- and every replay must equal the eager result bit for bit
@@ -103,8 +105,8 @@ def test_captured_decode_step_replays_match_eager(gpu):
 
 def test_graph_replays_after_the_stream_arena_grows(gpu):
     # A graph captured on a small split-K call keeps addressing the arena block
-    # it was captured on after a larger call on the same stream outgrows that
-    # block: the outgrown block stays allocated until the stream is destroyed.
+    # it was captured on after a larger call on the same stream outgrows the
+    # stream's arena: the graph owns the blocks it was captured on.
     rng = np.random.default_rng(8)
     K, N = 512, 1024
     W = gpu.upload(f16(gpu, 0.03 * rng.standard_normal((K, N))))      # [in x out]: split-K
@@ -142,3 +144,126 @@ def test_graph_replays_after_the_stream_arena_grows(gpu):
 def test_capture_on_the_null_stream_is_refused(gpu):
     assert gpu.status("eng_graph_capture_begin", None) == 1
     assert "capture needs a created stream" in gpu.last_error()
+
+
+def _kn_case(gpu, orc, rng, K, N, M):
+    """Reference-layout fp16 RMSNorm+linear inputs (split-K: scratch partials)."""
+    W16 = f16(gpu, 0.02 * rng.standard_normal((K, N)))
+    gam = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    return W16, gam, x
+
+
+def _check_kn(got, x, gam, W16, K, what):
+    import helpers
+
+    y64 = helpers.as_f64(helpers.oracle(0).rmsnorm_linear(x, gam, W16, EPS))
+    derived, _ = helpers.rmsnorm_linear_bounds(x, gam, W16, y64, K)
+    helpers.assert_within(got, y64, derived, what)
+
+
+def test_graph_replayed_on_another_stream_while_eager_calls_run(gpu, orc):
+    # The graph owns the scratch blocks it was captured on; eager calls on the
+    # capture stream continue on fresh blocks. Replays on a second stream
+    # interleaved with eager calls (different inputs, no synchronisation in
+    # between) must each match the oracle for their own inputs.
+    rng = np.random.default_rng(21)
+    K, N, M = 4096, 4096, 4            # split-K partials for 4 rows: 4 MiB of scratch
+    W16, gam, xg = _kn_case(gpu, orc, rng, K, N, M)
+    xe = rng.standard_normal((M, K)).astype(np.float32)
+    dW, dg = gpu.upload(W16), gpu.upload(gam)
+    dxg, dxe = gpu.upload(xg), gpu.upload(xe)
+    yg = gpu.empty((M, N), np.float32)
+    ye = [gpu.empty((M, N), np.float32) for _ in range(4)]
+    a, b = gpu.stream(), gpu.stream()
+    graph = None
+    try:
+        gpu.call("eng_rmsnorm_linear_f16w", dxg.ptr, dg.ptr, dW.ptr, yg.ptr, M, N, K, EPS, a.handle)
+        a.sync()
+        graph = gpu.graph(a)
+        with graph:
+            gpu.call("eng_rmsnorm_linear_f16w", dxg.ptr, dg.ptr, dW.ptr, yg.ptr, M, N, K, EPS,
+                     a.handle)
+        for rep in range(3):
+            gpu.call("eng_memset", yg.ptr, 0xFF, yg.nbytes)
+            for y in ye:
+                gpu.call("eng_memset", y.ptr, 0xFF, y.nbytes)
+            for i, y in enumerate(ye):
+                gpu.call("eng_rmsnorm_linear_f16w", dxe.ptr, dg.ptr, dW.ptr, y.ptr, M, N, K, EPS,
+                         a.handle)
+                if i == 1:
+                    graph.launch(b)
+            a.sync()
+            b.sync()
+            _check_kn(yg.download(), xg, gam, W16, K, f"graph replay {rep} on a second stream")
+            for i, y in enumerate(ye):
+                _check_kn(y.download(), xe, gam, W16, K, f"eager call {i} during replay {rep}")
+    finally:
+        if graph is not None:
+            graph.destroy()
+        a.destroy()
+        b.destroy()
+
+
+def test_graph_outlives_its_capture_stream(gpu, orc):
+    rng = np.random.default_rng(22)
+    K, N, M = 2048, 3072, 1
+    W16, gam, x = _kn_case(gpu, orc, rng, K, N, M)
+    dW, dg, dx = gpu.upload(W16), gpu.upload(gam), gpu.upload(x)
+    y = gpu.empty((M, N), np.float32)
+    a, b = gpu.stream(), gpu.stream()
+    graph = None
+    try:
+        gpu.call("eng_rmsnorm_linear_f16w", dx.ptr, dg.ptr, dW.ptr, y.ptr, M, N, K, EPS, a.handle)
+        a.sync()
+        graph = gpu.graph(a)
+        with graph:
+            gpu.call("eng_rmsnorm_linear_f16w", dx.ptr, dg.ptr, dW.ptr, y.ptr, M, N, K, EPS,
+                     a.handle)
+        a.destroy()                      # frees the stream's own blocks, not the graph's
+        for rep in range(3):
+            gpu.call("eng_memset", y.ptr, 0xFF, y.nbytes)
+            graph.launch(b)
+            b.sync()
+            _check_kn(y.download(), x, gam, W16, K, f"replay {rep} after the capture stream died")
+    finally:
+        if graph is not None:
+            graph.destroy()
+        a.destroy()
+        b.destroy()
+
+
+def test_capture_that_would_grow_the_arena_is_refused(gpu):
+    # A fresh stream has no scratch arena yet: a split-K call captured before
+    # any eager call would have to allocate during the capture.
+    rng = np.random.default_rng(23)
+    K, N = 1024, 1024
+    W = gpu.upload(f16(gpu, 0.03 * rng.standard_normal((K, N))))
+    x = gpu.upload(rng.standard_normal(K).astype(np.float32))
+    y = gpu.empty(N, np.float32)
+    s = gpu.stream()
+    try:
+        gpu.call("eng_graph_capture_begin", s.handle)
+        rc = gpu.status("eng_gemv_f16w", W.ptr, x.ptr, y.ptr, N, K, s.handle)
+        msg = gpu.last_error()
+        import ctypes
+
+        h = ctypes.c_void_p(0)
+        if gpu.status("eng_graph_capture_end", s.handle, ctypes.byref(h)) == 0 and h.value:
+            gpu.call("eng_graph_destroy", h.value)
+        assert rc == 1, f"status {rc}: {msg}"
+        assert "run the same work once eagerly on this stream before capturing" in msg
+        # after an eager call, the same capture works
+        gpu.call("eng_gemv_f16w", W.ptr, x.ptr, y.ptr, N, K, s.handle)
+        s.sync()
+        eager = y.download().copy()
+        g = gpu.graph(s)
+        with g:
+            gpu.call("eng_gemv_f16w", W.ptr, x.ptr, y.ptr, N, K, s.handle)
+        gpu.call("eng_memset", y.ptr, 0, y.nbytes)
+        g.launch()
+        s.sync()
+        g.destroy()
+        assert np.array_equal(y.download(), eager)
+    finally:
+        s.destroy()
