@@ -107,6 +107,7 @@ SIGNATURES = {
     "eng_rmsnorm_f32": [_p, _p, _p, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_f32": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_f16w": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
+    "eng_rmsnorm_linear_f16w_noalloc": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_rmsnorm_linear_fused_direct_f32": [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p],
     "eng_gemv_f16w_nk": [_p, _p, _p, _i64, _i64, _p],
     "eng_gemv_f32_nk": [_p, _p, _p, _i64, _i64, _p],

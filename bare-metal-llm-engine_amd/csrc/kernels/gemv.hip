@@ -19,6 +19,8 @@
 
 #include <algorithm>
 #include <cstddef>
+#include <memory>
+#include <string>
 
 namespace eng {
 namespace {
@@ -88,8 +90,19 @@ void run_kn(const GemvArgs& a, hipStream_t stream) {
     return;
   }
   // fp32 partial sums [nsplit x MX x N], then partial sums of squares [nsplit x MX].
-  StreamScratch ws(stream, static_cast<std::size_t>(nsplit) * MX * (N + 1) * sizeof(float));
-  float* partials = static_cast<float*>(ws.get());
+  const std::size_t need = static_cast<std::size_t>(nsplit) * MX * (N + 1) * sizeof(float);
+  float* partials = nullptr;
+  std::unique_ptr<StreamScratch> ws;
+  if (a.scratch != nullptr) {
+    ENG_CHECK(need <= a.scratch_bytes,
+              "gemv: the split-K partial sums need " + std::to_string(need) +
+                  " bytes of scratch, more than the " + std::to_string(a.scratch_bytes) +
+                  " bytes provided");
+    partials = static_cast<float*>(a.scratch);
+  } else {
+    ws = std::make_unique<StreamScratch>(stream, need);
+    partials = static_cast<float*>(ws->get());
+  }
   float* partial_ss = partials + nsplit * MX * N;
   gemv_stream_kernel<WT, XT, YT, VEC, LPR, WAVES, U, true, RMS, true, MX>
       <<<static_cast<unsigned>(ncb * nsplit), WAVES * 64, 0, stream>>>(
@@ -113,6 +126,25 @@ void dispatch_kn(const GemvArgs& a, hipStream_t stream) {
   } else {
     run_kn<WT, XT, YT, 1, 64, 4, 8, RMS, MX>(a, stream);
   }
+}
+
+// Scratch bytes run_kn takes for mx activation rows with the configuration
+// dispatch_kn picks (0 when the K split is 1).
+std::size_t kn_scratch_bytes_for(const GemvArgs& a, long long mx) {
+  const long long wsize = a.w == Elem::F16 ? 2 : 4;
+  const long long vmax = 16 / wsize;
+  const bool vec_ok = (a.N % vmax == 0) && aligned_to(a.W, 16);
+  const long long lpr = vec_ok ? 32 : 64;
+  const long long vec = vec_ok ? vmax : 1;
+  const long long waves = vec_ok ? 8 : 4;
+  const long long u = vec_ok ? 4 : 8;
+  const long long step = waves * (64 / lpr);
+  const long long ncb = (a.N + lpr * vec - 1) / (lpr * vec);
+  long long nsplit = 0;
+  long long kchunk = 0;
+  kn_split(ncb, a.K, step, u, device_cu_count(), nsplit, kchunk);
+  if (nsplit == 1) return 0;
+  return static_cast<std::size_t>(nsplit) * mx * (a.N + 1) * sizeof(float);
 }
 
 // Output-major register-kernel launches: 256-thread workgroups of 4 waves, R
@@ -370,6 +402,10 @@ void kn_rows(const GemvArgs& a, int mx, hipStream_t stream) {
 }
 
 }  // namespace
+
+std::size_t gemv_kn_scratch_bytes(const GemvArgs& a, std::int64_t M) {
+  return kn_scratch_bytes_for(a, std::min<std::int64_t>(M, 4));
+}
 
 // Small-batch decode with reference-layout weights A [K x N]: y[M x N] =
 // x[M x K] . A, up to 4 rows per pass over A (the split-K kernel with MX

@@ -5,6 +5,7 @@
 
 #include "../engine_internal.hpp"
 
+#include <cstddef>
 #include <cstdint>
 
 namespace eng {
@@ -27,6 +28,11 @@ struct GemvArgs {
   std::int64_t K = 0;
   bool rms = false;
   float eps = 0.0f;
+  // Caller-provided device scratch for the reference-layout split-K partial
+  // sums (used instead of the stream's arena when set; a launch that needs
+  // more than scratch_bytes fails with an error and launches nothing).
+  void* scratch = nullptr;
+  std::size_t scratch_bytes = 0;
 };
 void launch_gemv(const GemvArgs& a, hipStream_t stream);
 // Largest dynamic LDS of the staged-activation kernels with fp16 weights:
@@ -43,6 +49,10 @@ void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes);
 bool launch_gemv_nk_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
 // Reference-layout W [K x N] counterpart of launch_gemv_nk_rows.
 bool launch_gemv_kn_rows(const GemvArgs& a, std::int64_t M, hipStream_t stream);
+// Largest scratch (bytes) that launch_gemv / launch_gemv_kn_rows take for the
+// split-K partial sums of a reference-layout call over M rows (M <= 16; the
+// first pass, of min(M, 4) rows, needs the most).
+std::size_t gemv_kn_scratch_bytes(const GemvArgs& a, std::int64_t M);
 // Reference-layout gate / up + SwiGLU for M decode rows: a.y = SiLU(RMSNorm(a.x)
 // . a.W) * (RMSNorm(a.x) . Wu), equal bit for bit to the two RMSNorm + linear
 // calls and swiglu. Returns false, launching nothing, for more than 16 rows or

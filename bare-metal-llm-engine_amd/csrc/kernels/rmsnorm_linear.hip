@@ -17,9 +17,39 @@
 #include "launch.hpp"
 
 #include <cstddef>
+#include <mutex>
+#include <string>
 
 namespace eng {
 namespace {
+
+// Scratch of eng_rmsnorm_linear_f16w_noalloc: the split-K partial sums of up
+// to 4 rows per pass, [nsplit][4][N] plus [nsplit][4] sums of squares, where
+// nsplit * N <= 4 x CUs x 256 (one round of 4 workgroups per CU, 256 fp16
+// columns each): 4 MiB on a 256-CU MI355X, plus 64 KiB for the sums of
+// squares and the split rounding. Each device holds its own copy for the
+// life of the process.
+constexpr std::size_t kNoAllocScratchBytes = (std::size_t{4} << 20) + (std::size_t{64} << 10);
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the host-side name is a stand-in, never a device address).
+void* noalloc_scratch_ptr() {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {nullptr};
+  int dev = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  ENG_CHECK(dev >= 0 && dev < kMaxDevices, "rmsnorm_linear_f16w_noalloc: device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (ptrs[dev] == nullptr) {
+    void* p = nullptr;
+    ENG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    ENG_CHECK(p != nullptr, "rmsnorm_linear_f16w_noalloc: no device address for the scratch");
+    ptrs[dev] = p;
+  }
+  return ptrs[dev];
+}
 
 void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W, Elem w_elem,
                         bool nk, float* out, int64_t M, int64_t N, int64_t K, float eps,
@@ -62,10 +92,59 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
   launch_gemm(g, s);
 }
 
+// rmsnorm_linear_any for reference-layout fp16 W and M <= 16 rows, with the
+// split-K partial sums in the static `scratch` instead of the stream's arena:
+// no allocation of any kind. The kernels and their configuration are
+// eng_rmsnorm_linear_f16w's, so the results are the same bits.
+void rmsnorm_linear_f16w_noalloc(const float* in, const float* rms_weight, const void* W,
+                                 float* out, int64_t M, int64_t N, int64_t K, float eps,
+                                 eng_stream stream) {
+  ENG_CHECK(M >= 0 && N >= 0 && K >= 0, "rmsnorm_linear: negative dimension");
+  ENG_CHECK(in != nullptr && W != nullptr && out != nullptr,
+            "rmsnorm_linear: null device pointer");
+  ENG_CHECK(eps >= 0.0f, "rmsnorm_linear: eps must be non-negative");
+  ENG_CHECK(M <= 16, "rmsnorm_linear_f16w_noalloc: at most 16 rows (M = " + std::to_string(M) +
+                         "); larger batches need eng_rmsnorm_linear_f16w");
+  if (M == 0 || N == 0 || K == 0) return;
+  GemvArgs g1;
+  g1.W = W;
+  g1.w = Elem::F16;
+  g1.w_nk = false;
+  g1.x = in;
+  g1.gamma = rms_weight;
+  g1.y = out;
+  g1.N = N;
+  g1.K = K;
+  g1.rms = true;
+  g1.eps = eps;
+  const std::size_t need = gemv_kn_scratch_bytes(g1, M);
+  ENG_CHECK(need <= kNoAllocScratchBytes,
+            "rmsnorm_linear_f16w_noalloc: this shape needs " + std::to_string(need) +
+                " bytes of scratch, more than the static " +
+                std::to_string(kNoAllocScratchBytes) + " bytes");
+  g1.scratch = noalloc_scratch_ptr();
+  g1.scratch_bytes = kNoAllocScratchBytes;
+  hipStream_t s = as_stream(stream);
+  if (M == 1) {
+    launch_gemv(g1, s);
+    return;
+  }
+  const bool launched = launch_gemv_kn_rows(g1, M, s);
+  ENG_CHECK(launched, "rmsnorm_linear_f16w_noalloc: internal error (small-batch path refused)");
+}
+
 }  // namespace
 }  // namespace eng
 
 extern "C" {
+
+int eng_rmsnorm_linear_f16w_noalloc(const float* in, const float* rms_weight, const eng_half* W,
+                                    float* out, int64_t M, int64_t N, int64_t K, float eps,
+                                    eng_stream stream) {
+  return eng::guarded([&] {
+    eng::rmsnorm_linear_f16w_noalloc(in, rms_weight, W, out, M, N, K, eps, stream);
+  });
+}
 
 int eng_rmsnorm_linear_f32(const float* in, const float* rms_weight, const float* W, float* out,
                            int64_t M, int64_t N, int64_t K, float eps, eng_stream stream) {

@@ -251,6 +251,20 @@ int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_
                             float* out, int64_t M, int64_t N, int64_t K, float eps,
                             eng_stream stream);
 
+/* eng_rmsnorm_linear_f16w for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): no counterpart in the reference. Same arguments, kernels and
+ * bits as eng_rmsnorm_linear_f16w, for M <= 16 rows (decode and small
+ * batches); the split-K partial sums live in a static device buffer of
+ * 4 MiB + 64 KiB per GPU, held until the process ends, instead of the stream's
+ * scratch arena. Nothing is allocated. Fails with a message (status 1) for
+ * M > 16 or a shape whose partial sums would exceed the buffer. Every call on
+ * a GPU shares that GPU's buffer: calls that overlap on one GPU (different
+ * streams or host threads without ordering) race, so order them. */
+int eng_rmsnorm_linear_f16w_noalloc(const float* in, const float* rms_weight, const eng_half* W,
+                                    float* out, int64_t M, int64_t N, int64_t K, float eps,
+                                    eng_stream stream);
+
 /* Output-major weights (no reference counterpart; additive). W is row-major
  * [N x K] -- one contiguous row of K weights per output, the layout of the
  * decode configurations "y = W.x, W [out x in]" -- and
