@@ -26,6 +26,7 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 
 namespace eng {
@@ -70,7 +71,7 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
     constexpr int WAVES = sizeof(WT) == 2 ? 16 : 4;
     const long long wgs = (N + WAVES - 1) / WAVES;
     ENG_CHECK(wgs <= 0x7fffffffLL, "rmsnorm_linear_swiglu: N too large for one launch");
-    static bool allowed[64] = {false};
+    static std::atomic<bool> allowed[64] = {};
     allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>),
                      allowed, static_cast<std::size_t>(padded) * 4);
     gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>

@@ -18,6 +18,7 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <atomic>
 #include <cstddef>
 #include <memory>
 #include <string>
@@ -166,7 +167,7 @@ void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t strea
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
   const long long wgs = ((a.N + R - 1) / R + WAVES - 1) / WAVES;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
-  static bool allowed[64] = {false};
+  static std::atomic<bool> allowed[64] = {};
   allow_staged_lds(reinterpret_cast<const void*>(&gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>),
                    allowed, lds_bytes);
   gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>
@@ -225,25 +226,31 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes) {
+// Per-device flags and counts shared by host threads: relaxed atomics (two
+// threads may both set the attribute or read the count once; both are
+// idempotent).
+void allow_staged_lds(const void* kernel, std::atomic<bool> (&done)[64], std::size_t bytes) {
   if (bytes <= 64 * 1024) return;
   int dev = 0;
   ENG_HIP_CHECK(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && done[dev]) return;
+  if (dev >= 0 && dev < 64 && done[dev].load(std::memory_order_relaxed)) return;
   ENG_HIP_CHECK(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                     static_cast<int>(kStagedLdsMax)));
-  if (dev >= 0 && dev < 64) done[dev] = true;
+  if (dev >= 0 && dev < 64) done[dev].store(true, std::memory_order_relaxed);
 }
 
 int device_cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   ENG_HIP_CHECK(hipGetDevice(&dev));
-  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev >= 0 && dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   ENG_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   if (cus <= 0) cus = 1;
-  if (dev >= 0 && dev < 64) cached[dev] = cus;
+  if (dev >= 0 && dev < 64) cached[dev].store(cus, std::memory_order_relaxed);
   return cus;
 }
 
@@ -303,7 +310,7 @@ void launch_rows_multi(const GemvArgs& a, std::size_t lds_bytes, hipStream_t str
       WAVES == 16 ? (lds_bytes <= 32 * 1024 ? 2 : 1)
                   : std::max<long long>(1, std::min<long long>(4, (160LL * 1024) / static_cast<long long>(lds_bytes + 64)));
   const long long wgs = std::min(blocks, per_cu * device_cu_count());
-  static bool allowed[64] = {false};
+  static std::atomic<bool> allowed[64] = {};
   allow_staged_lds(
       reinterpret_cast<const void*>(&gemv_rows_lds_multi_kernel<WT, VEC, R, 4, MX, RMS, WAVES>),
       allowed, lds_bytes);

@@ -5,6 +5,7 @@
 
 #include "../engine_internal.hpp"
 
+#include <atomic>
 #include <cstddef>
 #include <cstdint>
 
@@ -41,7 +42,7 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream);
 constexpr long long kStagedLdsMax = 128 * 1024;
 // Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
 // device per kernel (`done` is that kernel's flag array); a no-op below.
-void allow_staged_lds(const void* kernel, bool (&done)[64], std::size_t bytes);
+void allow_staged_lds(const void* kernel, std::atomic<bool> (&done)[64], std::size_t bytes);
 // Output-major W only: y[M x N] = x[M x K] . W^T for a few rows (x and y
 // row-major, pitches K and N; a.x / a.y point at row 0), in groups that share
 // a pass over W. Returns false, launching nothing, when the shape is better
