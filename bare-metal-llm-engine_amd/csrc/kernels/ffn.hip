@@ -71,6 +71,19 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
     constexpr int WAVES = sizeof(WT) == 2 ? 16 : 4;
     const long long wgs = (N + WAVES - 1) / WAVES;
     ENG_CHECK(wgs <= 0x7fffffffLL, "rmsnorm_linear_swiglu: N too large for one launch");
+    const std::size_t lds = static_cast<std::size_t>(padded) * 4;
+    if constexpr (sizeof(WT) == 2) {
+      // fixed-K form for common widths (unmasked loads, 2 x CH2 in flight)
+      const bool fixed = with_fixed_k_f16(K, [&](auto fk) {
+        using F = decltype(fk);
+        auto kern = gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES, F::NP, F::KT, F::CH2>;
+        static std::atomic<bool> allowed_fixed[64] = {};
+        allow_staged_lds(reinterpret_cast<const void*>(kern), allowed_fixed, lds);
+        kern<<<static_cast<unsigned>(wgs), WAVES * 64, lds, s>>>(Wg, Wu, in, gamma, act, N, K, eps);
+        ENG_LAUNCH_CHECK();
+      });
+      if (fixed) return;
+    }
     static std::atomic<bool> allowed[64] = {};
     allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES>),
                      allowed, static_cast<std::size_t>(padded) * 4);

@@ -161,16 +161,21 @@ void launch_rows(const GemvArgs& a, hipStream_t stream) {
 }
 
 // LDS-staged output-major launches: workgroups of WAVES waves, R rows per
-// wave, U loads per row in flight.
-template <typename WT, int R, int U, bool RMS, int WAVES>
+// wave, U loads per row in flight; NP > 0 selects the fixed-K form (K must be
+// (NP - 1) * 512 + KT, groups of CH pieces).
+template <typename WT, int R, int U, bool RMS, int WAVES, int NP = 0, int KT = 0, int CH = 0>
 void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t stream) {
   constexpr int VEC = 16 / static_cast<int>(sizeof(WT));
+  if constexpr (NP > 0) {
+    ENG_CHECK(a.K == (NP - 1) * 64LL * VEC + KT, "gemv: fixed-K kernel for another K");
+  }
   const long long wgs = ((a.N + R - 1) / R + WAVES - 1) / WAVES;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
   static std::atomic<bool> allowed[64] = {};
-  allow_staged_lds(reinterpret_cast<const void*>(&gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>),
-                   allowed, lds_bytes);
-  gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES>
+  allow_staged_lds(
+      reinterpret_cast<const void*>(&gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES, NP, KT, CH>),
+      allowed, lds_bytes);
+  gemv_rows_lds_kernel<WT, VEC, R, U, RMS, WAVES, NP, KT, CH>
       <<<static_cast<unsigned>(wgs), WAVES * 64, lds_bytes, stream>>>(
           static_cast<const WT*>(a.W), static_cast<const float*>(a.x), a.gamma,
           static_cast<float*>(a.y), a.N, a.K, a.eps);
@@ -205,6 +210,23 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     constexpr long long kPiece = 64 * VMAX;
     const long long padded = (a.K + kPiece - 1) / kPiece * kPiece;
     const bool fits = padded * 4 <= kStagedLdsMax;
+    // Widths with a fixed-K form: the LDS-staged kernel once the rows give
+    // every CU at least 8 waves (16-wave workgroups from 16 rows per CU, else
+    // 8-wave) -- at 4096 x 4096 6.84 us against 7.31 us for the register
+    // kernel, whose per-row re-read of x through the vector L1 costs 0.8 us.
+    if (fits && (RMS || a.N >= one_round / 2 || a.K > 4096)) {
+      const std::size_t lds = static_cast<std::size_t>(padded) * 4;
+      const bool wide = RMS || a.N >= one_round || a.K > 4096;
+      const bool fixed = with_fixed_k_f16(a.K, [&](auto fk) {
+        using F = decltype(fk);
+        if (wide) {
+          launch_rows_lds<WT, 1, 4, RMS, 16, F::NP, F::KT, F::CH1>(a, lds, stream);
+        } else {
+          launch_rows_lds<WT, 1, 4, RMS, 8, F::NP, F::KT, F::CH1>(a, lds, stream);
+        }
+      });
+      if (fixed) return;
+    }
     if (fits && (RMS || a.N > one_round || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       if (a.K > 4096) {

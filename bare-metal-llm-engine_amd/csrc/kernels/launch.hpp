@@ -40,6 +40,31 @@ void launch_gemv(const GemvArgs& a, hipStream_t stream);
 // 128 KiB (x of up to K = 32768 for one row, two rows at K = 11008 for a
 // small-batch pass; one 16-wave workgroup per CU past 64 KiB).
 constexpr long long kStagedLdsMax = 128 * 1024;
+// Widths K with a compile-time form of the fp16 LDS-staged decode kernels
+// (dot_rows_lds_fixed): K = (NP - 1) * 512 + KT, streamed in groups of CH1
+// pieces for one weight row per wave and CH2 for two (the FFN's gate and up).
+// The groups keep a wave's loads in flight within the VGPRs of 16-wave
+// workgroups (CH1 x 4 and 2 CH2 x 4 registers of weights).
+template <int NP_, int KT_, int CH1_, int CH2_>
+struct FixedK {
+  static constexpr int NP = NP_;
+  static constexpr int KT = KT_;
+  static constexpr int CH1 = CH1_;
+  static constexpr int CH2 = CH2_;
+};
+// Calls f(FixedK<...>{}) and returns true when K has a fixed form.
+template <class F>
+bool with_fixed_k_f16(long long K, F&& f) {
+  switch (K) {
+    case 2048: f(FixedK<4, 512, 4, 4>{}); return true;
+    case 4096: f(FixedK<8, 512, 8, 8>{}); return true;
+    case 5120: f(FixedK<10, 512, 10, 5>{}); return true;
+    case 8192: f(FixedK<16, 512, 16, 8>{}); return true;
+    case 11008: f(FixedK<22, 256, 22, 8>{}); return true;
+    case 14336: f(FixedK<28, 512, 14, 7>{}); return true;
+    default: return false;
+  }
+}
 // Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
 // device per kernel (`done` is that kernel's flag array); a no-op below.
 void allow_staged_lds(const void* kernel, std::atomic<bool> (&done)[64], std::size_t bytes);

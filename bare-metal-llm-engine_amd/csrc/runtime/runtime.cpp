@@ -6,6 +6,8 @@
 // (33-92), exposed as plain C functions.
 #include "../engine_internal.hpp"
 
+#include <engine/config.hpp>
+
 #include <dirent.h>
 
 #include <cctype>
@@ -159,12 +161,16 @@ extern "C" {
 
 const char* eng_last_error(void) { return eng::g_last_error.c_str(); }
 
+#ifndef ENGINE_GIT_REV
+#define ENGINE_GIT_REV "unknown"
+#endif
+
 const char* eng_build_info(void) {
-  return "engine_hip 0.1 gfx950 -O3 packed-fp32-off"
+  return "engine_hip " ENGINE_VERSION_STRING " " ENGINE_HIP_ARCH_STRING " -O3 packed-fp32-off"
 #ifdef ENGINE_ALWAYS_SYNC_CHECK
          " sync-check"
 #endif
-      ;
+         " git " ENGINE_GIT_REV;
 }
 
 int eng_device_count(int* count) {

@@ -2,7 +2,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
                     [--only config2,config3,refapi,gemm,ffn,attention,stack,layout,stackfused,
-                            gemvsweep,attn32k]
+                            gemvsweep,attn32k,launch]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
@@ -224,52 +224,101 @@ def _stats(samples: list) -> dict:
             "samples": len(a), "noisy": iqr > 10.0}
 
 
+CLOCK_FLOOR = 0.75  # the reference's steady-clock floor: 75% of the nominal engine clock
+
+
 class Timer:
+    """HIP-event timing on one stream, with the reference harness's clock
+    handling (bench_harness.hpp:215-310): warm-up continues until the live
+    engine clock reaches 75% of nominal (bounded), and the live engine and
+    memory clocks are read while each timed batch is in flight."""
+
     def __init__(self, eng, pkg):
         self.eng = eng
         self.stream = eng.stream(pkg.STREAM_NON_BLOCKING)
         self.e0 = eng.event()
         self.e1 = eng.event()
         self.calls = 0
+        self.nominal_mhz = eng.clock_rate_khz() // 1000
+        self.sm_samples = []   # every clock read of the run, for the environment block
+        self.mem_samples = []
 
-    def _window(self, launch, n: int) -> float:
+    def _clocks(self, record: bool = True):
+        sm, mem = self.eng.live_clocks_mhz()
+        if record and sm > 0:
+            self.sm_samples.append(sm)
+        if record and mem > 0:
+            self.mem_samples.append(mem)
+        return sm, mem
+
+    def _window(self, launch, n: int, clocks=None) -> float:
         self.e0.record(self.stream)
         for _ in range(n):
             launch(self.calls, self.stream.handle)
             self.calls += 1
         self.e1.record(self.stream)
+        if clocks is not None:     # read while the batch runs
+            clocks.append(self._clocks())
         self.e1.sync()
         return self.e0.elapsed_ms(self.e1)
 
-    def run(self, launch, steps: int, warmup: int) -> float:
-        """Average ms per launch over exactly `steps` back-to-back launches on
-        one stream, after `warmup` untimed ones."""
+    def _warm(self, launch, min_calls: int, warmup_ms: float, max_wait_ms: float = 500.0) -> None:
+        """At least `min_calls` calls and `warmup_ms` of them, then until the
+        engine clock read during a batch reaches the floor (or `max_wait_ms`)."""
+        t0 = time.perf_counter()
+        n = 0
+        floor = CLOCK_FLOOR * self.nominal_mhz
+        while True:
+            for _ in range(max(1, min(min_calls, 64))):
+                launch(self.calls, self.stream.handle)
+                self.calls += 1
+                n += 1
+            sm, _ = self._clocks(record=False)
+            self.stream.sync()
+            el = (time.perf_counter() - t0) * 1e3
+            if n >= min_calls and el >= warmup_ms and (sm == 0 or sm >= floor or el >= max_wait_ms):
+                return
+
+    def clock_stats(self, clocks) -> dict:
+        sm = sorted(c[0] for c in clocks if c[0] > 0)
+        mem = sorted(c[1] for c in clocks if c[1] > 0)
+        out = {}
+        if sm:
+            out.update({"sm_clock_min_mhz": sm[0], "sm_clock_med_mhz": sm[len(sm) // 2],
+                        "sm_clock_max_mhz": sm[-1]})
+            if sm[0] < CLOCK_FLOOR * self.nominal_mhz:
+                out["clock_dip"] = True
+        if mem:
+            out["mem_clock_med_mhz"] = mem[len(mem) // 2]
+        return out
+
+    def run(self, launch, steps: int, warmup: int) -> tuple:
+        """(average ms per launch over exactly `steps` back-to-back launches on
+        one stream after `warmup` untimed ones, clocks read during them)."""
         for _ in range(warmup):
             launch(self.calls, self.stream.handle)
             self.calls += 1
         self.stream.sync()
         self.eng.sync()
-        ms = self._window(launch, steps) / steps
+        clocks = []
+        ms = self._window(launch, steps, clocks) / steps
         self.eng.sync()
-        return ms
+        return ms, self.clock_stats(clocks)
 
     def sampled(self, launch, samples: int = 15, target_ms: float = 1.5, max_batch: int = 256,
                 warmup_ms: float = 20.0) -> dict:
-        """The reference's protocol: warm up for >= `warmup_ms`, size a batch of
-        back-to-back calls to ~`target_ms` (at most `max_batch`), time
-        `samples` batches; per-call median / quartiles / IQR %."""
-        t_end = time.perf_counter() + warmup_ms * 1e-3
-        n = 0
-        while time.perf_counter() < t_end or n < 2:
-            launch(self.calls, self.stream.handle)
-            self.calls += 1
-            n += 1
-        self.stream.sync()
+        """The reference's protocol: warm up for >= `warmup_ms` and until the
+        clock floor, size a batch of back-to-back calls to ~`target_ms` (at
+        most `max_batch`), time `samples` batches; per-call median / quartiles
+        / IQR %, and the clocks read during the batches."""
+        self._warm(launch, 2, warmup_ms)
         one = self._window(launch, 4) / 4
         batch = int(max(1, min(max_batch, round(target_ms / max(one, 1e-6)))))
-        per_call = [self._window(launch, batch) / batch for _ in range(samples)]
+        clocks = []
+        per_call = [self._window(launch, batch, clocks) / batch for _ in range(samples)]
         st = _stats(per_call)
         st["batch"] = batch
+        st.update(self.clock_stats(clocks))
         return st
 
 
@@ -288,10 +337,14 @@ def rotating(eng, host, count):
     return bufs
 
 
+CLOCK_KEYS = ("sm_clock_min_mhz", "sm_clock_med_mhz", "mem_clock_med_mhz", "clock_dip")
+
+
 def _spread(st: dict) -> dict:
     return {"p25_us": round(st["p25_ms"] * 1e3, 3), "p75_us": round(st["p75_ms"] * 1e3, 3),
             "iqr_pct": st["iqr_pct"], "samples": st["samples"], "batch": st["batch"],
-            **({"noisy": True} if st["noisy"] else {})}
+            **({"noisy": True} if st["noisy"] else {}),
+            **{k: st[k] for k in CLOCK_KEYS if k in st}}
 
 
 def hbm_row(name, st, nbytes, extra=None):
@@ -657,19 +710,57 @@ def rows_gemv_sweep(eng, timer) -> list:
     return rows
 
 
+def rows_launch(eng, timer) -> list:
+    """Per-launch floors: the probe library (bare-metal-llm-engine_amd/lib/
+    liblaunch_interval.so, built with the engine) times empty kernels at several
+    grid shapes and a plain streaming read with the output-major GEMV's access
+    pattern over the config-2 / config-3 / fused-q/k/v weight sizes, back to
+    back on one stream; plus the engine's own smallest launch, a K == 0 GEMV
+    (one 256-thread zero-fill workgroup)."""
+    import ctypes
+
+    rows = []
+    path = os.path.join(REPO, "bare-metal-llm-engine_amd", "lib", "liblaunch_interval.so")
+    probe = ctypes.CDLL(path)
+    probe.launch_interval_run.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int]
+    probe.launch_interval_run.restype = ctypes.c_int
+    buf = ctypes.create_string_buffer(1 << 16)
+    if probe.launch_interval_run(buf, len(buf), 0 if NO_GRAPHS else 1) != 0:
+        raise RuntimeError(f"{path}: {buf.value.decode()}")
+    for ln in buf.value.decode().splitlines():
+        d = json.loads(ln)
+        row = {"name": "launch floor: " + d.pop("what"), **d}
+        if "bytes" in d:
+            row["frac_hbm_peak"] = round(d["GB/s"] / HBM_PEAK_GBS, 4)
+        rows.append(row)
+    dy = eng.empty(1, np.float32)
+    f = eng.lib.eng_gemv_f16w_nk
+    st = timer.sampled(lambda i, s: f(dy.ptr, dy.ptr, dy.ptr, 1, 0, s))
+    rows.append({"name": "launch floor: eng_gemv_f16w_nk with K = 0 (one zero-fill workgroup)",
+                 "us_per_call": round(st["median_ms"] * 1e3, 3), **_spread(st)})
+    dy.free()
+    return rows
+
+
 def rows_stack_fused(eng, timer) -> list:
     """Only the fastest config-5 arrangement (for profiling its kernels alone)."""
     return [bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
 
 
+# --no-graphs: rows that replay HIP graphs issue the same launches eagerly
+# instead (rocprofv3's kernel trace crashes inside hipGraphLaunch on this
+# image, so profiling runs use it).
+NO_GRAPHS = False
+
+
 # Groups that repeat or sweep a row for profiling; not part of the default run.
-PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k")
+PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k", "launch")
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
           "layout": rows_layout,
           "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep,
-          "attn32k": rows_attention_tinyllama_32k}
+          "attn32k": rows_attention_tinyllama_32k, "launch": rows_launch}
 
 
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
@@ -741,6 +832,7 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
                 rl(o.ptr, g.ptr, lay["up"].ptr, up.ptr, 1, F, H, 1e-5, s)
             gv(lay["down"].ptr, gate.ptr, xh.ptr, H, F, s)
 
+    graph = graph and not NO_GRAPHS
     if graph:
         token(0, timer.stream.handle)         # eager first: capture needs nothing allocated
         timer.stream.sync()
@@ -777,11 +869,15 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--quick", action="store_true", help="headline only (no secondary rows)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="issue the launches of graph-replay rows eagerly (for rocprofv3 kernel traces)")
     ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
                     + ", ".join(GROUPS) + " (default: all but the profiling groups "
                     + ", ".join(PROFILING_GROUPS) + ", which repeat or sweep single rows)")
     args = ap.parse_args()
 
+    global NO_GRAPHS
+    NO_GRAPHS = args.no_graphs
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus}, WORLD_SIZE {world} requested): "
@@ -805,9 +901,11 @@ def main() -> int:
 
     head = GemvF16w(eng, nk=True)
     nbytes = head.nbytes
-    ms = timer.run(head, args.steps, args.warmup)
+    timer._warm(head, args.warmup, 20.0)  # clocks up before the untimed warm-up and the window
+    ms, head_clocks = timer.run(head, args.steps, args.warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s")
+    log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s "
+        f"{head_clocks}")
     spread = None if args.quick else _spread(timer.sampled(head))
     head.free()
 
@@ -858,14 +956,96 @@ def main() -> int:
         },
         "timing": {
             "value_from": f"{args.steps} back-to-back launches between two HIP events, after {args.warmup} warm-up",
+            "clocks_during_window": head_clocks,
             "spread": spread,
         },
         "cpu_baseline": cpu,
+        "environment": environment(eng, timer),
         "secondary": secondary,
         "host": platform.node(),
     }
+    # Last key, so the end of the line (what a log tail shows) carries the key figures.
+    line["summary"] = summary(line, secondary)
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _git_rev() -> str:
+    import subprocess
+
+    try:
+        r = subprocess.run(["git", "-C", REPO, "describe", "--always", "--dirty", "--abbrev=12"],
+                           capture_output=True, text=True, timeout=10)
+        return r.stdout.strip() or "unavailable (no .git in this copy)"
+    except (OSError, subprocess.SubprocessError):
+        return "unavailable (no git)"
+
+
+def environment(eng, timer) -> dict:
+    """Run provenance (the reference's print_json environment block,
+    bench_harness.hpp:679-710): device, driver, clocks read during the timed
+    batches, peak bandwidth, source revision and build."""
+    sm = sorted(timer.sm_samples)
+    mem = sorted(timer.mem_samples)
+    return {
+        "device": eng.device_summary(),
+        "arch": eng.device_arch(),
+        "driver_version": eng.driver_version(),
+        "nominal_sm_clock_mhz": timer.nominal_mhz,
+        "live_sm_clock_mhz": {"min": sm[0], "median": sm[len(sm) // 2], "max": sm[-1],
+                              "samples": len(sm)} if sm else None,
+        "live_mem_clock_mhz": {"min": mem[0], "median": mem[len(mem) // 2], "max": mem[-1],
+                               "samples": len(mem)} if mem else None,
+        "clock_source": eng.live_clock_source(),
+        "clock_floor": f"warm-up continues until the engine clock read during a batch is >= "
+                       f"{CLOCK_FLOOR:.0%} of nominal (at most 500 ms); rows whose minimum read is below "
+                       f"it carry clock_dip",
+        "peak_bandwidth_gbs": eng.peak_bandwidth_gbs(),
+        "build": eng.build_info(),
+        "bench_git_rev": _git_rev(),
+        "cpu": _cpu_model(),
+    }
+
+
+# (summary key, row-name prefix, field) for the compact end-of-line summary.
+SUMMARY_ROWS = (
+    ("cfg2_ref_layout_us", "config 2 gemv fp16-W 4096x4096 cold, reference layout", "us_per_call"),
+    ("cfg3_out_major_us", "config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, output-major", "us_per_call"),
+    ("cfg3_out_major_frac", "config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, output-major", "frac_hbm_peak"),
+    ("cfg3_ref_layout_us", "config 3 rmsnorm_linear fp16-W 1x11008x4096 cold, reference layout", "us_per_call"),
+    ("cfg1_gemm_512_ms", "matmul_f32 512x512x512 (config 1)", "ms_per_call"),
+    ("cfg4_gemm_4096_tflops", "matmul_f32 4096x4096x4096 (config 4)", "TFLOP/s"),
+    ("cfg4_gemm_4096_frac", "matmul_f32 4096x4096x4096 (config 4)", "frac_fp32_mfma_peak"),
+    ("cfg4_gemm_512x11008x4096_tflops", "matmul_f32 512x11008x4096 (config 4)", "TFLOP/s"),
+    ("cfg4_gemm_512x4096x11008_tflops", "matmul_f32 512x4096x11008 (config 4)", "TFLOP/s"),
+    ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
+    ("gemv_fp16_halfio_4096_us", "gemv_fp16 (half x/out) 4096x4096 cold", "us_per_call"),
+)
+
+
+def summary(line: dict, secondary: list) -> dict:
+    """Key figures of the run in a few hundred bytes."""
+    out = {"cfg2_us": round(line["ms_per_step"] * 1e3, 3), "cfg2_frac": line["roofline"]["frac"]}
+    for key, prefix, field in SUMMARY_ROWS:
+        for r in secondary:
+            if r.get("name", "").startswith(prefix) and field in r:
+                out[key] = r[field]
+                break
+    stack = [r for r in secondary if r.get("name", "").startswith("config 5 ")]
+    if stack:
+        ref = [r for r in stack if r["name"].endswith("reference layout W[in x out]")]
+        best = min(stack, key=lambda r: r["us_per_call"])
+        if ref:
+            out["cfg5_reference_call_sequence_ms"] = round(ref[0]["us_per_call"] / 1e3, 3)
+        out["cfg5_best_ms"] = round(best["us_per_call"] / 1e3, 3)
+        out["cfg5_best_frac"] = best["frac_hbm_peak"]
+    env = line.get("environment") or {}
+    if env.get("live_sm_clock_mhz"):
+        out["sm_clock_mhz_min_med"] = [env["live_sm_clock_mhz"]["min"], env["live_sm_clock_mhz"]["median"]]
+    dips = [r["name"] for r in secondary if r.get("clock_dip")]
+    if dips:
+        out["clock_dip_rows"] = len(dips)
+    return out
 
 
 if __name__ == "__main__":

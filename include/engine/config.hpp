@@ -9,4 +9,4 @@
 
 #define ENGINE_HAS_HIP 1
 #define ENGINE_HIP_ARCH_STRING "gfx950"
-#define ENGINE_VERSION_STRING "0.1"
+#define ENGINE_VERSION_STRING "0.2"

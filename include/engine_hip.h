@@ -60,7 +60,7 @@ typedef struct eng_pool_s* eng_pool;
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* eng_last_error(void);
-/* Library build string: "<version> gfx950 <build flags>". */
+/* Library build string: "engine_hip <version> gfx950 <build flags> git <source revision>". */
 const char* eng_build_info(void);
 
 /* ------------------------------------------------------------------------
