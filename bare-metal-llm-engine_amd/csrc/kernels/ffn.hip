@@ -47,6 +47,36 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
   constexpr long long kPiece = 64 * VEC;
   constexpr long long kMaxLds = sizeof(WT) == 2 ? kStagedLdsMax : 64 * 1024;
   const long long padded = (K + kPiece - 1) / kPiece * kPiece;
+  // 5 to 64 rows: gate and up each in one pass over its matrix on the matrix
+  // cores (skinny.hip), then SwiGLU.
+  {
+    SkinnyArgs sk;
+    sk.W = Wg;
+    sk.w = elem;
+    sk.w_nk = nk;
+    sk.x = in;
+    sk.gamma = gamma;
+    sk.M = M;
+    sk.N = N;
+    sk.K = K;
+    sk.rms = true;
+    sk.eps = eps;
+    SkinnyArgs sku = sk;
+    sku.W = Wu;
+    if (skinny_applies(sk) && skinny_applies(sku)) {
+      const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
+      // Level 1: the few-row launches lease their partial sums at level 0.
+      StreamScratch gu(s, 2 * mn * sizeof(float), 1);
+      float* gate = static_cast<float*>(gu.get());
+      float* up = gate + mn;
+      sk.y = gate;
+      sku.y = up;
+      launch_skinny(sk, s);
+      launch_skinny(sku, s);
+      launch_swiglu_f32(gate, up, act, static_cast<long long>(mn), s);
+      return;
+    }
+  }
   if (!nk) {
     // Reference layout, up to 16 rows: per pass of up to 4 rows, one stream
     // launch over Wg and Wu and the reduce with the SwiGLU epilogue.

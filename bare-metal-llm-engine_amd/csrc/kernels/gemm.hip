@@ -668,6 +668,14 @@ int eng_matmul_f32(const float* A, const float* B, float* C, int64_t M, int64_t 
       eng::launch_gemv(gv, s);
       return;
     }
+    // 5 to 64 rows: one pass over B on the matrix cores (the 64-row GEMM tile
+    // would leave most CUs idle); 2 to 4 rows: GEMV passes, each row equal to
+    // its single-row product.
+    const eng::SkinnyArgs sk = eng::skinny_args(gv, M);
+    if (eng::skinny_applies(sk)) {
+      eng::launch_skinny(sk, s);
+      return;
+    }
     if (eng::launch_gemv_kn_rows(gv, M, s)) return;
     eng::GemmArgs g;
     g.A = A;

@@ -85,6 +85,54 @@ std::size_t gemv_kn_scratch_bytes(const GemvArgs& a, std::int64_t M);
 // when the vector path's requirements fail.
 bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, std::int64_t M, hipStream_t stream);
 
+// Few-row linear layers on FP32 MFMA (skinny.hip): y[M x N] = x'[M x K] . W
+// (W [K x N]) or x' . W^T (w_nk, W [N x K]), x' = x (or, with rms, x * gamma
+// with row m scaled by 1/sqrt(mean_k x[m][k]^2 + eps) after the sum), W read
+// once for all rows. Rows of one call are independent of each other and of M.
+constexpr std::int64_t kSkinnyMinRows = 5;
+constexpr std::int64_t kSkinnyMaxRows = 64;
+struct SkinnyArgs {
+  const void* W = nullptr;
+  Elem w = Elem::F32;
+  bool w_nk = false;
+  const float* x = nullptr;
+  const float* gamma = nullptr;  // rms only (optional)
+  float* y = nullptr;
+  std::int64_t M = 0;
+  std::int64_t N = 0;
+  std::int64_t K = 0;
+  bool rms = false;
+  float eps = 0.0f;
+  // Caller-provided device scratch for the split-K partial sums (instead of
+  // the stream's arena; a launch needing more than scratch_bytes fails).
+  void* scratch = nullptr;
+  std::size_t scratch_bytes = 0;
+};
+// Whether the few-row kernel takes this call: kSkinnyMinRows <= M <=
+// kSkinnyMaxRows, K % 8 == 0, N a multiple of the 16-byte vector in the
+// reference layout, and 16-byte aligned W, x and gamma.
+bool skinny_applies(const SkinnyArgs& a);
+// Scratch bytes launch_skinny takes (0 when K is not split).
+std::size_t skinny_scratch_bytes(const SkinnyArgs& a);
+void launch_skinny(const SkinnyArgs& a, hipStream_t stream);
+// The few-row form of an M-row GEMV-style call (fp32 x and y only; other
+// element types give M = 0, which no kernel takes).
+inline SkinnyArgs skinny_args(const GemvArgs& g, std::int64_t M) {
+  SkinnyArgs a;
+  a.W = g.W;
+  a.w = g.w;
+  a.w_nk = g.w_nk;
+  a.x = static_cast<const float*>(g.x);
+  a.gamma = g.rms ? g.gamma : nullptr;
+  a.y = static_cast<float*>(g.y);
+  a.M = (g.x_elem == Elem::F32 && g.y_elem == Elem::F32) ? M : 0;
+  a.N = g.N;
+  a.K = g.K;
+  a.rms = g.rms;
+  a.eps = g.eps;
+  return a;
+}
+
 // C[M x N] = A'[M x K] . B[K x N] on FP32 MFMA, where A' = A with column k
 // scaled by gamma_k when gamma is given; with rms, row r of C is further
 // multiplied by 1/sqrt(sum_k A[r][k]^2 / K + eps).

@@ -23,13 +23,15 @@
 namespace eng {
 namespace {
 
-// Scratch of eng_rmsnorm_linear_f16w_noalloc: the split-K partial sums of up
-// to 4 rows per pass, [nsplit][4][N] plus [nsplit][4] sums of squares, where
-// nsplit * N <= 4 x CUs x 256 (one round of 4 workgroups per CU, 256 fp16
-// columns each): 4 MiB on a 256-CU MI355X, plus 64 KiB for the sums of
-// squares and the split rounding. Each device holds its own copy for the
-// life of the process.
-constexpr std::size_t kNoAllocScratchBytes = (std::size_t{4} << 20) + (std::size_t{64} << 10);
+// Scratch of eng_rmsnorm_linear_f16w_noalloc: the split-K partial sums.
+// Up to 4 rows (split-K GEMV passes): [nsplit][4][N] plus [nsplit][4] sums of
+// squares, nsplit * N <= 4 x CUs x 256 (one round of 4 workgroups per CU, 256
+// fp16 columns each): 4 MiB on a 256-CU MI355X. 5 to 16 rows (the few-row
+// MFMA kernel): [nsplit][M][N] plus [nsplit][M], nsplit * N <= 2 x CUs x 128
+// + 128 x ceil(N / 128) <= 4 x CUs x 128: 8 MiB at 16 rows on 256 CUs. Plus
+// 64 KiB for the sums of squares and the split rounding. Each device holds
+// its own copy for the life of the process.
+constexpr std::size_t kNoAllocScratchBytes = (std::size_t{8} << 20) + (std::size_t{64} << 10);
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 // Device address of `scratch` on the current device, looked up once per
@@ -75,7 +77,14 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     launch_gemv(g1, s);
     return;
   }
-  // A few rows (small-batch decode): the rows share passes over W.
+  // 5 to 64 rows: one pass over W on the matrix cores.
+  SkinnyArgs sk = skinny_args(g1, M);
+  if (skinny_applies(sk)) {
+    launch_skinny(sk, s);
+    return;
+  }
+  // 2 to 4 rows (small-batch decode, each row equal to its single-row call),
+  // or rows the few-row kernel does not take: the rows share passes over W.
   if (nk ? launch_gemv_nk_rows(g1, M, s) : launch_gemv_kn_rows(g1, M, s)) return;
   StreamScratch normed(s, static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * sizeof(float));
   float* xn = static_cast<float*>(normed.get());
@@ -93,7 +102,8 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
 }
 
 // rmsnorm_linear_any for reference-layout fp16 W and M <= 16 rows, with the
-// split-K partial sums in the static `scratch` instead of the stream's arena:
+// split-K partial sums (GEMV passes for up to 4 rows, the few-row MFMA kernel
+// from 5) in the static `scratch` instead of the stream's arena:
 // no allocation of any kind. The kernels and their configuration are
 // eng_rmsnorm_linear_f16w's, so the results are the same bits.
 void rmsnorm_linear_f16w_noalloc(const float* in, const float* rms_weight, const void* W,
@@ -117,14 +127,23 @@ void rmsnorm_linear_f16w_noalloc(const float* in, const float* rms_weight, const
   g1.K = K;
   g1.rms = true;
   g1.eps = eps;
-  const std::size_t need = gemv_kn_scratch_bytes(g1, M);
+  hipStream_t s = as_stream(stream);
+  SkinnyArgs sk = skinny_args(g1, M);
+  const bool few_rows = M > 1 && skinny_applies(sk);
+  const std::size_t need = few_rows ? skinny_scratch_bytes(sk) : gemv_kn_scratch_bytes(g1, M);
   ENG_CHECK(need <= kNoAllocScratchBytes,
             "rmsnorm_linear_f16w_noalloc: this shape needs " + std::to_string(need) +
                 " bytes of scratch, more than the static " +
                 std::to_string(kNoAllocScratchBytes) + " bytes");
-  g1.scratch = noalloc_scratch_ptr();
+  void* scratch_ptr = noalloc_scratch_ptr();
+  if (few_rows) {
+    sk.scratch = scratch_ptr;
+    sk.scratch_bytes = kNoAllocScratchBytes;
+    launch_skinny(sk, s);
+    return;
+  }
+  g1.scratch = scratch_ptr;
   g1.scratch_bytes = kNoAllocScratchBytes;
-  hipStream_t s = as_stream(stream);
   if (M == 1) {
     launch_gemv(g1, s);
     return;

@@ -1,7 +1,7 @@
 """Benchmark of the MI355X matrix-multiply engine (one GPU).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
-                    [--only config2,config3,refapi,gemm,ffn,attention,stack,layout,stackfused,
+                    [--only config2,config3,fewrows,refapi,gemm,ffn,attention,stack,layout,stackfused,
                             gemvsweep,attn32k,launch]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
@@ -421,10 +421,11 @@ def rows_config3(eng, timer) -> list:
                             2 * K * N + 8 * K + 4 * N))
         for w in Ws:
             w.free()
-    # Small-batch decode at the config 3 shape: M rows share passes over W.
+    # Small-batch decode at the config 3 shape: up to 4 rows share passes over
+    # W (GEMV kernels; 5 to 64 rows are the "fewrows" group).
     Ws = rotating(eng, rand_f16(np.random.default_rng(2), (N, K)), R)
     f = eng.lib.eng_rmsnorm_linear_f16w_nk
-    for M in (4, 16):
+    for M in (4,):
         dxm = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
         dym = eng.empty((M, N), np.float32)
         st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
@@ -454,6 +455,59 @@ def rows_config3(eng, timer) -> list:
     dxm.free(), dym.free()
     for w in Ws:
         w.free()
+    return rows
+
+
+def rows_few_rows(eng, timer) -> list:
+    """Few-row linear layers (5 to 64 activation rows, the MFMA kernel that
+    streams W once): RMSNorm + linear at config 3's shape in both layouts,
+    the down-projection shape, and a few-row FP32 matmul. Bytes: W once plus
+    the activation rows in and out; FLOPs 2 M N K."""
+    rows = []
+    rng = np.random.default_rng(9)
+    K, N, R = 4096, 11008, 12
+    dg = eng.upload((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    for nk in (True, False):
+        Ws = rotating(eng, rand_f16(np.random.default_rng(2), (N, K) if nk else (K, N)), R)
+        f = eng.lib.eng_rmsnorm_linear_f16w_nk if nk else eng.lib.eng_rmsnorm_linear_f16w
+        tag = "output-major W[NxK]" if nk else "reference layout W[KxN]"
+        for M in ((5, 8, 16, 32, 64) if nk else (16, 64)):
+            dxm = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
+            dym = eng.empty((M, N), np.float32)
+            st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
+            row = hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (few rows, MFMA), {tag}", st,
+                          2 * K * N + 4 * M * K + 4 * K + 4 * M * N)
+            row["TFLOP/s"] = round(2.0 * M * N * K / (st["median_ms"] * 1e-3) / 1e12, 2)
+            rows.append(row)
+            dxm.free(), dym.free()
+        if nk:
+            # the same buffers read as the down projection [4096 x 11008]
+            Kd, Nd, M = N, K, 16
+            dxd = eng.upload(rng.standard_normal((M, Kd), dtype=np.float32))
+            dyd = eng.empty((M, Nd), np.float32)
+            st = timer.sampled(lambda i, s: f(dxd.ptr, None, Ws[i % R].ptr, dyd.ptr, M, Nd, Kd, 1e-5, s))
+            rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold (few rows, MFMA, "
+                                "down-projection shape), output-major W[NxK]", st,
+                                2 * Kd * Nd + 4 * M * Kd + 4 * M * Nd))
+            dxd.free(), dyd.free()
+        for w in Ws:
+            w.free()
+    # FP32 matmul with 16 and 64 rows (B [4096 x 4096] fp32, 8 rotating copies)
+    Kf = Nf = 4096
+    Bs = rotating(eng, rng.uniform(-1, 1, (Kf, Nf)).astype(np.float32), 8)
+    for M in (16, 64):
+        dA = eng.upload(rng.uniform(-1, 1, (M, Kf)).astype(np.float32))
+        dC = eng.empty((M, Nf), np.float32)
+        fm = eng.lib.eng_matmul_f32
+        st = timer.sampled(lambda i, s: fm(dA.ptr, Bs[i % 8].ptr, dC.ptr, M, Nf, Kf, s))
+        row = hbm_row(f"matmul_f32 {M}x4096x4096 cold B (few rows, MFMA)", st,
+                      4 * Kf * Nf + 4 * M * Kf + 4 * M * Nf)
+        row["TFLOP/s"] = round(2.0 * M * Nf * Kf / (st["median_ms"] * 1e-3) / 1e12, 2)
+        rows.append(row)
+        dA.free(), dC.free()
+    for b in Bs:
+        b.free()
+    dg.free()
     return rows
 
 
@@ -756,7 +810,8 @@ NO_GRAPHS = False
 # Groups that repeat or sweep a row for profiling; not part of the default run.
 PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k", "launch")
 
-GROUPS = {"config2": rows_config2, "config3": rows_config3, "refapi": rows_reference_api,
+GROUPS = {"config2": rows_config2, "config3": rows_config3, "fewrows": rows_few_rows,
+          "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
           "layout": rows_layout,
           "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep,

@@ -329,6 +329,18 @@ def assert_within(got, exp, bound, what: str) -> float:
     return float(ratio.max()) if ratio.size else 0.0
 
 
+def peer_row(run, x, m):
+    """Row m of run(x) recomputed in another call that must give the same bits:
+    alone when x has at most 4 rows (small-batch GEMV passes: each row equals
+    the single-row call), else inside a 5-row window of x (the few-row MFMA
+    kernel gives a row the same bits in any batch of 5 to 64 rows)."""
+    M = x.shape[0]
+    if M <= 4:
+        return run(x[m:m + 1])[0]
+    lo = min(m, M - 5)
+    return run(x[lo:lo + 5])[m - lo]
+
+
 def dot_bounds(a, y64, K):
     """(derived, statistical) bounds of an fp32 dot product (see module doc)."""
     derived = K * U32 * a + U32 * np.abs(y64)

@@ -278,12 +278,13 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (1, 64, 100, "f16", True),       # K % 8 != 0: GEMV fallback with arena scratch
     (1, 64, 20000, "f16", True),     # 80 KiB of staged x: fused launch past the default LDS size
     (1, 64, 33000, "f16", True),     # K past the 128 KiB budget: GEMV fallback
-    (5, 200, 512, "f16", True),      # small batch: multi-row GEMV passes + SwiGLU kernel
+    (5, 200, 512, "f16", True),      # few rows: MFMA kernel for gate and up + SwiGLU kernel
     (4, 11008, 4096, "f16", True),   # small batch at the config 5 gate/up shape
     (3, 300, 1000, "f32", False),    # small batch, fp32 weights, null gain
-    (40, 200, 512, "f16", True),     # prefill: MFMA GEMMs + SwiGLU kernel
+    (40, 200, 512, "f16", True),     # few rows (three m-blocks) + SwiGLU kernel
     (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
-    (64, 256, 512, "f16", False),
+    (64, 256, 512, "f16", False),    # 64 rows: the few-row kernel's largest batch
+    (65, 256, 512, "f16", True),     # past it: rmsnorm + MFMA GEMMs + SwiGLU kernel
 ])
 def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma):
     rng = np.random.default_rng(M + N + K)
@@ -304,8 +305,10 @@ def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma
                                          (5, 4096, 4096, "f16"), (16, 11008, 4096, "f16"),
                                          (4, 512, 1024, "f32")])
 def test_rmsnorm_linear_swiglu_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, dtype):
-    # A few rows share each pass over Wg and Wu (fused SwiGLU epilogue); each
-    # row's act equals the M = 1 fused call bit for bit.
+    # Up to 4 rows share each pass over Wg and Wu (fused SwiGLU epilogue), each
+    # row's act equal to the M = 1 fused call bit for bit; 5 or more take the
+    # few-row MFMA kernel for gate and up, each row the same bits in any batch
+    # of 5 to 64 rows.
     rng = np.random.default_rng(M * 13 + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
@@ -314,7 +317,8 @@ def test_rmsnorm_linear_swiglu_small_batch_rows_match_single_row_calls(gpu, orc,
     Wg, Wu = (orc.f32_to_f16(W) if dtype == "f16" else W for W in (Wgf, Wuf))
     got = gpu_glu_nk(gpu, x, g, Wg, Wu)
     for m in sorted({0, M // 2, M - 1}):
-        assert np.array_equal(got[m], gpu_glu_nk(gpu, x[m:m + 1], g, Wg, Wu)[0]), f"row {m} of {M}"
+        one = helpers.peer_row(lambda xs: gpu_glu_nk(gpu, xs, g, Wg, Wu), x, m)
+        assert np.array_equal(got[m], one), f"row {m} of {M}"
     rows = np.array(sorted({0, M - 1}))
     Wg_kn, Wu_kn = np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T)
     act64, bd, bs = glu_reference(x[rows], g, Wg_kn, Wu_kn)
@@ -365,10 +369,13 @@ def test_rmsnorm_linear_swiglu_kn_matches_golden(gpu, orc, stem):
     (1, 1000, 1024, "f32", True),    # fp32 weights: fused
     (1, 36, 20, "f16", True),        # N % 8 != 0 for fp16: composition
     (3, 300, 1000, "f16", True),     # small batch: one fused pass of 3 rows
-    (16, 1024, 512, "f16", False),   # 4 fused passes of 4 rows
-    (6, 400, 256, "f32", True),      # passes of 4 and 2 rows, fp32 weights
-    (17, 256, 512, "f32", True),     # past 4 passes: MFMA GEMMs + SwiGLU kernel
-    (40, 200, 512, "f16", True),     # prefill: MFMA GEMMs + SwiGLU kernel
+    (4, 1024, 512, "f16", False),    # one fused pass of 4 rows
+    (16, 1024, 512, "f16", False),   # few rows: MFMA kernel for gate and up + SwiGLU kernel
+    (6, 400, 256, "f32", True),      # few rows, fp32 weights
+    (17, 256, 512, "f32", True),
+    (40, 200, 512, "f16", True),
+    (12, 36, 20, "f16", True),       # N % 8 != 0: GEMV passes of up to 4 rows + SwiGLU kernel
+    (80, 200, 512, "f16", True),     # prefill: rmsnorm + MFMA GEMMs + SwiGLU kernel
 ])
 def test_rmsnorm_linear_swiglu_kn_against_oracle_and_composition(gpu, orc, M, N, K, dtype, gamma):
     # Against the oracle, and bit for bit against the reference's composition

@@ -2,7 +2,7 @@
 
 The launchers are meant to be capturable: zero fills are kernels, and the
 scratch they pass between their kernels (split-K GEMV and split-KV attention
-partials, rmsnorm_linear's normalised rows at M > 1, the FFN's gate / up) is
+partials, the few-row kernel's partial sums, the FFN's gate / up) is
 the stream's arena, sized by an eager call before the capture; the graph takes
 those blocks over when the capture ends, so replays on other streams never
 share scratch with eager calls (checked against the oracle below). The graph is
@@ -29,14 +29,14 @@ def test_captured_decode_step_replays_match_eager(gpu):
     rng = np.random.default_rng(5)
     Hd, F = 1024, 2752            # hidden and FFN width
     heads, kv_heads, D, L = 8, 2, 64, 700
-    M = 64                        # prefill rows for rmsnorm_linear at M > 1
+    M = 64                        # rows for rmsnorm_linear at M > 1 (the few-row kernel)
     up = gpu.upload
     Wq = up(f16(gpu, 0.03 * rng.standard_normal((Hd, Hd))))          # [out x in]
     Wg = up(f16(gpu, 0.03 * rng.standard_normal((F, Hd))))
     Wu = up(f16(gpu, 0.03 * rng.standard_normal((F, Hd))))
     Wd = up(f16(gpu, 0.03 * rng.standard_normal((Hd, F))))
     Wkn = up(f16(gpu, 0.03 * rng.standard_normal((Hd, Hd))))         # [in x out]: split-K
-    Wp = up((0.03 * rng.standard_normal((Hd, 512))).astype(np.float32))  # rmsnorm_linear M > 1
+    Wp = up((0.03 * rng.standard_normal((Hd, 512))).astype(np.float32))  # rmsnorm_linear, 64 rows
     x = up(rng.standard_normal(Hd).astype(np.float32))
     xm = up(rng.standard_normal((M, Hd)).astype(np.float32))
     g = up((1 + 0.1 * rng.standard_normal(Hd)).astype(np.float32))

@@ -334,7 +334,7 @@ def test_gemv_is_linear_in_x(gpu):
 
 def test_rmsnorm_linear_fused_equals_separate(gpu):
     rng = np.random.default_rng(16)
-    for M in (1, 32):
+    for M in (1, 32, 80):
         x = rng.standard_normal((M, 512), dtype=np.float32)
         g = (1 + 0.1 * rng.standard_normal(512)).astype(np.float32)
         W = (rng.standard_normal((512, 256)) / np.sqrt(512)).astype(np.float32)
@@ -345,8 +345,9 @@ def test_rmsnorm_linear_fused_equals_separate(gpu):
         check_rmsnorm_linear(sep, y, x, g, W, 512, f"separate M={M}")
         direct = gpu_rmsnorm_linear(gpu, x, g, W, fn="eng_rmsnorm_linear_fused_direct_f32")
         assert np.array_equal(direct, fused)
-        if M > 1:
-            # M > 1 is rmsnorm into scratch, then the GEMM -- the same launches.
+        if M > 64:
+            # past the few-row kernel (M <= 64, RMS scale applied after its
+            # sums): rmsnorm into scratch, then the GEMM -- the same launches.
             assert np.array_equal(fused, sep)
 
 
@@ -595,11 +596,11 @@ def test_rmsnorm_linear_nk_prefill_against_oracle(gpu, orc, M, N, K, dtype):
     check_rmsnorm_linear(got[rows], y, x[rows], g, Wt, K, f"rmsnorm_linear nk {M}x{N}x{K} {dtype}")
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (128, 512, 256), (256, 128, 1024)])
+@pytest.mark.parametrize("M,N,K", [(192, 256, 512), (128, 512, 256), (256, 128, 1024)])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f32_full_tiles_against_oracle(gpu, orc, M, N, K, layout, with_gamma):
-    # M > 1 normalises into scratch; whole 64/128-row tiles with
+    # M > 64 normalises into scratch; whole 64/128-row tiles with
     # K % 32 == 0 then take the direct-to-LDS GEMM.
     rng = np.random.default_rng(7 * M + N + K + (layout == "nk"))
     x = rng.standard_normal((M, K), dtype=np.float32)
@@ -614,12 +615,12 @@ def test_rmsnorm_linear_f32_full_tiles_against_oracle(gpu, orc, M, N, K, layout,
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f32 {layout} {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (128, 512, 256), (256, 128, 1024),
+@pytest.mark.parametrize("M,N,K", [(192, 256, 512), (128, 512, 256), (256, 128, 1024),
                                    (512, 11008, 4096)])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f16w_full_tiles_against_oracle(gpu, orc, M, N, K, layout, with_gamma):
-    # fp16 weights at M > 1: whole tiles take the direct-to-LDS GEMM with the
+    # fp16 weights at M > 64: whole tiles take the direct-to-LDS GEMM with the
     # B tile loaded as halves and converted while the fragments are read.
     rng = np.random.default_rng(11 * M + N + K + (layout == "nk"))
     x = rng.standard_normal((M, K), dtype=np.float32)
@@ -639,16 +640,17 @@ def test_rmsnorm_linear_f16w_full_tiles_against_oracle(gpu, orc, M, N, K, layout
                                    (2, 4096, 11008), (4, 4096, 11008)])
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f16w_nk_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, with_gamma):
-    # Small-batch decode: the rows share passes over W (multi-row kernel), and
-    # each row's result is the single-row call's, bit for bit.
+    # Small-batch decode: up to 4 rows share passes over W (multi-row kernel),
+    # each row the single-row call's bits; 5 or more take the few-row MFMA
+    # kernel, each row the same bits in any batch of 5 to 64 rows.
     rng = np.random.default_rng(M * 100 + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
     W = (0.02 * rng.standard_normal((N, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
     got = gpu_rmsnorm_linear_nk(gpu, x, g, W)
     for m in sorted({0, M // 2, M - 1}):
-        one = gpu_rmsnorm_linear_nk(gpu, x[m:m + 1], g, W)
-        assert np.array_equal(got[m], one[0]), f"row {m} of {M}"
+        one = helpers.peer_row(lambda xs: gpu_rmsnorm_linear_nk(gpu, xs, g, W), x, m)
+        assert np.array_equal(got[m], one), f"row {m} of {M}"
     Wt = np.ascontiguousarray(W.T)
     rows = np.array(sorted({0, M - 1}))
     y = orc.rmsnorm_linear(x[rows], g, Wt, EPS).astype(np.float64)
@@ -660,8 +662,9 @@ def test_rmsnorm_linear_f16w_nk_small_batch_rows_match_single_row_calls(gpu, orc
                                          (16, 4096, 4096, "f16"), (5, 4096, 4096, "f32"),
                                          (4, 257, 100, "f32")])
 def test_rmsnorm_linear_kn_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, dtype):
-    # Reference-layout weights A [K x N]: the split-K kernel with several
-    # activation rows; each row equals the single-row call bit for bit.
+    # Reference-layout weights A [K x N]: up to 4 rows take the split-K kernel
+    # with several activation rows, each row equal to the single-row call bit
+    # for bit; 5 or more the few-row MFMA kernel (same bits in any batch).
     rng = np.random.default_rng(M * 77 + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
@@ -670,8 +673,8 @@ def test_rmsnorm_linear_kn_small_batch_rows_match_single_row_calls(gpu, orc, M, 
         A = orc.f32_to_f16(A)
     got = gpu_rmsnorm_linear(gpu, x, g, A)
     for m in sorted({0, M // 2, M - 1}):
-        one = gpu_rmsnorm_linear(gpu, x[m:m + 1], g, A)
-        assert np.array_equal(got[m], one[0]), f"row {m} of {M}"
+        one = helpers.peer_row(lambda xs: gpu_rmsnorm_linear(gpu, xs, g, A), x, m)
+        assert np.array_equal(got[m], one), f"row {m} of {M}"
     rows = np.array(sorted({0, M - 1}))
     y = orc.rmsnorm_linear(x[rows], g, A, EPS).astype(np.float64)
     check_rmsnorm_linear(got[rows], y, x[rows], g, A, K, f"small batch kn {dtype} {M}x{N}x{K}")
@@ -679,14 +682,16 @@ def test_rmsnorm_linear_kn_small_batch_rows_match_single_row_calls(gpu, orc, M, 
 
 @pytest.mark.parametrize("M,N,K", [(2, 4096, 4096), (3, 130, 77), (8, 11008, 4096), (16, 64, 1000)])
 def test_matmul_small_m_rows_match_gemv(gpu, orc, M, N, K):
-    # matmul with a few rows shares passes over B; row m equals the M = 1
-    # product of A[m] bit for bit.
+    # matmul with up to 4 rows shares GEMV passes over B (row m equals the
+    # M = 1 product of A[m] bit for bit); with 5 to 64 the few-row MFMA kernel
+    # (row m has the same bits in any such batch).
     rng = np.random.default_rng(M + N + K)
     A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
     B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
     got = gpu_matmul(gpu, A, B)
     for m in sorted({0, M - 1}):
-        assert np.array_equal(got[m], gpu_matmul(gpu, A[m:m + 1], B)[0]), f"row {m} of {M}"
+        one = helpers.peer_row(lambda a: gpu_matmul(gpu, a, B), A, m)
+        assert np.array_equal(got[m], one), f"row {m} of {M}"
     y = orc.matmul(A, B).astype(np.float64)
     check_dot(got, y, helpers.absdot(A, B) + np.abs(y), K, f"matmul small M {M}x{N}x{K}")
 

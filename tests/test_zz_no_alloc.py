@@ -2,12 +2,12 @@
 eng_rmsnorm_linear_f16w (split-K partial sums in a static device buffer).
 
 Through the C-ABI: each call must equal eng_rmsnorm_linear_f16w's output bit
-for bit (same kernels and configuration) and the oracle within the derived
-bound, on consecutive calls whose second input is smaller (the static buffer
-keeps the last call's contents), on the null stream and a created stream, at
-the decode and small-batch row counts. Shapes past the limits fail with a
-message and write nothing.
-"""
+for bit (same kernels and configuration: split-K GEMV passes up to 4 rows,
+the few-row MFMA kernel from 5) and the oracle within the derived bound, on
+consecutive calls whose second input is smaller (the static buffer keeps the
+last call's contents), on the null stream and a created stream, at the decode
+and small-batch row counts. Shapes past the limits fail with a message and
+write nothing."""
 
 from __future__ import annotations
 
@@ -45,8 +45,8 @@ def test_noalloc_matches_the_allocating_entry_on_consecutive_calls(gpu, orc, use
     try:
         # larger first, then smaller: the second call reads a buffer the first
         # one filled further
-        for M, N, K in ((4, 11008, 4096), (1, 4096, 4096), (16, 2048, 1024), (3, 1000, 777),
-                        (1, 512, 256)):
+        for M, N, K in ((16, 11008, 4096), (4, 11008, 4096), (1, 4096, 4096), (16, 2048, 1024),
+                        (5, 1000, 776), (3, 1000, 777), (1, 512, 256)):
             W16, g, x = _case(gpu, rng, M, N, K)
             dW, dg, dx = gpu.upload(W16), gpu.upload(g), gpu.upload(x)
             want = _run(gpu, "eng_rmsnorm_linear_f16w", dW, dg, dx, M, N, K, h)
