@@ -18,6 +18,7 @@
 #include "launch.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <atomic>
 #include <cstddef>
 #include <memory>
@@ -182,6 +183,33 @@ void launch_rows_lds(const GemvArgs& a, std::size_t lds_bytes, hipStream_t strea
   ENG_LAUNCH_CHECK();
 }
 
+// Fixed-K fp16 GEMV launches (no RMSNorm) of 16-wave workgroups with x
+// staged by direct-to-LDS loads issued beside the first weight loads
+// (gemv_rows_dma_kernel; the same bits as the register-staged
+// gemv_rows_lds_kernel, which ENGINE_GEMV_NO_DMA=1 selects instead).
+bool gemv_dma_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMV_NO_DMA");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
+template <int NP, int KT, int CH>
+void launch_rows_dma(const GemvArgs& a, hipStream_t stream) {
+  ENG_CHECK(a.K == (NP - 1) * 512LL + KT, "gemv: fixed-K kernel for another K");
+  const long long wgs = (a.N + 15) / 16;
+  ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
+  const std::size_t lds = static_cast<std::size_t>(NP) * 512 * 4;
+  static std::atomic<bool> allowed[64] = {};
+  allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_dma_kernel<NP, KT, CH>),
+                   allowed, lds);
+  gemv::gemv_rows_dma_kernel<NP, KT, CH><<<static_cast<unsigned>(wgs), 1024, lds, stream>>>(
+      static_cast<const _Float16*>(a.W), static_cast<const float*>(a.x),
+      static_cast<float*>(a.y), a.N);
+  ENG_LAUNCH_CHECK();
+}
+
 // Output-major configuration, from sweeps on MI355X at the decode shapes
 // (cold weights): one wave per row fills the GPU once when N <= 16 x CUs
 // (4 waves per SIMD), and 4 x 1 KiB loads per row in flight is then best;
@@ -214,12 +242,16 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     // every CU at least 8 waves (16-wave workgroups from 16 rows per CU, else
     // 8-wave) -- at 4096 x 4096 6.84 us against 7.31 us for the register
     // kernel, whose per-row re-read of x through the vector L1 costs 0.8 us.
+    // Without RMSNorm, 16-wave workgroups stage x by direct-to-LDS loads that
+    // overlap the first weight loads: 6.72 us against 6.92 at 4096 x 4096.
     if (fits && (RMS || a.N >= one_round / 2 || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       const bool wide = RMS || a.N >= one_round || a.K > 4096;
       const bool fixed = with_fixed_k_f16(a.K, [&](auto fk) {
         using F = decltype(fk);
-        if (wide) {
+        if (!RMS && wide && gemv_dma_enabled()) {
+          launch_rows_dma<F::NP, F::KT, F::CH1>(a, stream);
+        } else if (wide) {
           launch_rows_lds<WT, 1, 4, RMS, 16, F::NP, F::KT, F::CH1>(a, lds, stream);
         } else {
           launch_rows_lds<WT, 1, 4, RMS, 8, F::NP, F::KT, F::CH1>(a, lds, stream);

@@ -686,6 +686,145 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __r
   }
 }
 
+// 16-byte direct global -> LDS load: lane l's 16 bytes land at lds + 16 l
+// (lds the same in every lane of the wave), from any address the lane names.
+// The builtin is device-only.
+__device__ __forceinline__ void dma16(const float* src, float* lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+#endif
+}
+
+// s_waitcnt immediate waiting for vmcnt <= n only (expcnt 7 and lgkmcnt 15
+// are the "don't wait" values).
+constexpr int vmcnt_le(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
+// s_waitcnt immediate waiting for lgkmcnt == 0 only (LDS stores done).
+constexpr int lgkmcnt_zero() { return 15 | (7 << 4) | (3 << 14); }
+
+// Workgroup barrier without a memory fence: __syncthreads()'s fence compiles
+// to a wait for every load in flight (here the weight rows already issued);
+// the memory clobber keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
+
+// Output-major fp16 GEMV (no RMSNorm) for K fixed at compile time
+// (K = (NP - 1) * 512 + KT), workgroups of 16 waves, one row per wave: the
+// arithmetic of gemv_rows_lds_kernel<_Float16, 8, 1, 4, false, 16, NP, KT, CH>
+// -- the same bits -- with x staged by direct global -> LDS loads issued
+// together with the row's first weight loads: a thread issues its staging
+// loads, then its wave's first CH weight pieces, and only then waits for the
+// staging (vmcnt counts its weight loads out) and meets the other waves at a
+// barrier without a fence, so the weight stream starts at once instead of
+// after the staging round trip. The LDS slot layout is lds_slot<8>: each
+// 16-byte chunk of it is 4 consecutive elements of x, so a lane fetches the
+// chunk its LDS position holds; chunks past K are zeroed with LDS stores.
+// (With RMSNorm the sum of squares and the x * gamma product need a second
+// barrier after the staging, which costs more than the early start gains:
+// measured 2% slower at 11008 x 4096, so RMSNorm keeps the staging kernel.)
+// Dynamic LDS: NP * 512 floats.
+template <int NP, int KT, int CH>
+__global__ __launch_bounds__(1024) void gemv_rows_dma_kernel(const _Float16* __restrict__ W,
+                                                             const float* __restrict__ x,
+                                                             float* __restrict__ y, long long N) {
+  using V = typename RawVec<_Float16, 8>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 512;
+  constexpr int WAVES = 16;
+  constexpr int K = (NP - 1) * PIECE + KT;
+  constexpr int CHUNKS = NP * PIECE / 4;           // 16-byte chunks of the staged vector
+  constexpr int INSTR = (CHUNKS + 1023) / 1024;    // staging loads per thread
+  constexpr int G = (NP + CH - 1) / CH;
+  constexpr int LAST = NP - (G - 1) * CH;
+  static_assert(KT > 0 && KT <= PIECE && KT % 8 == 0, "K = (NP - 1) * 512 + KT");
+  extern __shared__ float xs[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const long long n0 = static_cast<long long>(blockIdx.x) * WAVES + wave;
+
+  // Staging: wave w's i-th load fills chunks (16 i + w) * 64 .. + 63 of the
+  // LDS vector; chunk q holds elements chunk_k0(q) .. + 3 of x. Chunks past K
+  // (the last piece when KT < 512) are zeroed first, with LDS stores (a store
+  // after a direct load the compiler cannot prove disjoint would make it
+  // wait for the load).
+  auto chunk_k0 = [](int q) {
+    const int p = q >> 7;
+    const int r = q & 127;
+    return p * PIECE + (r & 63) * 8 + (r >> 6) * 4;
+  };
+  if constexpr (KT < PIECE) {
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int q = (16 * i + wave) * 64 + lane;
+      if (q < CHUNKS && chunk_k0(q) >= K) *reinterpret_cast<F4*>(xs + 4 * q) = F4{};
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < INSTR; ++i) {
+    const int q0 = (16 * i + wave) * 64;
+    if (q0 < CHUNKS) {  // wave-uniform
+      const int q = q0 + lane;
+      if (q < CHUNKS && chunk_k0(q) < K) dma16(x + chunk_k0(q), xs + 4 * q0);
+    }
+  }
+  // The staging loads must be issued before the weight loads: the wait below
+  // counts the weight loads out, and loads complete in issue order.
+  __builtin_amdgcn_sched_barrier(0);
+
+  const bool active = n0 < N;
+  const _Float16* row = W + (active ? n0 : N - 1) * static_cast<long long>(K);
+  const int lk = lane * 8;
+  float acc = 0.0f;
+  auto use = [&](int p, const V& w) {
+    const float* base = xs + p * PIECE + lane * 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const F4 a = *reinterpret_cast<const F4*>(base + h * 256);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(a[e], static_cast<float>(w[h * 4 + e]), acc);
+    }
+  };
+  // A partial last piece is loaded by every lane (lanes past K read the
+  // piece's first 16 bytes, in bounds) and zeroed where it is used: no branch
+  // around a load, and nothing that needs the data before the first wait (a
+  // branch or an early select there makes the compiler wait for every load).
+  auto ok = [&](int p) { return p < NP - 1 || KT == PIECE || lk < KT; };
+  auto load = [&](int p) -> V {
+    return __builtin_nontemporal_load(reinterpret_cast<const V*>(row + p * PIECE + (ok(p) ? lk : 0)));
+  };
+
+  // First group of weight pieces, then wait for the staging only.
+  {
+    constexpr int FIRST = G > 1 ? CH : LAST;
+    V cur[FIRST];
+#pragma unroll
+    for (int u = 0; u < FIRST; ++u) cur[u] = load(u);
+#if defined(__HIP_DEVICE_COMPILE__)
+    // loads complete in order: at most FIRST (this wave's weight loads)
+    // outstanding means the staging loads have landed; the zero stores of
+    // padding chunks must be done too
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(FIRST));
+    __builtin_amdgcn_s_waitcnt(lgkmcnt_zero());
+#endif
+    __builtin_amdgcn_sched_barrier(0);
+    barrier_no_fence();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < FIRST; ++u) use(u, ok(u) ? cur[u] : V{});
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll 1
+  for (int c = 1; c < G; ++c) {
+    V cur[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) cur[u] = load(c * CH + u);
+#pragma unroll
+    for (int u = 0; u < CH; ++u) use(c * CH + u, ok(c * CH + u) ? cur[u] : V{});
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  acc = wave_sum(acc);
+  if (lane == 0 && active) y[n0] = acc;
+}
+
 // acc[m][j] = sum_k rows[j][k] * xs_m[k] for MX staged activation rows (row m
 // at xs + m * pitch), folded across the wave: the weight pieces are loaded and
 // converted once and used for every activation row. Each (m, j) sum runs over

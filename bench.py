@@ -44,8 +44,8 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
 METRIC = "decode GEMV HBM GB/s (% of peak); FP32 GEMM TFLOP/s at 4096^3 (% MFMA peak)"
 
 
-HEADLINE_KERNEL = "eng::gemv::gemv_rows_lds_kernel<_Float16, 8, 1, 4, false, 16, 8, 512, 8>"
-TRAFFIC_PROFILE = os.path.join("profiles", "gemv_rows_lds_fixed_f16w_4096x4096_cold.md")
+HEADLINE_KERNEL = "eng::gemv::gemv_rows_dma_kernel<8, 512, 8>"
+TRAFFIC_PROFILE = os.path.join("profiles", "gemv_rows_dma_fixed_f16w_4096x4096_cold.md")
 
 
 def log(msg: str) -> None:
