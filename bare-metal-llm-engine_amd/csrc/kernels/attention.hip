@@ -429,33 +429,15 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_lds_kernel(
 // compiler then need not make a fragment read wait for the loads in flight
 // into the other stages. Each thread issues the same CPT loads per tile, and
 // waits with vmcnt = CPT x (tiles issued after the one it needs).
-__device__ __forceinline__ void lds_dma16(const _Float16* src, _Float16* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#endif
-}
-
-// s_waitcnt immediate waiting for vmcnt <= n only (expcnt 7 and lgkmcnt 15
-// are the "don't wait" values).
-constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
-
-// Workgroup barrier without a memory fence. __syncthreads() also fences, and
-// the compiler implements that fence with a wait for every load in flight --
-// all stages of the pipeline, not just the tile the next step needs. The
-// tile loop writes no LDS, and each wave waits for its own loads of the next
-// tile before it arrives, so a bare s_barrier is all it needs; the memory
-// clobber keeps the compiler from moving LDS reads across it.
-__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
-
 template <int CPT>
 __device__ __forceinline__ void wait_tiles_after(int outstanding) {
 #if defined(__HIP_DEVICE_COMPILE__)
   if (outstanding >= 2) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * CPT));
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(2 * CPT));
   } else if (outstanding == 1) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(CPT));
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(CPT));
   } else {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
   }
 #endif
 }
@@ -535,8 +517,8 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
       long long j = j0 + static_cast<long long>(t) * T + slot / LPK;
       j = j < j1 ? j : j1 - 1;
       const long long off = j * D + (slot % LPK) * 8;
-      lds_dma16(kb + off, ks + 8 * slot0);
-      lds_dma16(vb + off, vs + 8 * slot0);
+      dma16(kb + off, ks + 8 * slot0);
+      dma16(vb + off, vs + 8 * slot0);
     }
   };
   // One resident tile. Each K row is read once for the wave's HPW heads;
@@ -785,8 +767,8 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_mfma_kernel(
       const int pos = slot & 7;
       long long j = j0 + static_cast<long long>(t) * T + r;
       j = j < j1 ? j : j1 - 1;
-      lds_dma16(kb + j * D + 8 * (pos ^ ((r >> 1) & 7)), st + 8 * slot0);
-      lds_dma16(vb + j * D + 8 * pos, st + T * D + 8 * slot0);
+      dma16(kb + j * D + 8 * (pos ^ ((r >> 1) & 7)), st + 8 * slot0);
+      dma16(vb + j * D + 8 * pos, st + T * D + 8 * slot0);
     }
   };
 

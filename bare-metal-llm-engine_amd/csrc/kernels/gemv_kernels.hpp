@@ -25,6 +25,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "device_sync.hpp"
+
 namespace eng {
 namespace gemv {
 
@@ -686,25 +688,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __r
   }
 }
 
-// 16-byte direct global -> LDS load: lane l's 16 bytes land at lds + 16 l
-// (lds the same in every lane of the wave), from any address the lane names.
-// The builtin is device-only.
-__device__ __forceinline__ void dma16(const float* src, float* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#endif
-}
-
-// s_waitcnt immediate waiting for vmcnt <= n only (expcnt 7 and lgkmcnt 15
-// are the "don't wait" values).
-constexpr int vmcnt_le(int n) { return (n & 15) | (7 << 4) | (15 << 8) | (((n >> 4) & 3) << 14); }
-// s_waitcnt immediate waiting for lgkmcnt == 0 only (LDS stores done).
-constexpr int lgkmcnt_zero() { return 15 | (7 << 4) | (3 << 14); }
-
-// Workgroup barrier without a memory fence: __syncthreads()'s fence compiles
-// to a wait for every load in flight (here the weight rows already issued);
-// the memory clobber keeps the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_barrier" ::: "memory"); }
 
 // Output-major fp16 GEMV (no RMSNorm) for K fixed at compile time
 // (K = (NP - 1) * 512 + KT), workgroups of 16 waves, one row per wave: the

@@ -1,5 +1,5 @@
 // skinny.hip -- linear layers over a few activation rows (5 <= M <= 64) on
-// FP32 MFMA, streaming the weights once.
+// the matrix cores, streaming the weights once.
 //
 // Y[M x N] = X'[M x K] . W with X' = X (matmul) or X * gamma (rmsnorm_linear,
 // whose row scale s_m = 1/sqrt(mean_k X[m][k]^2 + eps) is applied after the
@@ -10,39 +10,22 @@
 // its tile and leaves most CUs idle (the MFMA GEMM here: ~114 us at
 // 11008 x 4096 for any M <= 64 against ~15 us to read W once).
 //
-// v_mfma_f32_16x16x4_f32 (A[i][k] lane i + 16 k, B[k][j] lane j + 16 k,
-// D[i][j] lane j + 16 (i / 4) element i % 4) with the weights loaded straight
-// from HBM into the operand registers -- no LDS staging, every weight element
-// passes through exactly one lane once:
-//   * lane (j = l % 16, s = l / 16); the dot products run over k in a
-//     lane-friendly order: k-group g (32 values of k) gives slot s the 8
-//     consecutive k = g + 8 s + t, t = 0..7, at MFMA step t (a sum over k
-//     does not care which slot takes which k);
-//   * reference layout: lane (j, s) reads W row g + 8 s + t at columns
-//     n0 + 4 j .. 4 j + 3 (16 lanes = 128 contiguous bytes of a row for
-//     fp16), and column element e feeds MFMA block e as the B operand: block
-//     e's column j is physical column n0 + 4 j + e, so 4 blocks cover a tile
-//     of 64 columns. X is the A operand (rows m).
-//   * output-major layout: lane (j, s) reads row n0 + 16 b + j of W at
-//     k = g + 8 s .. + 7 (element t feeds step t) as the A operand of block
-//     b; X^T is the B operand. 4 blocks b cover 64 rows of W.
-//   * the X fragment is the same in both: lane (j, s) holds X[m0 + j][g + 8 s
-//     + t] for t = 0..7 (two 16-byte loads from L2 per m-block; X is at most
-//     64 x K floats and stays cached), times gamma[k].
-//
-// Work split (stream-K): the work is tiles of 64 columns of Y times units of
-// 128 values of k (one k-group per wave); a grid of exactly P = 2 workgroups
-// per CU (one round) takes equal runs of consecutive units, tile by tile, so
-// every CU streams the same number of weight bytes whatever N is (N = 11008
-// is 172 tiles: no whole number of tiles or K chunks per CU). A workgroup's 4
-// waves take the k-groups of each unit in turn and their accumulators are
-// summed through LDS in wave order. A tile a workgroup covers whole is
-// written to Y directly (scaled by its rows' RMS factors); a tile split
+// Work split (stream-K), shared by both layouts: the work is tiles of 64
+// weight rows (output-major) or columns (reference layout) times units of
+// 128 values of k; a grid of exactly P = 2 workgroups per CU (one round)
+// takes equal runs of consecutive units, tile by tile, so every CU streams
+// the same number of weight bytes whatever N is (N = 11008 is 172 tiles: no
+// whole number of tiles or K chunks per CU). A tile a workgroup covers whole
+// is written to Y directly (scaled by its rows' RMS factors); a tile split
 // between workgroups gets one record of partial sums (and sums of squares)
 // per workgroup, added by skinny_reduce_kernel in workgroup order. The split
 // points depend on N, K and the CU count only -- never on M -- and each
 // output's arithmetic involves only its own row of X, so a row's result is
 // the same bits whichever M (5..64) it is computed in.
+//
+// skinny_nk_kernel (output-major W) and skinny_mfma_kernel (reference
+// layout) differ in how a workgroup covers a unit; see each kernel.
+#include "device_sync.hpp"
 #include "launch.hpp"
 
 #include <algorithm>
@@ -115,13 +98,23 @@ struct Plan {
   long long P = 0;      // workgroups
 };
 
+// floor(a / b) for 0 <= a < 2^53, b > 0: a double-precision estimate
+// corrected with integer multiplies (a 64-bit integer division costs ~150
+// instructions on the GPU; the reduce kernel needs several per thread).
+__host__ __device__ inline long long floor_div(long long a, long long b) {
+  long long q = static_cast<long long>(static_cast<double>(a) / static_cast<double>(b));
+  while (q > 0 && q * b > a) --q;
+  while ((q + 1) * b <= a) ++q;
+  return q;
+}
+
 __host__ __device__ inline long long unit_begin(long long w, long long U, long long P) {
-  return w * U / P;
+  return floor_div(w * U, P);
 }
 
 // Workgroup whose run contains unit u.
 __host__ __device__ inline long long worker_of(long long u, long long U, long long P) {
-  long long w = (u * P + P - 1) / U;
+  long long w = floor_div(u * P + P - 1, U);
   if (w >= P) w = P - 1;
   while (w + 1 < P && unit_begin(w + 1, U, P) <= u) ++w;
   while (w > 0 && unit_begin(w, U, P) > u) --w;
@@ -137,8 +130,23 @@ Plan make_plan(long long N, long long K, long long cus) {
   return p;
 }
 
-// MB m-blocks of 16 rows (M <= 16 MB). NK: W output-major [N x K]. RMS: X is
-// multiplied by gamma (if given) and the sums of squares are produced.
+// Reference layout (used with NK false; the output-major instantiation is
+// superseded by skinny_nk_kernel). v_mfma_f32_16x16x4_f32 (A[i][k] lane
+// i + 16 k, B[k][j] lane j + 16 k, D[i][j] lane j + 16 (i / 4) element i % 4)
+// with the weights loaded straight from HBM into the operand registers:
+//   * lane (j = l % 16, s = l / 16); k-group g (32 values of k) gives slot s
+//     the 8 consecutive k = g + 8 s + t, t = 0..7, at MFMA step t (a sum over
+//     k does not care which slot takes which k);
+//   * lane (j, s) reads W row g + 8 s + t at columns n0 + 4 j .. 4 j + 3 (16
+//     lanes = 128 contiguous bytes of a row for fp16), and column element e
+//     feeds MFMA block e as the B operand: block e's column j is physical
+//     column n0 + 4 j + e, so 4 blocks cover a tile of 64 columns. X is the A
+//     operand (rows m): lane (j, s) holds X[m0 + j][g + 8 s + t] for t = 0..7
+//     (two 16-byte loads from L2 per m-block), times gamma[k].
+// A workgroup's 4 waves take the k-groups of each unit in turn and their
+// accumulators are summed through LDS in wave order.
+// MB m-blocks of 16 rows (M <= 16 MB). RMS: X is multiplied by gamma (if
+// given) and the sums of squares are produced.
 // rec: [P][2][M][64] partial sums of the (at most two) tiles a workgroup
 // shares with others -- slot 0 its first tile, slot 1 its last --, rec_ss
 // [P][2][M] their sums of squares.
@@ -418,6 +426,347 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_mfma_kernel(
   }
 }
 
+template <typename WT>
+struct WVec;
+template <>
+struct WVec<_Float16> {
+  using type = halfx8;
+};
+template <>
+struct WVec<float> {
+  using type = floatx4;
+};
+
+// Output-major W [N x K]: wave w of a workgroup owns the 16 weight rows
+// n0 + 16 w .. + 15 of each tile and runs the workgroup's whole range of
+// units over them; the activations of a unit (16 MB rows x 128 values of k,
+// times gamma) are staged in LDS once per workgroup. Lane (j, s) loads 16
+// bytes of row n0 + 16 w + j at k = k_u + 4 E i + E s (E elements per 16
+// bytes, i the load of the unit), so one load instruction covers 16 rows x 64
+// bytes and a wave's consecutive loads continue along the same rows: each row
+// is read in 256-byte runs per unit (64-byte runs spread over row blocks and
+// waves streamed at 4.4-4.7 TB/s).
+//
+// fp16 weights: v_mfma_f32_16x16x32_f16 takes a load as it arrives (lane
+// (j, s) holds A[j][8 s .. 8 s + 7] of the 32 values of k of load i). The
+// activations enter as two fp16 planes: per unit and row, t = x' 2^e with
+// the power of two 2^e putting max |t| in [2^14, 2^15), hi = fp16(t) and
+// lo = fp16((t - hi) 2^11) -- t - hi is exact in fp32 and lo keeps its top
+// 11 bits, so hi + lo 2^-11 carries 22 significant bits of each x' and the
+// products hi w, lo w are exact in fp32. Two MFMAs per load and m-block
+// (hi and lo accumulators); after each unit the row's partial
+// (acc_hi + acc_lo 2^-11) 2^-e is added to its running sum. That is 4x fewer
+// matrix cycles than fp32 MFMA on the same data, within 2^-22 relative of
+// each x' (fp32 products round at 2^-24).
+// fp32 weights: v_mfma_f32_16x16x4_f32, 8 MFMAs per load (step t takes
+// element t, k slot s), X' in fp32 planes.
+// Both: D[i][j] (lane j + 16 (i / 4), element i % 4) is weight row 16 w + i
+// against activation row 16 mb + j.
+//
+// Units run in one software pipeline across the workgroup's tiles: each
+// weight load is reissued for the next unit right after its values are
+// taken (one unit of weights in flight per wave -- with this access pattern
+// more in flight measured slower: 16 rows x 256 bytes per wave streams 90 MB
+// in 18.2 us, two units ahead 21.6, three 22.4), the next unit's X loaded at
+// the start of a unit and written to the other LDS buffer at its end; one
+// barrier per unit.
+// Staging: thread t takes k chunk t % 32 (4 values) of rows t / 32 + 8 r,
+// whatever MB: it multiplies by gamma, adds the squares of x into its per-row
+// sum of squares (RMS), and for fp16 weights folds |x'| over the row's 32
+// chunk threads (adjacent lanes, xor butterfly) for the scale. The tile end
+// folds the sums of squares the same way -- orders fixed by the plan, never
+// by M.
+// LDS, per buffer: fp32 X' as 16-byte chunks, row m at m * 32, chunk c at
+// c ^ (m & 7); fp16 planes with 8-value chunks, row m at m * 16, chunk c at
+// c ^ (m & 7) (the 16 rows one MFMA operand read touches land in different
+// banks).
+template <typename WT, int MB, bool RMS>
+__global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
+    const WT* __restrict__ W, const float* __restrict__ x, const float* __restrict__ gamma,
+    float* __restrict__ y, int M, long long N, long long K, Plan plan,
+    float* __restrict__ rec, float* __restrict__ rec_ss, float eps) {
+  using WV = typename WVec<WT>::type;
+  constexpr bool H = std::is_same<WT, _Float16>::value;    // fp16 MFMA path
+  constexpr int E = 16 / static_cast<int>(sizeof(WT));     // elements per 16-byte load
+  constexpr int LPU = static_cast<int>(kUnitK) / (4 * E);  // loads per unit per lane
+  constexpr int ROWS = 16 * MB;
+  constexpr int CPR = static_cast<int>(kUnitK) / 4;        // 4-value chunks per row per unit
+  constexpr int THREADS = kWaves * 64;
+  constexpr int SPT = ROWS * CPR / THREADS;                // staged chunks per thread
+  constexpr int HCR = static_cast<int>(kUnitK) / 8;        // 8-value chunks per fp16 plane row
+  static_assert(SPT * THREADS == ROWS * CPR, "staging covers the unit");
+  // One LDS buffer: fp32 X' (ROWS x 32 16-byte chunks), or the fp16 hi and
+  // lo planes (ROWS x 16 chunks each) and the rows' descale factors 2^-e.
+  struct XBuf {
+    floatx4 f[H ? 1 : ROWS * CPR];
+    halfx8 hi[H ? ROWS * HCR : 1];
+    halfx8 lo[H ? ROWS * HCR : 1];
+    float ds[H ? ROWS : 1];
+  };
+  __shared__ XBuf xbuf[2];
+  __shared__ float ssc[RMS ? ROWS : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = lane & 15;
+  const int s = lane >> 4;
+  const long long w_id = blockIdx.x;
+  const long long u0 = unit_begin(w_id, plan.U, plan.P);
+  const long long u1 = unit_begin(w_id + 1, plan.U, plan.P);
+  if (u0 >= u1) return;  // (only when U < P, which the host avoids)
+  const long long upt = plan.upt;
+  const long long t_first = u0 / upt;
+
+  // ---- staging ----
+  // Loads past K or past the range read offset 0 of the same row and are
+  // zeroed at the store (no branch around a load); without a gain the gamma
+  // loads read x and are replaced by ones.
+  const bool has_g = gamma != nullptr;
+  const float* gsrc = has_g ? gamma : x;
+  const int qc = tid % CPR;
+  // One unit's X and gamma in registers, and whether its k chunk is in range.
+  struct XStage {
+    floatx4 xr[SPT];
+    floatx4 gr;
+    bool xok;
+  };
+  float ssr[RMS ? SPT : 1];
+#pragma unroll
+  for (int r = 0; r < (RMS ? SPT : 1); ++r) ssr[r] = 0.0f;
+  // X of unit u, which is unit ku of its tile.
+  auto load_x = [&](XStage& S, long long u, long long ku) __attribute__((always_inline)) {
+    const long long k = ku * kUnitK + 4 * qc;
+    S.xok = u < u1 && k < K;
+    const long long ko = S.xok ? k : 0;
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) {
+      const int m = tid / CPR + (THREADS / CPR) * r;
+      S.xr[r] = *reinterpret_cast<const floatx4*>(x + static_cast<long long>(m < M ? m : M - 1) * K + ko);
+    }
+    S.gr = *reinterpret_cast<const floatx4*>(gsrc + ko);
+  };
+  auto store_x = [&](const XStage& S, XBuf& xb) __attribute__((always_inline)) {
+    const auto& xr = S.xr;
+    const auto& gr = S.gr;
+    const bool xok = S.xok;
+    const floatx4 zero = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const floatx4 g = has_g ? gr : floatx4{1.0f, 1.0f, 1.0f, 1.0f};
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) {
+      const int m = tid / CPR + (THREADS / CPR) * r;
+      const floatx4 v = xok ? xr[r] : zero;
+      if constexpr (RMS) {
+        ssr[r] = fmaf(v[0], v[0], ssr[r]);
+        ssr[r] = fmaf(v[1], v[1], ssr[r]);
+        ssr[r] = fmaf(v[2], v[2], ssr[r]);
+        ssr[r] = fmaf(v[3], v[3], ssr[r]);
+      }
+      const floatx4 xv = v * g;
+      if constexpr (H) {
+        float amax = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
+#pragma unroll
+        for (int o = CPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        int ex = 0;
+        (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1) (ex = 0 for 0, inf, nan)
+        const int e = min(15 - ex, 126);
+        halfx4 h, l;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float t = ldexpf(xv[q], e);
+          h[q] = static_cast<_Float16>(t);
+          l[q] = static_cast<_Float16>((t - static_cast<float>(h[q])) * 2048.0f);
+        }
+        const int pos = m * HCR + ((qc >> 1) ^ (m & 7));
+        reinterpret_cast<halfx4*>(&xb.hi[pos])[qc & 1] = h;
+        reinterpret_cast<halfx4*>(&xb.lo[pos])[qc & 1] = l;
+        if (qc == 0) xb.ds[m] = ldexpf(1.0f, -e);
+      } else {
+        xb.f[m * CPR + (qc ^ (m & 7))] = xv;
+      }
+    }
+  };
+
+  // ---- weights ----
+  // Cursor over the workgroup's units: unit, tile, unit within the tile, and
+  // the lane's weight row.
+  struct Cursor {
+    long long u, tile, ku;
+    const WT* row;
+  };
+  auto row_of = [&](long long tile) {
+    long long n = tile * kCols + 16 * wave + j;
+    n = n < N ? n : N - 1;
+    return W + n * K;
+  };
+  auto advance = [&](Cursor& c) {
+    ++c.u;
+    if (++c.ku == upt) {
+      c.ku = 0;
+      ++c.tile;
+      c.row = row_of(c.tile);
+    }
+  };
+  // Load i of the cursor's unit (past K or past the range: offset 0 of the
+  // row, zeroed at use or never used).
+  auto w_src = [&](const Cursor& c, int i) -> const WV* {
+    const long long k = c.ku * kUnitK + 4 * E * i + E * s;
+    return reinterpret_cast<const WV*>(c.row + ((c.u < u1 && k < K) ? k : 0));
+  };
+  auto load_w = [&](WV (&w)[LPU], const Cursor& c) {
+#pragma unroll
+    for (int i = 0; i < LPU; ++i) w[i] = __builtin_nontemporal_load(w_src(c, i));
+  };
+
+  // acc: the running sums (fp32 path: the MFMA accumulators themselves);
+  // acl: the fp16 path's lo accumulators (acc_hi is ach).
+  floatx4 acc[MB], ach[H ? MB : 1], acl[H ? MB : 1];
+  auto zero4 = [] { return floatx4{0.0f, 0.0f, 0.0f, 0.0f}; };
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
+  if constexpr (H) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) ach[mb] = acl[mb] = zero4();
+  }
+
+  // The LPU loads of the unit at cur against buffer xb; load i of w is
+  // reissued for the cursor `next` once its values are taken (scheduling
+  // barriers keep the reload below that point, so it reuses the set's
+  // registers and the loop carries no register copies, which would wait for
+  // the loads in flight). Pieces past K (the last unit of a row when
+  // K % 128 != 0) are zeroed here.
+  auto compute = [&](WV (&w)[LPU], const XBuf& xb, const Cursor& cur, const Cursor& next)
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < LPU; ++i) {
+      const bool kok = cur.ku * kUnitK + 4 * E * i + E * s < K;
+      if constexpr (H) {
+        const halfx8 wi = kok ? w[i] : halfx8{};
+        halfx8 bh[MB], bl[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 7));
+          bh[mb] = xb.hi[pos];
+          bl[mb] = xb.lo[pos];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        w[i] = __builtin_nontemporal_load(w_src(next, i));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          ach[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bh[mb], ach[mb], 0, 0, 0);
+          acl[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bl[mb], acl[mb], 0, 0, 0);
+        }
+      } else {
+        const WV wi = kok ? w[i] : WV{};
+        floatx4 xf[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) xf[mb] = xb.f[(16 * mb + j) * CPR + ((4 * i + s) ^ (j & 7))];
+        __builtin_amdgcn_sched_barrier(0);
+        w[i] = __builtin_nontemporal_load(w_src(next, i));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wi[t], xf[mb][t], acc[mb], 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (H) {
+      // the unit's partial, descaled, into the running sums
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const float d = xb.ds[16 * mb + j];
+        const floatx4 p = ach[mb] + acl[mb] * (1.0f / 2048.0f);
+        acc[mb] += p * d;
+        ach[mb] = acl[mb] = zero4();
+      }
+    }
+  };
+
+  // Tile end: whole tiles go to y (scaled by their rows' RMS factors), split
+  // tiles to this workgroup's record slot.
+  auto finish = [&](const Cursor& c) __attribute__((always_inline)) {
+    const long long tile = c.tile;
+    const bool whole = tile * upt >= u0 && c.ku == upt - 1;
+    const int slot = tile == t_first ? 0 : 1;
+    float tot[MB];
+    if constexpr (RMS) {
+      // a row's 32 chunk threads are 32 adjacent lanes: xor butterfly
+      // (every lane ends with the same bits)
+#pragma unroll
+      for (int r = 0; r < SPT; ++r) {
+        float v = ssr[r];
+#pragma unroll
+        for (int o = CPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        if (qc == 0) ssc[tid / CPR + (THREADS / CPR) * r] = v;
+        ssr[r] = 0.0f;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) tot[mb] = ssc[16 * mb + j];
+    }
+    const int cbase = 16 * wave + 4 * s;  // column of element 0 within the tile
+    float* rec_tile = rec + (w_id * 2 + slot) * static_cast<long long>(M) * kCols;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int m = 16 * mb + j;
+      if (m >= M) continue;
+      if (whole) {
+        const float scale = RMS ? 1.0f / sqrtf(tot[mb] / static_cast<float>(K) + eps) : 1.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const long long n = tile * kCols + cbase + e;
+          if (n < N) y[static_cast<long long>(m) * N + n] = acc[mb][e] * scale;
+        }
+      } else {
+        *reinterpret_cast<floatx4*>(rec_tile + static_cast<long long>(m) * kCols + cbase) = acc[mb];
+        if (RMS && wave == 0 && s == 0) rec_ss[(w_id * 2 + slot) * M + m] = tot[mb];
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
+  };
+
+  // Prologue: X of unit u0 (loaded before the weights, so the wait for it
+  // leaves them in flight), the weights of unit u0, X' of u0 to LDS.
+  Cursor cc{u0, t_first, u0 - t_first * upt, row_of(t_first)};  // unit being computed
+  Cursor cl = cc;                                                 // next weight load
+  XStage S;
+  long long xu = u0, xku = u0 - t_first * upt;  // next X to load: unit, unit in its tile
+  auto x_next = [&]() __attribute__((always_inline)) {
+    load_x(S, xu, xku);
+    ++xu;
+    if (++xku == upt) xku = 0;
+  };
+  x_next();
+  WV w[LPU];
+  load_w(w, cl);
+  advance(cl);
+  store_x(S, xbuf[0]);
+  lds_barrier();
+
+  // One unit per iteration with X' in buffer b: loads X of the next unit
+  // first, then computes (reloading w for the next unit load by load),
+  // writes the next unit's X' to the other buffer. A single loop body (no
+  // unrolling) keeps the weight registers in place across iterations: two
+  // copies of the body assigned them differently, and the copies between
+  // them waited for every load in flight.
+  for (int b = 0;; b ^= 1) {
+    x_next();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(w, xbuf[b], cc, cl);
+    advance(cl);
+    if (cc.ku == upt - 1 || cc.u == u1 - 1) finish(cc);
+    if (cc.u + 1 < u1) store_x(S, xbuf[b ^ 1]);
+    lds_barrier();
+    advance(cc);
+    if (cc.u >= u1) break;
+  }
+}
+
 // Tiles split between workgroups: y[m][n] = s_m * sum over the tile's
 // workgroups, in workgroup order, of their records (s_m = 1 without RMS;
 // with RMS from the records' sums of squares, added in the same order).
@@ -439,13 +788,15 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
   if (wf == wl) return;  // one workgroup covered the tile: written directly
   float v = 0.0f;
   float tot = 0.0f;
+  // Every workgroup after wf starts inside the tile (its first tile, slot
+  // 0); wf's record is slot 0 only when it starts exactly at the tile.
+  const int slot_f = unit_begin(wf, plan.U, plan.P) == tile * plan.upt ? 0 : 1;
   for (long long w0 = wf; w0 <= wl; w0 += 4) {
     float p[4], q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const long long w = w0 + i <= wl ? w0 + i : wl;
-      const int slot = unit_begin(w, plan.U, plan.P) / plan.upt == tile ? 0 : 1;
-      const long long r = w * 2 + slot;
+      const long long r = w * 2 + (w == wf ? slot_f : 0);
       p[i] = rec[(r * M + m) * kCols + c];
       if constexpr (RMS) q[i] = rec_ss[r * M + m];
     }
@@ -484,8 +835,15 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
     rec = static_cast<float*>(ws->get());
   }
   float* rec_ss = rec + plan.P * 2 * static_cast<long long>(M) * kCols;
-  skinny_mfma_kernel<WT, NK, MB, RMS><<<static_cast<unsigned>(plan.P), kWaves * 64, 0, stream>>>(
-      static_cast<const WT*>(a.W), a.x, a.gamma, a.y, M, N, K, plan, rec, rec_ss, a.eps);
+  const unsigned grid = static_cast<unsigned>(plan.P);
+  const WT* W = static_cast<const WT*>(a.W);
+  if constexpr (NK) {
+    skinny_nk_kernel<WT, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(
+        W, a.x, RMS ? a.gamma : nullptr, a.y, M, N, K, plan, rec, rec_ss, a.eps);
+  } else {
+    skinny_mfma_kernel<WT, NK, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(
+        W, a.x, a.gamma, a.y, M, N, K, plan, rec, rec_ss, a.eps);
+  }
   ENG_LAUNCH_CHECK();
   // Every workgroup takes whole tiles: nothing left to add.
   if (plan.U % plan.P == 0 && (plan.U / plan.P) % plan.upt == 0) return;
