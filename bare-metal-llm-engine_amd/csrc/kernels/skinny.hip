@@ -770,44 +770,52 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
 // Tiles split between workgroups: y[m][n] = s_m * sum over the tile's
 // workgroups, in workgroup order, of their records (s_m = 1 without RMS;
 // with RMS from the records' sums of squares, added in the same order).
-// Row m is blockIdx.y; columns of tiles that one workgroup covered whole are
-// skipped (already written). Up to 4 records' loads in flight per batch.
+// One block per (tile, 16 rows): the plan arithmetic runs once per block
+// (the same for every thread), thread (r, c4) adds 4 consecutive columns of
+// row 16 blockIdx.y + r with one 16-byte load per record, up to 4 records
+// in flight. Tiles one workgroup covered whole are skipped (written
+// directly).
 template <bool RMS>
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ rec,
                                                             const float* __restrict__ rec_ss,
                                                             float* __restrict__ y, int M,
                                                             long long N, long long K, Plan plan,
                                                             float eps) {
-  const long long n = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
-  const int m = blockIdx.y;
-  if (n >= N) return;
-  const long long tile = n / kCols;
-  const int c = static_cast<int>(n - tile * kCols);
+  const long long tile = blockIdx.x;
   const long long wf = worker_of(tile * plan.upt, plan.U, plan.P);
   const long long wl = worker_of(tile * plan.upt + plan.upt - 1, plan.U, plan.P);
   if (wf == wl) return;  // one workgroup covered the tile: written directly
-  float v = 0.0f;
-  float tot = 0.0f;
+  const int r = threadIdx.x / 16;
+  const int c = 4 * (threadIdx.x % 16);
+  const int m = 16 * static_cast<int>(blockIdx.y) + r;
+  if (m >= M) return;
   // Every workgroup after wf starts inside the tile (its first tile, slot
   // 0); wf's record is slot 0 only when it starts exactly at the tile.
   const int slot_f = unit_begin(wf, plan.U, plan.P) == tile * plan.upt ? 0 : 1;
+  floatx4 v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  float tot = 0.0f;
   for (long long w0 = wf; w0 <= wl; w0 += 4) {
-    float p[4], q[4];
+    floatx4 p[4];
+    float q[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const long long w = w0 + i <= wl ? w0 + i : wl;
-      const long long r = w * 2 + (w == wf ? slot_f : 0);
-      p[i] = rec[(r * M + m) * kCols + c];
-      if constexpr (RMS) q[i] = rec_ss[r * M + m];
+      const long long rr = w * 2 + (w == wf ? slot_f : 0);
+      p[i] = *reinterpret_cast<const floatx4*>(rec + (rr * M + m) * kCols + c);
+      if constexpr (RMS) q[i] = rec_ss[rr * M + m];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v += w0 + i <= wl ? p[i] : 0.0f;
+      v += w0 + i <= wl ? p[i] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
       if constexpr (RMS) tot += w0 + i <= wl ? q[i] : 0.0f;
     }
   }
   if constexpr (RMS) v *= 1.0f / sqrtf(tot / static_cast<float>(K) + eps);
-  y[static_cast<long long>(m) * N + n] = v;
+  float* yr = y + static_cast<long long>(m) * N + tile * kCols + c;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if (tile * kCols + c + e < N) yr[e] = v[e];
+  }
 }
 
 std::size_t scratch_for(const Plan& p, long long M) {
@@ -820,7 +828,8 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
   const long long K = a.K;
   const int M = static_cast<int>(a.M);
   const Plan plan = make_plan(N, K, device_cu_count());
-  ENG_CHECK(plan.P <= 0x7fffffffLL, "linear: grid too large for one launch");
+  ENG_CHECK(plan.P <= 0x7fffffffLL && plan.tiles <= 0x7fffffffLL,
+            "linear: grid too large for one launch");
   const std::size_t need = scratch_for(plan, M);
   float* rec = nullptr;
   std::unique_ptr<StreamScratch> ws;
@@ -847,7 +856,7 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
   ENG_LAUNCH_CHECK();
   // Every workgroup takes whole tiles: nothing left to add.
   if (plan.U % plan.P == 0 && (plan.U / plan.P) % plan.upt == 0) return;
-  skinny_reduce_kernel<RMS><<<dim3(static_cast<unsigned>((N + 255) / 256), M), 256, 0, stream>>>(
+  skinny_reduce_kernel<RMS><<<dim3(static_cast<unsigned>(plan.tiles), (M + 15) / 16), 256, 0, stream>>>(
       rec, rec_ss, a.y, M, N, K, plan, a.eps);
   ENG_LAUNCH_CHECK();
 }
