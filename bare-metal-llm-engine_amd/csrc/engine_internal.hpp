@@ -89,7 +89,9 @@ void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
 // per level, and a composite launcher that keeps a lease while it calls other
 // launchers (the FFN's gate / up buffers around the GEMV launches, which may
 // lease split-K partials) takes level 1, so the inner lease (level 0) never
-// waits on its own caller's lock.
+// waits on its own caller's lock. The GEMM's stream-K records take level 2:
+// its callers (rmsnorm_linear's normalised rows at level 0, the FFN's
+// buffers at level 1) hold their leases across it.
 class StreamScratch {
  public:
   StreamScratch(hipStream_t stream, std::size_t bytes, int level = 0);

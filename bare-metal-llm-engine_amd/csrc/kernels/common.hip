@@ -36,7 +36,7 @@ struct Key {
   }
 };
 
-constexpr int kScratchLevels = 2;
+constexpr int kScratchLevels = 3;
 
 struct Arena {
   std::mutex mu;  // held by the live lease

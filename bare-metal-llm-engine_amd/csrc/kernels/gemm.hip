@@ -330,10 +330,16 @@ __device__ __forceinline__ int swz_kn_h(int k) { return ((k >> 4) & 1) * 4; }
 // B) or 16-byte column chunks ([K x N] B) past the matrix read the last valid
 // one instead -- in bounds, and only ever multiplied into accumulators whose
 // C element is outside the matrix -- and those elements are not stored.
-template <int BM, int BN, bool BNK, typename BT = float, bool EDGE = false>
-__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
-    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
-    int K, int tiles_m, int tiles_n) {
+template <int BM, int BN>
+using TileAcc = floatx16[BM / 64][BN / 64];
+
+// The K tiles [kt0, kt1) of the output tile at (m0, n0), accumulated into
+// acc (zeroed here); ends with a barrier, so a following call may refill
+// the LDS stages.
+template <int BM, int BN, bool BNK, typename BT, bool EDGE>
+__device__ __forceinline__ void dma_tile(const float* __restrict__ A, const BT* __restrict__ B,
+                                         int M, int N, int K, int m0, int n0, int kt0, int kt1,
+                                         TileAcc<BM, BN>& acc) {
   constexpr bool HB = std::is_same<BT, _Float16>::value;
   constexpr int BV = 16 / static_cast<int>(sizeof(BT));  // B elements per 16-byte chunk
   constexpr int WM = BM / 2;
@@ -358,11 +364,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
   const int lg = lane >> 5;
   const int wm = wave >> 1;
   const int wn = wave & 1;
-
-  int tm, tn;
-  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * BM;
-  const int n0 = tn * BN;
 
   // Issue the direct loads of K tile kt into one stage. Wave w's j-th
   // instruction fills chunk slots (4 j + w) * 64 + lane.
@@ -409,7 +410,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     }
   };
 
-  floatx16 acc[MB][NB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -480,35 +480,160 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
     }
   };
 
-  const int nk = K / BK;
-  fetch(As0, Bs0, 0);
+  fetch(As0, Bs0, kt0);
   wait_all_memory();
   __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    if (kt + 1 < nk) fetch(As1, Bs1, kt + 1);
+  for (int kt = kt0; kt < kt1; kt += 2) {
+    if (kt + 1 < kt1) fetch(As1, Bs1, kt + 1);
     compute(As0, Bs0);
     wait_all_memory();  // this wave's loads of the next tile have landed
     __syncthreads();
-    if (kt + 1 < nk) {
-      if (kt + 2 < nk) fetch(As0, Bs0, kt + 2);
+    if (kt + 1 < kt1) {
+      if (kt + 2 < kt1) fetch(As0, Bs0, kt + 2);
       compute(As1, Bs1);
       wait_all_memory();
       __syncthreads();
     }
   }
+}
 
+// Stores a tile's accumulators: element (r, c) of the tile to out[r * ld + c]
+// (out at the tile's first element), rows < rows_left and columns < cols_left
+// only (EDGE).
+template <int BM, int BN, bool EDGE>
+__device__ __forceinline__ void store_acc(const TileAcc<BM, BN>& acc, float* __restrict__ out,
+                                          long long ld, int rows_left, int cols_left) {
+  constexpr int WM = BM / 2;
+  constexpr int WN = BN / 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 31;
+  const int lg = lane >> 5;
+  const int wm = wave >> 1;
+  const int wn = wave & 1;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
+  for (int mb = 0; mb < BM / 64; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int col = n0 + wn * WN + nb * 32 + li;
+    for (int nb = 0; nb < BN / 64; ++nb) {
+      const int col = wn * WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = m0 + wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
-        if (!EDGE || (row < M && col < N)) C[static_cast<long long>(row) * N + col] = acc[mb][nb][v];
+        const int row = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        if (!EDGE || (row < rows_left && col < cols_left)) out[row * ld + col] = acc[mb][nb][v];
       }
     }
   }
+}
+
+template <int BM, int BN, bool BNK, typename BT = float, bool EDGE = false>
+__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
+    int K, int tiles_m, int tiles_n) {
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM;
+  const int n0 = tn * BN;
+  TileAcc<BM, BN> acc;
+  dma_tile<BM, BN, BNK, BT, EDGE>(A, B, M, N, K, m0, n0, 0, K / BK, acc);
+  store_acc<BM, BN, EDGE>(acc, C + static_cast<long long>(m0) * N + n0, N, M - m0, N - n0);
+}
+
+// Stream-K tail (full tiles only): T tiles, of which the first `dp` in
+// tile_of order are computed whole by workgroups 0 .. dp - 1 (one round of
+// one per CU), and the remaining T - dp tiles' k-iterations are split evenly
+// over the workgroups dp .. dp + nsk - 1 (nsk = min(dp, I): none is empty):
+// workgroup dp + s takes iterations [s I / nsk, (s + 1) I / nsk) of the
+// tail's I = (T - dp) nk, tile by tile.
+// Running beside the data-parallel round (two workgroups per CU), every CU
+// then does the same work whatever T is (512 x 11008 x 4096: 344 tiles on
+// 256 CUs). A tail tile one workgroup covers whole is stored to C; a split
+// tile leaves one record per workgroup (slot 0 its first tile, slot 1 its
+// last), which gemm_sk_fixup_kernel adds in workgroup order.
+struct SkPlan {
+  int dp = 0;        // data-parallel tiles (one per CU)
+  int nsk = 0;       // stream-K workgroups
+  int nk = 0;        // K tiles per output tile
+  long long I = 0;   // tail iterations (tail tiles x nk)
+};
+
+__host__ __device__ inline long long sk_begin(long long s, const SkPlan& p) {
+  return s * p.I / p.nsk;
+}
+
+// Stream-K workgroup whose range holds tail iteration it.
+__device__ inline long long sk_worker(long long it, const SkPlan& p) {
+  long long s = (it * p.nsk + p.nsk - 1) / p.I;
+  if (s >= p.nsk) s = p.nsk - 1;
+  while (s + 1 < p.nsk && sk_begin(s + 1, p) <= it) ++s;
+  while (s > 0 && sk_begin(s, p) > it) --s;
+  return s;
+}
+
+template <int BM, int BN, bool BNK, typename BT>
+__global__ __launch_bounds__(kThreads, 2) void gemm_sk_kernel(
+    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C,
+    float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n, SkPlan plan) {
+  TileAcc<BM, BN> acc;
+  const int g = blockIdx.x;
+  if (g < plan.dp) {
+    int tm, tn;
+    tile_of(g, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    dma_tile<BM, BN, BNK, BT, false>(A, B, M, N, K, m0, n0, 0, plan.nk, acc);
+    store_acc<BM, BN, false>(acc, C + static_cast<long long>(m0) * N + n0, N, BM, BN);
+    return;
+  }
+  const long long s = g - plan.dp;
+  const long long i0 = sk_begin(s, plan);
+  const long long i1 = sk_begin(s + 1, plan);
+  for (long long it = i0; it < i1;) {
+    const long long t = it / plan.nk;  // tail tile
+    const int ka = static_cast<int>(it - t * plan.nk);
+    const long long tend = (t + 1) * plan.nk;
+    const int kb = static_cast<int>((i1 < tend ? i1 : tend) - t * plan.nk);
+    int tm, tn;
+    tile_of(plan.dp + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    dma_tile<BM, BN, BNK, BT, false>(A, B, M, N, K, m0, n0, ka, kb, acc);
+    if (ka == 0 && kb == plan.nk) {
+      store_acc<BM, BN, false>(acc, C + static_cast<long long>(m0) * N + n0, N, BM, BN);
+    } else {
+      const int slot = it == i0 ? 0 : 1;
+      store_acc<BM, BN, false>(acc, rec + (s * 2 + slot) * static_cast<long long>(BM * BN), BN,
+                               BM, BN);
+    }
+    it = t * plan.nk + kb;
+  }
+}
+
+// Split tail tiles: C = the tile's records added in workgroup order. One
+// block per (tail tile, 1024 elements); tiles one workgroup covered whole are
+// skipped (already stored).
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_sk_fixup_kernel(const float* __restrict__ rec,
+                                                            float* __restrict__ C, int N,
+                                                            int tiles_m, int tiles_n,
+                                                            SkPlan plan) {
+  const long long t = blockIdx.x;
+  const long long sf = sk_worker(t * plan.nk, plan);
+  const long long sl = sk_worker(t * plan.nk + plan.nk - 1, plan);
+  if (sf == sl) return;
+  // workgroups after sf start inside the tile (slot 0); sf only when it
+  // starts exactly at the tile
+  const int slot_f = sk_begin(sf, plan) == t * plan.nk ? 0 : 1;
+  const int e = 4 * (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x));
+  floatx4 v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (long long s = sf; s <= sl; ++s) {
+    const long long r = s * 2 + (s == sf ? slot_f : 0);
+    v += *reinterpret_cast<const floatx4*>(rec + r * static_cast<long long>(BM * BN) + e);
+  }
+  int tm, tn;
+  tile_of(plan.dp + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
+  const int row = e / BN;
+  const int col = e % BN;
+  *reinterpret_cast<floatx4*>(C + static_cast<long long>(tm * BM + row) * N + tn * BN + col) = v;
 }
 
 // The direct-load kernel can be switched off (ENGINE_GEMM_NO_DMA=1) to
@@ -596,8 +721,51 @@ Tile choose_tile(long long M, long long N) {
   return Tile::T64x64;
 }
 
+// Stream-K tail for 128 x 128 tiles when their count T falls between one
+// and two rounds of one tile per CU (CUs < T < 2 CUs; every other shape
+// keeps choose_tile's tiling): full tiles and the direct-load conditions
+// only. ENGINE_GEMM_NO_SK=1 switches it off.
+bool sk_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_NO_SK");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
+template <typename BT, bool BNK>
+bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
+  constexpr int BM = 128, BN = 128;
+  constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
+  if (!sk_enabled() || !dma_enabled()) return false;
+  if (a.M % BM != 0 || a.N % BN != 0 || a.K % BK != 0 || a.K / BK < 8) return false;
+  if (!aligned_to(a.A, 16) || !aligned_to(a.B, 16) || (!BNK && a.N % kBVec != 0)) return false;
+  const long long cus = device_cu_count();
+  const int tiles_m = static_cast<int>(a.M / BM);
+  const int tiles_n = static_cast<int>(a.N / BN);
+  const long long T = static_cast<long long>(tiles_m) * tiles_n;
+  if (T <= cus || T >= 2 * cus) return false;
+  SkPlan plan;
+  plan.dp = static_cast<int>(cus);
+  plan.nk = static_cast<int>(a.K / BK);
+  plan.I = (T - cus) * plan.nk;
+  plan.nsk = static_cast<int>(std::min<long long>(plan.dp, plan.I));
+  StreamScratch records(stream, static_cast<std::size_t>(plan.nsk) * 2 * BM * BN * sizeof(float), 2);
+  float* rec = static_cast<float*>(records.get());
+  const BT* B = static_cast<const BT*>(a.B);
+  const int M = static_cast<int>(a.M), N = static_cast<int>(a.N), K = static_cast<int>(a.K);
+  gemm_sk_kernel<BM, BN, BNK, BT><<<static_cast<unsigned>(plan.dp + plan.nsk), kThreads, 0, stream>>>(
+      a.A, B, a.C, rec, M, N, K, tiles_m, tiles_n, plan);
+  ENG_LAUNCH_CHECK();
+  gemm_sk_fixup_kernel<BM, BN><<<dim3(static_cast<unsigned>(T - cus), BM * BN / 1024), 256, 0,
+                                 stream>>>(rec, a.C, N, tiles_m, tiles_n, plan);
+  ENG_LAUNCH_CHECK();
+  return true;
+}
+
 template <typename BT, bool BNK>
 void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
+  if (run_gemm_sk<BT, BNK>(a, stream)) return;
   switch (choose_tile(a.M, a.N)) {
     case Tile::T128x128:
       run_gemm<128, 128, BT, BNK>(a, stream);

@@ -187,6 +187,29 @@ def test_config4_matmul_sampled_rows(gpu, orc, M, N, K):
     helpers.assert_within(colsum, ref, bound, f"config 4 {M}x{N}x{K} column sums")
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 16640, 512), (384, 19200, 256), (1024, 4224, 1024)])
+def test_matmul_stream_k_tail(gpu, orc, M, N, K):
+    # 128 x 128 tile counts between one and two rounds of one tile per CU
+    # (260, 450 and 264 tiles on 256 CUs): a data-parallel round plus the
+    # remaining tiles' k-iterations split over as many workgroups, partial
+    # tiles added by the fix-up kernel in workgroup order. Sampled rows of
+    # every row tile against the oracle, column sums over the whole matrix,
+    # and bit-equal results on a second call.
+    rng = np.random.default_rng(M + N + K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    rows = np.unique(np.concatenate([np.arange(0, M, 64), np.arange(63, M, 64), rng.integers(0, M, 4)]))
+    y = orc.matmul(A[rows], B).astype(np.float64)
+    check_dot(got[rows], y, helpers.absdot(A[rows], B) + np.abs(y), K, f"stream-K {M}x{N}x{K}")
+    colsum = got.astype(np.float64).sum(axis=0)
+    ref = A.astype(np.float64).sum(axis=0) @ B.astype(np.float64)
+    bound = (K + M) * helpers.U32 * (np.abs(A).astype(np.float64).sum(axis=0) @ np.abs(B).astype(np.float64))
+    helpers.assert_within(colsum, ref, bound, f"stream-K {M}x{N}x{K} column sums")
+    again = gpu_matmul(gpu, A, B)
+    assert np.array_equal(again, got), "stream-K result not deterministic"
+
+
 # -------------------------------------------------------- odd / fallback paths
 @pytest.mark.parametrize("M,N,K", [(3, 7, 11), (65, 137, 73), (129, 257, 65), (1, 65, 127),
                                    (71, 97, 113), (2, 5, 1), (300, 8, 4), (130, 130, 33)])
