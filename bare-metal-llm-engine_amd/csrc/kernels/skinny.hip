@@ -151,7 +151,7 @@ Plan make_plan(long long N, long long K, long long cus) {
 // shares with others -- slot 0 its first tile, slot 1 its last --, rec_ss
 // [P][2][M] their sums of squares.
 template <typename WT, bool NK, int MB, bool RMS>
-__global__ __launch_bounds__(kWaves * 64, 2) void skinny_mfma_kernel(
+__global__ __launch_bounds__(kWaves * 64, MB >= 3 ? 1 : 2) void skinny_mfma_kernel(
     const WT* __restrict__ W, const float* __restrict__ x, const float* __restrict__ gamma,
     float* __restrict__ y, int M, long long N, long long K, Plan plan,
     float* __restrict__ rec, float* __restrict__ rec_ss, float eps) {
