@@ -195,16 +195,17 @@ bool gemv_dma_enabled() {
   return on;
 }
 
-template <int NP, int KT, int CH>
+template <int NP, int KT, int CH, int WAVES>
 void launch_rows_dma(const GemvArgs& a, hipStream_t stream) {
   ENG_CHECK(a.K == (NP - 1) * 512LL + KT, "gemv: fixed-K kernel for another K");
-  const long long wgs = (a.N + 15) / 16;
+  const long long wgs = (a.N + WAVES - 1) / WAVES;
   ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
   const std::size_t lds = static_cast<std::size_t>(NP) * 512 * 4;
   static std::atomic<bool> allowed[64] = {};
-  allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_dma_kernel<NP, KT, CH>),
+  allow_staged_lds(reinterpret_cast<const void*>(&gemv::gemv_rows_dma_kernel<NP, KT, CH, WAVES>),
                    allowed, lds);
-  gemv::gemv_rows_dma_kernel<NP, KT, CH><<<static_cast<unsigned>(wgs), 1024, lds, stream>>>(
+  gemv::gemv_rows_dma_kernel<NP, KT, CH, WAVES>
+      <<<static_cast<unsigned>(wgs), 64 * WAVES, lds, stream>>>(
       static_cast<const _Float16*>(a.W), static_cast<const float*>(a.x),
       static_cast<float*>(a.y), a.N);
   ENG_LAUNCH_CHECK();
@@ -244,13 +245,22 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     // kernel, whose per-row re-read of x through the vector L1 costs 0.8 us.
     // Without RMSNorm, 16-wave workgroups stage x by direct-to-LDS loads that
     // overlap the first weight loads: 6.72 us against 6.92 at 4096 x 4096.
+    // Rows longer than 4096 with at most one 16-wave workgroup per CU take
+    // 8-wave workgroups (two per CU, the same waves): the down projection
+    // 4096 x 11008 15.4 us against 16.0 (4096 x 4096 the same either way;
+    // with RMSNorm, and for the fused gate / up, 8-wave workgroups measured
+    // 6% slower).
     if (fits && (RMS || a.N >= one_round / 2 || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       const bool wide = RMS || a.N >= one_round || a.K > 4096;
       const bool fixed = with_fixed_k_f16(a.K, [&](auto fk) {
         using F = decltype(fk);
         if (!RMS && wide && gemv_dma_enabled()) {
-          launch_rows_dma<F::NP, F::KT, F::CH1>(a, stream);
+          if (a.K > 4096 && a.N <= one_round) {
+            launch_rows_dma<F::NP, F::KT, F::CH1, 8>(a, stream);
+          } else {
+            launch_rows_dma<F::NP, F::KT, F::CH1, 16>(a, stream);
+          }
         } else if (wide) {
           launch_rows_lds<WT, 1, 4, RMS, 16, F::NP, F::KT, F::CH1>(a, lds, stream);
         } else {

@@ -704,17 +704,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __r
 // barrier after the staging, which costs more than the early start gains:
 // measured 2% slower at 11008 x 4096, so RMSNorm keeps the staging kernel.)
 // Dynamic LDS: NP * 512 floats.
-template <int NP, int KT, int CH>
-__global__ __launch_bounds__(1024) void gemv_rows_dma_kernel(const _Float16* __restrict__ W,
+template <int NP, int KT, int CH, int WAVES = 16>
+__global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float16* __restrict__ W,
                                                              const float* __restrict__ x,
                                                              float* __restrict__ y, long long N) {
   using V = typename RawVec<_Float16, 8>::type;
   using F4 = typename RawVec<float, 4>::type;
   constexpr int PIECE = 512;
-  constexpr int WAVES = 16;
   constexpr int K = (NP - 1) * PIECE + KT;
   constexpr int CHUNKS = NP * PIECE / 4;           // 16-byte chunks of the staged vector
-  constexpr int INSTR = (CHUNKS + 1023) / 1024;    // staging loads per thread
+  constexpr int NT = 64 * WAVES;
+  constexpr int INSTR = (CHUNKS + NT - 1) / NT;    // staging loads per thread
   constexpr int G = (NP + CH - 1) / CH;
   constexpr int LAST = NP - (G - 1) * CH;
   static_assert(KT > 0 && KT <= PIECE && KT % 8 == 0, "K = (NP - 1) * 512 + KT");
@@ -724,7 +724,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_dma_kernel(const _Float16* __r
   const int wave = tid >> 6;
   const long long n0 = static_cast<long long>(blockIdx.x) * WAVES + wave;
 
-  // Staging: wave w's i-th load fills chunks (16 i + w) * 64 .. + 63 of the
+  // Staging: wave w's i-th load fills chunks (WAVES i + w) * 64 .. + 63 of the
   // LDS vector; chunk q holds elements chunk_k0(q) .. + 3 of x. Chunks past K
   // (the last piece when KT < 512) are zeroed first, with LDS stores (a store
   // after a direct load the compiler cannot prove disjoint would make it
@@ -737,13 +737,13 @@ __global__ __launch_bounds__(1024) void gemv_rows_dma_kernel(const _Float16* __r
   if constexpr (KT < PIECE) {
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
-      const int q = (16 * i + wave) * 64 + lane;
+      const int q = (WAVES * i + wave) * 64 + lane;
       if (q < CHUNKS && chunk_k0(q) >= K) *reinterpret_cast<F4*>(xs + 4 * q) = F4{};
     }
   }
 #pragma unroll
   for (int i = 0; i < INSTR; ++i) {
-    const int q0 = (16 * i + wave) * 64;
+    const int q0 = (WAVES * i + wave) * 64;
     if (q0 < CHUNKS) {  // wave-uniform
       const int q = q0 + lane;
       if (q < CHUNKS && chunk_k0(q) < K) dma16(x + chunk_k0(q), xs + 4 * q0);
