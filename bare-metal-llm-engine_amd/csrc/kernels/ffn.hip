@@ -106,6 +106,18 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
       // fixed-K form for common widths (unmasked loads, 2 x CH2 in flight)
       const bool fixed = with_fixed_k_f16(K, [&](auto fk) {
         using F = decltype(fk);
+        if (gemv_rms_early_enabled()) {
+          // weight stream started before x * gamma is staged, the same bits;
+          // 4 pieces per row in flight (11008 x 4096: 28.0 us against 29.1
+          // staged first; rings of 2, 3, 5, 6 pieces 30.0, 28.2, 29.2, 30.7)
+          auto kern = gemv::gemv_rows_rms_early_kernel<F::NP, F::KT, (F::NP < 4 ? F::NP : 4), true>;
+          static std::atomic<bool> allowed_early[64] = {};
+          const std::size_t lds_early = static_cast<std::size_t>(gemv::rms_early_lds_floats(F::NP)) * 4;
+          allow_staged_lds(reinterpret_cast<const void*>(kern), allowed_early, lds_early);
+          kern<<<static_cast<unsigned>(wgs), WAVES * 64, lds_early, s>>>(Wg, Wu, in, gamma, act, N, eps);
+          ENG_LAUNCH_CHECK();
+          return;
+        }
         auto kern = gemv::gemv_rows_glu_kernel<WT, VEC, 1, 4, true, WAVES, F::NP, F::KT, F::CH2>;
         static std::atomic<bool> allowed_fixed[64] = {};
         allow_staged_lds(reinterpret_cast<const void*>(kern), allowed_fixed, lds);

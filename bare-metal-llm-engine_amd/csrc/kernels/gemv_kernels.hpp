@@ -808,6 +808,148 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float1
   if (lane == 0 && active) y[n0] = acc;
 }
 
+// Fixed-K fp16 RMSNorm GEMV (GLU = false: y[n] = s W[n] . xs) or fused gate /
+// up + SwiGLU (GLU = true: y[n] = SiLU(s Wg[n] . xs) * (s Wu[n] . xs)),
+// xs = x * gamma, K = (NP - 1) * 512 + KT, 16-wave workgroups, one output per
+// wave: the bits of gemv_rows_lds_kernel<_Float16, 8, 1, 4, true, 16, NP, KT,
+// CH> (GLU: gemv_rows_glu_kernel<...>), with the weight stream started before
+// the staging completes and kept at CH pieces per row in flight (a ring: the
+// registers of a used piece take the piece CH further on; GLU streams two
+// rows, so CH = 4 keeps its 16 waves at 64 VGPRs, two workgroups per CU).
+// Each thread loads its x and gamma chunks (the chunks
+// stage_xs gives virtual thread tid, so the sum of squares has stage_xs's
+// order), then its wave's first CH weight pieces per row, and only then
+// waits for its x and gamma, writes x * gamma to LDS and its wave's sum of
+// squares, and meets the other waves at one barrier without a fence (a
+// fence would wait for the weights). Loads complete in issue order, so the
+// wait for x and gamma leaves the weight loads in flight. All loads use
+// in-bounds offsets (chunks past K read chunk 0, weight lanes past K the
+// piece's first 16 bytes) and are zeroed where used: no branch or select
+// between a load and the wait; every thread stores its chunk, so the LDS
+// vector is rounded up to whole rounds of 1024 chunks (the slots past NP
+// pieces are written and never read).
+// Dynamic LDS: rms_early_lds_floats(NP) floats.
+constexpr int rms_early_lds_floats(int np) { return (np * 512 + 4095) / 4096 * 4096; }
+
+template <int NP, int KT, int CH, bool GLU>
+__global__ __launch_bounds__(1024) void gemv_rows_rms_early_kernel(
+    const _Float16* __restrict__ W0, const _Float16* __restrict__ W1,
+    const float* __restrict__ x, const float* __restrict__ gamma, float* __restrict__ y,
+    long long N, float eps) {
+  using V = typename RawVec<_Float16, 8>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 512;
+  constexpr int K = (NP - 1) * PIECE + KT;
+  constexpr int VT = kStageWaves * 64;            // stage_xs's virtual threads: one per thread
+  constexpr int ITER = rms_early_lds_floats(NP) / (VT * 4);
+  constexpr int NR = GLU ? 2 : 1;
+  static_assert(KT > 0 && KT <= PIECE && KT % 8 == 0, "K = (NP - 1) * 512 + KT");
+  static_assert(CH >= 1 && CH <= NP, "ring of 1 to NP pieces");
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[kStageWaves];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const long long n0 = static_cast<long long>(blockIdx.x) * kStageWaves + wave;
+
+  // Staging loads: x and gamma chunk i * VT + tid (gamma == nullptr: x again,
+  // read as 1 below).
+  const float* gp = gamma != nullptr ? gamma : x;
+  F4 xv[ITER], gv[ITER];
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int k = (i * VT + tid) * 4;
+    const int kc = k < K ? k : 0;
+    xv[i] = *reinterpret_cast<const F4*>(x + kc);
+    gv[i] = *reinterpret_cast<const F4*>(gp + kc);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const bool active = n0 < N;
+  const long long nr = active ? n0 : N - 1;
+  const _Float16* rows[NR];
+  rows[0] = W0 + nr * K;
+  if constexpr (GLU) rows[1] = W1 + nr * K;
+  const int lk = lane * 8;
+  auto ok = [&](int p) { return p < NP - 1 || KT == PIECE || lk < KT; };
+  auto load = [&](int j, int p) -> V {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const V*>(rows[j] + p * PIECE + (ok(p) ? lk : 0)));
+  };
+  float acc[NR];
+#pragma unroll
+  for (int j = 0; j < NR; ++j) acc[j] = 0.0f;
+  auto use = [&](int p, const V (&w)[NR]) {
+    const float* base = xs + p * PIECE + lane * 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const F4 a = *reinterpret_cast<const F4*>(base + h * 256);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+#pragma unroll
+        for (int j = 0; j < NR; ++j) acc[j] = fmaf(a[e], static_cast<float>(w[j][h * 4 + e]), acc[j]);
+      }
+    }
+  };
+
+  // Ring of the next CH pieces (per row): pieces 0 .. CH - 1 now, piece
+  // p + CH loaded once piece p is used.
+  V ring[CH][NR];
+#pragma unroll
+  for (int u = 0; u < CH; ++u) {
+#pragma unroll
+    for (int j = 0; j < NR; ++j) ring[u][j] = load(j, u);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // x * gamma into LDS (zero past K), the sum of squares in stage_xs's order.
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < ITER; ++i) {
+    const int k = (i * VT + tid) * 4;
+    F4 v = k < K ? xv[i] : F4{};
+    ss = fmaf(v[0], v[0], ss);
+    ss = fmaf(v[1], v[1], ss);
+    ss = fmaf(v[2], v[2], ss);
+    ss = fmaf(v[3], v[3], ss);
+    if (gamma != nullptr) v *= gv[i];
+    *reinterpret_cast<F4*>(xs + lds_slot<8>(k)) = v;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) wave_ss[wave] = ss;
+  lds_barrier();
+  float total = wave_ss[0];
+#pragma unroll
+  for (int w = 1; w < kStageWaves; ++w) total += wave_ss[w];
+  const float scale = rms_scale(total, K, eps);
+
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    V w[NR];
+#pragma unroll
+    for (int j = 0; j < NR; ++j) w[j] = ok(p) ? ring[p % CH][j] : V{};
+    use(p, w);
+    if (p + CH < NP) {
+#pragma unroll
+      for (int j = 0; j < NR; ++j) ring[p % CH][j] = load(j, p + CH);
+    }
+    // each load issued right after the use that frees its registers, and no
+    // later LDS reads hoisted above it (the compiler fence keeps memory
+    // operations in place, the scheduling barrier everything else)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+#pragma unroll
+  for (int j = 0; j < NR; ++j) acc[j] = wave_sum(acc[j]);
+  if (lane == 0 && active) {
+    if constexpr (GLU) {
+      y[n0] = swiglu_f32(acc[0] * scale, acc[1] * scale);
+    } else {
+      y[n0] = acc[0] * scale;
+    }
+  }
+}
+
 // acc[m][j] = sum_k rows[j][k] * xs_m[k] for MX staged activation rows (row m
 // at xs + m * pitch), folded across the wave: the weight pieces are loaded and
 // converted once and used for every activation row. Each (m, j) sum runs over
