@@ -155,6 +155,49 @@ def test_attention_decode_concurrent_streams_reuse_scratch(gpu, orc):
     check_decode(db.download(), q, k, v, H, Hkv, D, 257, L * D, sc, orc, "stream B (kv_len 257)")
 
 
+def test_attention_decode_repeated_calls_and_streams(gpu, orc):
+    """Back-to-back GQA calls (D = 64, the MFMA kernel) with new data on one
+    stream, reusing the stream's partial-state scratch at several split
+    counts; the same data twice (fixed merge order: equal bits); and two
+    streams interleaving calls of different lengths and split counts."""
+    H, Hkv, D = 32, 4, 64
+    sc = 1.0 / np.sqrt(D)
+    rng = np.random.default_rng(77)
+    first = None
+    for rep, (L, split) in enumerate([(2048, 0), (2048, 0), (1500, 16), (777, 5), (2048, 0)]):
+        q = rand_half(orc, rng, (H, D))
+        k = rand_half(orc, rng, (Hkv, L, D))
+        v = rand_half(orc, rng, (Hkv, L, D))
+        got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split)
+        check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"call {rep} L={L} split={split}")
+        if rep == 0:
+            first = (q, k, v, got)
+    q, k, v, got0 = first
+    again = gpu_decode(gpu, q, k, v, 2048, H, Hkv, D, 2048 * D, sc, 0)
+    assert np.array_equal(again, got0), "same inputs, different bits"
+
+    La, Lb = 2048, 1200
+    qa, ka, va = (rand_half(orc, rng, sh) for sh in ((H, D), (Hkv, La, D), (Hkv, La, D)))
+    qb, kb, vb = (rand_half(orc, rng, sh) for sh in ((H, D), (Hkv, Lb, D), (Hkv, Lb, D)))
+    dqa, dka, dva = gpu.upload(qa), gpu.upload(ka), gpu.upload(va)
+    dqb, dkb, dvb = gpu.upload(qb), gpu.upload(kb), gpu.upload(vb)
+    da, db = gpu.empty((H, D), np.uint16), gpu.empty((H, D), np.uint16)
+    sa, sb = gpu.stream(), gpu.stream()
+    try:
+        for _ in range(4):
+            gpu.call("eng_attention_decode_f16", dqa.ptr, dka.ptr, dva.ptr, da.ptr, La, H, Hkv, D,
+                     La * D, sc, 0, sa.handle)
+            gpu.call("eng_attention_decode_f16", dqb.ptr, dkb.ptr, dvb.ptr, db.ptr, Lb, H, Hkv, D,
+                     Lb * D, sc, 24, sb.handle)
+        sa.sync()
+        sb.sync()
+    finally:
+        sa.destroy()
+        sb.destroy()
+    check_decode(da.download(), qa, ka, va, H, Hkv, D, La, La * D, sc, orc, "stream A")
+    check_decode(db.download(), qb, kb, vb, H, Hkv, D, Lb, Lb * D, sc, orc, "stream B")
+
+
 # --------------------------------------------------------- model shapes
 @pytest.mark.parametrize("H,Hkv,D,L,split", [
     (32, 32, 128, 2048, 0),   # Llama-2-7B, MHA
