@@ -718,6 +718,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float1
   constexpr int G = (NP + CH - 1) / CH;
   constexpr int LAST = NP - (G - 1) * CH;
   static_assert(KT > 0 && KT <= PIECE && KT % 8 == 0, "K = (NP - 1) * 512 + KT");
+  static_assert(CH >= 1 && CH <= NP, "groups of 1 to NP pieces");
   extern __shared__ float xs[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -795,14 +796,25 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float1
     for (int u = 0; u < FIRST; ++u) use(u, ok(u) ? cur[u] : V{});
     __builtin_amdgcn_sched_barrier(0);
   }
+  // Whole groups of CH pieces, then (when CH does not divide NP) the last
+  // LAST pieces: no load past piece NP - 1.
+  constexpr int FULL = LAST == CH ? G : G - 1;
 #pragma unroll 1
-  for (int c = 1; c < G; ++c) {
+  for (int c = 1; c < FULL; ++c) {
     V cur[CH];
 #pragma unroll
     for (int u = 0; u < CH; ++u) cur[u] = load(c * CH + u);
 #pragma unroll
     for (int u = 0; u < CH; ++u) use(c * CH + u, ok(c * CH + u) ? cur[u] : V{});
     __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (FULL < G && G > 1) {
+    constexpr int P0 = (G - 1) * CH;
+    V cur[LAST];
+#pragma unroll
+    for (int u = 0; u < LAST; ++u) cur[u] = load(P0 + u);
+#pragma unroll
+    for (int u = 0; u < LAST; ++u) use(P0 + u, ok(P0 + u) ? cur[u] : V{});
   }
   acc = wave_sum(acc);
   if (lane == 0 && active) y[n0] = acc;
