@@ -23,8 +23,11 @@
 // output's arithmetic involves only its own row of X, so a row's result is
 // the same bits whichever M (5..64) it is computed in.
 //
-// skinny_nk_kernel (output-major W) and skinny_mfma_kernel (reference
-// layout) differ in how a workgroup covers a unit; see each kernel.
+// skinny_nk_kernel covers a unit the same way for output-major W and, with
+// KN, for reference-layout fp16 W (through LDS, transposed);
+// skinny_mfma_kernel takes reference-layout fp32 W. At 11008 x 4096 fp16 W
+// [K x N] the KN form takes 30.2 us at M = 16 and 64.9 us at M = 64, against
+// 31.1 and 88.5 us for skinny_mfma_kernel (fp32 MFMA on converted weights).
 #include "device_sync.hpp"
 #include "launch.hpp"
 
@@ -480,13 +483,14 @@ struct WVec<float> {
 // c ^ (m & 7); fp16 planes with 8-value chunks, row m at m * 16, chunk c at
 // c ^ (m & 7) (the 16 rows one MFMA operand read touches land in different
 // banks).
-template <typename WT, int MB, bool RMS>
+template <typename WT, int MB, bool RMS, bool KN = false>
 __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     const WT* __restrict__ W, const float* __restrict__ x, const float* __restrict__ gamma,
     float* __restrict__ y, int M, long long N, long long K, Plan plan,
     float* __restrict__ rec, float* __restrict__ rec_ss, float eps) {
   using WV = typename WVec<WT>::type;
   constexpr bool H = std::is_same<WT, _Float16>::value;    // fp16 MFMA path
+  static_assert(!KN || H, "the reference-layout form is fp16 only");
   constexpr int E = 16 / static_cast<int>(sizeof(WT));     // elements per 16-byte load
   constexpr int LPU = static_cast<int>(kUnitK) / (4 * E);  // loads per unit per lane
   constexpr int ROWS = 16 * MB;
@@ -503,8 +507,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     halfx8 lo[H ? ROWS * HCR : 1];
     float ds[H ? ROWS : 1];
   };
-  __shared__ XBuf xbuf[2];
+  // KN: one X buffer past 32 rows (LDS for two workgroups per CU), read and
+  // rewritten between two barriers per unit.
+  constexpr int XB = (KN && MB > 2) ? 1 : 2;
+  __shared__ XBuf xbuf[XB];
   __shared__ float ssc[RMS ? ROWS : 1];
+  // KN: two stages of a unit's weights, 128 rows (k) x 8 chunks of 16 bytes
+  // (64 columns); chunk c of row r at position c ^ ((r / 8) & 7).
+  __shared__ halfx8 wst[KN ? 2 * 128 * 8 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -686,6 +696,63 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     }
   };
 
+  // KN (reference layout W [K x N], fp16): a unit's 128 x 64 block of W is
+  // loaded straight into an LDS stage -- thread slot g = (4 q + wave) * 64 +
+  // lane takes 16 bytes of row g / 8 (one wave load: 8 rows x 128 bytes) --
+  // and each wave reads its A operands from there transposed: lane (j, s)
+  // of load i gathers column 16 wave + j at k = 32 i + 8 s + t, t = 0..7
+  // (the same fragment skinny_nk_kernel loads from an output-major row; the
+  // position swizzle puts the four lane groups' rows in different banks).
+  // Rows past K read row 0 of the unit and columns past N chunk 0 of the
+  // tile; both are zeroed or dropped at use.
+  auto dma_w = [&](const Cursor& c, int st) __attribute__((always_inline)) {
+    const long long kbase = c.ku * kUnitK;
+    const long long n0 = c.tile * kCols;
+    const WT* base = W + kbase * N + n0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = (4 * q + wave) * 64 + lane;
+      const int r = g >> 3;
+      const int cch = (g & 7) ^ ((r >> 3) & 7);
+      const long long off = (kbase + r < K ? static_cast<long long>(r) * N : 0) +
+                            (n0 + 8 * cch < N ? 8 * cch : 0);
+      dma16(base + off, reinterpret_cast<WT*>(&wst[st * 1024 + (4 * q + wave) * 64]));
+    }
+  };
+  auto compute_kn = [&](const XBuf& xb, int st, const Cursor& cur) __attribute__((always_inline)) {
+    const _Float16* ws = reinterpret_cast<const _Float16*>(&wst[st * 1024]);
+#pragma unroll
+    for (int i = 0; i < LPU; ++i) {
+      const bool kok = cur.ku * kUnitK + 4 * E * i + E * s < K;
+      const int r0 = 32 * i + 8 * s;
+      const int pch = (2 * wave + (j >> 3)) ^ ((4 * i + s) & 7);
+      const _Float16* src = ws + (r0 * 8 + pch) * 8 + (j & 7);
+      halfx8 wv;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wv[t] = src[t * 64];
+      const halfx8 wi = kok ? wv : halfx8{};
+      halfx8 bh[MB], bl[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 7));
+        bh[mb] = xb.hi[pos];
+        bl[mb] = xb.lo[pos];
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        ach[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bh[mb], ach[mb], 0, 0, 0);
+        acl[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bl[mb], acl[mb], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const float d = xb.ds[16 * mb + j];
+      const floatx4 p = ach[mb] + acl[mb] * (1.0f / 2048.0f);
+      acc[mb] += p * d;
+      ach[mb] = acl[mb] = zero4();
+    }
+  };
+
   // Tile end: whole tiles go to y (scaled by their rows' RMS factors), split
   // tiles to this workgroup's record slot.
   auto finish = [&](const Cursor& c) __attribute__((always_inline)) {
@@ -742,28 +809,61 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     if (++xku == upt) xku = 0;
   };
   x_next();
-  WV w[LPU];
-  load_w(w, cl);
-  advance(cl);
-  store_x(S, xbuf[0]);
-  lds_barrier();
-
-  // One unit per iteration with X' in buffer b: loads X of the next unit
-  // first, then computes (reloading w for the next unit load by load),
-  // writes the next unit's X' to the other buffer. A single loop body (no
-  // unrolling) keeps the weight registers in place across iterations: two
-  // copies of the body assigned them differently, and the copies between
-  // them waited for every load in flight.
-  for (int b = 0;; b ^= 1) {
-    x_next();
-    __builtin_amdgcn_sched_barrier(0);
-    compute(w, xbuf[b], cc, cl);
+  if constexpr (KN) {
+    // Unit per iteration from stage b: X of the next unit and its weights
+    // (into the other stage) issued first, the unit computed, the next X'
+    // written, then every load waited for and one barrier (two with one X
+    // buffer: the rewrite waits until every wave has read it).
+    dma_w(cl, 0);
     advance(cl);
-    if (cc.ku == upt - 1 || cc.u == u1 - 1) finish(cc);
-    if (cc.u + 1 < u1) store_x(S, xbuf[b ^ 1]);
+    store_x(S, xbuf[0]);
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+#endif
     lds_barrier();
-    advance(cc);
-    if (cc.u >= u1) break;
+    for (int b = 0;; b ^= 1) {
+      x_next();
+      __builtin_amdgcn_sched_barrier(0);
+      if (cl.u < u1) dma_w(cl, b ^ 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_kn(xbuf[XB == 2 ? b : 0], b, cc);
+      advance(cl);
+      if (cc.ku == upt - 1 || cc.u == u1 - 1) finish(cc);
+      if (cc.u + 1 < u1) {
+        if constexpr (XB == 1) lds_barrier();
+        store_x(S, xbuf[XB == 2 ? (b ^ 1) : 0]);
+      }
+#if defined(__HIP_DEVICE_COMPILE__)
+      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
+#endif
+      lds_barrier();
+      advance(cc);
+      if (cc.u >= u1) break;
+    }
+  } else {
+    WV w[LPU];
+    load_w(w, cl);
+    advance(cl);
+    store_x(S, xbuf[0]);
+    lds_barrier();
+
+    // One unit per iteration with X' in buffer b: loads X of the next unit
+    // first, then computes (reloading w for the next unit load by load),
+    // writes the next unit's X' to the other buffer. A single loop body (no
+    // unrolling) keeps the weight registers in place across iterations: two
+    // copies of the body assigned them differently, and the copies between
+    // them waited for every load in flight.
+    for (int b = 0;; b ^= 1) {
+      x_next();
+      __builtin_amdgcn_sched_barrier(0);
+      compute(w, xbuf[b], cc, cl);
+      advance(cl);
+      if (cc.ku == upt - 1 || cc.u == u1 - 1) finish(cc);
+      if (cc.u + 1 < u1) store_x(S, xbuf[b ^ 1]);
+      lds_barrier();
+      advance(cc);
+      if (cc.u >= u1) break;
+    }
   }
 }
 
@@ -848,6 +948,9 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
   const WT* W = static_cast<const WT*>(a.W);
   if constexpr (NK) {
     skinny_nk_kernel<WT, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(
+        W, a.x, RMS ? a.gamma : nullptr, a.y, M, N, K, plan, rec, rec_ss, a.eps);
+  } else if constexpr (std::is_same<WT, _Float16>::value) {
+    skinny_nk_kernel<WT, MB, RMS, true><<<grid, kWaves * 64, 0, stream>>>(
         W, a.x, RMS ? a.gamma : nullptr, a.y, M, N, K, plan, rec, rec_ss, a.eps);
   } else {
     skinny_mfma_kernel<WT, NK, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(
