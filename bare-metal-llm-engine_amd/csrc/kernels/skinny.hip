@@ -51,6 +51,24 @@ constexpr int kCols = 16 * kNB;
 constexpr long long kUnitK = static_cast<long long>(kGroup) * kWaves;  // k per unit
 constexpr int kRS = kCols + 4;  // LDS row stride of the wave-sum tiles (floats)
 
+// Maximum over each group of 32 consecutive lanes, in all of them: DPP
+// quad_perm xor-1 and xor-2, row_half_mirror and row_mirror give each 16-lane
+// row's maximum, one shuffle joins the two rows of a group. A maximum is
+// exact, so any combining order gives the same bits as a shuffle tree (five
+// LDS-crossbar round trips, where this takes one).
+template <int CTRL>
+__device__ __forceinline__ float dpp_max(float x) {
+  const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false);
+  return fmaxf(x, __builtin_bit_cast(float, y));
+}
+__device__ __forceinline__ float group32_max(float x) {
+  x = dpp_max<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+  x = dpp_max<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+  x = dpp_max<0x141>(x);  // row_half_mirror
+  x = dpp_max<0x140>(x);  // row_mirror
+  return fmaxf(x, __shfl_xor(x, 16));
+}
+
 // One weight register set: E consecutive elements (E = 8 or 4) of a row,
 // converted to fp32 at use.
 template <typename WT, int E>
@@ -475,13 +493,13 @@ struct WVec<float> {
 // barrier per unit.
 // Staging: thread t takes k chunk t % 32 (4 values) of rows t / 32 + 8 r,
 // whatever MB: it multiplies by gamma, adds the squares of x into its per-row
-// sum of squares (RMS), and for fp16 weights folds |x'| over the row's 32
-// chunk threads (adjacent lanes, xor butterfly) for the scale. The tile end
+// sum of squares (RMS), and for fp16 weights takes the maximum |x'| over the
+// row's 32 chunk threads (adjacent lanes, group32_max) for the scale. The tile end
 // folds the sums of squares the same way -- orders fixed by the plan, never
 // by M.
 // LDS, per buffer: fp32 X' as 16-byte chunks, row m at m * 32, chunk c at
 // c ^ (m & 7); fp16 planes with 8-value chunks, row m at m * 16, chunk c at
-// c ^ (m & 7) (the 16 rows one MFMA operand read touches land in different
+// c ^ (m & 15) (the 16 rows one MFMA operand read touches land in different
 // banks).
 template <typename WT, int MB, bool RMS, bool KN = false>
 __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
@@ -574,9 +592,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       }
       const floatx4 xv = v * g;
       if constexpr (H) {
-        float amax = fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3])));
-#pragma unroll
-        for (int o = CPR / 2; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        static_assert(CPR == 32, "a row's chunk threads are one 32-lane group");
+        const float amax = group32_max(
+            fmaxf(fmaxf(fabsf(xv[0]), fabsf(xv[1])), fmaxf(fabsf(xv[2]), fabsf(xv[3]))));
         int ex = 0;
         (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1) (ex = 0 for 0, inf, nan)
         const int e = min(15 - ex, 126);
@@ -587,7 +605,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
           h[q] = static_cast<_Float16>(t);
           l[q] = static_cast<_Float16>((t - static_cast<float>(h[q])) * 2048.0f);
         }
-        const int pos = m * HCR + ((qc >> 1) ^ (m & 7));
+        const int pos = m * HCR + ((qc >> 1) ^ (m & 15));
         reinterpret_cast<halfx4*>(&xb.hi[pos])[qc & 1] = h;
         reinterpret_cast<halfx4*>(&xb.lo[pos])[qc & 1] = l;
         if (qc == 0) xb.ds[m] = ldexpf(1.0f, -e);
@@ -655,7 +673,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
         halfx8 bh[MB], bl[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 7));
+          const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 15));
           bh[mb] = xb.hi[pos];
           bl[mb] = xb.lo[pos];
         }
@@ -734,7 +752,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       halfx8 bh[MB], bl[MB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 7));
+        const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 15));
         bh[mb] = xb.hi[pos];
         bl[mb] = xb.lo[pos];
       }
