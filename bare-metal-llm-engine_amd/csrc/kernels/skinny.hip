@@ -26,7 +26,7 @@
 // skinny_nk_kernel covers a unit the same way for output-major W and, with
 // KN, for reference-layout fp16 W (through LDS, transposed);
 // skinny_mfma_kernel takes reference-layout fp32 W. At 11008 x 4096 fp16 W
-// [K x N] the KN form takes 30.2 us at M = 16 and 64.9 us at M = 64, against
+// [K x N] the KN form takes 26.9 us at M = 16 and 55.3 us at M = 64, against
 // 31.1 and 88.5 us for skinny_mfma_kernel (fp32 MFMA on converted weights).
 #include "device_sync.hpp"
 #include "launch.hpp"
@@ -715,15 +715,18 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   };
 
   // KN (reference layout W [K x N], fp16): a unit's 128 x 64 block of W is
-  // loaded straight into an LDS stage -- thread slot g = (4 q + wave) * 64 +
-  // lane takes 16 bytes of row g / 8 (one wave load: 8 rows x 128 bytes) --
-  // and each wave reads its A operands from there transposed: lane (j, s)
-  // of load i gathers column 16 wave + j at k = 32 i + 8 s + t, t = 0..7
-  // (the same fragment skinny_nk_kernel loads from an output-major row; the
-  // position swizzle puts the four lane groups' rows in different banks).
-  // Rows past K read row 0 of the unit and columns past N chunk 0 of the
-  // tile; both are zeroed or dropped at use.
-  auto dma_w = [&](const Cursor& c, int st) __attribute__((always_inline)) {
+  // loaded in 16-byte pieces -- thread slot g = (4 q + wave) * 64 + lane
+  // takes 16 bytes of row g / 8 (one wave load: 8 rows x 128 bytes) --
+  // written to an LDS stage, and each wave reads its A operands from there
+  // transposed: lane (j, s) of load i gathers column 16 wave + j at k = 32 i
+  // + 8 s + t, t = 0..7 (the same fragment skinny_nk_kernel loads from an
+  // output-major row; the position swizzle puts the four lane groups' rows
+  // in different banks). Rows past K read row 0 of the unit and columns past
+  // N chunk 0 of the tile; both are zeroed or dropped at use. (Loading
+  // straight into LDS measured no faster: the compiler then waits for those
+  // loads before any LDS access it cannot prove disjoint, which serialises
+  // them with the unit's arithmetic.)
+  auto load_wk = [&](halfx8 (&wr)[4], const Cursor& c) __attribute__((always_inline)) {
     const long long kbase = c.ku * kUnitK;
     const long long n0 = c.tile * kCols;
     const WT* base = W + kbase * N + n0;
@@ -734,8 +737,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       const int cch = (g & 7) ^ ((r >> 3) & 7);
       const long long off = (kbase + r < K ? static_cast<long long>(r) * N : 0) +
                             (n0 + 8 * cch < N ? 8 * cch : 0);
-      dma16(base + off, reinterpret_cast<WT*>(&wst[st * 1024 + (4 * q + wave) * 64]));
+      wr[q] = __builtin_nontemporal_load(reinterpret_cast<const halfx8*>(base + off));
     }
+  };
+  auto put_wk = [&](const halfx8 (&wr)[4], int st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) wst[st * 1024 + (4 * q + wave) * 64 + lane] = wr[q];
   };
   auto compute_kn = [&](const XBuf& xb, int st, const Cursor& cur) __attribute__((always_inline)) {
     const _Float16* ws = reinterpret_cast<const _Float16*>(&wst[st * 1024]);
@@ -828,21 +835,22 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   };
   x_next();
   if constexpr (KN) {
-    // Unit per iteration from stage b: X of the next unit and its weights
-    // (into the other stage) issued first, the unit computed, the next X'
-    // written, then every load waited for and one barrier (two with one X
-    // buffer: the rewrite waits until every wave has read it).
-    dma_w(cl, 0);
+    // Unit per iteration from stage b: X and weights of the next unit loaded
+    // first, the unit computed, then the next unit's X' and weights written
+    // (X' and the weights into the other buffer and stage) and one barrier
+    // (two with one X buffer: the rewrite waits until every wave has read
+    // it). Every iteration issues the same loads -- past the range the
+    // current unit again.
+    halfx8 wr[4];
+    load_wk(wr, cl);
     advance(cl);
     store_x(S, xbuf[0]);
-#if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
-#endif
+    put_wk(wr, 0);
     lds_barrier();
     for (int b = 0;; b ^= 1) {
       x_next();
       __builtin_amdgcn_sched_barrier(0);
-      if (cl.u < u1) dma_w(cl, b ^ 1);
+      load_wk(wr, cl.u < u1 ? cl : cc);
       __builtin_amdgcn_sched_barrier(0);
       compute_kn(xbuf[XB == 2 ? b : 0], b, cc);
       advance(cl);
@@ -850,10 +858,8 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       if (cc.u + 1 < u1) {
         if constexpr (XB == 1) lds_barrier();
         store_x(S, xbuf[XB == 2 ? (b ^ 1) : 0]);
+        put_wk(wr, b ^ 1);
       }
-#if defined(__HIP_DEVICE_COMPILE__)
-      __builtin_amdgcn_s_waitcnt(vmcnt_le(0));
-#endif
       lds_barrier();
       advance(cc);
       if (cc.u >= u1) break;
