@@ -700,9 +700,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __r
 // after the staging round trip. The LDS slot layout is lds_slot<8>: each
 // 16-byte chunk of it is 4 consecutive elements of x, so a lane fetches the
 // chunk its LDS position holds; chunks past K are zeroed with LDS stores.
-// (With RMSNorm the sum of squares and the x * gamma product need a second
-// barrier after the staging, which costs more than the early start gains:
-// measured 2% slower at 11008 x 4096, so RMSNorm keeps the staging kernel.)
+// (With RMSNorm, staging x this way needs a second barrier for the sum of
+// squares and measured 2% slower at 11008 x 4096; gemv_rows_rms_early_kernel
+// starts the weight stream early with register staging instead.)
 // Dynamic LDS: NP * 512 floats.
 template <int NP, int KT, int CH, int WAVES = 16>
 __global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float16* __restrict__ W,

@@ -23,11 +23,13 @@
 // output's arithmetic involves only its own row of X, so a row's result is
 // the same bits whichever M (5..64) it is computed in.
 //
-// skinny_nk_kernel covers a unit the same way for output-major W and, with
-// KN, for reference-layout fp16 W (through LDS, transposed);
-// skinny_mfma_kernel takes reference-layout fp32 W. At 11008 x 4096 fp16 W
-// [K x N] the KN form takes 26.9 us at M = 16 and 55.3 us at M = 64, against
-// 31.1 and 88.5 us for skinny_mfma_kernel (fp32 MFMA on converted weights).
+// skinny_nk_kernel covers a unit the same way for output-major W (its
+// weights straight into registers, or at one m-block of fp16 W through LDS
+// stages) and for reference-layout fp16 W (through LDS stages, read
+// transposed); skinny_mfma_kernel takes reference-layout fp32 W. At 11008 x
+// 4096 fp16 W [K x N] the staged form takes 25.5 us at M = 16 and 54.6 us at
+// M = 64, against 31.1 and 88.5 us for skinny_mfma_kernel (fp32 MFMA on
+// converted weights).
 #include "device_sync.hpp"
 #include "launch.hpp"
 
@@ -501,14 +503,18 @@ struct WVec<float> {
 // c ^ (m & 7); fp16 planes with 8-value chunks, row m at m * 16, chunk c at
 // c ^ (m & 15) (the 16 rows one MFMA operand read touches land in different
 // banks).
-template <typename WT, int MB, bool RMS, bool KN = false>
+template <typename WT, int MB, bool RMS, int WMODE = 0>
 __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     const WT* __restrict__ W, const float* __restrict__ x, const float* __restrict__ gamma,
     float* __restrict__ y, int M, long long N, long long K, Plan plan,
     float* __restrict__ rec, float* __restrict__ rec_ss, float eps) {
   using WV = typename WVec<WT>::type;
   constexpr bool H = std::is_same<WT, _Float16>::value;    // fp16 MFMA path
-  static_assert(!KN || H, "the reference-layout form is fp16 only");
+  // WMODE 0: output-major W into registers; 1: reference layout (KN) and 2:
+  // output-major, both through LDS stages (fp16).
+  constexpr bool KN = WMODE == 1;
+  constexpr bool STAGED = WMODE != 0;
+  static_assert(!STAGED || H, "the LDS-staged forms are fp16 only");
   constexpr int E = 16 / static_cast<int>(sizeof(WT));     // elements per 16-byte load
   constexpr int LPU = static_cast<int>(kUnitK) / (4 * E);  // loads per unit per lane
   constexpr int ROWS = 16 * MB;
@@ -525,14 +531,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     halfx8 lo[H ? ROWS * HCR : 1];
     float ds[H ? ROWS : 1];
   };
-  // KN: one X buffer past 32 rows (LDS for two workgroups per CU), read and
+  // Staged weights: one X buffer past 32 rows (LDS for two workgroups per CU), read and
   // rewritten between two barriers per unit.
-  constexpr int XB = (KN && MB > 2) ? 1 : 2;
+  constexpr int XB = (STAGED && MB > 2) ? 1 : 2;
   __shared__ XBuf xbuf[XB];
   __shared__ float ssc[RMS ? ROWS : 1];
-  // KN: two stages of a unit's weights, 128 rows (k) x 8 chunks of 16 bytes
-  // (64 columns); chunk c of row r at position c ^ ((r / 8) & 7).
-  __shared__ halfx8 wst[KN ? 2 * 128 * 8 : 1];
+  // Staged weights: two stages of a unit's 16 KiB block of W (KN: 128 rows
+  // of k x 8 chunks of 16 bytes; output-major: 64 rows x 16 chunks).
+  __shared__ halfx8 wst[STAGED ? 2 * 128 * 8 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -717,44 +723,65 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   // KN (reference layout W [K x N], fp16): a unit's 128 x 64 block of W is
   // loaded in 16-byte pieces -- thread slot g = (4 q + wave) * 64 + lane
   // takes 16 bytes of row g / 8 (one wave load: 8 rows x 128 bytes) --
-  // written to an LDS stage, and each wave reads its A operands from there
-  // transposed: lane (j, s) of load i gathers column 16 wave + j at k = 32 i
-  // + 8 s + t, t = 0..7 (the same fragment skinny_nk_kernel loads from an
-  // output-major row; the position swizzle puts the four lane groups' rows
-  // in different banks). Rows past K read row 0 of the unit and columns past
+  // written to an LDS stage (chunk c of row r at position c ^ 2 ((r / 8) & 3)),
+  // and each wave reads its A operands from there transposed: lane (j, s) of
+  // load i gathers column 16 wave + j at k = 32 i + 8 s + t, t = 0..7 (the same
+  // fragment skinny_nk_kernel loads from an output-major row). The swizzle
+  // gives the 4 lane groups' rows (8 apart) and the wave's two 8-column
+  // chunks 8 distinct chunk positions: one read touches 32 distinct banks. Rows past K read row 0 of the unit and columns past
   // N chunk 0 of the tile; both are zeroed or dropped at use. (Loading
   // straight into LDS measured no faster: the compiler then waits for those
   // loads before any LDS access it cannot prove disjoint, which serialises
   // them with the unit's arithmetic.)
+  // WMODE 2 (output-major W through LDS): thread slot g takes 16 bytes (8
+  // values of k) of weight row g / 16 of the tile at k chunk g % 16 (one wave
+  // load: 4 rows x 256 bytes), stored at chunk position (g % 16) ^ (row % 16)
+  // of the row's 256 bytes; lane (j, s) of load i reads row 16 wave + j, chunk
+  // 4 i + s with one 16-byte read (the 16 rows of a lane group hit 16
+  // distinct chunk positions). Rows past N read row N - 1, chunks past K the
+  // row's first; zeroed or dropped at use.
   auto load_wk = [&](halfx8 (&wr)[4], const Cursor& c) __attribute__((always_inline)) {
     const long long kbase = c.ku * kUnitK;
     const long long n0 = c.tile * kCols;
-    const WT* base = W + kbase * N + n0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int g = (4 * q + wave) * 64 + lane;
-      const int r = g >> 3;
-      const int cch = (g & 7) ^ ((r >> 3) & 7);
-      const long long off = (kbase + r < K ? static_cast<long long>(r) * N : 0) +
-                            (n0 + 8 * cch < N ? 8 * cch : 0);
-      wr[q] = __builtin_nontemporal_load(reinterpret_cast<const halfx8*>(base + off));
+      if constexpr (KN) {
+        const int r = g >> 3;
+        const int cch = (g & 7) ^ (((r >> 3) & 3) << 1);
+        const long long off = (kbase + r < K ? static_cast<long long>(r) * N : 0) +
+                              (n0 + 8 * cch < N ? 8 * cch : 0);
+        wr[q] = __builtin_nontemporal_load(reinterpret_cast<const halfx8*>(W + kbase * N + n0 + off));
+      } else {
+        const long long n = n0 + (g >> 4) < N ? n0 + (g >> 4) : N - 1;
+        const long long k = kbase + 8 * (g & 15);
+        wr[q] = __builtin_nontemporal_load(reinterpret_cast<const halfx8*>(W + n * K + (k < K ? k : 0)));
+      }
     }
   };
   auto put_wk = [&](const halfx8 (&wr)[4], int st) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) wst[st * 1024 + (4 * q + wave) * 64 + lane] = wr[q];
+    for (int q = 0; q < 4; ++q) {
+      const int g = (4 * q + wave) * 64 + lane;
+      const int pos = KN ? g : (g & ~15) | ((g & 15) ^ ((g >> 4) & 15));
+      wst[st * 1024 + pos] = wr[q];
+    }
   };
   auto compute_kn = [&](const XBuf& xb, int st, const Cursor& cur) __attribute__((always_inline)) {
     const _Float16* ws = reinterpret_cast<const _Float16*>(&wst[st * 1024]);
 #pragma unroll
     for (int i = 0; i < LPU; ++i) {
       const bool kok = cur.ku * kUnitK + 4 * E * i + E * s < K;
-      const int r0 = 32 * i + 8 * s;
-      const int pch = (2 * wave + (j >> 3)) ^ ((4 * i + s) & 7);
-      const _Float16* src = ws + (r0 * 8 + pch) * 8 + (j & 7);
       halfx8 wv;
+      if constexpr (KN) {
+        const int r0 = 32 * i + 8 * s;
+        const int pch = (2 * wave + (j >> 3)) ^ (s << 1);
+        const _Float16* src = ws + (r0 * 8 + pch) * 8 + (j & 7);
 #pragma unroll
-      for (int t = 0; t < 8; ++t) wv[t] = src[t * 64];
+        for (int t = 0; t < 8; ++t) wv[t] = src[t * 64];
+      } else {
+        wv = wst[st * 1024 + (16 * wave + j) * 16 + ((4 * i + s) ^ j)];
+      }
       const halfx8 wi = kok ? wv : halfx8{};
       halfx8 bh[MB], bl[MB];
 #pragma unroll
@@ -834,7 +861,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
     if (++xku == upt) xku = 0;
   };
   x_next();
-  if constexpr (KN) {
+  if constexpr (STAGED) {
     // Unit per iteration from stage b: X and weights of the next unit loaded
     // first, the unit computed, then the next unit's X' and weights written
     // (X' and the weights into the other buffer and stage) and one barrier
@@ -946,6 +973,14 @@ std::size_t scratch_for(const Plan& p, long long M) {
   return static_cast<std::size_t>(p.P) * 2 * M * (kCols + 1) * sizeof(float);
 }
 
+// Output-major fp16 W through LDS stages (WMODE 2) at one m-block, straight
+// into registers (0) otherwise and for fp32 W: at 11008 x 4096, 16 rows 24.2
+// against 27.3 us, 32 rows 33.2 against 33.0, 48 rows 43.3 against 41.2, 64
+// rows 52.2 against 49.0 (past 32 rows the staged form keeps one X' buffer
+// and two barriers per unit). Both give the same bits.
+template <typename WT, int MB>
+constexpr int kNkMode = (std::is_same<WT, _Float16>::value && MB == 1) ? 2 : 0;
+
 template <typename WT, bool NK, int MB, bool RMS>
 void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
   const long long N = a.N;
@@ -971,10 +1006,10 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
   const unsigned grid = static_cast<unsigned>(plan.P);
   const WT* W = static_cast<const WT*>(a.W);
   if constexpr (NK) {
-    skinny_nk_kernel<WT, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(
+    skinny_nk_kernel<WT, MB, RMS, kNkMode<WT, MB>><<<grid, kWaves * 64, 0, stream>>>(
         W, a.x, RMS ? a.gamma : nullptr, a.y, M, N, K, plan, rec, rec_ss, a.eps);
   } else if constexpr (std::is_same<WT, _Float16>::value) {
-    skinny_nk_kernel<WT, MB, RMS, true><<<grid, kWaves * 64, 0, stream>>>(
+    skinny_nk_kernel<WT, MB, RMS, 1><<<grid, kWaves * 64, 0, stream>>>(
         W, a.x, RMS ? a.gamma : nullptr, a.y, M, N, K, plan, rec, rec_ss, a.eps);
   } else {
     skinny_mfma_kernel<WT, NK, MB, RMS><<<grid, kWaves * 64, 0, stream>>>(

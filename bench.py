@@ -44,7 +44,7 @@ FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense FP32 matrix, published
 METRIC = "decode GEMV HBM GB/s (% of peak); FP32 GEMM TFLOP/s at 4096^3 (% MFMA peak)"
 
 
-HEADLINE_KERNEL = "eng::gemv::gemv_rows_dma_kernel<8, 512, 8>"
+HEADLINE_KERNEL = "eng::gemv::gemv_rows_dma_kernel<8, 512, 8, 16>"
 TRAFFIC_PROFILE = os.path.join("profiles", "gemv_rows_dma_fixed_f16w_4096x4096_cold.md")
 
 
