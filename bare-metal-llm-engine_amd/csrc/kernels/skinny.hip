@@ -71,6 +71,16 @@ __device__ __forceinline__ float group32_max(float x) {
   return fmaxf(x, __shfl_xor(x, 16));
 }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// Chunk swizzle of the reference-layout weight stage: row r (one k, 64
+// columns = 8 chunks of 16 bytes) keeps chunk c at position c ^ kn_swz(r).
+// A transposing read touches 16 rows x 32 bytes (rows 8 s + e and 8 s + e
+// + 4 for the four lane groups s, e = 0..3); an even swizzle keeps each
+// 32-byte pair whole, and (s + e / 2) spreads the pairs evenly over the
+// four pair positions, so no bank takes more than the minimum.
+__device__ __forceinline__ int kn_swz(int r) { return (((r >> 3) + (r >> 1)) & 3) << 1; }
+
 // One weight register set: E consecutive elements (E = 8 or 4) of a row,
 // converted to fp32 at use.
 template <typename WT, int E>
@@ -723,12 +733,11 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   // KN (reference layout W [K x N], fp16): a unit's 128 x 64 block of W is
   // loaded in 16-byte pieces -- thread slot g = (4 q + wave) * 64 + lane
   // takes 16 bytes of row g / 8 (one wave load: 8 rows x 128 bytes) --
-  // written to an LDS stage (chunk c of row r at position c ^ 2 ((r / 8) & 3)),
-  // and each wave reads its A operands from there transposed: lane (j, s) of
-  // load i gathers column 16 wave + j at k = 32 i + 8 s + t, t = 0..7 (the same
-  // fragment skinny_nk_kernel loads from an output-major row). The swizzle
-  // gives the 4 lane groups' rows (8 apart) and the wave's two 8-column
-  // chunks 8 distinct chunk positions: one read touches 32 distinct banks. Rows past K read row 0 of the unit and columns past
+  // written to an LDS stage (chunk c of row r at position c ^ kn_swz(r)), and
+  // each wave reads its A operands from there transposed: lane (j, s) of load
+  // i gets column 16 wave + j at k = 32 i + 8 s + t, t = 0..7 (the same
+  // fragment skinny_nk_kernel loads from an output-major row), with two gfx950
+  // transposing LDS reads (ds_read_b64_tr_b16) per fragment. Rows past K read row 0 of the unit and columns past
   // N chunk 0 of the tile; both are zeroed or dropped at use. (Loading
   // straight into LDS measured no faster: the compiler then waits for those
   // loads before any LDS access it cannot prove disjoint, which serialises
@@ -748,7 +757,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       const int g = (4 * q + wave) * 64 + lane;
       if constexpr (KN) {
         const int r = g >> 3;
-        const int cch = (g & 7) ^ (((r >> 3) & 3) << 1);
+        const int cch = (g & 7) ^ kn_swz(r);
         const long long off = (kbase + r < K ? static_cast<long long>(r) * N : 0) +
                               (n0 + 8 * cch < N ? 8 * cch : 0);
         wr[q] = __builtin_nontemporal_load(reinterpret_cast<const halfx8*>(W + kbase * N + n0 + off));
@@ -774,11 +783,21 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       const bool kok = cur.ku * kUnitK + 4 * E * i + E * s < K;
       halfx8 wv;
       if constexpr (KN) {
-        const int r0 = 32 * i + 8 * s;
-        const int pch = (2 * wave + (j >> 3)) ^ (s << 1);
-        const _Float16* src = ws + (r0 * 8 + pch) * 8 + (j & 7);
+        // Two transposing reads of 4 rows each: within each 16-lane group,
+        // lane L names 8 bytes (row r0 + L / 4, columns 16 wave + 4 (L % 4)
+        // .. + 3) and lane j receives column 16 wave + j of the 4 rows.
+        const int a4 = j & 3;
+        const int c = 2 * wave + (a4 >> 1);
 #pragma unroll
-        for (int t = 0; t < 8; ++t) wv[t] = src[t * 64];
+        for (int h = 0; h < 2; ++h) {
+          const int r = 32 * i + 8 * s + 4 * h + (j >> 2);
+          const int off = r * 128 + ((c ^ kn_swz(r)) << 4) + ((a4 & 1) << 3);
+          const halfx4 v = __builtin_bit_cast(
+              halfx4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(
+                          (__attribute__((address_space(3))) char*)ws + off)));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) wv[4 * h + e] = v[e];
+        }
       } else {
         wv = wst[st * 1024 + (16 * wave + j) * 16 + ((4 * i + s) ^ j)];
       }
