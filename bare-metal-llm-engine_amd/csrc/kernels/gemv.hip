@@ -195,24 +195,6 @@ bool gemv_dma_enabled() {
   return on;
 }
 
-// Fixed-K fp16 RMSNorm GEMV with the weight stream started before the
-// staging completes (gemv_rows_rms_early_kernel: the bits of the staged
-// gemv_rows_lds_kernel, which ENGINE_GEMV_NO_EARLY_RMS=1 selects instead).
-template <int NP, int KT, int CH>
-void launch_rows_rms_early(const GemvArgs& a, hipStream_t stream) {
-  ENG_CHECK(a.K == (NP - 1) * 512LL + KT, "gemv: fixed-K kernel for another K");
-  const long long wgs = (a.N + gemv::kStageWaves - 1) / gemv::kStageWaves;
-  ENG_CHECK(wgs <= 0x7fffffffLL, "gemv: N too large for one launch");
-  const std::size_t lds = static_cast<std::size_t>(gemv::rms_early_lds_floats(NP)) * 4;
-  static std::atomic<bool> allowed[64] = {};
-  auto kern = gemv::gemv_rows_rms_early_kernel<NP, KT, CH, false>;
-  allow_staged_lds(reinterpret_cast<const void*>(kern), allowed, lds);
-  kern<<<static_cast<unsigned>(wgs), 64 * gemv::kStageWaves, lds, stream>>>(
-      static_cast<const _Float16*>(a.W), nullptr, static_cast<const float*>(a.x), a.gamma,
-      static_cast<float*>(a.y), a.N, a.eps);
-  ENG_LAUNCH_CHECK();
-}
-
 template <int NP, int KT, int CH, int WAVES>
 void launch_rows_dma(const GemvArgs& a, hipStream_t stream) {
   ENG_CHECK(a.K == (NP - 1) * 512LL + KT, "gemv: fixed-K kernel for another K");
@@ -267,18 +249,16 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     // 8-wave workgroups (two per CU, the same waves): the down projection
     // 4096 x 11008 15.4 us against 16.0 (4096 x 4096 the same either way;
     // with RMSNorm, and for the fused gate / up, 8-wave workgroups measured
-    // 6% slower). With RMSNorm, x and gamma are loaded before the first
-    // weight loads and staged while those are in flight, 8 pieces per row in
-    // flight: 11008 x 4096 15.5 us against 15.9 staged first, 12288 x 4096
-    // 16.8 against 17.2, 4096 x 11008 16.0 against 16.9.
+    // 6% slower). With RMSNorm the register-staged kernel stays: the
+    // early-start form (gemv_rows_rms_early_kernel, which the fused gate / up
+    // uses) ran config 3 in 15.5 us on some boxes of the pool and 17.5 us on
+    // others, against 15.8-15.9 us staged on both.
     if (fits && (RMS || a.N >= one_round / 2 || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       const bool wide = RMS || a.N >= one_round || a.K > 4096;
       const bool fixed = with_fixed_k_f16(a.K, [&](auto fk) {
         using F = decltype(fk);
-        if (RMS && gemv_rms_early_enabled()) {
-          launch_rows_rms_early<F::NP, F::KT, (F::CH1 < 8 ? F::CH1 : 8)>(a, stream);
-        } else if (!RMS && wide && gemv_dma_enabled()) {
+        if (!RMS && wide && gemv_dma_enabled()) {
           if (a.K > 4096 && a.N <= one_round) {
             // half a row's pieces in flight past 16 (4096 x 11008: 15.3 us
             // against 15.5 with all 22)

@@ -65,9 +65,9 @@ bool with_fixed_k_f16(long long K, F&& f) {
     default: return false;
   }
 }
-// False when ENGINE_GEMV_NO_EARLY_RMS=1: the fixed-K fp16 RMSNorm GEMV and
-// fused gate / up kernels then stage x * gamma before starting the weight
-// stream (the same bits, for comparison).
+// False when ENGINE_GEMV_NO_EARLY_RMS=1: the fixed-K fp16 fused gate / up
+// kernel then stages x * gamma before starting the weight stream (the same
+// bits, for comparison).
 bool gemv_rms_early_enabled();
 // Past 64 KiB a kernel's dynamic LDS must be allowed explicitly: once per
 // device per kernel (`done` is that kernel's flag array); a no-op below.
