@@ -85,6 +85,9 @@ def check_rows(orc, got, x, g, W_kn, rows, what):
     (6, 65536, 256, "f16", "kn", True),     # one K chunk: RMS scale applied in the kernel
     (7, 40000, 256, "f16", "nk", True),
     (9, 64, 8, "f16", "kn", True),          # K = 8: a single partial k-group
+    (9, 1000, 776, "f16", "nk", True),      # one m-block, weights through LDS: ragged tile and unit
+    (36, 1000, 776, "f16", "kn", False),    # three m-blocks, one X' buffer: ragged tile and unit
+    (50, 11008, 4096, "f16", "kn", True),   # four m-blocks at the config-3 shape
 ])
 def test_rmsnorm_linear_few_rows_against_oracle(gpu, orc, M, N, K, dtype, layout, gamma):
     rng = np.random.default_rng(M * 1000 + N + K)
