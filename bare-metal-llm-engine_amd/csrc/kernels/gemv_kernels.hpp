@@ -455,14 +455,32 @@ __device__ __forceinline__ int lds_slot(int k) {
   return p * PIECE + (e >> 2) * 256 + l * 4 + (e & 3);
 }
 
+// Element index of the first of the 4 values at LDS float position pos (a
+// multiple of 4): the inverse of lds_slot<VEC>.
+template <int VEC>
+__device__ __forceinline__ int slot_elem(int pos) {
+  if constexpr (VEC == 4) {
+    return pos;
+  } else {
+    const int p = pos >> 9;
+    const int r = pos & 511;
+    return p * 512 + ((r & 255) >> 2) * 8 + (r >> 8) * 4;
+  }
+}
+
 // Workgroup-cooperative staging for the LDS kernels (THREADS threads):
 // writes xs = x * gamma (gamma optional, applied only with RMS) into LDS
 // slots, zero-padded to whole pieces, sums x^2 (RMS) into *total_ss, and ends
 // with a barrier. K % 4 == 0 and 16-byte aligned x / gamma are required.
 // The sum has one fixed order for every workgroup size: 1024 virtual threads,
-// v taking the 16-byte chunks v, v + 1024, v + 2048, ... in turn; each virtual
-// wave (64 consecutive v) folded by shuffles; the 16 virtual-wave sums added
-// in order. A workgroup of THREADS threads plays virtual threads tid,
+// v taking the 16-byte LDS positions v, v + 1024, v + 2048, ... in turn (each
+// holding the 4 values slot_elem gives); each virtual wave (64 consecutive v)
+// folded by wave_sum; the 16 virtual-wave sums added in order. (Positions
+// rather than elements, so that the kernels staging x by direct-to-LDS loads
+// -- wave w's load i filling positions 1024 i + 64 w .. + 63 -- can take the
+// same sum from the values each thread loaded. A direct-staged RMSNorm
+// GEMV built that way, gamma staged beside x and multiplied in as each wave
+// reads it, ran config 3 in 16.1-16.3 us against 15.7-15.8 for this staging.) A workgroup of THREADS threads plays virtual threads tid,
 // tid + THREADS, ..., so kernels with different workgroup sizes (and the
 // small-batch kernels, which stage row by row) compute the same bits.
 // wave_ss holds kStageWaves floats of shared memory.
@@ -486,8 +504,9 @@ __device__ __forceinline__ void stage_xs(const float* __restrict__ x,
   for (int base = 0; base < padded; base += VT * 4) {
 #pragma unroll
     for (int j = 0; j < JV; ++j) {
-      const int k = base + (tid + j * THREADS) * 4;
-      if (k < padded) {
+      const int pos = base + (tid + j * THREADS) * 4;
+      if (pos < padded) {
+        const int k = slot_elem<VEC>(pos);
         F4 v = F4{};
         if (k < K) {
           v = *reinterpret_cast<const F4*>(x + k);
@@ -499,7 +518,7 @@ __device__ __forceinline__ void stage_xs(const float* __restrict__ x,
             if (gamma != nullptr) v *= *reinterpret_cast<const F4*>(gamma + k);
           }
         }
-        *reinterpret_cast<F4*>(xs + lds_slot<VEC>(k)) = v;
+        *reinterpret_cast<F4*>(xs + pos) = v;
       }
     }
   }
@@ -831,7 +850,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_rows_dma_kernel(const _Float1
 // the staging completes and kept at CH pieces per row in flight (a ring: the
 // registers of a used piece take the piece CH further on; GLU streams two
 // rows, so CH = 4 keeps its 16 waves at 64 VGPRs, two workgroups per CU).
-// Each thread loads its x and gamma chunks (the chunks
+// Each thread loads its x and gamma chunks (the LDS positions
 // stage_xs gives virtual thread tid, so the sum of squares has stage_xs's
 // order), then its wave's first CH weight pieces per row, and only then
 // waits for its x and gamma, writes x * gamma to LDS and its wave's sum of
@@ -873,7 +892,7 @@ __global__ __launch_bounds__(1024) void gemv_rows_rms_early_kernel(
   F4 xv[ITER], gv[ITER];
 #pragma unroll
   for (int i = 0; i < ITER; ++i) {
-    const int k = (i * VT + tid) * 4;
+    const int k = slot_elem<8>((i * VT + tid) * 4);
     const int kc = k < K ? k : 0;
     xv[i] = *reinterpret_cast<const F4*>(x + kc);
     gv[i] = *reinterpret_cast<const F4*>(gp + kc);
@@ -921,14 +940,15 @@ __global__ __launch_bounds__(1024) void gemv_rows_rms_early_kernel(
   float ss = 0.0f;
 #pragma unroll
   for (int i = 0; i < ITER; ++i) {
-    const int k = (i * VT + tid) * 4;
+    const int pos = (i * VT + tid) * 4;
+    const int k = slot_elem<8>(pos);
     F4 v = k < K ? xv[i] : F4{};
     ss = fmaf(v[0], v[0], ss);
     ss = fmaf(v[1], v[1], ss);
     ss = fmaf(v[2], v[2], ss);
     ss = fmaf(v[3], v[3], ss);
     if (gamma != nullptr) v *= gv[i];
-    *reinterpret_cast<F4*>(xs + lds_slot<8>(k)) = v;
+    *reinterpret_cast<F4*>(xs + pos) = v;
   }
   ss = wave_sum(ss);
   if (lane == 0) wave_ss[wave] = ss;
