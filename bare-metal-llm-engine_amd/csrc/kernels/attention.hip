@@ -942,10 +942,20 @@ __global__ __launch_bounds__(kReduceThreads) void flash_decode_reduce_kernel(
     }
   };
   if (nsplit <= 2 * C) {
-    // One or two states per thread.
-    for (int sp = c; sp < nsplit; sp += C) {
-      merge(part_ml[2 * (base + sp)], part_ml[2 * (base + sp) + 1], part_o[(base + sp) * D + d]);
-    }
+    // One or two states per thread (splits c and c + C), all six loads issued
+    // before the first merge and held in registers past it (the asm), so the
+    // walk costs one round trip: left to the compiler, the l and o loads sink
+    // into merge's branch and each state costs two (TinyLlama at 32 splits:
+    // four round trips in a row). A second slot past nsplit re-reads the first.
+    const int s0 = c < nsplit ? c : nsplit - 1;
+    const int s1 = c + C < nsplit ? c + C : s0;
+    float m0 = part_ml[2 * (base + s0)], l0 = part_ml[2 * (base + s0) + 1];
+    float o0 = part_o[(base + s0) * D + d];
+    float m1 = part_ml[2 * (base + s1)], l1 = part_ml[2 * (base + s1) + 1];
+    float o1 = part_o[(base + s1) * D + d];
+    asm volatile("" : "+v"(m0), "+v"(l0), "+v"(o0), "+v"(m1), "+v"(l1), "+v"(o1));
+    if (c < nsplit) merge(m0, l0, o0);
+    if (c + C < nsplit) merge(m1, l1, o1);
   } else {
     // Batches of kBatch states: every load of a batch is issued before the first
     // merge (slots past nsplit re-read the last state and are skipped), so a
