@@ -302,6 +302,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
   float v[PLANES];
 #pragma unroll
   for (int q = 0; q < PLANES; ++q) v[q] = 0.0f;
+  // RMS: the first sum-of-squares state of lane c (split c) is loaded ahead of
+  // the partials and held past their loop (the asm), so with up to 64 splits
+  // the scale costs no round trip after theirs (left to the compiler, the
+  // load sank into wave 0's branch behind the partials' wait).
+  [[maybe_unused]] float ss0 = 0.0f;
+  if constexpr (RMS) ss0 = part_ss[static_cast<long long>(c < nsplit ? c : nsplit - 1) * mx + m];
   for (int s = s0; s < s1; s += 8) {
     float t[PLANES][8];
 #pragma unroll
@@ -316,6 +322,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
       for (int q = 0; q < PLANES; ++q) v[q] += s + i < s1 ? t[q][i] : 0.0f;
     }
   }
+  if constexpr (RMS) asm volatile("" : "+v"(ss0));
 #pragma unroll
   for (int q = 0; q < PLANES; ++q) group_sum[q][g][c] = v[q];
   // Sum of squares over the splits: lane c of wave 0 takes splits c, c + 64,
@@ -323,7 +330,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_reduce_kernel(
   float tot = 0.0f;
   if constexpr (RMS) {
     if (g == 0) {
-      for (int s = c; s < nsplit; s += 64) tot += part_ss[s * mx + m];
+      if (c < nsplit) tot += ss0;
+      for (int s = c + 64; s < nsplit; s += 64) tot += part_ss[s * mx + m];
       tot = wave_sum(tot);
     }
   }
