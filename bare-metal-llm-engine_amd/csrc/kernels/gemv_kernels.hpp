@@ -476,10 +476,12 @@ __device__ __forceinline__ int slot_elem(int pos) {
   }
 }
 
-// Workgroup-cooperative staging for the LDS kernels (THREADS threads):
-// writes xs = x * gamma (gamma optional, applied only with RMS) into LDS
-// slots, zero-padded to whole pieces, sums x^2 (RMS) into *total_ss, and ends
-// with a barrier. K % 4 == 0 and 16-byte aligned x / gamma are required.
+// Workgroup-cooperative staging for the LDS kernels (THREADS threads) of MX
+// activation rows (row m at x + m K, staged at xs + m pitch, its wave sums at
+// wave_ss + 16 m): writes xs = x * gamma (gamma optional, applied only with
+// RMS) into LDS slots, zero-padded to whole pieces, sums each row's x^2 (RMS)
+// into total_ss[m], and ends with one barrier. K % 4 == 0 and 16-byte aligned
+// x / gamma are required. Each row's arithmetic is the single row's.
 // The sum has one fixed order for every workgroup size: 1024 virtual threads,
 // v taking the 16-byte LDS positions v, v + 1024, v + 2048, ... in turn (each
 // holding the 4 values slot_elem gives); each virtual wave (64 consecutive v)
@@ -503,73 +505,96 @@ __device__ __forceinline__ void pin_here(float& v) {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int VEC, bool RMS, int THREADS = 256>
-__device__ __forceinline__ void stage_xs(const float* __restrict__ x,
-                                         const float* __restrict__ gamma, long long K,
-                                         int npieces, float* xs, float* wave_ss,
-                                         float* total_ss) {
+template <int VEC, bool RMS, int THREADS, int MX>
+__device__ __forceinline__ void stage_xs_rows(const float* __restrict__ x,
+                                              const float* __restrict__ gamma, long long K,
+                                              int npieces, float* xs, int pitch,
+                                              float* wave_ss, float* total_ss) {
   static_assert(THREADS == 256 || THREADS == 512 || THREADS == 1024, "4, 8 or 16 waves");
   using F4 = typename RawVec<float, 4>::type;
   constexpr int PIECE = 64 * VEC;
   constexpr int VT = kStageWaves * 64;  // virtual threads
   constexpr int JV = VT / THREADS;      // virtual threads per thread
   const int tid = threadIdx.x;
-  float ss[JV];
+  float ss[MX][JV];
 #pragma unroll
-  for (int j = 0; j < JV; ++j) ss[j] = 0.0f;
+  for (int m = 0; m < MX; ++m)
+#pragma unroll
+    for (int j = 0; j < JV; ++j) ss[m][j] = 0.0f;
   const int padded = npieces * PIECE;
-  // A round's x and gamma loads are all issued before any is used (in-bounds
-  // offsets: positions past K read element 0 and store zeros), so the
-  // staging waits once per round, not once per load.
+  // A round's x and gamma loads (every row's x, gamma once) are all issued
+  // before any is used (in-bounds offsets: positions past K read element 0
+  // and store zeros), so the staging waits once per round, not once per load
+  // or per row.
   const float* gp = (RMS && gamma != nullptr) ? gamma : x;
   for (int base = 0; base < padded; base += VT * 4) {
-    F4 xv[JV];
+    F4 xv[MX][JV];
     [[maybe_unused]] F4 gv[JV];
 #pragma unroll
     for (int j = 0; j < JV; ++j) {
       const int pos = base + (tid + j * THREADS) * 4;
       const int k = pos < padded ? slot_elem<VEC>(pos) : 0;
       const int kc = k < K ? k : 0;
-      xv[j] = *reinterpret_cast<const F4*>(x + kc);
+#pragma unroll
+      for (int m = 0; m < MX; ++m) xv[m][j] = *reinterpret_cast<const F4*>(x + m * K + kc);
       if constexpr (RMS) gv[j] = *reinterpret_cast<const F4*>(gp + kc);
     }
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
     for (int j = 0; j < JV; ++j) {
       const int pos = base + (tid + j * THREADS) * 4;
       if (pos < padded) {
         const int k = slot_elem<VEC>(pos);
-        F4 v = F4{};
-        if (k < K) {
-          v = xv[j];
+        const bool in = k < K;
+#pragma unroll
+        for (int m = 0; m < MX; ++m) {
+          // Branch-free (selects), so the gamma load is not sunk into a
+          // branch behind the wait for x: positions past K square and store
+          // zeros (adding 0 * 0 leaves a sum of squares unchanged).
+          F4 v = in ? xv[m][j] : F4{};
           if constexpr (RMS) {
-            ss[j] = fmaf(v[0], v[0], ss[j]);
-            ss[j] = fmaf(v[1], v[1], ss[j]);
-            ss[j] = fmaf(v[2], v[2], ss[j]);
-            ss[j] = fmaf(v[3], v[3], ss[j]);
-            // unconditional (x * 1 is exact), so the load is not sunk into a
-            // branch behind the wait for x
-            v *= gamma != nullptr ? gv[j] : F4{1.0f, 1.0f, 1.0f, 1.0f};
+            ss[m][j] = fmaf(v[0], v[0], ss[m][j]);
+            ss[m][j] = fmaf(v[1], v[1], ss[m][j]);
+            ss[m][j] = fmaf(v[2], v[2], ss[m][j]);
+            ss[m][j] = fmaf(v[3], v[3], ss[m][j]);
+            const F4 g = gamma != nullptr ? gv[j] : F4{1.0f, 1.0f, 1.0f, 1.0f};
+            v = in ? v * g : F4{};
           }
+          *reinterpret_cast<F4*>(xs + m * pitch + pos) = v;
         }
-        *reinterpret_cast<F4*>(xs + pos) = v;
       }
     }
   }
   if constexpr (RMS) {
 #pragma unroll
-    for (int j = 0; j < JV; ++j) {
-      const float w = wave_sum(ss[j]);
-      if ((tid & 63) == 0) wave_ss[(tid >> 6) + j * (THREADS / 64)] = w;
+    for (int m = 0; m < MX; ++m) {
+#pragma unroll
+      for (int j = 0; j < JV; ++j) {
+        const float w = wave_sum(ss[m][j]);
+        if ((tid & 63) == 0) wave_ss[m * kStageWaves + (tid >> 6) + j * (THREADS / 64)] = w;
+      }
     }
   }
   __syncthreads();
   if constexpr (RMS) {
-    float t = wave_ss[0];
 #pragma unroll
-    for (int w = 1; w < kStageWaves; ++w) t += wave_ss[w];
-    pin_here(t);
-    *total_ss = t;
+    for (int m = 0; m < MX; ++m) {
+      float t = wave_ss[m * kStageWaves];
+#pragma unroll
+      for (int w = 1; w < kStageWaves; ++w) t += wave_ss[m * kStageWaves + w];
+      pin_here(t);
+      total_ss[m] = t;
+    }
   }
+}
+
+// One activation row: stage_xs_rows with MX = 1.
+template <int VEC, bool RMS, int THREADS = 256>
+__device__ __forceinline__ void stage_xs(const float* __restrict__ x,
+                                         const float* __restrict__ gamma, long long K,
+                                         int npieces, float* xs, float* wave_ss,
+                                         float* total_ss) {
+  stage_xs_rows<VEC, RMS, THREADS, 1>(x, gamma, K, npieces, xs, 0, wave_ss, total_ss);
 }
 
 // acc[j] = sum_k rows[j][k] * xs[k]: each lane sums its elements, then
@@ -1103,10 +1128,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_multi_kernel(const W
   const int pitch = npieces * PIECE;
 
   float total_ss[MX];
-#pragma unroll
-  for (int m = 0; m < MX; ++m)
-    stage_xs<VEC, RMS, WAVES * 64>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m],
-                                   &total_ss[m]);
+  stage_xs_rows<VEC, RMS, WAVES * 64, MX>(x, gamma, K, npieces, xs, pitch, &wave_ss[0][0],
+                                          total_ss);
   float scale[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
@@ -1203,10 +1226,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_glu_multi_kernel(
   const int pitch = npieces * PIECE;
 
   float total_ss[MX];
-#pragma unroll
-  for (int m = 0; m < MX; ++m)
-    stage_xs<VEC, RMS, WAVES * 64>(x + m * K, gamma, K, npieces, xs + m * pitch, wave_ss[m],
-                                   &total_ss[m]);
+  stage_xs_rows<VEC, RMS, WAVES * 64, MX>(x, gamma, K, npieces, xs, pitch, &wave_ss[0][0],
+                                          total_ss);
   float scale[MX];
 #pragma unroll
   for (int m = 0; m < MX; ++m) scale[m] = RMS ? rms_scale(total_ss[m], K, eps) : 1.0f;
