@@ -131,13 +131,28 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(
     const T* rr = reinterpret_cast<const T*>(res + r * cols);
     T* sr = reinterpret_cast<T*>(sum + r * cols);
     T* nr = reinterpret_cast<T*>(norm + r * cols);
+    // The first PER items of x, the residual and the weight are loaded
+    // together (in-bounds indices, no branch around a load) before any is
+    // used, so a row of up to PER kThreads items costs one round trip instead
+    // of one per item; the sums run in the same order (same bits).
+    const T* wr = reinterpret_cast<const T*>(w != nullptr ? w : x);  // read, unused when null
+    T xk[PER], rk[PER], wk[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const long long i = t + static_cast<long long>(j) * kThreads;
+      const long long ic = i < items ? i : 0;
+      xk[j] = xr[ic];
+      rk[j] = rr[ic];
+      wk[j] = wr[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     T keep[PER];
     float ss = 0.0f;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const long long i = t + static_cast<long long>(j) * kThreads;
       if (i < items) {
-        const T s = xr[i] + rr[i];
+        const T s = xk[j] + rk[j];
         sr[i] = s;
         keep[j] = s;
         if constexpr (VEC) {
@@ -165,18 +180,18 @@ __global__ __launch_bounds__(kThreads) void residual_rmsnorm_kernel(
     const float total = ((red[0] + red[1]) + red[2]) + red[3];
     const float scale = gemv::rms_scale(total, cols, eps);
 
-    auto finish = [&](long long i, T s) {
+    auto finish = [&](long long i, T s, T g) {
       T v = s * scale;
-      if (w != nullptr) v *= reinterpret_cast<const T*>(w)[i];
+      if (w != nullptr) v *= g;
       nr[i] = v;
     };
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const long long i = t + static_cast<long long>(j) * kThreads;
-      if (i < items) finish(i, keep[j]);
+      if (i < items) finish(i, keep[j], wk[j]);
     }
     for (long long i = t + static_cast<long long>(PER) * kThreads; i < items; i += kThreads) {
-      finish(i, xr[i] + rr[i]);
+      finish(i, xr[i] + rr[i], wr[i]);
     }
     __syncthreads();  // red[] is reused by the next row
   }

@@ -25,9 +25,36 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restri
     const float* src = in + r * cols;
     float* dst = out + r * cols;
     float ss = 0.0f;
+    // VEC: the first kPer float4 items of the thread (and their weights) are
+    // loaded together -- in-bounds indices, no branch around a load -- and
+    // kept in registers for the second pass, so a row of up to 4 kPer kThreads
+    // columns costs one round trip instead of one per item and pass; the sum
+    // runs over the items in the same order as the plain loop (same bits).
+    constexpr int kPer = 8;
+    [[maybe_unused]] float4 keep[VEC ? kPer : 1];
+    [[maybe_unused]] float4 wk[VEC ? kPer : 1];
     if constexpr (VEC) {
       const long long n4 = cols / 4;
-      for (long long i = t; i < n4; i += kThreads) {
+      const float* wp = weight != nullptr ? weight : src;  // read and unused when null
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const long long i = t + static_cast<long long>(j) * kThreads;
+        const long long ic = i < n4 ? i : 0;
+        keep[j] = reinterpret_cast<const float4*>(src)[ic];
+        wk[j] = make_float4(wp[4 * ic], wp[4 * ic + 1], wp[4 * ic + 2], wp[4 * ic + 3]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        if (t + static_cast<long long>(j) * kThreads < n4) {
+          const float4 v = keep[j];
+          ss = fmaf(v.x, v.x, ss);
+          ss = fmaf(v.y, v.y, ss);
+          ss = fmaf(v.z, v.z, ss);
+          ss = fmaf(v.w, v.w, ss);
+        }
+      }
+      for (long long i = t + static_cast<long long>(kPer) * kThreads; i < n4; i += kThreads) {
         const float4 v = reinterpret_cast<const float4*>(src)[i];
         ss = fmaf(v.x, v.x, ss);
         ss = fmaf(v.y, v.y, ss);
@@ -45,19 +72,30 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(const float* __restri
     const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + eps);
     if constexpr (VEC) {
       const long long n4 = cols / 4;
-      for (long long i = t; i < n4; i += kThreads) {
-        float4 v = reinterpret_cast<const float4*>(src)[i];
+      auto finish = [&](long long i, float4 v, float4 g) {
         v.x *= scale;
         v.y *= scale;
         v.z *= scale;
         v.w *= scale;
         if (weight != nullptr) {
-          v.x *= weight[4 * i];
-          v.y *= weight[4 * i + 1];
-          v.z *= weight[4 * i + 2];
-          v.w *= weight[4 * i + 3];
+          v.x *= g.x;
+          v.y *= g.y;
+          v.z *= g.z;
+          v.w *= g.w;
         }
         reinterpret_cast<float4*>(dst)[i] = v;
+      };
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const long long i = t + static_cast<long long>(j) * kThreads;
+        if (i < n4) finish(i, keep[j], wk[j]);
+      }
+      for (long long i = t + static_cast<long long>(kPer) * kThreads; i < n4; i += kThreads) {
+        const float4 g = weight != nullptr
+                             ? make_float4(weight[4 * i], weight[4 * i + 1], weight[4 * i + 2],
+                                           weight[4 * i + 3])
+                             : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        finish(i, reinterpret_cast<const float4*>(src)[i], g);
       }
     } else {
       for (long long c = t; c < cols; c += kThreads) {
