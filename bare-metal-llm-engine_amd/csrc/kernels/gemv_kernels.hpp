@@ -767,6 +767,87 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_rows_lds_kernel(const WT* __r
 }
 
 
+// Persistent form of gemv_rows_lds_kernel<_Float16, 8, 1, 4, RMS, 16, NP, KT,
+// NP> for more rows than one resident round (two 16-wave workgroups per CU):
+// a grid of P workgroups stages x * gamma once each, and wave w of workgroup
+// b takes rows 16 b + w, then + 16 P, ... (a workgroup's waves read 16
+// consecutive rows, as in the staged kernel). Its row's NP pieces (all of a
+// row of K <= 4096) sit in a ring: the registers of piece p take piece p of
+// the wave's next row right after the use that frees them, so the next row
+// streams in while this one is summed -- no second round of workgroups, whose
+// staging would start late. At 11008 x 4096 with RMSNorm 15.3 us against
+// 15.8-15.9 staged (12288 rows: 16.8 against 17.1-17.2); loading the next row
+// only after summing this one ran 22.8 us, and rows w P + b per wave (16 rows
+// 4 MiB apart per workgroup) 17.0 us with the ring. Each row's sum is the
+// staged kernel's (pieces in order, then the 4-float LDS groups, then
+// elements) with the same scale: the same bits. Dynamic LDS: NP * 512 floats.
+template <int NP, int KT, bool RMS>
+__global__ __launch_bounds__(1024) void gemv_rows_persist_kernel(const _Float16* __restrict__ W,
+                                                                  const float* __restrict__ x,
+                                                                  const float* __restrict__ gamma,
+                                                                  float* __restrict__ y,
+                                                                  long long N, float eps) {
+  using V = typename RawVec<_Float16, 8>::type;
+  using F4 = typename RawVec<float, 4>::type;
+  constexpr int PIECE = 512;
+  constexpr int K = (NP - 1) * PIECE + KT;
+  constexpr int WAVES = kStageWaves;
+  static_assert(KT > 0 && KT <= PIECE && KT % 8 == 0, "K = (NP - 1) * 512 + KT");
+  static_assert(NP >= 1 && NP <= 8, "a ring of the row's pieces (K <= 4096)");
+  extern __shared__ float xs[];
+  __shared__ float wave_ss[kStageWaves];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const long long stride = static_cast<long long>(WAVES) * gridDim.x;
+  long long r = static_cast<long long>(blockIdx.x) * WAVES + wave;
+
+  float total_ss = 0.0f;
+  stage_xs<8, RMS, WAVES * 64>(x, gamma, K, NP, xs, wave_ss, &total_ss);
+  const float scale = RMS ? rms_scale(total_ss, K, eps) : 1.0f;
+  if (r >= N) return;  // no barrier follows
+
+  const int lk = lane * 8;
+  auto ok = [&](int p) { return p < NP - 1 || KT == PIECE || lk < KT; };
+  auto load = [&](const _Float16* row, int p) -> V {
+    return __builtin_nontemporal_load(
+        reinterpret_cast<const V*>(row + p * PIECE + (ok(p) ? lk : 0)));
+  };
+  auto use = [&](int p, const V& w, float& acc) {
+    const float* base = xs + p * PIECE + lane * 4;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const F4 a = *reinterpret_cast<const F4*>(base + h * 256);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc = fmaf(a[e], static_cast<float>(w[h * 4 + e]), acc);
+    }
+  };
+  V ring[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) ring[p] = load(W + r * K, p);
+  for (;;) {
+    const long long rn = r + stride;
+    float acc = 0.0f;
+    if (rn < N) {  // wave-uniform
+      const _Float16* next = W + rn * K;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        use(p, ok(p) ? ring[p] : V{}, acc);
+        ring[p] = load(next, p);
+        // the reload stays right after the use that frees its registers
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int p = 0; p < NP; ++p) use(p, ok(p) ? ring[p] : V{}, acc);
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) y[r] = RMS ? acc * scale : acc;
+    if (rn >= N) break;
+    r = rn;
+  }
+}
+
 // Output-major fp16 GEMV (no RMSNorm) for K fixed at compile time
 // (K = (NP - 1) * 512 + KT), workgroups of 16 waves, one row per wave: the
 // arithmetic of gemv_rows_lds_kernel<_Float16, 8, 1, 4, false, 16, NP, KT, CH>
