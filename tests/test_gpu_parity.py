@@ -589,6 +589,31 @@ def test_nk_fp16_kernel_selection_against_oracle(gpu, orc, N, K, rms, gamma):
         check_dot(got, y, helpers.absdot(x, Wt) + np.abs(y), K, f"gemv nk {N}x{K}")
 
 
+@pytest.mark.parametrize("N,K,gamma", [
+    (8193, 4096, True),    # one row past one resident round of 16-wave workgroups (256 CUs)
+    (9000, 2048, True),    # ring of 4 pieces; some waves with one row, some with two
+    (8200, 4096, False),   # null gain
+    (16389, 4096, True),   # three rows for a few waves, N not a multiple of 16
+])
+def test_rmsnorm_linear_nk_persistent_grid(gpu, orc, N, K, gamma):
+    """Fixed-K RMSNorm GEMV past one resident round (the persistent grid whose
+    waves stream a second and third row through their ring) against the
+    oracle, and each row equal bit for bit to the 2-row kernel's first row
+    (the staged kernels' arithmetic)."""
+    rng = np.random.default_rng(N + K)
+    W = orc.f32_to_f16(rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K))
+    Wt = np.ascontiguousarray(W.T)
+    x2 = rng.standard_normal((2, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if gamma else None
+    got = gpu_rmsnorm_linear_nk(gpu, x2[:1], g, W)
+    y = orc.rmsnorm_linear(x2[:1], g, Wt, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x2[:1], g, Wt, K, f"rmsnorm_linear nk persistent {N}x{K}")
+    two = gpu_rmsnorm_linear_nk(gpu, x2, g, W)
+    assert np.array_equal(np.asarray(got, np.float32).reshape(-1).view(np.uint32),
+                          np.asarray(two[0], np.float32).reshape(-1).view(np.uint32)), \
+        f"{N}x{K}: single-row and 2-row results differ"
+
+
 def test_gemv_nk_misaligned_x_takes_scalar_path(gpu, orc):
     rng = np.random.default_rng(21)
     N, K = 256, 2048
