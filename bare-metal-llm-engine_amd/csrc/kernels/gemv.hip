@@ -266,10 +266,12 @@ void dispatch_nk(const GemvArgs& a, hipStream_t stream) {
     // 8-wave workgroups (two per CU, the same waves): the down projection
     // 4096 x 11008 15.4 us against 16.0 (4096 x 4096 the same either way;
     // with RMSNorm, and for the fused gate / up, 8-wave workgroups measured
-    // 6% slower). With RMSNorm the register-staged kernel stays: the
-    // early-start form (gemv_rows_rms_early_kernel, which the fused gate / up
-    // uses) ran config 3 in 15.5 us on some boxes of the pool and 17.5 us on
-    // others, against 15.8-15.9 us staged on both.
+    // 6% slower). With RMSNorm x * gamma is staged from registers before the
+    // weight stream starts: the early-start form (gemv_rows_rms_early_kernel,
+    // which the fused gate / up uses) ran config 3 in 15.5 us on some boxes of
+    // the pool and 17.5 us on others, against 15.8-15.9 us staged on both;
+    // past one resident round the staged rows run on the persistent grid
+    // (gemv_rows_persist_kernel, below).
     if (fits && (RMS || a.N >= one_round / 2 || a.K > 4096)) {
       const std::size_t lds = static_cast<std::size_t>(padded) * 4;
       const bool wide = RMS || a.N >= one_round || a.K > 4096;
