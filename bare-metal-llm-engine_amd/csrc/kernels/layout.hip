@@ -7,7 +7,8 @@
 // patterns are copied, never converted, so it is exact for any value).
 //
 // One 256-thread workgroup moves 64 x 64 tiles through LDS, looping over
-// tiles in a grid sized to about eight workgroups per CU. Rows of the tile
+// tiles in a grid sized to about eight workgroups per CU, with the next
+// tile's loads in flight while the current one is written out. Rows of the tile
 // are read with 16-byte loads (8 halves or 4 floats per lane, consecutive
 // lanes along a source row) and written back with 16-byte stores along
 // destination rows; the LDS tile keeps one element per 32-bit word with a
@@ -43,48 +44,84 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const T* __restrict
   const long long tiles_c = (cols + kTile - 1) / kTile;
   const long long ntiles = ((rows + kTile - 1) / kTile) * tiles_c;
 
-  for (long long tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
-    const long long r0 = tl / tiles_c * kTile;
-    const long long c0 = tl % tiles_c * kTile;
+  if constexpr (VEC) {
+    // The next tile's loads are issued before this tile goes through LDS and
+    // out, so each thread keeps two tiles' chunks in flight instead of waiting
+    // for one round trip per tile. Addresses are clamped into the matrix so
+    // every load is unconditional (rows past the edge re-read the last row,
+    // chunks past it the last chunk: cols % E == 0); only in-range values are
+    // written to LDS.
+    constexpr int LP = kTile / RPP;  // chunk loads per thread per tile
+    auto fetch = [&](long long tl, vec_t* v) __attribute__((always_inline)) {
+      const long long r0 = tl / tiles_c * kTile;
+      const long long c0 = tl % tiles_c * kTile;
+      const long long gc = std::min(c0 + ch * E, cols - E);
 #pragma unroll
-    for (int p = 0; p < kTile / RPP; ++p) {
-      const int r = p * RPP + sub;
-      const long long gr = r0 + r;
-      const long long gc = c0 + ch * E;
-      if constexpr (VEC) {
-        if (gr < rows && gc < cols) {  // cols % E == 0: the whole chunk is inside
-          const vec_t v = *reinterpret_cast<const vec_t*>(src + gr * cols + gc);
+      for (int p = 0; p < LP; ++p) {
+        const long long gr = std::min(r0 + p * RPP + sub, rows - 1);
+        v[p] = *reinterpret_cast<const vec_t*>(src + gr * cols + gc);
+      }
+    };
+    vec_t cur[LP], nxt[LP];
+    long long tl = blockIdx.x;
+    if (tl < ntiles) fetch(tl, cur);
+    for (; tl < ntiles; tl += gridDim.x) {
+      const long long tn = tl + gridDim.x;
+      if (tn < ntiles) fetch(tn, nxt);
+      const long long r0 = tl / tiles_c * kTile;
+      const long long c0 = tl % tiles_c * kTile;
 #pragma unroll
-          for (int e = 0; e < E; ++e) tile[r][ch * E + e] = static_cast<uint32_t>(v[e]);
-        }
-      } else {
+      for (int p = 0; p < LP; ++p) {
+        const int r = p * RPP + sub;
+        if (r0 + r < rows && c0 + ch * E < cols) {
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
-          if (gr < rows && gc + e < cols) tile[r][ch * E + e] = static_cast<uint32_t>(src[gr * cols + gc + e]);
+          for (int e = 0; e < E; ++e) tile[r][ch * E + e] = static_cast<uint32_t>(cur[p][e]);
         }
       }
-    }
-    __syncthreads();
+      __syncthreads();
 #pragma unroll
-    for (int p = 0; p < kTile / RPP; ++p) {
-      const int c = p * RPP + sub;          // source column = destination row
-      const long long gdr = c0 + c;
-      const long long gdc = r0 + ch * E;    // destination column = source row
-      if constexpr (VEC) {
+      for (int p = 0; p < LP; ++p) {
+        const int c = p * RPP + sub;        // source column = destination row
+        const long long gdr = c0 + c;
+        const long long gdc = r0 + ch * E;  // destination column = source row
         if (gdr < cols && gdc < rows) {     // rows % E == 0
           vec_t v;
 #pragma unroll
           for (int e = 0; e < E; ++e) v[e] = static_cast<T>(tile[ch * E + e][c]);
           *reinterpret_cast<vec_t*>(dst + gdr * rows + gdc) = v;
         }
-      } else {
+      }
+      __syncthreads();
+#pragma unroll
+      for (int p = 0; p < LP; ++p) cur[p] = nxt[p];
+    }
+  } else {
+    for (long long tl = blockIdx.x; tl < ntiles; tl += gridDim.x) {
+      const long long r0 = tl / tiles_c * kTile;
+      const long long c0 = tl % tiles_c * kTile;
+#pragma unroll
+      for (int p = 0; p < kTile / RPP; ++p) {
+        const int r = p * RPP + sub;
+        const long long gr = r0 + r;
+        const long long gc = c0 + ch * E;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          if (gr < rows && gc + e < cols) tile[r][ch * E + e] = static_cast<uint32_t>(src[gr * cols + gc + e]);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int p = 0; p < kTile / RPP; ++p) {
+        const int c = p * RPP + sub;
+        const long long gdr = c0 + c;
+        const long long gdc = r0 + ch * E;
 #pragma unroll
         for (int e = 0; e < E; ++e) {
           if (gdr < cols && gdc + e < rows) dst[gdr * rows + gdc + e] = static_cast<T>(tile[ch * E + e][c]);
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
