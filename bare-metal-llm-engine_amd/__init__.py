@@ -78,6 +78,7 @@ SIGNATURES = {
     "eng_stream_destroy": [_p],
     "eng_stream_sync": [_p],
     "eng_stream_wait_event": [_p, _p, ctypes.c_uint],
+    "eng_stream_delay": [_p, ctypes.c_uint],
     "eng_event_create": [_pp, ctypes.c_uint],
     "eng_event_destroy": [_p],
     "eng_graph_capture_begin": [_p],

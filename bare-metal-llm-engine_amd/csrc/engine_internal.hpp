@@ -68,6 +68,11 @@ inline bool aligned_to(const void* p, std::uintptr_t bytes) {
 // K == 0 results; a fill kernel rather than hipMemsetAsync so that callers may
 // capture these launches in a HIP graph).
 void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream);
+// The same fill with the low byte of `value` (eng_memset_async).
+void fill_bytes_async(void* ptr, int value, std::size_t bytes, hipStream_t stream);
+// A one-wave kernel on `stream` that returns after `microseconds` of GPU time
+// (eng_stream_delay).
+void stream_delay_async(unsigned microseconds, hipStream_t stream);
 
 // Per-(device, stream) scratch arena for launchers whose kernels pass data to
 // a later kernel of the same call (split-K GEMV and split-KV attention

@@ -1,4 +1,4 @@
-// common.hip -- zero-fill kernel and the per-stream scratch arenas.
+// common.hip -- fill and delay kernels and the per-stream scratch arenas.
 #include "../engine_internal.hpp"
 
 #include <algorithm>
@@ -11,18 +11,28 @@
 namespace eng {
 namespace {
 
-// Grid-stride zero fill; 16-byte stores for the aligned body, bytes for the rest.
-__global__ __launch_bounds__(256) void fill_zero_kernel(unsigned char* __restrict__ p,
-                                                        std::size_t bytes) {
+// Grid-stride byte fill; 16-byte stores for the aligned body, bytes for the rest.
+__global__ __launch_bounds__(256) void fill_bytes_kernel(unsigned char* __restrict__ p,
+                                                         std::size_t bytes, unsigned value) {
   const std::size_t tid = static_cast<std::size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const std::size_t stride = static_cast<std::size_t>(gridDim.x) * blockDim.x;
   const std::size_t head = (16 - (reinterpret_cast<std::uintptr_t>(p) & 15)) & 15;
   const std::size_t pre = head < bytes ? head : bytes;
-  for (std::size_t i = tid; i < pre; i += stride) p[i] = 0;
+  const unsigned char b = static_cast<unsigned char>(value);
+  const unsigned word = b * 0x01010101u;
+  for (std::size_t i = tid; i < pre; i += stride) p[i] = b;
   uint4* body = reinterpret_cast<uint4*>(p + pre);
   const std::size_t nvec = (bytes - pre) / 16;
-  for (std::size_t i = tid; i < nvec; i += stride) body[i] = make_uint4(0, 0, 0, 0);
-  for (std::size_t i = pre + nvec * 16 + tid; i < bytes; i += stride) p[i] = 0;
+  for (std::size_t i = tid; i < nvec; i += stride) body[i] = make_uint4(word, word, word, word);
+  for (std::size_t i = pre + nvec * 16 + tid; i < bytes; i += stride) p[i] = b;
+}
+
+// One wave that sleeps until `ticks` of the constant-rate wall clock have
+// passed since it started; every lane leaves once the deadline is reached, so
+// the wait is bounded by its argument.
+__global__ __launch_bounds__(64) void stream_delay_kernel(unsigned long long ticks) {
+  const unsigned long long start = wall_clock64();
+  while (wall_clock64() - start < ticks) __builtin_amdgcn_s_sleep(127);
 }
 
 struct Key {
@@ -55,13 +65,28 @@ std::map<Key, std::unique_ptr<Arena>>& arenas() {
 
 }  // namespace
 
-void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream) {
+void fill_bytes_async(void* ptr, int value, std::size_t bytes, hipStream_t stream) {
   if (bytes == 0) return;
   const std::size_t vec = bytes / 16 + 1;
   std::size_t blocks = (vec + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  fill_zero_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(
-      static_cast<unsigned char*>(ptr), bytes);
+  fill_bytes_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(
+      static_cast<unsigned char*>(ptr), bytes, static_cast<unsigned>(value) & 0xFFu);
+  ENG_LAUNCH_CHECK();
+}
+
+void fill_zero_async(void* ptr, std::size_t bytes, hipStream_t stream) {
+  fill_bytes_async(ptr, 0, bytes, stream);
+}
+
+void stream_delay_async(unsigned microseconds, hipStream_t stream) {
+  if (microseconds == 0) return;
+  int dev = 0, khz = 0;
+  ENG_HIP_CHECK(hipGetDevice(&dev));
+  ENG_HIP_CHECK(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  ENG_CHECK(khz > 0, "eng_stream_delay: the device reports no constant clock rate");
+  const unsigned long long ticks = static_cast<unsigned long long>(khz) * microseconds / 1000ull;
+  stream_delay_kernel<<<1, 64, 0, stream>>>(ticks);
   ENG_LAUNCH_CHECK();
 }
 

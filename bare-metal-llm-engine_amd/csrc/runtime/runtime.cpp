@@ -364,7 +364,9 @@ int eng_memset_async(void* ptr, int value, std::size_t bytes, eng_stream stream)
   return guarded([&] {
     if (bytes == 0) return;
     ENG_CHECK(ptr != nullptr, "eng_memset_async: ptr is null");
-    ENG_HIP_CHECK(hipMemsetAsync(ptr, value, bytes, eng::as_stream(stream)));
+    // A fill kernel, not hipMemsetAsync: memset nodes recorded into a HIP
+    // graph have given wrong results on replays after the first.
+    eng::fill_bytes_async(ptr, value, bytes, eng::as_stream(stream));
   });
 }
 
@@ -408,6 +410,13 @@ int eng_stream_wait_event(eng_stream stream, eng_event event, unsigned int flags
   return guarded([&] {
     ENG_CHECK(event != nullptr, "eng_stream_wait_event: event is null");
     ENG_HIP_CHECK(hipStreamWaitEvent(eng::as_stream(stream), eng::as_event(event), flags));
+  });
+}
+
+int eng_stream_delay(eng_stream stream, unsigned int microseconds) {
+  return guarded([&] {
+    ENG_CHECK(microseconds <= 1000000u, "eng_stream_delay: microseconds must be at most 1000000");
+    eng::stream_delay_async(microseconds, eng::as_stream(stream));
   });
 }
 

@@ -2,28 +2,31 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--quick]
                     [--only config2,config3,fewrows,refapi,gemm,ffn,attention,stack,layout,stackfused,
-                            gemvsweep,attn32k,launch]
+                            gemvsweep,attn32k]
 
 Headline (BASELINE config 2 as written): the fp16-weight decode GEMV
 y = W . x with W [4096 x 4096] fp16 row-major (out x in), fp32 x / y, batch 1,
 through eng_gemv_f16w_nk. One step is one GEMV launch over one weight matrix;
 the steps are spread over 32 distinct 32 MiB weight buffers (1 GiB) so every
-launch reads cold weights (the MI355X Infinity Cache holds 256 MB). `value` is
-algorithmic bytes (2KN + 4K + 4N per launch) over the event-timed region, in
-GB/s. All inputs are synthetic and already resident in HBM when timing starts.
-The same GEMV through the reference-layout entry (eng_gemv_f16w, out = x . A
-with A [in x out]) is reported in "secondary".
+launch reads cold weights (the MI355X Infinity Cache holds 256 MB). The steps
+are queued behind a GPU-side hold (eng_stream_delay) and run back to back
+between two HIP events on the launch stream. `value` is algorithmic bytes
+(2KN + 4K + 4N per launch) over that region, in GB/s. All inputs are synthetic
+and already resident in HBM when timing starts. The metric's second figure,
+the FP32 GEMM at 4096^3 (config 4), is timed the same way and reported in
+"gemm_4096" (TFLOP/s and fraction of the 157.3 TFLOP/s FP32 MFMA peak).
 
-Also reported on the same JSON line (key "secondary"): the other BASELINE
-configs -- fused RMSNorm+linear at K=4096, N=11008 (config 3), the FP32 GEMMs
-(config 4), the 32-layer Llama-7B-shape decode linear stack (config 5) -- the
-reference API's fp32 / half-I/O GEMVs and warm-cache rows, each with its
-roofline fraction. Secondary rows follow the reference harness's protocol:
-warm-up, batches of back-to-back calls sized to ~1.5 ms (at most 256), 15
-batches, per-call median with p25 / p75 and IQR % (flagged "noisy" above
-10%). The CPU baseline runs the scalar C oracle (a restatement of the
-reference's src/cpu_ref, double accumulation) on one pinned core before the
-GPU is touched: config 2 for `cpu_baseline.value`, configs 1, 3, 4, 5 in
+stdout carries exactly one JSON line (a few KB): the headline, "roofline",
+"gemm_4096", "cpu_baseline", "timing" and a "summary" of the key secondary
+figures. Everything else goes to stderr, one JSON object per line: the
+secondary rows (the reference-layout GEMVs, config 3, the other config-4
+GEMMs, the config-5 32-layer decode stack, the FFN, attention and layout
+rows), then the environment block. Secondary rows follow the reference
+harness's protocol: warm-up, batches of back-to-back calls sized to ~1.5 ms
+(at most 256), 15 batches, per-call median with p25 / p75 and IQR % (flagged
+"noisy" above 10%). The CPU baseline runs the scalar C oracle (a restatement
+of the reference's src/cpu_ref, double accumulation) on one pinned core before
+the GPU is touched: config 2 for `cpu_baseline.value`, configs 1, 3, 4, 5 in
 `cpu_baseline.per_config`.
 """
 
@@ -67,6 +70,20 @@ def profiled_traffic():
         return None
     m = re.search(r"^traffic_bytes_per_launch: (\d+)\s*$", text, re.M)
     return int(m.group(1)) if m else None
+
+
+def profiled_trace_avg_us():
+    """Average duration (us) of the headline kernel in the committed
+    rocprofv3 kernel-trace summary of the bench command, or None."""
+    import re
+
+    try:
+        with open(os.path.join(REPO, TRAFFIC_PROFILE)) as f:
+            text = f.read()
+    except OSError:
+        return None
+    m = re.search(r"^trace_avg_us: ([0-9.]+)\s*$", text, re.M)
+    return float(m.group(1)) if m else None
 
 
 def load_package():
@@ -232,7 +249,14 @@ class Timer:
     """HIP-event timing on one stream, with the reference harness's clock
     handling (bench_harness.hpp:215-310): warm-up continues until the live
     engine clock reaches 75% of nominal (bounded), and the live engine and
-    memory clocks are read while each timed batch is in flight."""
+    memory clocks are read while each timed batch is in flight.
+
+    Every timed window starts behind a hold (eng_stream_delay: one wave that
+    sleeps on the GPU's constant clock) sized from the host's measured issue
+    time per launch, so all launches of the window are queued before the
+    first one starts: the window measures the GPU running them back to back,
+    not the rate at which Python issues them (which under rocprofv3 drops to
+    one launch per ~12 us). Windows whose issue outran the hold are counted."""
 
     def __init__(self, eng, pkg):
         self.eng = eng
@@ -243,6 +267,9 @@ class Timer:
         self.nominal_mhz = eng.clock_rate_khz() // 1000
         self.sm_samples = []   # every clock read of the run, for the environment block
         self.mem_samples = []
+        self.issue_us = None   # host issue time per launch (running maximum of recent windows)
+        self.windows = 0
+        self.windows_unheld = 0
 
     def _clocks(self, record: bool = True):
         sm, mem = self.eng.live_clocks_mhz()
@@ -252,15 +279,29 @@ class Timer:
             self.mem_samples.append(mem)
         return sm, mem
 
+    def hold_us(self, n: int) -> int:
+        per = self.issue_us if self.issue_us is not None else 20.0
+        return int(min(1_000_000, 100 + 1.5 * per * n))
+
     def _window(self, launch, n: int, clocks=None) -> float:
+        hold = self.hold_us(n)
+        self.eng.call("eng_stream_delay", self.stream.handle, hold)
         self.e0.record(self.stream)
+        t0 = time.perf_counter()
         for _ in range(n):
             launch(self.calls, self.stream.handle)
             self.calls += 1
+        issued_us = (time.perf_counter() - t0) * 1e6
         self.e1.record(self.stream)
         if clocks is not None:     # read while the batch runs
             clocks.append(self._clocks())
         self.e1.sync()
+        self.windows += 1
+        if issued_us > hold:
+            self.windows_unheld += 1
+        per = issued_us / max(n, 1)
+        self.issue_us = per if self.issue_us is None else max(per, 0.8 * self.issue_us)
+        self.last_hold_us, self.last_issued_us = hold, issued_us
         return self.e0.elapsed_ms(self.e1)
 
     def _warm(self, launch, min_calls: int, warmup_ms: float, max_wait_ms: float = 500.0,
@@ -272,10 +313,14 @@ class Timer:
         n = 0
         floor = floor_frac * self.nominal_mhz
         while True:
-            for _ in range(max(1, min(min_calls, 64))):
+            batch = max(1, min(min_calls, 64))
+            tb = time.perf_counter()
+            for _ in range(batch):
                 launch(self.calls, self.stream.handle)
                 self.calls += 1
                 n += 1
+            per = (time.perf_counter() - tb) * 1e6 / batch
+            self.issue_us = per if self.issue_us is None else max(per, 0.8 * self.issue_us)
             sm, _ = self._clocks(record=False)
             self.stream.sync()
             el = (time.perf_counter() - t0) * 1e3
@@ -478,7 +523,8 @@ def rows_few_rows(eng, timer) -> list:
             dxm = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
             dym = eng.empty((M, N), np.float32)
             st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
-            row = hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (few rows, MFMA), {tag}", st,
+            row = hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (few rows, fp16 MFMA, activations "
+                          f"as two fp16 terms = 22 significant bits), {tag}", st,
                           2 * K * N + 4 * M * K + 4 * K + 4 * M * N)
             row["TFLOP/s"] = round(2.0 * M * N * K / (st["median_ms"] * 1e-3) / 1e12, 2)
             rows.append(row)
@@ -489,7 +535,8 @@ def rows_few_rows(eng, timer) -> list:
             dxd = eng.upload(rng.standard_normal((M, Kd), dtype=np.float32))
             dyd = eng.empty((M, Nd), np.float32)
             st = timer.sampled(lambda i, s: f(dxd.ptr, None, Ws[i % R].ptr, dyd.ptr, M, Nd, Kd, 1e-5, s))
-            rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold (few rows, MFMA, "
+            rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold (few rows, fp16 MFMA, "
+                                "activations as two fp16 terms = 22 significant bits, "
                                 "down-projection shape), output-major W[NxK]", st,
                                 2 * Kd * Nd + 4 * M * Kd + 4 * M * Nd))
             dxd.free(), dyd.free()
@@ -767,38 +814,6 @@ def rows_gemv_sweep(eng, timer) -> list:
     return rows
 
 
-def rows_launch(eng, timer) -> list:
-    """Per-launch floors: the probe library (bare-metal-llm-engine_amd/lib/
-    liblaunch_interval.so, built with the engine) times empty kernels at several
-    grid shapes and a plain streaming read with the output-major GEMV's access
-    pattern over the config-2 / config-3 / fused-q/k/v weight sizes, back to
-    back on one stream; plus the engine's own smallest launch, a K == 0 GEMV
-    (one 256-thread zero-fill workgroup)."""
-    import ctypes
-
-    rows = []
-    path = os.path.join(REPO, "bare-metal-llm-engine_amd", "lib", "liblaunch_interval.so")
-    probe = ctypes.CDLL(path)
-    probe.launch_interval_run.argtypes = [ctypes.c_char_p, ctypes.c_size_t, ctypes.c_int]
-    probe.launch_interval_run.restype = ctypes.c_int
-    buf = ctypes.create_string_buffer(1 << 16)
-    if probe.launch_interval_run(buf, len(buf), 0 if NO_GRAPHS else 1) != 0:
-        raise RuntimeError(f"{path}: {buf.value.decode()}")
-    for ln in buf.value.decode().splitlines():
-        d = json.loads(ln)
-        row = {"name": "launch floor: " + d.pop("what"), **d}
-        if "bytes" in d:
-            row["frac_hbm_peak"] = round(d["GB/s"] / HBM_PEAK_GBS, 4)
-        rows.append(row)
-    dy = eng.empty(1, np.float32)
-    f = eng.lib.eng_gemv_f16w_nk
-    st = timer.sampled(lambda i, s: f(dy.ptr, dy.ptr, dy.ptr, 1, 0, s))
-    rows.append({"name": "launch floor: eng_gemv_f16w_nk with K = 0 (one zero-fill workgroup)",
-                 "us_per_call": round(st["median_ms"] * 1e3, 3), **_spread(st)})
-    dy.free()
-    return rows
-
-
 def rows_stack_fused(eng, timer) -> list:
     """Only the fastest config-5 arrangement (for profiling its kernels alone)."""
     return [bench_llama_stack(eng, timer, nk=True, fused_glu=True, graph=True, fused_qkv=True)]
@@ -811,14 +826,14 @@ NO_GRAPHS = False
 
 
 # Groups that repeat or sweep a row for profiling; not part of the default run.
-PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k", "launch")
+PROFILING_GROUPS = ("stackfused", "gemvsweep", "attn32k")
 
 GROUPS = {"config2": rows_config2, "config3": rows_config3, "fewrows": rows_few_rows,
           "refapi": rows_reference_api,
           "gemm": rows_gemm, "ffn": rows_ffn, "attention": rows_attention, "stack": rows_stack,
           "layout": rows_layout,
           "stackfused": rows_stack_fused, "gemvsweep": rows_gemv_sweep,
-          "attn32k": rows_attention_tinyllama_32k, "launch": rows_launch}
+          "attn32k": rows_attention_tinyllama_32k}
 
 
 def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_qkv=False) -> dict:
@@ -965,11 +980,16 @@ def main() -> int:
     # where the same kernel reads 6.77 us at the steady 2.38 GHz.
     timer._warm(head, args.warmup, 200.0, max_wait_ms=1500.0, floor_frac=HEADLINE_CLOCK_FLOOR)
     ms, head_clocks = timer.run(head, args.steps, args.warmup)
+    head_hold = {"hold_us": timer.last_hold_us, "issue_us": round(timer.last_issued_us, 1),
+                 "queued_ahead": timer.last_issued_us <= timer.last_hold_us}
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s "
-        f"{head_clocks}")
+    log(f"config 2 y=W.x, W[4096x4096] fp16 row-major, cold: {ms * 1e3:.3f} us/launch, {gbs:.1f} GB/s "
+        f"{head_clocks} {head_hold}")
     spread = None if args.quick else _spread(timer.sampled(head))
     head.free()
+
+    gemm = headline_gemm(eng, timer, args.steps, args.warmup)
+    log(f"config 4 matmul_f32 4096^3: {gemm['ms_per_call']} ms/call, {gemm['TFLOP/s']} TFLOP/s")
 
     secondary = []
     if not args.quick:
@@ -982,13 +1002,29 @@ def main() -> int:
                 log(json.dumps(r))
                 secondary.append(r)
 
+    env = environment(eng, timer)
+    log(json.dumps({"environment": env}))
+    line = result_line(steps=args.steps, warmup=args.warmup, ms=ms, nbytes=nbytes,
+                       head_clocks=head_clocks, head_hold=head_hold, spread=spread, gemm=gemm,
+                       cpu=cpu, secondary=secondary, env=env,
+                       windows=(timer.windows, timer.windows_unheld))
+    print(json.dumps(line, separators=(",", ":")), flush=True)
+    return 0
+
+
+def result_line(*, steps, warmup, ms, nbytes, head_clocks, head_hold, spread, gemm, cpu,
+                secondary, env, windows) -> dict:
+    """The one stdout JSON line: headline, roofline, the 4096^3 GEMM, the CPU
+    baseline, timing and a summary of the secondary rows (which themselves
+    go to stderr)."""
+    gbs = nbytes / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
         "value": round(gbs, 1),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -996,10 +1032,9 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded numpy; weights ~N(0,0.02^2) fp16, x ~N(0,1) fp32), resident in HBM",
         "config": {
-            "workload": ("BASELINE config 2: fp16-weight decode GEMV y=W.x, W [4096x4096] fp16 row-major "
-                         "(out x in), x/y fp32, fp32 accumulate, batch 1, seed 1, cold weights "
-                         "(32 rotating 32 MiB buffers); entry point eng_gemv_f16w_nk. The reference-"
-                         "layout entry (eng_gemv_f16w, out=x.A with A [in x out]) is in 'secondary'"),
+            "workload": ("BASELINE config 2: fp16-weight decode GEMV y=W.x, W [4096x4096] fp16 "
+                         "(out x in), x/y fp32, fp32 accumulate, batch 1, seed 1, 32 rotating 32 MiB "
+                         "weight buffers (cold); entry eng_gemv_f16w_nk"),
             "weight_dtype": "f16",
             "bytes_per_step": nbytes,
             "parallelism": "single GPU",
@@ -1011,25 +1046,56 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": profiled_traffic(),
-            "traffic_source": TRAFFIC_PROFILE + " (rocprofv3 FETCH_SIZE + WRITE_SIZE per dispatch, "
-                              "scaled by the counters of a 32 MiB device copy)",
             "kernel": HEADLINE_KERNEL,
-            "achieved_from": "algorithmic bytes per launch / event-timed average launch duration on the launch stream",
+            "event_avg_us": round(ms * 1e3, 3),
+            "trace_avg_us": profiled_trace_avg_us(),
+            "profile": TRAFFIC_PROFILE,
         },
+        "gemm_4096": gemm,
+        "cpu_baseline": cpu,
         "timing": {
-            "value_from": f"{args.steps} back-to-back launches between two HIP events, after {args.warmup} warm-up",
-            "clocks_during_window": head_clocks,
+            "value_from": (f"{steps} launches queued behind a {head_hold['hold_us']} us GPU-side "
+                           f"hold, run back to back between two HIP events on the launch stream, "
+                           f"after {warmup} warm-up"),
+            "queued_ahead": head_hold["queued_ahead"],
+            "clocks": head_clocks,
             "spread": spread,
         },
-        "cpu_baseline": cpu,
-        "environment": environment(eng, timer),
-        "secondary": secondary,
-        "host": platform.node(),
     }
-    # Last key, so the end of the line (what a log tail shows) carries the key figures.
-    line["summary"] = summary(line, secondary)
-    print(json.dumps(line), flush=True)
-    return 0
+    line["summary"] = summary(line, secondary, env, windows)
+    return line
+
+
+HEADLINE_GEMM_KERNEL = "eng::gemm_f32_mfma_dma_kernel<128, 128, false>"
+GEMM_PROFILE = os.path.join("profiles", "gemm_f32_mfma_configs1_4.md")
+
+
+def headline_gemm(eng, timer, steps: int, warmup: int) -> dict:
+    """The metric's second figure: FP32 GEMM C = A.B at M = N = K = 4096
+    (A, B ~ U[-1, 1], seed 3) through eng_matmul_f32, timed
+    like the GEMV headline: max(steps, 10) launches back to back between two HIP
+    events after a warm-up to the steady clock."""
+    M = N = K = 4096
+    r = np.random.default_rng(3)
+    dA = eng.upload(r.uniform(-1, 1, (M, K)).astype(np.float32))
+    dB = eng.upload(r.uniform(-1, 1, (K, N)).astype(np.float32))
+    dC = eng.empty((M, N), np.float32)
+    f = eng.lib.eng_matmul_f32
+
+    def launch(_i, s):
+        f(dA.ptr, dB.ptr, dC.ptr, M, N, K, s)
+
+    n = max(steps, 10)
+    timer._warm(launch, max(warmup, 4), 100.0, max_wait_ms=1000.0, floor_frac=HEADLINE_CLOCK_FLOOR)
+    ms, clocks = timer.run(launch, n, max(warmup, 2))
+    for d in (dA, dB, dC):
+        d.free()
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    return {"shape": "4096x4096x4096", "entry": "eng_matmul_f32", "ms_per_call": round(ms, 4),
+            "TFLOP/s": round(tf, 2), "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "launches": n,
+            "kernel": HEADLINE_GEMM_KERNEL, "profile": GEMM_PROFILE,
+            "sm_clock_med_mhz": clocks.get("sm_clock_med_mhz")}
 
 
 def _git_rev() -> str:
@@ -1086,7 +1152,7 @@ SUMMARY_ROWS = (
 )
 
 
-def summary(line: dict, secondary: list) -> dict:
+def summary(line: dict, secondary: list, env: dict, windows: tuple) -> dict:
     """Key figures of the run in a few hundred bytes."""
     out = {"cfg2_us": round(line["ms_per_step"] * 1e3, 3), "cfg2_frac": line["roofline"]["frac"]}
     for key, prefix, field in SUMMARY_ROWS:
@@ -1102,12 +1168,13 @@ def summary(line: dict, secondary: list) -> dict:
             out["cfg5_reference_call_sequence_ms"] = round(ref[0]["us_per_call"] / 1e3, 3)
         out["cfg5_best_ms"] = round(best["us_per_call"] / 1e3, 3)
         out["cfg5_best_frac"] = best["frac_hbm_peak"]
-    env = line.get("environment") or {}
     if env.get("live_sm_clock_mhz"):
         out["sm_clock_mhz_min_med"] = [env["live_sm_clock_mhz"]["min"], env["live_sm_clock_mhz"]["median"]]
     dips = [r["name"] for r in secondary if r.get("clock_dip")]
     if dips:
         out["clock_dip_rows"] = len(dips)
+    out["timed_windows"], out["windows_issue_outran_hold"] = windows
+    out["secondary_rows"] = len(secondary)
     return out
 
 

@@ -104,6 +104,8 @@ int eng_memcpy_d2d(void* dst, const void* src, size_t bytes);
 int eng_memcpy_h2d_async(void* dst, const void* src, size_t bytes, eng_stream stream);
 int eng_memcpy_d2h_async(void* dst, const void* src, size_t bytes, eng_stream stream);
 int eng_memset(void* ptr, int value, size_t bytes);
+/* The low byte of `value` into `bytes` bytes, ordered on `stream`. A fill
+ * kernel (not hipMemsetAsync), so it may be captured into a HIP graph. */
 int eng_memset_async(void* ptr, int value, size_t bytes, eng_stream stream);
 int eng_device_sync(void);
 /* hipGetLastError(), cleared; ENG_DEVICE_ERROR with its text if set. */
@@ -121,6 +123,14 @@ int eng_stream_create(eng_stream* stream, unsigned int flags);
 int eng_stream_destroy(eng_stream stream);
 int eng_stream_sync(eng_stream stream);
 int eng_stream_wait_event(eng_stream stream, eng_event event, unsigned int flags);
+/* Holds `stream` for `microseconds` of GPU time (at most 1,000,000): one
+ * one-wave kernel that sleeps until the device's constant-rate clock has
+ * advanced that far, then exits. A timing harness issues it before a window
+ * of launches so that every launch of the window is queued before the first
+ * one starts and the window measures the GPU's back-to-back rate, not the
+ * host's issue rate (no reference counterpart; the reference's harness times
+ * launches as the host issues them, bench/bench_harness.hpp:205-348). */
+int eng_stream_delay(eng_stream stream, unsigned int microseconds);
 int eng_event_create(eng_event* event, unsigned int flags);
 int eng_event_destroy(eng_event event);
 int eng_event_record(eng_event event, eng_stream stream);
@@ -256,7 +266,7 @@ int eng_rmsnorm_linear_f16w(const float* in, const float* rms_weight, const eng_
  * hipMalloc): no counterpart in the reference. Same arguments, kernels and
  * bits as eng_rmsnorm_linear_f16w, for M <= 16 rows (decode and small
  * batches); the split-K partial sums live in a static device buffer of
- * 4 MiB + 64 KiB per GPU, held until the process ends, instead of the stream's
+ * 8 MiB + 64 KiB per GPU, held until the process ends, instead of the stream's
  * scratch arena. Nothing is allocated. Fails with a message (status 1) for
  * M > 16 or a shape whose partial sums would exceed the buffer. Every call on
  * a GPU shares that GPU's buffer: calls that overlap on one GPU (different
