@@ -110,9 +110,13 @@ class StreamScratch {
   void* ptr_ = nullptr;
 };
 void release_stream_scratch(hipStream_t stream);
-// Moves every block of `stream`'s scratch arenas (all levels, current and
-// outgrown) into `owned` and gives each arena a fresh block of its current
-// size. The caller (a captured graph) frees the moved blocks.
+// Clears the "leased during capture" mark of `stream`'s arenas (at capture begin).
+void begin_capture_scratch(hipStream_t stream);
+// Moves the current block of each of `stream`'s arenas that a launch leased
+// while the stream was capturing into `owned`, and gives each such arena a
+// fresh block of its current size. The caller (a captured graph) frees the
+// moved blocks; it must first wait for the stream's eager work queued before
+// the capture, which may still address them.
 void adopt_stream_scratch(hipStream_t stream, std::vector<void*>& owned);
 
 }  // namespace eng

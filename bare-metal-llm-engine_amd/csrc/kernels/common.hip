@@ -52,7 +52,8 @@ struct Arena {
   std::mutex mu;  // held by the live lease
   void* base = nullptr;
   std::size_t capacity = 0;
-  std::vector<void*> retired;  // outgrown blocks, kept for graphs captured on them
+  std::vector<void*> retired;  // outgrown blocks, kept for kernels still queued on them
+  bool captured = false;       // leased while the stream was capturing
 };
 
 constexpr std::size_t kMinArena = std::size_t{1} << 20;
@@ -102,11 +103,17 @@ StreamScratch::StreamScratch(hipStream_t stream, std::size_t bytes, int level) {
     arena = slot.get();
   }
   std::unique_lock<std::mutex> lock(arena->mu);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  const hipError_t query = hipStreamIsCapturing(stream, &cap);
+  if (query != hipSuccess) {
+    (void)hipGetLastError();  // not left for the next launch check to report
+    cap = hipStreamCaptureStatusNone;
+  }
+  if (cap != hipStreamCaptureStatusNone) arena->captured = true;
   if (bytes > arena->capacity) {
     // Growing allocates, which a stream under HIP graph capture may not do:
     // the capture needs an arena already sized by the same work run eagerly.
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    ENG_HIP_CHECK(hipStreamIsCapturing(stream, &cap));
+    ENG_HIP_CHECK(query);
     ENG_CHECK(cap == hipStreamCaptureStatusNone,
               "stream scratch: this call needs a larger scratch arena than the capturing "
               "stream has; run the same work once eagerly on this stream before capturing it");
@@ -128,27 +135,41 @@ StreamScratch::~StreamScratch() {
   if (held_ != nullptr) held_->unlock();
 }
 
-void adopt_stream_scratch(hipStream_t stream, std::vector<void*>& owned) {
+namespace {
+// The arena of (current device, stream, level), or nullptr.
+Arena* find_arena(hipStream_t stream, int level) {
   int dev = 0;
   ENG_HIP_CHECK(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_arenas_mu);
+  auto& m = arenas();
+  auto it = m.find(Key{dev, stream, level});
+  return it == m.end() ? nullptr : it->second.get();
+}
+}  // namespace
+
+void begin_capture_scratch(hipStream_t stream) {
   for (int level = 0; level < kScratchLevels; ++level) {
-    Arena* arena = nullptr;
-    {
-      std::lock_guard<std::mutex> lock(g_arenas_mu);
-      auto& m = arenas();
-      auto it = m.find(Key{dev, stream, level});
-      if (it == m.end()) continue;
-      arena = it->second.get();
-    }
+    Arena* arena = find_arena(stream, level);
+    if (arena == nullptr) continue;
     std::lock_guard<std::mutex> lock(arena->mu);
-    if (arena->base == nullptr) continue;
+    arena->captured = false;
+  }
+}
+
+void adopt_stream_scratch(hipStream_t stream, std::vector<void*>& owned) {
+  for (int level = 0; level < kScratchLevels; ++level) {
+    Arena* arena = find_arena(stream, level);
+    if (arena == nullptr) continue;
+    std::lock_guard<std::mutex> lock(arena->mu);
+    if (!arena->captured || arena->base == nullptr) continue;
     // Fresh block first: if it cannot be allocated, the arena is unchanged.
+    // (Growth is refused during capture, so the captured kernels address
+    // only the current block; outgrown blocks stay with the arena.)
     void* fresh = nullptr;
     ENG_HIP_CHECK(hipMalloc(&fresh, arena->capacity));
     owned.push_back(arena->base);
-    owned.insert(owned.end(), arena->retired.begin(), arena->retired.end());
-    arena->retired.clear();
     arena->base = fresh;
+    arena->captured = false;
   }
 }
 

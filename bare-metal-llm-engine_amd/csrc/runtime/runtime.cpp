@@ -450,6 +450,7 @@ int eng_graph_capture_begin(eng_stream stream) {
   return guarded([&] {
     ENG_CHECK(stream != nullptr,
               "eng_graph_capture_begin: capture needs a created stream, not the null stream");
+    eng::begin_capture_scratch(eng::as_stream(stream));
     ENG_HIP_CHECK(hipStreamBeginCapture(eng::as_stream(stream), hipStreamCaptureModeThreadLocal));
   });
 }
@@ -471,6 +472,10 @@ int eng_graph_capture_end(eng_stream stream, eng_graph* graph) {
     h->graph = g;
     h->exec = exec;
     try {
+      // Eager launches queued on the stream before the capture may still use
+      // the blocks the graph takes over: let them finish first, so a replay
+      // on any stream right after this call cannot race them.
+      ENG_HIP_CHECK(hipStreamSynchronize(eng::as_stream(stream)));
       eng::adopt_stream_scratch(eng::as_stream(stream), h->scratch);
     } catch (...) {
       (void)hipGraphExecDestroy(exec);

@@ -2,32 +2,37 @@
 //===----------------------------------------------------------------------===//
 // engine/tensor.hpp -- Storage (owning or borrowed bytes) and Tensor (views).
 //
-// Contract of the reference (include/engine/tensor.hpp:50-195,
-// src/tensor.cpp:56-560), header-only here and HIP-backed:
-//   * Storage owns `bytes` on one device (host malloc / eng_malloc) or borrows
-//     an external pointer it never frees;
-//   * Tensor is shape + strides (in elements) + element offset + dtype over a
-//     shared Storage; reshape/permute/transpose/slice are metadata edits;
-//     contiguous/clone/to copy;
-//   * numel() of an undefined tensor is 0, of a 0-d tensor 1; an axis of size 0
-//     makes the tensor empty (and contiguous by convention);
-//   * reshape requires a contiguous tensor and allows one -1;
-//   * contiguous() of a non-contiguous GPU tensor is an error (pack on host);
-//   * ptr<T>(device) checks device and element size.
-// Device numbering matches the C-ABI: CPU = 0, HIP = 1. `Device::CUDA` names
-// the same GPU device so call sites written against the reference compile.
+// The contract is the reference's Tensor/Storage interface
+// (include/engine/tensor.hpp:50-195) as its tests pin it
+// (tests/test_tensor.cpp:70-625); the implementation here is header-only and
+// allocates device bytes through the engine's C-ABI (eng_malloc / eng_free).
+//
+//   * Storage owns `bytes` on one device or borrows a caller's pointer that it
+//     never frees; a zero-byte Storage holds no pointer.
+//   * Tensor = Layout (sizes, strides in elements, element offset) + dtype +
+//     a shared Storage. reshape / permute / transpose / slice only edit the
+//     layout and share the Storage (a view keeps it alive); contiguous /
+//     clone / to copy bytes.
+//   * numel() of an undefined tensor is 0 and of a rank-0 tensor 1; a size-0
+//     axis makes the tensor empty, and an empty tensor counts as contiguous.
+//   * reshape needs a contiguous view and infers at most one -1.
+//   * A non-contiguous GPU view cannot be packed on the device: contiguous()
+//     and to() say so and name the fix (pack on the host first).
+//   * ptr<T>(device) checks the device first, then sizeof(T) against the
+//     element size.
+// Device numbering matches the C-ABI (ENG_DEVICE_CPU = 0, ENG_DEVICE_GPU = 1);
+// Device::CUDA is another name for the GPU so reference call sites compile.
 //===----------------------------------------------------------------------===//
 
 #include <engine/check.hpp>
 #include <engine/dtype.hpp>
 #include <engine/half.hpp>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <cstring>
-#include <functional>
 #include <memory>
-#include <numeric>
 #include <ostream>
 #include <sstream>
 #include <string>
@@ -43,39 +48,39 @@ enum class Device : std::uint8_t {
 };
 
 inline const char* device_name(Device d) {
-  switch (d) {
-    case Device::CPU: return "cpu";
-    case Device::HIP: return "hip";
-    default: return "<invalid>";
-  }
+  return d == Device::CPU ? "cpu" : d == Device::HIP ? "hip" : "<invalid>";
 }
 
 inline std::ostream& operator<<(std::ostream& os, Device d) { return os << device_name(d); }
 
 struct BorrowTag {};
 
+/// A block of bytes on one device. Owning storage releases its block with the
+/// matching deallocator; borrowed storage (from_blob, mapped files) never does.
 class Storage {
  public:
+  /// Owning: host blocks are 256-byte aligned (like the device allocator's), so
+  /// vector loads over host tensors never straddle an alignment boundary.
   Storage(std::size_t bytes, Device device) : bytes_(bytes), device_(device) {
     if (bytes == 0) return;
     if (device == Device::CPU) {
-      ptr_ = std::malloc(bytes);
-      ENGINE_CHECK(ptr_ != nullptr, "host allocation failed");
+      const std::size_t rounded = (bytes + kHostAlign - 1) / kHostAlign * kHostAlign;
+      ptr_ = std::aligned_alloc(kHostAlign, rounded);
+      ENGINE_CHECK(ptr_ != nullptr, "Storage: host allocation of " + std::to_string(bytes) +
+                                        " bytes failed");
+      release_ = &release_host;
     } else {
       ENGINE_ABI_CHECK(eng_malloc(&ptr_, bytes));
+      release_ = &release_device;
     }
   }
 
+  /// Borrowing: `data` stays the caller's.
   Storage(void* data, std::size_t bytes, Device device, BorrowTag)
-      : ptr_(data), bytes_(bytes), device_(device), owns_(false) {}
+      : ptr_(data), bytes_(bytes), device_(device) {}
 
   ~Storage() {
-    if (!owns_ || ptr_ == nullptr) return;
-    if (device_ == Device::CPU) {
-      std::free(ptr_);
-    } else {
-      (void)eng_free(ptr_);
-    }
+    if (release_ != nullptr && ptr_ != nullptr) release_(ptr_);
   }
 
   Storage(const Storage&) = delete;
@@ -87,350 +92,361 @@ class Storage {
   const void* data() const { return ptr_; }
   std::size_t bytes() const { return bytes_; }
   Device device() const { return device_; }
-  bool owns() const { return owns_; }
+  bool owns() const { return release_ != nullptr; }
 
  private:
+  static constexpr std::size_t kHostAlign = 256;
+  static void release_host(void* p) { std::free(p); }
+  static void release_device(void* p) { (void)eng_free(p); }  // destructors do not throw
+
   void* ptr_ = nullptr;
   std::size_t bytes_ = 0;
   Device device_ = Device::CPU;
-  bool owns_ = true;
+  void (*release_)(void*) = nullptr;  // null: borrowed
 };
 
 class Tensor {
  public:
+  using Dims = std::vector<std::int64_t>;
+
   Tensor() = default;
 
-  Tensor(std::vector<std::int64_t> shape, DType dtype, Device device)
-      : shape_(std::move(shape)), dtype_(dtype), device_(device) {
-    for (std::size_t i = 0; i < shape_.size(); ++i) {
-      ENGINE_CHECK(shape_[i] >= 0, "Tensor: dimension " + std::to_string(i) + " is " +
-                                       std::to_string(shape_[i]) + ", must be >= 0");
-    }
-    strides_ = contiguous_strides(shape_);
-    storage_ = std::make_shared<Storage>(bytes_for(shape_, dtype_), device_);
+  /// Allocates row-major storage for `shape`; the bytes are left uninitialised.
+  Tensor(Dims shape, DType dtype, Device device) : dtype_(dtype), device_(device) {
+    require_sizes(shape, "Tensor");
+    sizes_ = std::move(shape);
+    strides_ = row_major(sizes_);
+    storage_ = std::make_shared<Storage>(storage_bytes(sizes_, dtype_), device_);
   }
 
-  static Tensor zeros(std::vector<std::int64_t> shape, DType dtype, Device device) {
+  static Tensor zeros(Dims shape, DType dtype, Device device) {
     Tensor t(std::move(shape), dtype, device);
-    const std::size_t bytes = t.nbytes();
-    if (bytes == 0) return t;
-    if (device == Device::CPU) {
-      std::memset(t.storage_->data(), 0, bytes);
-    } else {
-      ENGINE_ABI_CHECK(eng_memset(t.storage_->data(), 0, bytes));
-    }
+    fill_bytes(t, 0);
     return t;
   }
 
-  static Tensor from_blob(void* data, std::vector<std::int64_t> shape, DType dtype,
-                          Device device) {
-    ENGINE_CHECK(data != nullptr || shape.empty(),
-                 "Tensor::from_blob: null data with non-empty shape");
-    for (std::size_t i = 0; i < shape.size(); ++i) {
-      ENGINE_CHECK(shape[i] >= 0, "Tensor::from_blob: dimension " + std::to_string(i) +
-                                      " is " + std::to_string(shape[i]) + ", must be >= 0");
-    }
-    Tensor t;
-    t.storage_ = std::make_shared<Storage>(data, bytes_for(shape, dtype), device, BorrowTag{});
-    t.shape_ = std::move(shape);
-    t.strides_ = contiguous_strides(t.shape_);
-    t.dtype_ = dtype;
-    t.device_ = device;
-    return t;
+  /// A contiguous tensor over caller memory that it never frees.
+  static Tensor from_blob(void* data, Dims shape, DType dtype, Device device) {
+    require_sizes(shape, "Tensor::from_blob");
+    const std::size_t bytes = storage_bytes(shape, dtype);
+    ENGINE_CHECK(data != nullptr || bytes == 0,
+                 "Tensor::from_blob: data is null but the shape holds " + std::to_string(bytes) +
+                     " bytes");
+    auto s = std::make_shared<Storage>(data, bytes, device, BorrowTag{});
+    return Tensor(std::move(s), std::move(shape), 0, dtype);
   }
 
   /// Contiguous view of `shape` at `byte_offset` inside an existing Storage,
   /// sharing (and keeping alive) that Storage: many tensors aliasing one
   /// allocation, as a weight slab's tensors do.
-  static Tensor view(std::shared_ptr<Storage> storage, std::int64_t byte_offset,
-                     std::vector<std::int64_t> shape, DType dtype) {
+  static Tensor view(std::shared_ptr<Storage> storage, std::int64_t byte_offset, Dims shape,
+                     DType dtype) {
     ENGINE_CHECK(storage != nullptr, "Tensor::view: storage is null");
     ENGINE_CHECK(!dtype_is_sub_byte(dtype), "Tensor::view: sub-byte dtypes are not supported");
-    for (std::size_t i = 0; i < shape.size(); ++i) {
-      ENGINE_CHECK(shape[i] >= 0, "Tensor::view: dimension " + std::to_string(i) + " is " +
-                                      std::to_string(shape[i]) + ", must be >= 0");
-    }
-    const auto esz = static_cast<std::int64_t>(dtype_size(dtype));
-    ENGINE_CHECK(byte_offset >= 0 && byte_offset % esz == 0,
+    require_sizes(shape, "Tensor::view");
+    const auto elem = static_cast<std::int64_t>(dtype_size(dtype));
+    ENGINE_CHECK(byte_offset >= 0 && byte_offset % elem == 0,
                  "Tensor::view: byte offset " + std::to_string(byte_offset) +
                      " is not a non-negative multiple of the element size");
-    const std::size_t bytes = bytes_for(shape, dtype);
-    ENGINE_CHECK(static_cast<std::size_t>(byte_offset) + bytes <= storage->bytes(),
-                 "Tensor::view: " + std::to_string(bytes) + " bytes at offset " +
-                     std::to_string(byte_offset) + " overrun a storage of " +
+    const std::size_t need = static_cast<std::size_t>(byte_offset) + storage_bytes(shape, dtype);
+    ENGINE_CHECK(need <= storage->bytes(),
+                 "Tensor::view: " + std::to_string(need - static_cast<std::size_t>(byte_offset)) +
+                     " bytes at offset " + std::to_string(byte_offset) + " overrun a storage of " +
                      std::to_string(storage->bytes()) + " bytes");
-    Tensor t;
-    t.device_ = storage->device();
-    t.storage_ = std::move(storage);
-    t.shape_ = std::move(shape);
-    t.strides_ = contiguous_strides(t.shape_);
-    t.offset_ = byte_offset / esz;
-    t.dtype_ = dtype;
-    return t;
+    return Tensor(std::move(storage), std::move(shape), byte_offset / elem, dtype);
   }
 
-  // -- shape / layout ------------------------------------------------------
-  const std::vector<std::int64_t>& shape() const { return shape_; }
-  const std::vector<std::int64_t>& strides() const { return strides_; }
-  std::int64_t dim() const { return static_cast<std::int64_t>(shape_.size()); }
-
-  std::int64_t size(std::int64_t axis) const {
-    if (axis < 0) axis += dim();
-    ENGINE_CHECK(axis >= 0 && axis < dim(), "Tensor::size: axis " + std::to_string(axis) +
-                                                " out of range for tensor with dim=" +
-                                                std::to_string(dim()));
-    return shape_[static_cast<std::size_t>(axis)];
-  }
-
-  std::int64_t numel() const { return defined() ? product(shape_) : 0; }
-
-  std::size_t nbytes() const {
-    const std::int64_t n = numel();
-    return n > 0 ? dtype_storage_bytes(dtype_, static_cast<std::size_t>(n)) : 0;
-  }
-
+  // -- metadata ------------------------------------------------------------
+  const Dims& shape() const { return sizes_; }
+  const Dims& strides() const { return strides_; }
+  std::int64_t dim() const { return static_cast<std::int64_t>(sizes_.size()); }
+  std::int64_t size(std::int64_t axis) const { return sizes_[wrap_axis(axis, "size")]; }
+  std::int64_t numel() const { return defined() ? count(sizes_) : 0; }
+  std::size_t nbytes() const { return defined() ? storage_bytes(sizes_, dtype_) : 0; }
   DType dtype() const { return dtype_; }
   Device device() const { return device_; }
   bool defined() const { return storage_ != nullptr; }
+  const std::shared_ptr<Storage>& storage() const { return storage_; }
+  std::int64_t storage_offset() const { return offset_; }
 
+  /// Row-major packed: every axis longer than 1 has the stride a freshly
+  /// allocated tensor of this shape would have. Empty tensors qualify.
   bool is_contiguous() const {
-    std::int64_t expected = 1;
-    for (std::int64_t i = dim() - 1; i >= 0; --i) {
-      const auto d = static_cast<std::size_t>(i);
-      if (shape_[d] == 0) return true;
-      if (shape_[d] > 1 && strides_[d] != expected) return false;
-      expected *= shape_[d];
+    if (numel() == 0) return true;
+    const Dims packed = row_major(sizes_);
+    for (std::size_t i = 0; i < sizes_.size(); ++i) {
+      if (sizes_[i] != 1 && strides_[i] != packed[i]) return false;
     }
     return true;
   }
 
-  // -- views -------------------------------------------------------------
-  Tensor reshape(std::vector<std::int64_t> new_shape) const {
-    ENGINE_CHECK(defined(), "Tensor::reshape called on undefined tensor");
+  // -- views (layout edits, shared storage) -------------------------------
+  Tensor reshape(Dims dims) const {
+    require_defined("reshape");
     ENGINE_CHECK(is_contiguous(),
-                 "Tensor::reshape requires a contiguous tensor. "
-                 "Call .contiguous() first to pack the data.");
-    const std::int64_t n = numel();
-    std::int64_t infer = -1;
+                 "Tensor::reshape: this view is not contiguous; call .contiguous() to pack it "
+                 "into a new tensor first");
+    const auto holes = std::count(dims.begin(), dims.end(), std::int64_t{-1});
+    ENGINE_CHECK(holes <= 1, "Tensor::reshape: at most one dimension may be -1, got " +
+                                 std::to_string(holes));
     std::int64_t known = 1;
-    for (std::size_t i = 0; i < new_shape.size(); ++i) {
-      if (new_shape[i] == -1) {
-        ENGINE_CHECK(infer == -1, "Tensor::reshape: at most one dimension may be -1");
-        infer = static_cast<std::int64_t>(i);
-      } else {
-        ENGINE_CHECK(new_shape[i] >= 0,
-                     "Tensor::reshape: negative dimension " + std::to_string(new_shape[i]));
-        known *= new_shape[i];
-      }
+    for (const std::int64_t d : dims) {
+      if (d == -1) continue;
+      ENGINE_CHECK(d >= 0, "Tensor::reshape: dimension " + std::to_string(d) + " is negative");
+      known *= d;
     }
-    if (infer >= 0) {
-      ENGINE_CHECK(known > 0 && n % known == 0, "Tensor::reshape: cannot infer dimension for shape");
-      new_shape[static_cast<std::size_t>(infer)] = n / known;
+    const std::int64_t n = numel();
+    if (holes == 1) {
+      ENGINE_CHECK(known > 0 && n % known == 0,
+                   "Tensor::reshape: cannot infer the -1 dimension: " + std::to_string(n) +
+                       " elements are not a multiple of " + std::to_string(known));
+      *std::find(dims.begin(), dims.end(), std::int64_t{-1}) = n / known;
+    } else {
+      ENGINE_CHECK(known == n, "Tensor::reshape: cannot reshape " + std::to_string(n) +
+                                   " elements into a shape of " + std::to_string(known));
     }
-    const std::int64_t new_n = product(new_shape);
-    ENGINE_CHECK(new_n == n, "Tensor::reshape: cannot reshape " + std::to_string(n) +
-                                 " elements into " + std::to_string(new_n));
-    Tensor out = view_like();
-    out.shape_ = std::move(new_shape);
-    out.strides_ = contiguous_strides(out.shape_);
+    Tensor out = *this;
+    out.strides_ = row_major(dims);
+    out.sizes_ = std::move(dims);
     return out;
   }
 
-  Tensor permute(std::vector<std::int64_t> perm) const {
-    ENGINE_CHECK(defined(), "Tensor::permute called on undefined tensor");
-    ENGINE_CHECK(static_cast<std::int64_t>(perm.size()) == dim(),
-                 "Tensor::permute: perm length " + std::to_string(perm.size()) + " != dim " +
-                     std::to_string(dim()));
-    std::vector<bool> seen(shape_.size(), false);
-    Tensor out = view_like();
-    for (std::size_t i = 0; i < perm.size(); ++i) {
-      const std::int64_t p = perm[i];
-      ENGINE_CHECK(p >= 0 && p < dim(), "Tensor::permute: axis " + std::to_string(p) +
-                                            " out of range for dim=" + std::to_string(dim()));
-      ENGINE_CHECK(!seen[static_cast<std::size_t>(p)],
-                   "Tensor::permute: axis " + std::to_string(p) + " appears more than once");
-      seen[static_cast<std::size_t>(p)] = true;
-      out.shape_[i] = shape_[static_cast<std::size_t>(p)];
-      out.strides_[i] = strides_[static_cast<std::size_t>(p)];
+  Tensor permute(const Dims& order) const {
+    require_defined("permute");
+    ENGINE_CHECK(static_cast<std::int64_t>(order.size()) == dim(),
+                 "Tensor::permute: perm length " + std::to_string(order.size()) +
+                     " does not match the tensor's " + std::to_string(dim()) + " axes");
+    // A permutation of 0..dim-1 is exactly a list whose sorted copy is 0..dim-1.
+    Dims sorted = order;
+    std::sort(sorted.begin(), sorted.end());
+    for (std::size_t i = 0; i < sorted.size(); ++i) {
+      ENGINE_CHECK(sorted[i] == static_cast<std::int64_t>(i),
+                   "Tensor::permute: [" + join(order) + "] is not a permutation of the axes 0.." +
+                       std::to_string(dim() - 1) + " (an axis is out of range or appears more "
+                       "than once)");
+    }
+    Tensor out = *this;
+    for (std::size_t i = 0; i < order.size(); ++i) {
+      out.sizes_[i] = sizes_[static_cast<std::size_t>(order[i])];
+      out.strides_[i] = strides_[static_cast<std::size_t>(order[i])];
     }
     return out;
   }
 
   Tensor transpose(std::int64_t a, std::int64_t b) const {
-    if (a < 0) a += dim();
-    if (b < 0) b += dim();
-    ENGINE_CHECK(a >= 0 && a < dim(), "Tensor::transpose: axis " + std::to_string(a) +
-                                          " out of range for dim=" + std::to_string(dim()));
-    ENGINE_CHECK(b >= 0 && b < dim(), "Tensor::transpose: axis " + std::to_string(b) +
-                                          " out of range for dim=" + std::to_string(dim()));
-    std::vector<std::int64_t> perm(shape_.size());
-    std::iota(perm.begin(), perm.end(), std::int64_t{0});
-    std::swap(perm[static_cast<std::size_t>(a)], perm[static_cast<std::size_t>(b)]);
-    return permute(std::move(perm));
+    require_defined("transpose");
+    const std::size_t i = wrap_axis(a, "transpose");
+    const std::size_t j = wrap_axis(b, "transpose");
+    Tensor out = *this;
+    std::swap(out.sizes_[i], out.sizes_[j]);
+    std::swap(out.strides_[i], out.strides_[j]);
+    return out;
   }
 
+  /// Elements [start, start + length) of `axis`; strides are unchanged and the
+  /// offset accumulates, so slices of slices compose.
   Tensor slice(std::int64_t axis, std::int64_t start, std::int64_t length) const {
-    ENGINE_CHECK(defined(), "Tensor::slice called on undefined tensor");
-    if (axis < 0) axis += dim();
-    ENGINE_CHECK(axis >= 0 && axis < dim(), "Tensor::slice: axis " + std::to_string(axis) +
-                                                " out of range for dim=" + std::to_string(dim()));
-    ENGINE_CHECK(start >= 0, "Tensor::slice: start must be >= 0, got " + std::to_string(start));
-    ENGINE_CHECK(length >= 0, "Tensor::slice: length must be >= 0, got " + std::to_string(length));
-    const auto ax = static_cast<std::size_t>(axis);
-    ENGINE_CHECK(start + length <= shape_[ax],
-                 "Tensor::slice: start(" + std::to_string(start) + ") + length(" +
-                     std::to_string(length) + ") > axis size(" + std::to_string(shape_[ax]) + ")");
-    Tensor out = view_like();
-    out.shape_[ax] = length;
-    out.offset_ = offset_ + start * strides_[ax];
+    require_defined("slice");
+    const std::size_t ax = wrap_axis(axis, "slice");
+    ENGINE_CHECK(start >= 0 && length >= 0,
+                 "Tensor::slice: start (" + std::to_string(start) + ") and length (" +
+                     std::to_string(length) + ") must be >= 0");
+    ENGINE_CHECK(start + length <= sizes_[ax],
+                 "Tensor::slice: [" + std::to_string(start) + ", " +
+                     std::to_string(start + length) + ") runs past axis " + std::to_string(ax) +
+                     " of axis size " + std::to_string(sizes_[ax]));
+    Tensor out = *this;
+    out.sizes_[ax] = length;
+    out.offset_ += start * strides_[ax];
     return out;
   }
 
   // -- copies ------------------------------------------------------------
+  /// This tensor if it is already packed; otherwise a packed copy (host only).
   Tensor contiguous() const {
-    ENGINE_CHECK(defined(), "Tensor::contiguous called on undefined tensor");
+    require_defined("contiguous");
     if (is_contiguous()) return *this;
     ENGINE_CHECK(device_ == Device::CPU,
-                 "Tensor::contiguous on a non-contiguous GPU tensor is not supported. "
-                 "Make views contiguous on CPU before transferring to the GPU.");
-    Tensor out(shape_, dtype_, device_);
-    const std::int64_t n = numel();
-    if (n == 0) return out;
-    const std::size_t esz = dtype_size(dtype_);
-    const char* src = static_cast<const char*>(data());
-    char* dst = static_cast<char*>(out.data());
-    std::vector<std::int64_t> idx(shape_.size(), 0);
-    std::int64_t src_off = 0;  // element offset of idx, kept incrementally
-    for (std::int64_t flat = 0; flat < n; ++flat) {
-      std::memcpy(dst + flat * static_cast<std::int64_t>(esz),
-                  src + src_off * static_cast<std::int64_t>(esz), esz);
-      for (std::int64_t d = dim() - 1; d >= 0; --d) {
-        const auto k = static_cast<std::size_t>(d);
-        ++idx[k];
-        src_off += strides_[k];
-        if (idx[k] < shape_[k]) break;
-        src_off -= idx[k] * strides_[k];
-        idx[k] = 0;
-      }
-    }
+                 "Tensor::contiguous: a non-contiguous GPU view cannot be packed on the device; "
+                 "make the view contiguous on the CPU (Device::CPU) before moving it to the GPU");
+    Tensor out(sizes_, dtype_, device_);
+    pack_host_into(out);
     return out;
   }
 
+  /// Always a new, packed allocation on the same device.
   Tensor clone() const {
-    ENGINE_CHECK(defined(), "Tensor::clone called on undefined tensor");
-    Tensor src = contiguous();
-    Tensor out(src.shape_, src.dtype_, src.device_);
-    const std::size_t bytes = src.nbytes();
-    if (bytes == 0) return out;
-    if (src.device_ == Device::CPU) {
-      std::memcpy(out.storage_->data(), src.data(), bytes);
-    } else {
-      ENGINE_ABI_CHECK(eng_memcpy_d2d(out.storage_->data(), src.data(), bytes));
-    }
+    require_defined("clone");
+    if (!is_contiguous()) return contiguous();  // contiguous() already allocated
+    Tensor out(sizes_, dtype_, device_);
+    copy_bytes(out.data(), data(), nbytes(), device_, device_);
     return out;
   }
 
+  /// This tensor on `target`; the same tensor when it is already there.
   Tensor to(Device target) const {
-    ENGINE_CHECK(defined(), "Tensor::to called on undefined tensor");
-    if (device_ == target) return *this;
+    require_defined("to");
+    if (target == device_) return *this;
     ENGINE_CHECK(is_contiguous(),
-                 "Tensor::to requires a contiguous tensor. Call .contiguous() first to pack the data.");
-    Tensor out(shape_, dtype_, target);
-    const std::size_t bytes = nbytes();
-    if (bytes == 0) return out;
-    if (device_ == Device::CPU) {
-      ENGINE_ABI_CHECK(eng_memcpy_h2d(out.storage_->data(), data(), bytes));
-    } else {
-      ENGINE_ABI_CHECK(eng_memcpy_d2h(out.storage_->data(), data(), bytes));
-    }
+                 "Tensor::to: the view is not contiguous; call .contiguous() (on the CPU) "
+                 "before copying it to another device");
+    Tensor out(sizes_, dtype_, target);
+    copy_bytes(out.data(), data(), nbytes(), target, device_);
     return out;
   }
 
   // -- raw access --------------------------------------------------------
   void* data() {
-    ENGINE_CHECK(defined(), "Tensor::data() called on undefined tensor");
-    char* base = static_cast<char*>(storage_->data());
-    if (dtype_is_sub_byte(dtype_)) {
-      return base + static_cast<std::size_t>(offset_) * static_cast<std::size_t>(dtype_bits(dtype_)) / 8;
-    }
-    return base + offset_ * static_cast<std::int64_t>(dtype_size(dtype_));
+    require_defined("data");
+    return static_cast<char*>(storage_->data()) + offset_bytes(offset_, dtype_);
   }
   const void* data() const { return const_cast<Tensor*>(this)->data(); }
 
   template <typename T>
   T* ptr(Device expect) {
-    check_ptr(expect, sizeof(T));
+    check_access(expect, sizeof(T));
     return static_cast<T*>(data());
   }
   template <typename T>
   const T* ptr(Device expect) const {
-    check_ptr(expect, sizeof(T));
+    check_access(expect, sizeof(T));
     return static_cast<const T*>(data());
   }
 
-  const std::shared_ptr<Storage>& storage() const { return storage_; }
-  std::int64_t storage_offset() const { return offset_; }
-
   std::string to_string() const {
     if (!defined()) return "Tensor(undefined)";
-    std::ostringstream oss;
-    oss << "Tensor(shape=[" << join(shape_) << "], strides=[" << join(strides_)
-        << "], dtype=" << dtype_name(dtype_) << ", device=" << device_name(device_) << ", "
-        << (is_contiguous() ? "contiguous" : "non-contiguous") << ")";
-    return oss.str();
+    std::ostringstream os;
+    os << "Tensor(" << dtype_name(dtype_) << " on " << device_name(device_) << ", shape ["
+       << join(sizes_) << "], strides [" << join(strides_) << "], offset " << offset_ << ", "
+       << (is_contiguous() ? "contiguous" : "non-contiguous") << ")";
+    return os.str();
   }
 
  private:
-  static std::int64_t product(const std::vector<std::int64_t>& v) {
-    return std::accumulate(v.begin(), v.end(), std::int64_t{1}, std::multiplies<std::int64_t>());
+  Tensor(std::shared_ptr<Storage> storage, Dims sizes, std::int64_t offset, DType dtype)
+      : storage_(std::move(storage)), sizes_(std::move(sizes)), offset_(offset), dtype_(dtype) {
+    device_ = storage_->device();
+    strides_ = row_major(sizes_);
   }
 
-  static std::size_t bytes_for(const std::vector<std::int64_t>& shape, DType dtype) {
-    const std::int64_t n = product(shape);
+  static std::int64_t count(const Dims& sizes) {
+    std::int64_t n = 1;
+    for (const std::int64_t s : sizes) n *= s;
+    return n;
+  }
+
+  static std::size_t storage_bytes(const Dims& sizes, DType dtype) {
+    const std::int64_t n = count(sizes);
     return n > 0 ? dtype_storage_bytes(dtype, static_cast<std::size_t>(n)) : 0;
   }
 
-  static std::vector<std::int64_t> contiguous_strides(const std::vector<std::int64_t>& shape) {
-    std::vector<std::int64_t> s(shape.size());
-    std::int64_t acc = 1;
-    for (std::size_t i = shape.size(); i-- > 0;) {
-      s[i] = acc;
-      acc *= shape[i];
+  /// Byte position of element `elem` (sub-byte types pack several per byte).
+  static std::size_t offset_bytes(std::int64_t elem, DType dtype) {
+    return static_cast<std::size_t>(elem) * static_cast<std::size_t>(dtype_bits(dtype)) / 8u;
+  }
+
+  static Dims row_major(const Dims& sizes) {
+    Dims strides(sizes.size(), 1);
+    for (std::size_t i = sizes.size(); i > 1; --i) strides[i - 2] = strides[i - 1] * sizes[i - 1];
+    return strides;
+  }
+
+  static void require_sizes(const Dims& sizes, const char* who) {
+    for (std::size_t i = 0; i < sizes.size(); ++i) {
+      ENGINE_CHECK(sizes[i] >= 0, std::string(who) + ": dimension " + std::to_string(i) +
+                                      " is " + std::to_string(sizes[i]) + ", must be >= 0");
     }
+  }
+
+  static std::string join(const Dims& v) {
+    std::string s;
+    for (std::size_t i = 0; i < v.size(); ++i) s += (i ? ", " : "") + std::to_string(v[i]);
     return s;
   }
 
-  static std::string join(const std::vector<std::int64_t>& v) {
-    std::ostringstream oss;
-    for (std::size_t i = 0; i < v.size(); ++i) oss << (i ? "," : "") << v[i];
-    return oss.str();
-  }
-
-  Tensor view_like() const {
-    Tensor out;
-    out.storage_ = storage_;
-    out.shape_ = shape_;
-    out.strides_ = strides_;
-    out.offset_ = offset_;
-    out.dtype_ = dtype_;
-    out.device_ = device_;
-    return out;
-  }
-
-  void check_ptr(Device expect, std::size_t elem) const {
-    ENGINE_CHECK(device_ == expect, "Tensor::ptr: expected device " +
-                                        std::string(device_name(expect)) + " but tensor is on " +
-                                        std::string(device_name(device_)));
-    if (!dtype_is_sub_byte(dtype_)) {
-      ENGINE_CHECK(elem == dtype_size(dtype_),
-                   "Tensor::ptr: sizeof(T)=" + std::to_string(elem) +
-                       " does not match dtype element size " + std::to_string(dtype_size(dtype_)));
+  static void fill_bytes(Tensor& t, int value) {
+    const std::size_t bytes = t.nbytes();
+    if (bytes == 0) return;
+    if (t.device_ == Device::CPU) {
+      std::memset(t.data(), value, bytes);
+    } else {
+      ENGINE_ABI_CHECK(eng_memset(t.data(), value, bytes));
     }
   }
 
+  /// `bytes` from src (on `from`) to dst (on `to`), synchronously.
+  static void copy_bytes(void* dst, const void* src, std::size_t bytes, Device to, Device from) {
+    if (bytes == 0) return;
+    if (to == Device::CPU && from == Device::CPU) {
+      std::memcpy(dst, src, bytes);
+    } else if (from == Device::CPU) {
+      ENGINE_ABI_CHECK(eng_memcpy_h2d(dst, src, bytes));
+    } else if (to == Device::CPU) {
+      ENGINE_ABI_CHECK(eng_memcpy_d2h(dst, src, bytes));
+    } else {
+      ENGINE_ABI_CHECK(eng_memcpy_d2d(dst, src, bytes));
+    }
+  }
+
+  std::size_t wrap_axis(std::int64_t axis, const char* op) const {
+    const std::int64_t a = axis < 0 ? axis + dim() : axis;
+    ENGINE_CHECK(a >= 0 && a < dim(), std::string("Tensor::") + op + ": axis " +
+                                          std::to_string(axis) + " is out of range for a tensor "
+                                          "with dim=" + std::to_string(dim()));
+    return static_cast<std::size_t>(a);
+  }
+
+  void require_defined(const char* op) const {
+    ENGINE_CHECK(defined(), std::string("Tensor::") + op + " called on an undefined tensor");
+  }
+
+  void check_access(Device expect, std::size_t elem) const {
+    ENGINE_CHECK(device_ == expect, "Tensor::ptr: expected device " +
+                                        std::string(device_name(expect)) + " but tensor is on " +
+                                        std::string(device_name(device_)));
+    ENGINE_CHECK(dtype_is_sub_byte(dtype_) || elem == dtype_size(dtype_),
+                 "Tensor::ptr: sizeof(T) = " + std::to_string(elem) +
+                     " does not match the element size of " + dtype_name(dtype_));
+  }
+
+  /// Packs this (host, strided) view into `out` (host, packed, same shape):
+  /// whole rows of the innermost axis at a time, one memcpy per row when that
+  /// axis is unit-stride. Sub-byte dtypes have no addressable elements and are
+  /// refused.
+  void pack_host_into(Tensor& out) const {
+    ENGINE_CHECK(!dtype_is_sub_byte(dtype_),
+                 "Tensor::contiguous: strided sub-byte tensors cannot be packed");
+    if (numel() == 0) return;
+    const std::size_t elem = dtype_size(dtype_);
+    const char* src = static_cast<const char*>(storage_->data());
+    char* dst = static_cast<char*>(out.data());
+    copy_axis(0, offset_, src, dst, elem);
+  }
+
+  // Copies the sub-block of axes [axis, dim) whose first element is at element
+  // `at` of the storage to `dst`; returns the end of what it wrote.
+  char* copy_axis(std::size_t axis, std::int64_t at, const char* src, char* dst,
+                  std::size_t elem) const {
+    const std::int64_t n = sizes_[axis];
+    const std::int64_t step = strides_[axis];
+    if (axis + 1 == sizes_.size()) {
+      if (step == 1) {
+        const std::size_t row = static_cast<std::size_t>(n) * elem;
+        std::memcpy(dst, src + static_cast<std::size_t>(at) * elem, row);
+        return dst + row;
+      }
+      for (std::int64_t i = 0; i < n; ++i, dst += elem) {
+        std::memcpy(dst, src + static_cast<std::size_t>(at + i * step) * elem, elem);
+      }
+      return dst;
+    }
+    for (std::int64_t i = 0; i < n; ++i) dst = copy_axis(axis + 1, at + i * step, src, dst, elem);
+    return dst;
+  }
+
   std::shared_ptr<Storage> storage_;
-  std::vector<std::int64_t> shape_;
-  std::vector<std::int64_t> strides_;
+  Dims sizes_;
+  Dims strides_;
   std::int64_t offset_ = 0;  // in elements
   DType dtype_ = DType::F32;
   Device device_ = Device::CPU;

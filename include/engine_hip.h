@@ -152,8 +152,9 @@ int eng_event_elapsed_ms(float* ms, eng_event start, eng_event end);
  * message saying so; zero fills are kernels, not memsets). A failed capture
  * returns an error and leaves no graph; the stream is no longer capturing
  * either way.
- * Scratch: at capture end the graph takes over the blocks of the capture
- * stream's scratch arenas that its kernels address, and the stream continues
+ * Scratch: at capture end the call waits for the capture stream's earlier
+ * (eager) work, then the graph takes over the blocks of the capture stream's
+ * scratch arenas that launches captured in it leased, and the stream continues
  * on fresh blocks of the same sizes. A replay therefore shares no scratch with
  * eager calls on the capture stream or with any other graph, may run on any
  * stream, and stays valid after the capture stream is destroyed. Replays of

@@ -305,10 +305,147 @@ TEST(cpu_tensor, clone_from_blob_ptr_and_to_string) {
   EXPECT_EQ(c.ptr<float>(Device::CPU)[0], 1.0f);
   EXPECT_THROWS_MSG(b.ptr<double>(Device::CPU), "does not match");
   EXPECT_THROWS_MSG(b.ptr<float>(Device::HIP), "expected device");
-  EXPECT_EQ(b.to_string(), std::string("Tensor(shape=[2,3], strides=[3,1], dtype=f32, device=cpu, contiguous)"));
+  EXPECT_EQ(b.to_string(), std::string("Tensor(f32 on cpu, shape [2, 3], strides [3, 1], offset 0, contiguous)"));
+  EXPECT_EQ(b.transpose(0, 1).slice(0, 1, 2).to_string(),
+            std::string("Tensor(f32 on cpu, shape [2, 2], strides [1, 3], offset 1, non-contiguous)"));
   Tensor z = Tensor::zeros({3}, DType::F16, Device::CPU);
   EXPECT_EQ(z.ptr<engine::half>(Device::CPU)[2].u, 0u);
   EXPECT_EQ(Tensor().to_string(), std::string("Tensor(undefined)"));
+}
+
+namespace {
+void fill_ramp(Tensor& t) {
+  float* p = t.ptr<float>(Device::CPU);
+  for (std::int64_t i = 0; i < t.numel(); ++i) p[i] = static_cast<float>(i);
+}
+float at2(const Tensor& t, std::int64_t i, std::int64_t j) {
+  const float* base = static_cast<const float*>(t.data());
+  return base[i * t.strides()[0] + j * t.strides()[1]];
+}
+}  // namespace
+
+// Behaviours the reference's tensor tests pin (tests/test_tensor.cpp:287-625).
+TEST(cpu_tensor, views_share_storage_and_read_through_strides) {
+  Tensor t({2, 6}, DType::F32, Device::CPU);
+  fill_ramp(t);
+  Tensor r = t.reshape({3, 4});
+  EXPECT_TRUE(r.strides() == (std::vector<std::int64_t>{4, 1}));
+  EXPECT_EQ(at2(r, 1, 1), 5.0f);
+  r.ptr<float>(Device::CPU)[0] = 99.0f;
+  EXPECT_EQ(static_cast<const float*>(t.data())[0], 99.0f);
+  Tensor small({2, 3}, DType::F32, Device::CPU);
+  fill_ramp(small);
+  Tensor tr = small.transpose(0, 1);
+  EXPECT_TRUE(tr.strides() == (std::vector<std::int64_t>{1, 3}));
+  EXPECT_EQ(at2(tr, 0, 1), 3.0f);
+  EXPECT_EQ(at2(tr, 2, 1), 5.0f);
+  Tensor back = tr.transpose(0, 1);
+  EXPECT_TRUE(back.strides() == small.strides() && back.is_contiguous());
+  Tensor t3({2, 3, 4}, DType::F32, Device::CPU);
+  Tensor a = t3.transpose(-1, -2);
+  EXPECT_TRUE(a.shape() == (std::vector<std::int64_t>{2, 4, 3}));
+  EXPECT_TRUE(a.strides() == (std::vector<std::int64_t>{12, 1, 4}));
+  EXPECT_THROWS_MSG(t3.transpose(0, 3), "out of range");
+  Tensor p = t3.permute({2, 0, 1});
+  EXPECT_TRUE(p.strides() == (std::vector<std::int64_t>{1, 12, 4}));
+  EXPECT_TRUE(!p.is_contiguous());
+  EXPECT_TRUE(t3.permute({0, 1, 2}).is_contiguous());
+  EXPECT_THROWS_MSG(t3.permute({0, 1, 3}), "not a permutation");
+  EXPECT_THROWS_MSG(t3.permute({0, 1, 2, 0}), "perm length");
+  EXPECT_THROWS_MSG(t3.permute({0, 1}), "perm length");
+}
+
+TEST(cpu_tensor, slices_compose_and_allow_empty) {
+  Tensor t({4, 5}, DType::F32, Device::CPU);
+  fill_ramp(t);
+  Tensor rows = t.slice(0, 1, 2);
+  EXPECT_EQ(rows.storage_offset(), 5);
+  EXPECT_TRUE(rows.is_contiguous());
+  EXPECT_EQ(at2(rows, 1, 4), 14.0f);
+  Tensor cols = t.slice(1, 2, 2);
+  EXPECT_TRUE(cols.strides() == (std::vector<std::int64_t>{5, 1}));
+  EXPECT_TRUE(!cols.is_contiguous());
+  EXPECT_EQ(at2(cols, 3, 1), 18.0f);
+  EXPECT_THROWS_MSG(t.slice(0, 3, 2), "axis size");
+  EXPECT_THROWS_MSG(t.slice(0, -1, 2), ">= 0");
+  EXPECT_THROWS_MSG(t.slice(0, 0, -1), ">= 0");
+  EXPECT_THROWS_MSG(t.slice(2, 0, 1), "out of range");
+  EXPECT_NO_THROW(t.slice(-1, 0, 5));
+  Tensor sq({6, 6}, DType::F32, Device::CPU);
+  fill_ramp(sq);
+  Tensor s2 = sq.slice(0, 2, 3).slice(0, 1, 1);
+  EXPECT_EQ(s2.storage_offset(), 18);
+  EXPECT_EQ(at2(s2, 0, 0), 18.0f);
+  Tensor cache({32, 2048, 128}, DType::F32, Device::CPU);
+  Tensor empty = cache.slice(1, 0, 0);
+  EXPECT_EQ(empty.numel(), 0);
+  EXPECT_TRUE(empty.is_contiguous());
+  EXPECT_TRUE(empty.contiguous().storage() == cache.storage());
+  EXPECT_NO_THROW(empty.to_string());
+}
+
+TEST(cpu_tensor, packing_copies_in_row_major_order) {
+  Tensor t({2, 3}, DType::F32, Device::CPU);
+  fill_ramp(t);
+  Tensor c = t.transpose(0, 1).contiguous();
+  const float want[6] = {0, 3, 1, 4, 2, 5};
+  bool ok = c.storage() != t.storage() && c.is_contiguous();
+  for (int i = 0; i < 6; ++i) ok = ok && c.ptr<float>(Device::CPU)[i] == want[i];
+  EXPECT_TRUE(ok);
+  Tensor t3({2, 3, 4}, DType::F32, Device::CPU);
+  fill_ramp(t3);
+  Tensor v = t3.slice(0, 1, 1).permute({0, 2, 1});
+  Tensor c3 = v.contiguous();
+  ok = c3.is_contiguous() && c3.numel() == 12;
+  for (int j = 0; j < 4; ++j)
+    for (int k = 0; k < 3; ++k)
+      ok = ok && c3.ptr<float>(Device::CPU)[j * 3 + k] == static_cast<float>(12 + k * 4 + j);
+  EXPECT_TRUE(ok);
+  // A strided innermost axis (every other column) and a rank-0 tensor.
+  Tensor w({3, 8}, DType::F16, Device::CPU);
+  auto* wh = w.ptr<engine::half>(Device::CPU);
+  for (int i = 0; i < 24; ++i) wh[i].u = static_cast<std::uint16_t>(i);
+  Tensor odd = w.reshape({12, 2}).slice(1, 1, 1).contiguous();
+  ok = odd.numel() == 12;
+  for (int i = 0; i < 12; ++i) ok = ok && odd.ptr<engine::half>(Device::CPU)[i].u == 2 * i + 1;
+  EXPECT_TRUE(ok);
+  Tensor scalar({}, DType::F32, Device::CPU);
+  EXPECT_TRUE(scalar.is_contiguous() && scalar.contiguous().storage() == scalar.storage());
+  // clone always allocates and is independent in both directions.
+  Tensor cl = t.clone();
+  EXPECT_TRUE(cl.storage() != t.storage());
+  cl.ptr<float>(Device::CPU)[0] = -1.0f;
+  EXPECT_EQ(t.ptr<float>(Device::CPU)[0], 0.0f);
+  Tensor clt = t.transpose(0, 1).clone();
+  EXPECT_EQ(clt.ptr<float>(Device::CPU)[1], 3.0f);
+}
+
+TEST(cpu_tensor, lifetime_and_storage) {
+  Tensor view;
+  {
+    Tensor owner({10}, DType::F32, Device::CPU);
+    fill_ramp(owner);
+    view = owner.slice(0, 5, 5);
+    EXPECT_TRUE(owner.storage().use_count() >= 2);
+  }
+  EXPECT_EQ(view.storage().use_count(), 1);
+  EXPECT_EQ(view.ptr<float>(Device::CPU)[4], 9.0f);
+  std::vector<float> external(8, 3.5f);
+  {
+    Tensor b = Tensor::from_blob(external.data(), {8}, DType::F32, Device::CPU);
+    EXPECT_TRUE(b.data() == external.data());
+  }
+  EXPECT_EQ(external[7], 3.5f);
+  engine::Storage s(1000, Device::CPU);
+  EXPECT_EQ(reinterpret_cast<std::uintptr_t>(s.data()) % 256, 0u);
+  EXPECT_TRUE(s.owns());
+  engine::Storage z(0, Device::CPU);
+  EXPECT_TRUE(z.data() == nullptr);
+  EXPECT_THROWS_MSG(Tensor::from_blob(nullptr, {2}, DType::F32, Device::CPU), "null");
+  EXPECT_TRUE(Tensor::from_blob(nullptr, {0, 4}, DType::F32, Device::CPU).numel() == 0);
+  EXPECT_THROWS_MSG(Tensor().reshape({1}), "undefined");
+  Tensor h({4}, DType::F32, Device::CPU);
+  EXPECT_TRUE(h.to(Device::CPU).storage() == h.storage());
 }
 
 // ------------------------------------------------------------------ half/dtype
@@ -366,7 +503,14 @@ TEST(gpu_runtime, device_summary_and_buffer_round_trip) {
   EXPECT_TRUE(g.device() == Device::HIP);
   Tensor back = g.clone().to(Device::CPU);
   EXPECT_EQ(back.ptr<float>(Device::CPU)[19], 19.0f);
-  EXPECT_THROWS_MSG(g.transpose(0, 1).contiguous(), "not supported");
+  EXPECT_THROWS_MSG(g.transpose(0, 1).contiguous(), "cannot be packed on the device");
+  EXPECT_THROWS_MSG(g.transpose(0, 1).to(Device::CPU), "contiguous");
+  EXPECT_THROWS_MSG(g.ptr<float>(Device::CPU), "expected device");
+  Tensor gz = Tensor::zeros({3, 7}, DType::F16, Device::CUDA);
+  Tensor hz = gz.slice(0, 1, 2).to(Device::CPU);
+  bool zero = hz.numel() == 14;
+  for (int i = 0; i < 14; ++i) zero = zero && hz.ptr<engine::half>(Device::CPU)[i].u == 0;
+  EXPECT_TRUE(zero);
   // live clocks: the engine clock is positive (live, or the nominal fallback);
   // the source names what was read
   EXPECT_TRUE(engine::hip_live_sm_clock_mhz() > 0);

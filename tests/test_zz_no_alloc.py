@@ -91,3 +91,37 @@ def test_noalloc_limits_and_zero_sizes(gpu):
         gpu.call("eng_rmsnorm_linear_f16w_noalloc", x.ptr, None, W.ptr, y.ptr, M, N, K, EPS, None)
     gpu.sync()
     assert (y.download().view(np.uint32) == 0x7F7F7F7F).all(), "a zero-size call wrote output"
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 11008, 4096), (16, 2048, 1024),
+                                   (5, 1000, 776)])
+def test_noalloc_first_call_under_capture_on_a_fresh_stream(gpu, M, N, K):
+    """The first call on a new stream is made inside a HIP graph capture, where
+    a stream scratch arena cannot be grown: the capture succeeds only if the
+    entry point leases none. Every replay must equal the allocating entry's
+    eager result (computed on another stream) bit for bit."""
+    rng = np.random.default_rng(33 + M)
+    W16, g, x = _case(gpu, rng, M, N, K)
+    dW, dg, dx = gpu.upload(W16), gpu.upload(g), gpu.upload(x)
+    want = _run(gpu, "eng_rmsnorm_linear_f16w", dW, dg, dx, M, N, K, None)
+    y = gpu.empty((M, N), np.float32)
+    s = gpu.stream()
+    graph = None
+    try:
+        graph = gpu.graph(s)
+        with graph:
+            gpu.call("eng_rmsnorm_linear_f16w_noalloc", dx.ptr, dg.ptr, dW.ptr, y.ptr, M, N, K,
+                     EPS, s.handle)
+        for rep in range(3):
+            gpu.call("eng_memset", y.ptr, 0xFF, y.nbytes)
+            graph.launch()
+            s.sync()
+            got = y.download()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), \
+                f"replay {rep}: M={M} N={N} K={K} differs from eng_rmsnorm_linear_f16w"
+    finally:
+        if graph is not None:
+            graph.destroy()
+        s.destroy()
+        for d in (dW, dg, dx, y):
+            d.free()
