@@ -16,9 +16,11 @@
 // processed as a chunk (scores first, one rescale per chunk). Key-lane dot
 // products are summed with DPP; states merge exactly -- weights 2^(m_i - m)
 // -- across the key lanes of a wave by shuffles, across the 4 waves through
-// LDS, and across splits in flash_decode_reduce_kernel, always in a fixed
-// order. Splits write fp32 (o, m, l) partials to the stream's scratch arena
-// (reused in stream order: no allocation or event per call).
+// LDS, and across splits in a merge kernel, always in a fixed order. Splits
+// write fp32 (o, m, l) partials to the stream's scratch arena (reused in
+// stream order: no allocation or event per call). D = 64 GQA groups on
+// aligned caches take flash_decode_gqa_wave_kernel instead: the matrix cores,
+// K / V loaded straight into MFMA operand registers, 1 to 8 waves per split.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
@@ -26,6 +28,7 @@
 #include <cmath>
 #include <cstddef>
 #include <string>
+#include <type_traits>
 
 namespace eng {
 namespace {
@@ -686,125 +689,145 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
   }
 }
 
-// GQA groups at D = 64 on the matrix cores: the same pipeline as
-// flash_decode_gqa_dma_kernel (tiles of T = 64 keys loaded straight into LDS
-// through four stages), but wave w takes the 16 keys of a tile it owns for
-// all G <= 16 heads at once and computes
-//   scores  S^T[16 keys x 16 heads] = K_w . q^T   on v_mfma_f32_16x16x32_f16
-//           (fp16 products are exact in fp32, accumulated in fp32), and
-//   values  O^T[64 dims x 16 heads] += V_w^T . P^T on v_mfma_f32_16x16x4_f32
-//           (V converted to fp32, softmax weights in fp32),
-// with the online softmax in between held per head in registers. Lane l owns
-// head l % 16 (columns G.. are zero queries and are never written).
-// Layouts (checked on the device): A[i][k] is lane i + 16 (k / KPL) element
-// k % KPL, B[k][j] lane j + 16 (k / KPL), D[i][j] lane j + 16 (i / 4) element
-// i % 4, with KPL = 8 (16x16x32 f16) or 1 (16x16x4 f32). Accumulator row
-// rho = 4 g + s of the score block holds key sigma(rho) = 4 s + g of the
-// wave's 16, so that the p . V step s reads its B operand (p of key
-// sigma(4 g + s)) from the lane's own score registers and its A operand from
-// V row sigma(4 g + s): the four lane groups then read rows 4 s .. 4 s + 3,
-// alternating bank halves. Value block mb holds dims 4 i + mb (i = row), so a
-// lane's four blocks read four consecutive dims with one 8-byte LDS read. K
-// tiles are stored with 16-byte chunk c of row r at c ^ ((r >> 1) & 7) (chosen
-// by the load addresses), so the 16 rows one score read touches fall in 16
-// distinct bank groups.
-template <int G, int NW, bool PARTIAL>
-__global__ __launch_bounds__(64 * NW) void flash_decode_gqa_mfma_kernel(
-    const _Float16* __restrict__ q, const _Float16* __restrict__ k,
-    const _Float16* __restrict__ v, _Float16* __restrict__ out, float* __restrict__ part_o,
+// GQA decode at D = 64 for G <= 16 query heads of one KV head: NW waves (1, 2,
+// 4 or 8), each owning 32-key blocks (block b of the split goes to wave b % NW) that it
+// loads straight into the registers the matrix cores read them from -- no LDS
+// staging, no workgroup barrier until the final merge -- with P blocks in
+// flight per wave. Per block, on the matrix cores:
+//   scores  S^T[32 keys x 16 heads] = K . q^T  (two v_mfma_f32_16x16x32_f16 per
+//           16 keys; fp16 products are exact in fp32, summed in fp32),
+//   values  O^T[64 dims x 16 heads] += V^T . P^T over the 32 keys, on
+//           v_mfma_f32_16x16x32_f16 with the fp32 softmax weights split into two
+//           fp16 terms p = hi + lo (hi = fp16(p), lo = fp16(p - hi): 22
+//           significant bits, each product exact in fp32), two MFMAs per
+//           16-dim block,
+// with an online softmax in between, per head in registers, rescaled lazily:
+// weights are taken relative to a reference max m that is raised (rescaling o
+// and l) only when a block's max exceeds it by more than 2^kLazy, so weights
+// stay <= 2^kLazy (exact in fp32, and in fp16's range for the hi / lo split)
+// and the final o / l is the same ratio.
+// Lane l owns head l % 16 and lane group g = l / 16. MFMA layouts (gfx950):
+// A[i][k] is lane i + 16 (k / 8) element k % 8, B[k][j] lane j + 16 (k / 8)
+// element k % 8, D[i][j] lane j + 16 (i / 4) element i % 4. Score row
+// i = 4 g + e of half-block h is K row 16 h + g + 4 e (A row i loads K row
+// 16 h + i / 4 + 4 (i % 4)), so lane group g holds the weights of keys
+// {16 h + g + 4 e}; the value step's k index 8 g + e is key
+// 16 (e / 4) + g + 4 (e % 4) -- the lane's own weights, in order -- and its A
+// operand (V^T, row i = dim 4 i + mb of block mb) is one 8-byte load of dims
+// 4 i .. 4 i + 3 per key, the four lane groups reading four consecutive V rows
+// (512 contiguous bytes per load). A block is 128 bytes per lane: four 16-byte
+// K loads, eight 8-byte V loads. The waves' states merge through LDS in wave
+// order: the output, or an fp32 partial state per split.
+template <int G, int NW, int P, bool RING, bool PARTIAL>
+__global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
+    const _Float16* __restrict__ q, const _Float16* k, const _Float16* v,
+    _Float16* __restrict__ out, float* __restrict__ part_o,
     float* __restrict__ part_ml, long long kv_len, long long group_size,
     long long kv_head_stride, float scale, int nsplit) {
   static_assert(G >= 2 && G <= 16, "2 to 16 heads per workgroup");
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
+  static_assert(NW == 1 || NW == 2 || NW == 4 || NW == 8, "1, 2, 4 or 8 waves");
+  static_assert(P >= 1 && P <= 4, "1 to 4 blocks in flight per wave");
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
   typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   typedef float float4v __attribute__((ext_vector_type(4)));
   constexpr int D = 64;
-  constexpr int NT = 64 * NW;                // threads
-  constexpr int T = 16 * NW;                 // keys per tile, 16 per wave
-  constexpr int NST = 4;                     // pipeline stages
-  constexpr int CPH = T * D / 8 / NT;        // loads per thread per K (or V) tile
-  constexpr int CPT = 2 * CPH;
-  __shared__ __attribute__((aligned(1024))) _Float16 S0[2 * T * D], S1[2 * T * D], S2[2 * T * D],
-      S3[2 * T * D];
-  __shared__ float s_m[NW][G];
-  __shared__ float s_l[NW][G];
-  __shared__ float s_o[NW][G][D];
+  constexpr int KB = 32;                     // keys per block
+  constexpr int WS = 16 * D + 32;            // floats of one wave's state in LDS
+  __shared__ __attribute__((aligned(16))) float s_state[NW > 1 ? NW * WS : 4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15;                 // head of this lane
-  const int grp = lane >> 4;                 // lane group 0..3
+  const int col = lane & 15;
+  const int grp = lane >> 4;
   const long long hg0 = static_cast<long long>(blockIdx.x) * G;
   const long long kvh = hg0 / group_size;
   const int split = static_cast<int>(blockIdx.y);
   const long long j0 = kv_len * split / nsplit;
   const long long j1 = kv_len * (split + 1) / nsplit;
-  const int nkeys = static_cast<int>(j1 - j0);  // a split holds at most kv_len / 1 keys < 2^31
-  const int ntiles = (nkeys + T - 1) / T;
+  const int nkeys = static_cast<int>(j1 - j0);
+  const int nblocks = (nkeys + KB - 1) / KB;
+  const int nb = wave < nblocks ? (nblocks - wave + NW - 1) / NW : 0;  // this wave's blocks
   const float scale2 = scale * kLog2e;
 
-  // q^T as the B operand of the score MFMA: head col, dims 32 ks + 8 grp + j.
+  // q^T as the score B operand (head col, dims 32 ks + 8 grp + j). Columns
+  // past G repeat head G - 1 (no load is conditional): they compute its state
+  // again, vote as it does in the rescale test, and are never written.
   half8 qb[2];
+  const _Float16* qh = q + (hg0 + min(col, G - 1)) * D + 8 * grp;
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      qb[ks][j] = col < G ? q[(hg0 + col) * D + 32 * ks + 8 * grp + j] : static_cast<_Float16>(0.0f);
+    for (int j = 0; j < 8; ++j) qb[ks][j] = qh[32 * ks + j];
   }
 
-  const _Float16* kb = k + kvh * kv_head_stride;
-  const _Float16* vb = v + kvh * kv_head_stride;
-  // Load slot (4 i + wave) * 64 + lane holds row slot / 8, 16-byte chunk
-  // position slot % 8: K chunk (position ^ swizzle), V chunk (position).
-  auto fetch = [&](_Float16* st, int t) __attribute__((always_inline)) {
+  const _Float16* kb = k + kvh * kv_head_stride + j0 * D;
+  const _Float16* vb = v + kvh * kv_head_stride + j0 * D;
+  struct Block {
+    half8 k[2][2];                           // [half-block][32-dim step]
+    half4 v[8];                              // [k element]
+  };
+  // Every call issues the same 12 loads, so the compiler's waits count
+  // exactly P - 1 blocks in flight behind the one a compute needs. Rows past
+  // the split's end load its last key (in bounds; masked below), so a block
+  // past this wave's last one is the last key for every lane: one K and one
+  // V cache line, never read.
+  auto load = [&](Block& b, int t) __attribute__((always_inline)) {
+    const int key0 = (wave + NW * t) * KB;
 #pragma unroll
-    for (int i = 0; i < CPH; ++i) {
-      const int slot0 = (NW * i + wave) * 64;
-      const int slot = slot0 + lane;
-      const int r = slot >> 3;
-      const int pos = slot & 7;
-      long long j = j0 + static_cast<long long>(t) * T + r;
-      j = j < j1 ? j : j1 - 1;
-      dma16(kb + j * D + 8 * (pos ^ ((r >> 1) & 7)), st + 8 * slot0);
-      dma16(vb + j * D + 8 * pos, st + T * D + 8 * slot0);
+    for (int h = 0; h < 2; ++h) {
+      const int kk = min(key0 + 16 * h + (col >> 2) + 4 * (col & 3), nkeys - 1);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        b.k[h][s] = __builtin_nontemporal_load(
+            reinterpret_cast<const half8*>(kb + static_cast<long long>(kk) * D + 32 * s + 8 * grp));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int kk = min(key0 + 16 * (e >> 2) + grp + 4 * (e & 3), nkeys - 1);
+      b.v[e] = __builtin_nontemporal_load(
+          reinterpret_cast<const half4*>(vb + static_cast<long long>(kk) * D + 4 * col));
     }
   };
 
-  // Lazy rescaling: weights are taken relative to a reference max m that is
-  // raised (rescaling o and l) only when a tile's max exceeds it by more than
-  // 2^kLazy; the weights then stay <= 2^kLazy, exact in fp32, and the final
-  // o / l is the same ratio.
+  // max / sum over the four lane groups of a head (lanes l, l ^ 16, l ^ 32,
+  // l ^ 48): each swap leaves {x[l], x[l ^ 32]} (then ^ 16) in its two results.
+  auto group_max = [](float x) __attribute__((always_inline)) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  };
+  auto group_sum = [](float x) __attribute__((always_inline)) {
+    auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  };
+
   constexpr float kLazy = 8.0f;
   float m = kNegInf;
-  float lsum = 0.0f;                         // this lane's share of the head's sum
+  float lsum = 0.0f;
   float4v o[4];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) o[mb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-  auto compute = [&](const _Float16* st, int t) __attribute__((always_inline)) {
-    // Scores: A row i = key sigma(i) = 16 wave + 4 (i % 4) + i / 4.
-    const int arow = 16 * wave + 4 * (col & 3) + (col >> 2);
-    float4v sc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](const Block& b, int t) __attribute__((always_inline)) {
+    float4v sc[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int c = 4 * ks + grp;
-      const half8 a = *reinterpret_cast<const half8*>(st + arow * D + 8 * (c ^ ((arow >> 1) & 7)));
-      sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[ks], sc, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[h][0], qb[0], float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+      sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[h][1], qb[1], sc[h], 0, 0, 0);
     }
-    // Row 4 grp + s of the block is key 16 wave + 4 s + grp of the tile.
-    const int kbase = t * T + 16 * wave + grp;
-    float sv[4];
+    const int kbase = (wave + NW * t) * KB + grp;
+    float sv[8];
     float mx = kNegInf;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      sv[s] = kbase + 4 * s < nkeys ? sc[s] * scale2 : kNegInf;
-      mx = fmaxf(mx, sv[s]);
+    for (int e = 0; e < 8; ++e) {
+      sv[e] = kbase + 16 * (e >> 2) + 4 * (e & 3) < nkeys ? sc[e >> 2][e & 3] * scale2 : kNegInf;
+      mx = fmaxf(mx, sv[e]);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Every lane group of a head sees the same mx, so a head's lanes agree.
+    mx = group_max(mx);
     if (__any(mx > m + kLazy)) {
       const float mn = fmaxf(m, mx);
       const float alpha = merge_weight(m, mn);
@@ -813,87 +836,112 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_mfma_kernel(
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) o[mb] *= alpha;
     }
-    float p[4];
+    half8 ph, pl;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) p[s] = merge_weight(sv[s], m);
-    lsum += (p[0] + p[1]) + (p[2] + p[3]);
-    // Values: step s, k index grp = key 16 wave + 4 s + grp; dims 4 col + mb.
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int vrow = 16 * wave + 4 * s + grp;
-      const half4 h = *reinterpret_cast<const half4*>(st + T * D + vrow * D + 4 * col);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-        o[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(static_cast<float>(h[mb]), p[s], o[mb], 0, 0, 0);
+    for (int e = 0; e < 8; ++e) {
+      const float p = merge_weight(sv[e], m);
+      lsum += p;
+      ph[e] = static_cast<_Float16>(p);
+      pl[e] = static_cast<_Float16>(p - static_cast<float>(ph[e]));
     }
-  };
-  auto step = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
-    if (t + NST - 1 < ntiles) fetch(next, t + NST - 1);
-    compute(st, t);
-    const int last_issued = t + NST - 1 < ntiles - 1 ? t + NST - 1 : ntiles - 1;
-    wait_tiles_after<CPT>(last_issued - (t + 1));
-    barrier_no_fence();
-  };
-  auto steady = [&](const _Float16* st, _Float16* next, int t) __attribute__((always_inline)) {
-    fetch(next, t + NST - 1);
-    compute(st, t);
-    wait_tiles_after<CPT>(2);
-    barrier_no_fence();
-  };
-
-  fetch(S0, 0);
-  if (1 < ntiles) fetch(S1, 1);
-  if (2 < ntiles) fetch(S2, 2);
-  {
-    const int last_issued = ntiles - 1 < NST - 2 ? ntiles - 1 : NST - 2;
-    wait_tiles_after<CPT>(last_issued);
-    barrier_no_fence();
-  }
-  int t = 0;
-  for (; t + 2 * NST - 2 < ntiles; t += NST) {
-    steady(S0, S3, t);
-    steady(S1, S0, t + 1);
-    steady(S2, S1, t + 2);
-    steady(S3, S2, t + 3);
-  }
-  for (; t < ntiles; t += NST) {
-    step(S0, S3, t);
-    if (t + 1 < ntiles) step(S1, S0, t + 1);
-    if (t + 2 < ntiles) step(S2, S1, t + 2);
-    if (t + 3 < ntiles) step(S3, S2, t + 3);
-  }
-
-  // This wave's state per head: sum the four lane groups' shares of l; the
-  // value block mb row i = 4 grp + r is dim 4 i + mb.
-  float lt = lsum + __shfl_xor(lsum, 16);
-  lt += __shfl_xor(lt, 32);
-  if (col < G) {
-    if (grp == 0) {
-      s_m[wave][col] = m;
-      s_l[wave][col] = lt;
-    }
+    half8 av[4];
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s_o[wave][col][4 * (4 * grp + r) + mb] = o[mb][r];
+      for (int e = 0; e < 8; ++e) av[mb][e] = b.v[e][mb];
+    }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], ph, o[mb], 0, 0, 0);
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], pl, o[mb], 0, 0, 0);
+  };
+
+  // Ring of P blocks: block t lives in buf[t % P], every buffer named
+  // statically. Without RING the split has at most P blocks per wave (at
+  // most 256 P keys): all are loaded at once and the computes run
+  // straight-line, each waiting for exactly its own loads. With RING the
+  // wave loops over the ring (the compiler's waits at the loop head are
+  // coarser there).
+  // The loads stay here, in block order: left alone, the compiler sinks a
+  // block's loads into the branch that computes it (k and v are not declared
+  // __restrict__, so their loads do not move across the asm) and the
+  // scheduler interleaves the blocks (the sched_barrier).
+  Block buf[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    load(buf[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (!RING) {
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (i < nb) compute(buf[i], i);
+  } else {
+    for (int t = 0; t < nb; t += P) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        if (t + i < nb) compute(buf[i], t + i);
+        load(buf[i], t + i + P);
+      }
+    }
+  }
+
+  // Lane (col, grp) holds dims 16 grp + 4 r + mb of head col in o[mb][r].
+  const float lt = group_sum(lsum);
+  if constexpr (NW == 1) {
+    // One wave: its state is the workgroup's, written from registers.
+    if (col < G) {
+      const long long h = hg0 + col;
+      if constexpr (PARTIAL) {
+        const long long slot = h * nsplit + split;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *reinterpret_cast<float4v*>(part_o + slot * D + 16 * grp + 4 * r) =
+              float4v{o[0][r], o[1][r], o[2][r], o[3][r]};
+        if (grp == 0) {
+          part_ml[2 * slot] = m;
+          part_ml[2 * slot + 1] = lt;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb)  // out is only 2-byte aligned
+            out[h * D + 16 * grp + 4 * r + mb] = static_cast<_Float16>(lt > 0.0f ? o[mb][r] / lt : 0.0f);
+        }
+      }
+    }
+    return;
+  }
+  // Several waves: each state into LDS (o at [head][dim], then m and l),
+  // merged in wave order.
+  float* const ws = s_state + wave * WS;
+  if (col < G) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *reinterpret_cast<float4v*>(ws + col * D + 16 * grp + 4 * r) =
+          float4v{o[0][r], o[1][r], o[2][r], o[3][r]};
+    if (grp == 0) {
+      ws[16 * D + col] = m;
+      ws[16 * D + 16 + col] = lt;
     }
   }
   __syncthreads();
 
-  // Merge the NW waves (key slices) of each head, in wave order, and write.
-  for (int idx = tid; idx < G * D; idx += NT) {
+  for (int idx = tid; idx < G * D; idx += 64 * NW) {
     const int gh = idx / D;
     const int d = idx - gh * D;
     float mb = kNegInf;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) mb = fmaxf(mb, s_m[w][gh]);
+    for (int w = 0; w < NW; ++w) mb = fmaxf(mb, s_state[w * WS + 16 * D + gh]);
     float lb = 0.0f, ob = 0.0f;
     if (mb > kNegInf) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float wt = merge_weight(s_m[w][gh], mb);
-        lb = fmaf(s_l[w][gh], wt, lb);
-        ob = fmaf(s_o[w][gh][d], wt, ob);
+        const float wt = merge_weight(s_state[w * WS + 16 * D + gh], mb);
+        lb = fmaf(s_state[w * WS + 16 * D + 16 + gh], wt, lb);
+        ob = fmaf(s_state[w * WS + gh * D + d], wt, ob);
       }
     }
     const long long h = hg0 + gh;
@@ -1004,13 +1052,91 @@ __global__ __launch_bounds__(kReduceThreads) void flash_decode_reduce_kernel(
   }
 }
 
-// Splits when the caller passes split_kv = 0: about one workgroup per CU
-// across all head groups, at least 64 keys per split, at most 256 splits (a
-// sweep on MI355X over the reference's decode shapes -- 32/4 heads at D = 64
-// and 32/32 at D = 128, 512 to 32768 keys, cold caches -- put this choice at
-// the best split count, or within 2% of it, for every shape).
-int auto_splits(long long kv_len, long long head_blocks) {
+// Maximum over the 64 lanes of a wave, in every lane: DPP quad_perm xor-1,
+// xor-2, row_half_mirror and row_mirror leave each 16-lane row's maximum in
+// all of its lanes; the four rows are then read with v_readlane.
+__device__ __forceinline__ float wave_max(float x) {
+  const auto step = [](float a, auto ctrl) __attribute__((always_inline)) {
+    const int y = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), decltype(ctrl)::value,
+                                              0xF, 0xF, false);
+    return fmaxf(a, __builtin_bit_cast(float, y));
+  };
+  x = step(x, std::integral_constant<int, 0xB1>{});
+  x = step(x, std::integral_constant<int, 0x4E>{});
+  x = step(x, std::integral_constant<int, 0x141>{});
+  x = step(x, std::integral_constant<int, 0x140>{});
+  const int b = __builtin_bit_cast(int, x);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+// The merge for at most MAXS (8, 16, 32 or 64) splits: one wave per head, one
+// head per workgroup (a CU streams its loads at a few tens of GB/s, so the
+// heads are spread over CUs). Lane s < nsplit loads state s's (m, l); every lane
+// loads the D / 64 dims it owns of every state's o -- all loads issued before
+// the first is used, one round trip -- then w_s = 2^(m_s - max m) in lane s,
+// l = sum_s w_s l_s over the wave (gemv::wave_sum, a fixed order) and
+// o[d] = sum_s w_s o_s[d] in split order, w_s read from lane s with
+// v_readlane. No LDS and no barrier (the 1024-thread merge below pays one
+// barrier and an LDS pass; it stays for more than 64 splits).
+template <int D, int MAXS>
+__global__ __launch_bounds__(64) void flash_decode_merge_wave_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    _Float16* __restrict__ out, int nsplit) {
+  static_assert(MAXS == 8 || MAXS == 16 || MAXS == 32 || MAXS == 64, "8 to 64 splits");
+  constexpr int DPL = D / 64;                // dims per lane
+  const int lane = threadIdx.x;
+  const long long h = blockIdx.x;
+  const long long base = h * nsplit;
+  const int sl = lane < nsplit ? lane : nsplit - 1;
+  const float ms_raw = part_ml[2 * (base + sl)];
+  const float ls = part_ml[2 * (base + sl) + 1];
+  float os[MAXS][DPL];                       // states past nsplit re-read the last one
+#pragma unroll
+  for (int sp = 0; sp < MAXS; ++sp) {
+    const long long slot = base + (sp < nsplit ? sp : nsplit - 1);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) os[sp][j] = part_o[slot * D + lane + 64 * j];
+  }
+  const float ms = lane < nsplit ? ms_raw : kNegInf;
+  const float mx = wave_max(ms);
+  const float w = merge_weight(ms, mx);      // 0 past nsplit and for empty states
+  const float lw = gemv::wave_sum(w * ls);
+  float acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.0f;
+#pragma unroll
+  for (int sp = 0; sp < MAXS; ++sp) {
+    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), sp));
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[j] = fmaf(ws, os[sp][j], acc[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < DPL; ++j)
+    out[h * D + lane + 64 * j] = static_cast<_Float16>(lw > 0.0f ? acc[j] / lw : 0.0f);
+}
+
+// Splits when the caller passes split_kv = 0. For flash_decode_gqa_wave_kernel
+// (D = 64 GQA on aligned caches): up to 256 keys, one split (one 32-key block
+// per wave of an 8-wave workgroup, and no merge launch); longer, 32-key splits
+// up to 32 of them, then 512 keys per split (max(min(L / 32, 32), L / 512)),
+// at most one workgroup per CU over all head groups. A sweep on MI355X at
+// TinyLlama's 32 / 4 heads (4 head groups), cold caches, 1 to 128 splits, put
+// this at the best split count or within 1.5% of it for 128 to 32768 keys
+// (e.g. 512 keys: 16 splits, 5.15 us; 2048: 32, 6.4 us; 32768: 64, 11.3 us).
+// For the other kernels: about one workgroup per CU, at least 64 keys per
+// split, at most 256 splits (the same kind of sweep over 32 / 4 heads at
+// D = 64 and 32 / 32 at D = 128, 512 to 32768 keys).
+int auto_splits(long long kv_len, long long head_blocks, bool wave_kernel) {
   const long long cus = device_cu_count();
+  if (wave_kernel) {
+    if (kv_len <= 256) return 1;
+    const long long s = std::max(std::min(kv_len / 32, 32LL), kv_len / 512);
+    return static_cast<int>(std::max(1LL, std::min({s, std::max(1LL, cus / head_blocks), 256LL})));
+  }
   const long long wanted = (cus + head_blocks - 1) / head_blocks;
   const long long by_len = kv_len / 64;
   return static_cast<int>(std::max(1LL, std::min({wanted, by_len, 256LL})));
@@ -1026,22 +1152,46 @@ struct DecodeArgs {
   int splits;
 };
 
-// 16-byte aligned caches: the direct-to-LDS pipelined kernel for every G.
-// Otherwise one query head per workgroup (MHA, or GQA sharing switched off):
-// the register kernel with 8 key steps in flight per lane; GQA groups: the
-// register-staged LDS-tile kernel.
-// Waves per workgroup of the MFMA kernel: 8 waves (128-key tiles) stream a
-// single split 1.3x faster, but at the automatic split counts 4 waves are
-// 5% faster (the per-workgroup prologue and merge dominate short splits).
-constexpr int kMfmaWaves = 4;
+// 16-byte aligned caches: D = 64 GQA groups on flash_decode_gqa_wave_kernel
+// (matrix cores, K / V straight into registers); other shapes on the
+// direct-to-LDS pipelined kernel. Otherwise one query head per workgroup (MHA,
+// or GQA sharing switched off): the register kernel with 8 key steps in
+// flight per lane; GQA groups: the register-staged LDS-tile kernel.
+
+// flash_decode_gqa_wave_kernel's shape from the longest split's 32-key
+// blocks: up to 8 blocks, one wave per block (1, 2, 4 or 8 waves, so a
+// one-block split is one wave with no LDS merge); more, 8 waves with every
+// block in flight at once (2 or 4 per wave) or a ring of 4.
+template <int G, bool PARTIAL>
+void launch_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, hipStream_t s) {
+  const long long keys = (a.kv_len + a.splits - 1) / a.splits;
+  const long long blocks = (keys + 31) / 32;
+  auto go = [&](auto kernel, int waves) {
+    kernel<<<grid, 64 * waves, 0, s>>>(a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len,
+                                       a.group_size, a.kv_head_stride, a.scale, a.splits);
+  };
+  if (blocks <= 1) {
+    go(flash_decode_gqa_wave_kernel<G, 1, 1, false, PARTIAL>, 1);
+  } else if (blocks <= 2) {
+    go(flash_decode_gqa_wave_kernel<G, 2, 1, false, PARTIAL>, 2);
+  } else if (blocks <= 4) {
+    go(flash_decode_gqa_wave_kernel<G, 4, 1, false, PARTIAL>, 4);
+  } else if (blocks <= 8) {
+    go(flash_decode_gqa_wave_kernel<G, 8, 1, false, PARTIAL>, 8);
+  } else if (blocks <= 16) {
+    go(flash_decode_gqa_wave_kernel<G, 8, 2, false, PARTIAL>, 8);
+  } else if (blocks <= 32) {
+    go(flash_decode_gqa_wave_kernel<G, 8, 4, false, PARTIAL>, 8);
+  } else {
+    go(flash_decode_gqa_wave_kernel<G, 8, 4, true, PARTIAL>, 8);
+  }
+}
 
 template <int D, int G, bool VEC, bool PARTIAL>
 void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
   if constexpr (VEC && D == 64 && G >= 2) {
-    flash_decode_gqa_mfma_kernel<G, kMfmaWaves, PARTIAL><<<grid, 64 * kMfmaWaves, 0, s>>>(
-        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
-        a.scale, a.splits);
+    launch_wave<G, PARTIAL>(a, part_o, part_ml, grid, s);
   } else if constexpr (VEC) {
     flash_decode_gqa_dma_kernel<D, G, PARTIAL><<<grid, kThreads, 0, s>>>(
         a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
@@ -1069,8 +1219,19 @@ void run_decode(const DecodeArgs& a, hipStream_t s) {
   float* part_o = static_cast<float*>(scratch.get());
   float* part_ml = part_o + slots * D;
   launch_split<D, G, VEC, true>(a, part_o, part_ml, s);
-  flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), kReduceThreads, 0, s>>>(
-      part_o, part_ml, a.out, a.splits);
+  const unsigned heads = static_cast<unsigned>(a.n_heads);
+  if (a.splits <= 8) {
+    flash_decode_merge_wave_kernel<D, 8><<<heads, 64, 0, s>>>(part_o, part_ml, a.out, a.splits);
+  } else if (a.splits <= 16) {
+    flash_decode_merge_wave_kernel<D, 16><<<heads, 64, 0, s>>>(part_o, part_ml, a.out, a.splits);
+  } else if (a.splits <= 32) {
+    flash_decode_merge_wave_kernel<D, 32><<<heads, 64, 0, s>>>(part_o, part_ml, a.out, a.splits);
+  } else if (a.splits <= 64) {
+    flash_decode_merge_wave_kernel<D, 64><<<heads, 64, 0, s>>>(part_o, part_ml, a.out, a.splits);
+  } else {
+    flash_decode_reduce_kernel<D><<<static_cast<unsigned>(a.n_heads), kReduceThreads, 0, s>>>(
+        part_o, part_ml, a.out, a.splits);
+  }
   ENG_LAUNCH_CHECK();
 }
 
@@ -1135,9 +1296,10 @@ void attention_decode_any(const eng_half* q, const eng_half* k, const eng_half* 
   // Explicit requests are clamped to kv_len (as the reference does) and to
   // 256 (more splits only add partial states to merge); the result does not
   // depend on the split count beyond rounding.
-  const int req = split_kv == 0 ? auto_splits(kv_len, n_heads / G) : split_kv;
-  a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 256})));
   const bool vec = aligned_to(k, 16) && aligned_to(v, 16) && kv_head_stride % 8 == 0;
+  const bool wave_kernel = vec && head_dim == 64 && G >= 2;
+  const int req = split_kv == 0 ? auto_splits(kv_len, n_heads / G, wave_kernel) : split_kv;
+  a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 256})));
   if (head_dim == 64) {
     if (vec) {
       run_decode_g<64, true>(a, G, s);

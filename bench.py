@@ -256,7 +256,12 @@ class Timer:
     time per launch, so all launches of the window are queued before the
     first one starts: the window measures the GPU running them back to back,
     not the rate at which Python issues them (which under rocprofv3 drops to
-    one launch per ~12 us). Windows whose issue outran the hold are counted."""
+    one launch per ~12 us). Windows whose issue outran the hold are counted.
+    The headline window puts LEAD untimed launches between the hold and the
+    first event, so the timed launches do not include the queue's start-up
+    after the hold wave retires."""
+
+    LEAD = 2
 
     def __init__(self, eng, pkg):
         self.eng = eng
@@ -283,9 +288,15 @@ class Timer:
         per = self.issue_us if self.issue_us is not None else 20.0
         return int(min(1_000_000, 100 + 1.5 * per * n))
 
-    def _window(self, launch, n: int, clocks=None) -> float:
-        hold = self.hold_us(n)
+    def _window(self, launch, n: int, clocks=None, lead: int = 0) -> float:
+        """Queue a GPU-side hold, then `lead` untimed launches, then the `n`
+        timed ones between two events; all are issued before the hold ends, so
+        the timed launches run back-to-back on an already busy queue."""
+        hold = self.hold_us(n + lead)
         self.eng.call("eng_stream_delay", self.stream.handle, hold)
+        for _ in range(lead):
+            launch(self.calls, self.stream.handle)
+            self.calls += 1
         self.e0.record(self.stream)
         t0 = time.perf_counter()
         for _ in range(n):
@@ -349,7 +360,7 @@ class Timer:
         self.stream.sync()
         self.eng.sync()
         clocks = []
-        ms = self._window(launch, steps, clocks) / steps
+        ms = self._window(launch, steps, clocks, lead=self.LEAD) / steps
         self.eng.sync()
         return ms, self.clock_stats(clocks)
 
@@ -1055,8 +1066,8 @@ def result_line(*, steps, warmup, ms, nbytes, head_clocks, head_hold, spread, ge
         "cpu_baseline": cpu,
         "timing": {
             "value_from": (f"{steps} launches queued behind a {head_hold['hold_us']} us GPU-side "
-                           f"hold, run back to back between two HIP events on the launch stream, "
-                           f"after {warmup} warm-up"),
+                           f"hold and {Timer.LEAD} untimed ones, run back to back between two HIP "
+                           f"events on the launch stream, after {warmup} warm-up"),
             "queued_ahead": head_hold["queued_ahead"],
             "clocks": head_clocks,
             "spread": spread,

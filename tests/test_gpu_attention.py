@@ -206,6 +206,9 @@ def test_attention_decode_repeated_calls_and_streams(gpu, orc):
     (12, 3, 128, 1000, 0),    # GQA 4, ragged
     (10, 5, 64, 777, 3),      # GQA 2
     (6, 6, 64, 300, 0),       # short sequence: one split
+    (8, 2, 64, 96, 3),        # one 32-key block per split: one-wave splits
+    (32, 4, 64, 4096, 100),   # more than 64 splits: the 1024-thread merge
+    (16, 2, 64, 6000, 200),   # ragged splits of 30 keys, 200 states per head
 ])
 def test_attention_decode_shapes_against_oracle(gpu, orc, H, Hkv, D, L, split):
     rng = np.random.default_rng(H * 1000 + L)
