@@ -703,9 +703,9 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
 //           16-dim block,
 // with an online softmax in between, per head in registers, rescaled lazily:
 // weights are taken relative to a reference max m that is raised (rescaling o
-// and l) only when a block's max exceeds it by more than 2^kLazy, so weights
-// stay <= 2^kLazy (exact in fp32, and in fp16's range for the hi / lo split)
-// and the final o / l is the same ratio.
+// and l) only when a block's max exceeds it by more than kLazy (in log2), so
+// weights stay <= 2^kLazy before the fixed 2^kWeightShift scale that keeps
+// the hi / lo split in fp16's normal range; the final o / l is the same ratio.
 // Lane l owns head l % 16 and lane group g = l / 16. MFMA layouts (gfx950):
 // A[i][k] is lane i + 16 (k / 8) element k % 8, B[k][j] lane j + 16 (k / 8)
 // element k % 8, D[i][j] lane j + 16 (i / 4) element i % 4. Score row
@@ -806,6 +806,12 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   };
 
   constexpr float kLazy = 8.0f;
+  // Weights are 2^(s - m + kWeightShift): at most 2^15 (fp16 holds it), and
+  // the fp16 lo term stays normal for weights down to 2^-10 of the max's
+  // scale, so those carry 22 significant bits; smaller ones err by at most
+  // 2^-32 (unscaled). l and o carry the same factor, so o / l and the merge of
+  // split states (all from this kernel) are unchanged.
+  constexpr float kWeightShift = 7.0f;
   float m = kNegInf;
   float lsum = 0.0f;
   float4v o[4];
@@ -839,7 +845,7 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
     half8 ph, pl;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float p = merge_weight(sv[e], m);
+      const float p = merge_weight(sv[e], m - kWeightShift);
       lsum += p;
       ph[e] = static_cast<_Float16>(p);
       pl[e] = static_cast<_Float16>(p - static_cast<float>(ph[e]));

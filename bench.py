@@ -1160,6 +1160,10 @@ SUMMARY_ROWS = (
     ("cfg4_gemm_512x4096x11008_tflops", "matmul_f32 512x4096x11008 (config 4)", "TFLOP/s"),
     ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
     ("gemv_fp16_halfio_4096_us", "gemv_fp16 (half x/out) 4096x4096 cold", "us_per_call"),
+    ("attn_tinyllama_512_us", "attention_decode TinyLlama L=512 H=32/4 D=64 cold, auto splits", "us_per_call"),
+    ("attn_tinyllama_2048_us", "attention_decode TinyLlama L=2048 H=32/4 D=64 cold, auto splits", "us_per_call"),
+    ("attn_tinyllama_32768_us", "attention_decode TinyLlama L=32768 H=32/4 D=64 cold, auto splits", "us_per_call"),
+    ("attn_llama7b_8192_us", "attention_decode Llama-2-7B L=8192 H=32/32 D=128 cold, auto splits", "us_per_call"),
 )
 
 

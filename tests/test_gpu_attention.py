@@ -11,9 +11,12 @@ Two tolerances are checked everywhere:
   hardware exp2 rounding once each (<= 4 u max_j |s_j| + 8 u relative), so the
   weights carry at most 2 max_j e_j + 4 u max_j |s_j| + 8 u relative error;
   the fp32 sums of p_j v_j and p_j add (s_kv + 24) u relative to
-  sum_j w_j |v_j|; the output adds half rounding 2^-11 |y| + 2^-25:
-      |got - y| <= 2^-11 |y| + 2^-25
-                   + (2 max e + 4 u max |s| + (s_kv + 32) u) (sum_j w_j |v_j| / sum_j w_j + |y|).
+  sum_j w_j |v_j|; the matrix-core kernel (D = 64 GQA) multiplies V by each
+  weight as two fp16 terms (hi + lo, scaled by 2^7), which adds 4 u relative
+  and at most 2^-32 absolute per weight (the max key's weight is >= 1, so
+  s_kv 2^-32 max_j |v_j| in all); the output adds half rounding 2^-11 |y| + 2^-25:
+      |got - y| <= 2^-11 |y| + 2^-25 + s_kv 2^-32 max_j |v_j|
+                   + (2 max e + 4 u max |s| + (s_kv + 36) u) (sum_j w_j |v_j| / sum_j w_j + |y|).
 Long sequences (8K / 32K keys) also use the reference's output-scaled
 tolerance (test_kernels.cu:2565-2640): rtol = 2^-9, atol = rtol * rms(out).
 """
@@ -46,8 +49,9 @@ def decode64(q, k, v, H, Hkv, D, L, stride, scale):
         y[h] = (w @ vh) / w.sum()
         e = (D + 1) * U * scale * (np.abs(kh) @ np.abs(q64[h]))
         mag = (w @ np.abs(vh)) / w.sum() + np.abs(y[h])
-        rel = 2 * e.max() + 4 * U * np.abs(s).max() + (L + 32) * U
-        bound[h] = helpers.U16 * np.abs(y[h]) + 2.0**-25 + rel * mag
+        rel = 2 * e.max() + 4 * U * np.abs(s).max() + (L + 36) * U
+        bound[h] = (helpers.U16 * np.abs(y[h]) + 2.0**-25 + L * 2.0**-32 * np.abs(vh).max()
+                    + rel * mag)
     return y, bound
 
 
@@ -326,6 +330,35 @@ def adversarial_case(name, D, L, Hq=8, Hkv=2):
     v = (((j_ * 17 + d_ * 5 + g_ * 11 + 3) % 31) - 15).astype(np.float32) * 0.0625
     f16 = lambda a: a.astype(np.float16).view(np.uint16)
     return f16(q), f16(k), f16(v)
+
+
+@pytest.mark.parametrize("split", [1, 4])
+def test_attention_decode_many_small_weights(gpu, orc, split):
+    """One dominant key (score 10, V row 0) and 2047 keys at score -2.0254
+    (weight ~e^-12 ~ 2^-17.3 each, V = 1): every small weight rounds the same
+    way, so their errors add up coherently. The matrix-core kernel multiplies
+    V by each weight as fp16 hi + lo; taken unscaled, weights this small fall
+    below fp16's normal range, and this score puts the weight near the middle
+    of a subnormal step (2^-25 absolute each: 6.0e-5 in the output, against a
+    derived bound of about 1.2e-5); scaled by 2^7 they err by 2^-32 each
+    (2e-7 in the output)."""
+    H, Hkv, D, L = 32, 4, 64, 2048
+    q = np.zeros((H, D), np.float32)
+    q[:, :4] = 2.0                                   # score = k value on dims 0..3 (scale 1/8)
+    k = np.zeros((Hkv, L, D), np.float32)
+    k[:, 0, :4] = 10.0
+    kval = float(np.float16(-2.025))
+    k[:, 1:, :4] = kval
+    v = np.ones((Hkv, L, D), np.float32)
+    v[:, 0, :] = 0.0
+    f16 = lambda a: a.astype(np.float16).view(np.uint16)
+    q, k, v = f16(q), f16(k), f16(v)
+    sc = 1.0 / np.sqrt(D)
+    got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split)
+    check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"small weights split={split}")
+    w = (L - 1) * np.exp(kval - 10.0)
+    helpers.assert_within(helpers.as_f64(got), np.full((H, D), w / (1 + w)), 2.0**-11 * w,
+                          "small weights closed form")
 
 
 @pytest.mark.parametrize("name", ["neg_30_100", "mixed_30", "all_equal", "dominant"])
