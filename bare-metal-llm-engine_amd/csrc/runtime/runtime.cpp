@@ -333,6 +333,9 @@ int eng_memcpy_d2d(void* dst, const void* src, std::size_t bytes) {
     if (bytes == 0) return;
     ENG_CHECK(dst != nullptr && src != nullptr, "eng_memcpy_d2d: null pointer");
     ENG_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice));
+    // A device-to-device hipMemcpy may return before the copy has run, and
+    // work on a non-blocking stream does not wait for it: finish it here.
+    ENG_HIP_CHECK(hipStreamSynchronize(nullptr));
   });
 }
 
@@ -357,6 +360,9 @@ int eng_memset(void* ptr, int value, std::size_t bytes) {
     if (bytes == 0) return;
     ENG_CHECK(ptr != nullptr, "eng_memset: ptr is null");
     ENG_HIP_CHECK(hipMemset(ptr, value, bytes));
+    // hipMemset of device memory may return before the fill has run, and
+    // work on a non-blocking stream does not wait for it: finish it here.
+    ENG_HIP_CHECK(hipStreamSynchronize(nullptr));
   });
 }
 

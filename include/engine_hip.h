@@ -98,6 +98,9 @@ int eng_device_cu_count(int* cus);
  * ---------------------------------------------------------------------- */
 int eng_malloc(void** ptr, size_t bytes);
 int eng_free(void* ptr);
+/* The blocking calls (eng_memcpy_h2d / _d2h / _d2d, eng_memset) have finished
+ * on the device when they return, so work queued afterwards on any stream,
+ * non-blocking ones included, sees their bytes. */
 int eng_memcpy_h2d(void* dst, const void* src, size_t bytes);
 int eng_memcpy_d2h(void* dst, const void* src, size_t bytes);
 int eng_memcpy_d2d(void* dst, const void* src, size_t bytes);
