@@ -964,6 +964,217 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   }
 }
 
+// One query head per KV head (MHA, or GQA sharing switched off) at D = 64 or
+// 128 on aligned caches: the wave layout of flash_decode_gqa_wave_kernel --
+// NW waves (1, 2, 4 or 8), 32-key blocks (block b of the split to wave
+// b % NW) loaded straight into registers with P blocks in flight, no LDS or
+// barrier until the waves merge -- with the VALU arithmetic of
+// flash_decode_gqa_dma_kernel: LPK = D / 8 lanes hold a key (8 dims each, one
+// 16-byte load of K and of V), so one wave load reads KPL = 64 / LPK
+// consecutive keys (1 KiB); a score is the v_dot2 of the fp16 q and K pairs
+// summed over the key's lanes with DPP. Each of the KPL lane groups keeps its
+// own online softmax state (m, l, o of its 8 dims) over the keys it reads, so
+// a block needs no exchange between groups; the groups merge once at the end
+// (DPP row_ror:8, v_permlane16_swap, v_permlane32_swap: lanes i ^ 8, i ^ 16,
+// i ^ 32), then the waves through LDS in wave order.
+template <int D, int NW, int P, bool RING, bool PARTIAL>
+__global__ __launch_bounds__(64 * NW) void flash_decode_mha_wave_kernel(
+    const _Float16* __restrict__ q, const _Float16* k, const _Float16* v,
+    _Float16* __restrict__ out, float* __restrict__ part_o, float* __restrict__ part_ml,
+    long long kv_len, long long group_size, long long kv_head_stride, float scale, int nsplit) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
+  static_assert(NW == 1 || NW == 2 || NW == 4 || NW == 8, "1, 2, 4 or 8 waves");
+  static_assert(P >= 1 && P <= 4, "1 to 4 blocks in flight per wave");
+  constexpr int LPK = D / 8;                 // lanes per key
+  constexpr int KPL = 64 / LPK;              // keys per wave load
+  constexpr int KB = 32;                     // keys per block
+  constexpr int LPB = KB / KPL;              // loads of K (and of V) per lane per block
+  constexpr int WS = D + 2;                  // floats of one wave's state in LDS
+  __shared__ __attribute__((aligned(16))) float s_state[NW > 1 ? NW * WS : 4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sub = lane / LPK;                // key of a wave load
+  const int d0 = (lane % LPK) * 8;           // this lane's dims
+  const long long h = blockIdx.x;
+  const int split = static_cast<int>(blockIdx.y);
+  const long long j0 = kv_len * split / nsplit;
+  const long long j1 = kv_len * (split + 1) / nsplit;
+  const int nkeys = static_cast<int>(j1 - j0);
+  const int nblocks = (nkeys + KB - 1) / KB;
+  const int nb = wave < nblocks ? (nblocks - wave + NW - 1) / NW : 0;
+  const float scale2 = scale * kLog2e;
+
+  H2 qh[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) qh[p] = H2{q[h * D + d0 + 2 * p], q[h * D + d0 + 2 * p + 1]};
+
+  const long long kvh = h / group_size;
+  const _Float16* kb = k + kvh * kv_head_stride + j0 * D + d0;
+  const _Float16* vb = v + kvh * kv_head_stride + j0 * D + d0;
+  struct Block {
+    H8 k[LPB];
+    H8 v[LPB];
+  };
+  // Every call issues the same 2 LPB loads (rows past the split's end read
+  // its last key, in bounds, and are masked; a block past the wave's last
+  // one is the last key for every lane).
+  auto load = [&](Block& b, int t) __attribute__((always_inline)) {
+    const int key0 = (wave + NW * t) * KB + sub;
+#pragma unroll
+    for (int i = 0; i < LPB; ++i) {
+      const long long kk = min(key0 + i * KPL, nkeys - 1);
+      b.k[i] = __builtin_nontemporal_load(reinterpret_cast<const H8*>(kb + kk * D));
+    }
+#pragma unroll
+    for (int i = 0; i < LPB; ++i) {
+      const long long kk = min(key0 + i * KPL, nkeys - 1);
+      b.v[i] = __builtin_nontemporal_load(reinterpret_cast<const H8*>(vb + kk * D));
+    }
+  };
+
+  constexpr float kLazy = 8.0f;              // see flash_decode_gqa_wave_kernel
+  float m = kNegInf;
+  float l = 0.0f;
+  float o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+
+  auto compute = [&](const Block& b, int t) __attribute__((always_inline)) {
+    const int key0 = (wave + NW * t) * KB + sub;
+    float sc[LPB];
+    float cm = kNegInf;
+#pragma unroll
+    for (int i = 0; i < LPB; ++i) {
+      float part = 0.0f;
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+        part = __builtin_amdgcn_fdot2(qh[p], H2{b.k[i][2 * p], b.k[i][2 * p + 1]}, part, false);
+      part = sum_key_lanes<LPK>(part);
+      sc[i] = key0 + i * KPL < nkeys ? part * scale2 : kNegInf;
+      cm = fmaxf(cm, sc[i]);
+    }
+    if (__any(cm > m + kLazy)) {
+      const float mn = fmaxf(m, cm);
+      const float alpha = merge_weight(m, mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] *= alpha;
+    }
+#pragma unroll
+    for (int i = 0; i < LPB; ++i) {
+      const float p = merge_weight(sc[i], m);
+      l += p;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = fmaf(p, static_cast<float>(b.v[i][e]), o[e]);
+    }
+  };
+
+  Block buf[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    load(buf[i], i);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  asm volatile("" ::: "memory");
+  if constexpr (!RING) {
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+      if (i < nb) compute(buf[i], i);
+  } else {
+    for (int t = 0; t < nb; t += P) {
+#pragma unroll
+      for (int i = 0; i < P; ++i) {
+        if (t + i < nb) compute(buf[i], t + i);
+        load(buf[i], t + i + P);
+      }
+    }
+  }
+
+  // Merge the KPL lane groups of the wave: partner lanes i ^ off hold the same
+  // dims for other keys. x + y == y + x, so both lanes of a pair agree.
+  auto exchange = [&](float x, int off) __attribute__((always_inline)) -> float {
+    if (off == 8) {
+      return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+    }
+    const unsigned u = __float_as_uint(x);
+    const auto r = off == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                             : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    const unsigned r0 = r[0];
+    const unsigned r1 = r[1];
+    return __uint_as_float(r0 == u ? r1 : r0);  // the partner's value
+  };
+#pragma unroll
+  for (int off = LPK; off < 64; off <<= 1) {
+    const float mp = exchange(m, off);
+    const float lp = exchange(l, off);
+    float op[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) op[e] = exchange(o[e], off);
+    const float mn = fmaxf(m, mp);
+    const float wa = merge_weight(m, mn);
+    const float wb = merge_weight(mp, mn);
+    l = l * wa + lp * wb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = o[e] * wa + op[e] * wb;
+    m = mn;
+  }
+
+  if constexpr (NW == 1) {
+    if (sub == 0) {
+      if constexpr (PARTIAL) {
+        const long long slot = h * nsplit + split;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) part_o[slot * D + d0 + e] = o[e];
+        if (lane == 0) {
+          part_ml[2 * slot] = m;
+          part_ml[2 * slot + 1] = l;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[h * D + d0 + e] = static_cast<_Float16>(l > 0.0f ? o[e] / l : 0.0f);
+      }
+    }
+    return;
+  }
+  float* const ws = s_state + wave * WS;
+  if (sub == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ws[d0 + e] = o[e];
+    if (lane == 0) {
+      ws[D] = m;
+      ws[D + 1] = l;
+    }
+  }
+  __syncthreads();
+  for (int d = tid; d < D; d += 64 * NW) {
+    float mb = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mb = fmaxf(mb, s_state[w * WS + D]);
+    float lb = 0.0f, ob = 0.0f;
+    if (mb > kNegInf) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float wt = merge_weight(s_state[w * WS + D], mb);
+        lb = fmaf(s_state[w * WS + D + 1], wt, lb);
+        ob = fmaf(s_state[w * WS + d], wt, ob);
+      }
+    }
+    if constexpr (PARTIAL) {
+      const long long slot = h * nsplit + split;
+      part_o[slot * D + d] = ob;
+      if (d == 0) {
+        part_ml[2 * slot] = mb;
+        part_ml[2 * slot + 1] = lb;
+      }
+    } else {
+      out[h * D + d] = static_cast<_Float16>(lb > 0.0f ? ob / lb : 0.0f);
+    }
+  }
+}
+
 // out[h][d] = sum_s w_s o_s[d] / sum_s w_s l_s with w_s = 2^(m_s - max m).
 // One 1024-thread workgroup per head: thread (c, d), c = tid / D, merges the
 // states of splits c, c + C, ... (C = 1024 / D) online -- loads issued in
@@ -1159,10 +1370,12 @@ struct DecodeArgs {
 };
 
 // 16-byte aligned caches: D = 64 GQA groups on flash_decode_gqa_wave_kernel
-// (matrix cores, K / V straight into registers); other shapes on the
-// direct-to-LDS pipelined kernel. Otherwise one query head per workgroup (MHA,
-// or GQA sharing switched off): the register kernel with 8 key steps in
-// flight per lane; GQA groups: the register-staged LDS-tile kernel.
+// (matrix cores, K / V straight into registers), one head per workgroup (MHA,
+// or GQA sharing switched off) on flash_decode_mha_wave_kernel (VALU, K / V
+// straight into registers), D = 128 GQA groups and long D = 64 single-head
+// splits on the direct-to-LDS pipelined kernel. Unaligned caches: one query
+// head per workgroup on the register kernel with 8 key steps in flight per
+// lane; GQA groups on the register-staged LDS-tile kernel.
 
 // flash_decode_gqa_wave_kernel's shape from the longest split's 32-key
 // blocks: up to 8 blocks, one wave per block (1, 2, 4 or 8 waves, so a
@@ -1193,15 +1406,52 @@ void launch_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, 
   }
 }
 
+// flash_decode_mha_wave_kernel's shape, as launch_wave's: one wave per
+// 32-key block up to 8 blocks, then 8 waves with 2 (or, at D = 64, 4) blocks
+// in flight, then a ring.
+template <int D, bool PARTIAL>
+void launch_mha_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, hipStream_t s) {
+  const long long keys = (a.kv_len + a.splits - 1) / a.splits;
+  const long long blocks = (keys + 31) / 32;
+  auto go = [&](auto kernel, int waves) {
+    kernel<<<grid, 64 * waves, 0, s>>>(a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len,
+                                       a.group_size, a.kv_head_stride, a.scale, a.splits);
+  };
+  constexpr int PMAX = D == 64 ? 4 : 2;      // 32 (64) VGPRs per block at D = 64 (128)
+  if (blocks <= 1) {
+    go(flash_decode_mha_wave_kernel<D, 1, 1, false, PARTIAL>, 1);
+  } else if (blocks <= 2) {
+    go(flash_decode_mha_wave_kernel<D, 2, 1, false, PARTIAL>, 2);
+  } else if (blocks <= 4) {
+    go(flash_decode_mha_wave_kernel<D, 4, 1, false, PARTIAL>, 4);
+  } else if (blocks <= 8) {
+    go(flash_decode_mha_wave_kernel<D, 8, 1, false, PARTIAL>, 8);
+  } else if (blocks <= 16) {
+    go(flash_decode_mha_wave_kernel<D, 8, 2, false, PARTIAL>, 8);
+  } else if (blocks <= 8 * PMAX) {
+    go(flash_decode_mha_wave_kernel<D, 8, PMAX, false, PARTIAL>, 8);
+  } else {
+    go(flash_decode_mha_wave_kernel<D, 8, PMAX, true, PARTIAL>, 8);
+  }
+}
+
 template <int D, int G, bool VEC, bool PARTIAL>
 void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
   if constexpr (VEC && D == 64 && G >= 2) {
     launch_wave<G, PARTIAL>(a, part_o, part_ml, grid, s);
   } else if constexpr (VEC) {
-    flash_decode_gqa_dma_kernel<D, G, PARTIAL><<<grid, kThreads, 0, s>>>(
-        a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
-        a.scale, a.splits);
+    // One head per workgroup: the register-fed kernel, except at D = 64 for
+    // splits past 8 waves x 4 blocks (its ring streamed a TinyLlama head without
+    // GQA sharing, 4096-key splits, at 5.7 TB/s; the LDS pipeline at 6.3).
+    const long long blocks = ((a.kv_len + a.splits - 1) / a.splits + 31) / 32;
+    if (G == 1 && (D == 128 || blocks <= 32)) {
+      launch_mha_wave<D, PARTIAL>(a, part_o, part_ml, grid, s);
+    } else {
+      flash_decode_gqa_dma_kernel<D, G, PARTIAL><<<grid, kThreads, 0, s>>>(
+          a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
+          a.scale, a.splits);
+    }
   } else if constexpr (G == 1) {
     flash_decode_split_kernel<D, 1, 8, VEC, PARTIAL><<<grid, kThreads, 0, s>>>(
         a.q, a.k, a.v, a.out, part_o, part_ml, a.kv_len, a.group_size, a.kv_head_stride,
