@@ -242,6 +242,26 @@ def test_attention_decode_every_pipeline_depth(gpu, orc, D):
         check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"D={D} tiles={ntiles} L={L}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_decode_single_head_every_shape(gpu, orc, D):
+    """One query head per KV head, one split, lengths of 1 to 70 32-key blocks:
+    the register-fed single-head kernel with 1, 2, 4 and 8 waves, 1, 2 and 4
+    blocks in flight per wave and its ring (D = 128 past 16 blocks), and at
+    D = 64 the hand-over to the LDS kernel past 32 blocks; ragged last blocks,
+    and two splits with ragged ends, against the oracle."""
+    rng = np.random.default_rng(300 + D)
+    H = Hkv = 4
+    sc = 1.0 / np.sqrt(D)
+    for L, split in ((1, 1), (31, 1), (33, 1), (64, 1), (100, 1), (250, 1), (256, 1),
+                     (290, 1), (512, 1), (530, 1), (1000, 1), (1024, 1), (1060, 1),
+                     (2240, 1), (1111, 2), (777, 3)):
+        q = rand_half(orc, rng, (H, D))
+        k = rand_half(orc, rng, (Hkv, L, D))
+        v = rand_half(orc, rng, (Hkv, L, D))
+        got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split)
+        check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"single head D={D} L={L} split={split}")
+
+
 def test_attention_decode_unaligned_cache_takes_scalar_loads(gpu, orc):
     """K / V not 16-byte aligned, and a head stride that is not a multiple of 8."""
     rng = np.random.default_rng(41)
