@@ -10,9 +10,11 @@
 // and it sits between the LDS read and the MFMA.)
 //
 // Tiling for wave64 and v_mfma_f32_32x32x2_f32:
-//   * workgroup tile BM x BN (128 x 128, 128 x 64 or 64 x 64), K step 32,
-//     256 threads = 4 waves in 2 x 2, each wave owning (BM/2) x (BN/2) as
-//     32 x 32 MFMA blocks;
+//   * workgroup tile BM x BN (256 x 128, 128 x 128, 128 x 64 or 64 x 64), K
+//     step 32; 256 x 128 runs 512 threads = 8 waves in 4 x 2 with three LDS
+//     stages, one workgroup per CU, the others 256 threads = 4 waves in 2 x 2
+//     with two stages, two workgroups per CU; each wave owns its block of the
+//     tile as 32 x 32 MFMA blocks;
 //   * operand layout of the instruction: lane l supplies A[l % 32][k] and
 //     B[k][l % 32] with k = l / 32 of the pair; accumulator v of lane l is
 //     C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32]. Within a 32-deep K tile the
@@ -31,7 +33,9 @@
 //     band of tiles (grouped 8 tile-rows deep) and shares A/B panels in its L2;
 //   * the tile shape is chosen per call so the grid covers the 256 CUs evenly
 //     (small-M shapes such as 512 x 4096 x 11008 would leave half the CUs idle
-//     with 128 x 128 tiles).
+//     with 128 x 128 tiles);
+//   * fragments are read a quarter K tile (4 MFMA k-slices) ahead of the
+//     MFMAs that use them.
 #include "launch.hpp"
 
 #include <algorithm>
@@ -264,12 +268,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
   }
 }
 
-// Full-tile variant fed by direct global -> LDS loads
-// (global_load_lds_dwordx4: lane l of a wave writes 16 bytes at the wave's
-// LDS base + 16 l, from any global address the lane names). No staging
-// registers and no LDS store instructions: the next tile's loads are issued
-// at the top of the K step and land while the MFMAs run; one s_waitcnt and
-// one barrier end the step. LDS tiles are unpadded and the 16-byte chunk
+// Variant fed by direct global -> LDS loads (buffer_load_dwordx4 ... lds:
+// lane l of a wave writes 16 bytes at the wave's LDS base + 16 l, from the
+// offset the lane names past the descriptor's base). No staging registers and
+// no LDS store instructions: a stage's loads are issued one or two K tiles
+// before it is read and land while the MFMAs run; one s_waitcnt and one
+// barrier hand each stage over. LDS tiles are unpadded and the 16-byte chunk
 // positions are XOR-swizzled instead, which the fetch side applies by choosing
 // which global chunk each lane loads:
 //   * k-contiguous tiles (A, and B given [N x K]): chunk c of row r sits at
@@ -278,23 +282,33 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_kernel(
 //   * [K x N] B tiles: chunk c of row k sits at c ^ (8 ((k >> 4) & 1)), so the
 //     rows k and k + 16 read by the two half-waves of a ds_read_b32 use
 //     disjoint banks.
-// Requires M % BM == N % BN == K % 32 == 0 and 16-byte aligned A and B.
+// Requires K % 32 == 0 and 16-byte aligned A and B (ragged M / N: EDGE below).
 __device__ __forceinline__ int swz_rows(int r) { return (r >> 1) & 7; }
 
-// 16-byte direct global -> LDS load of this lane; the LDS address of lane l is
-// lds + 16 l (lds must be the same in every lane of the wave). The builtin is
-// device-only: the host pass of a kernel template that names it would drop
-// the template's launch stub.
-__device__ __forceinline__ void lds_dma16(const float* src, float* lds) {
+// 16-byte direct load into LDS through a buffer descriptor: lane l reads the
+// bytes [off, off + 16) past base and writes them to lds + 16 l (lds the same
+// in every lane of the wave). The descriptor covers `bytes` bytes from base
+// (reads past them return zeros). base must be wave-uniform. Buffer loads,
+// unlike global_load_lds, are not FLAT instructions: the compiler then counts
+// the in-flight direct loads on vmcnt only and keeps the LDS fragment reads'
+// waits partial instead of draining them with lgkmcnt(0).
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw dword access)
+
+template <typename T>
+__device__ __forceinline__ void lds_buf16(const T* base, unsigned bytes, unsigned off, T* lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base), 0, static_cast<int>(bytes), kRsrcWord3),
+      lds, 16, static_cast<int>(off), 0, 0, 0);
 #endif
 }
 
-__device__ __forceinline__ void lds_dma16(const _Float16* src, _Float16* lds) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
-#endif
+// Bytes from element `from` to the end of an n-element array, capped at the
+// 32-bit range of a buffer descriptor.
+template <typename T>
+__device__ __forceinline__ unsigned bytes_left(long long n, long long from) {
+  const long long b = (n - from) * static_cast<long long>(sizeof(T));
+  return b >= 0xFFFFFFFFLL ? 0xFFFFFFFFu : static_cast<unsigned>(b);
 }
 
 // Waits until this wave's outstanding memory operations, the direct LDS loads
@@ -302,6 +316,26 @@ __device__ __forceinline__ void lds_dma16(const _Float16* src, _Float16* lds) {
 __device__ __forceinline__ void wait_all_memory() {
 #if defined(__HIP_DEVICE_COMPILE__)
   __builtin_amdgcn_s_waitcnt(0);
+#endif
+}
+
+// Stage hand-over inside the K loop: waits until at most `vm` of this wave's
+// vector-memory operations (direct LDS loads, issued and completing in order)
+// are outstanding and all of its LDS reads have returned, then joins the
+// workgroup barrier. The barrier is the bare instruction rather than
+// __syncthreads(), whose release fence would drain every outstanding load
+// (vmcnt(0)) and so cap the ring at one tile in flight; the empty asm
+// statements keep the compiler from moving memory accesses across it.
+template <int VM>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt field");
+#if defined(__HIP_DEVICE_COMPILE__)
+  // gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt 6:4 (7 = no wait),
+  // lgkmcnt 11:8 (0 = wait for all)
+  __builtin_amdgcn_s_waitcnt((VM & 0xF) | ((VM >> 4) << 14) | (0x7 << 4));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 #endif
 }
 __device__ __forceinline__ int swz_kn(int k) { return ((k >> 4) & 1) * 8; }
@@ -314,12 +348,36 @@ __device__ __forceinline__ int swz_rows_h(int r) { return (r >> 2) & 3; }
 __device__ __forceinline__ int swz_kn_h(int k) { return ((k >> 4) & 1) * 4; }
 
 //
-// The two stages of each operand are separate LDS variables and the K loop is
-// unrolled by two, so every LDS access names its buffer statically. The
-// compiler models a direct load's LDS write per lane and may otherwise fail to
-// prove that a fragment read of the current stage cannot overlap the loads
-// into the other one; it then makes the read wait for the whole next tile.
-// With distinct variables the accesses carry distinct alias scopes.
+// Workgroup layout: WGM x WGN waves, each owning a (BM / WGM) x (BN / WGN)
+// block of the tile as 32 x 32 MFMA blocks, and S LDS stages per operand.
+// 128 x 128 and smaller tiles: 4 waves, 2 stages (64 KB for 128 x 128 fp32),
+// two workgroups per CU. 256 x 128: 8 waves, 3 stages (144 KB), one
+// workgroup per CU; a stage's loads then have two K tiles of MFMAs to land
+// in, and each byte loaded feeds a third more MFMA work than on 128 x 128.
+template <int BM, int BN>
+struct TileCfg {
+  static constexpr bool kBig = BM == 256;
+  static constexpr int WGM = kBig ? 4 : 2;
+  static constexpr int WGN = 2;
+  static constexpr int kWaves = WGM * WGN;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int S = kBig ? 3 : 2;
+  static constexpr int kMinBlocks = kBig ? 1 : 2;  // workgroups per CU
+  static constexpr int WM = BM / WGM;
+  static constexpr int WN = BN / WGN;
+  static constexpr int MB = WM / 32;
+  static constexpr int NB = WN / 32;
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile");
+};
+
+template <int BM, int BN>
+using TileAcc = floatx16[TileCfg<BM, BN>::MB][TileCfg<BM, BN>::NB];
+
+// The stages of each operand are separate LDS variables and the K loop is
+// unrolled by S, so every LDS access names its buffer statically: the
+// compiler tracks direct loads per variable, and a fragment read of one stage
+// then waits only for that stage's loads, not for the ones in flight into the
+// others.
 //
 // B may also be fp16 (BT = _Float16): its tiles are loaded into LDS as raw
 // halves, half the bytes of an fp32 tile, and converted to fp32 as each lane
@@ -330,9 +388,7 @@ __device__ __forceinline__ int swz_kn_h(int k) { return ((k >> 4) & 1) * 4; }
 // B) or 16-byte column chunks ([K x N] B) past the matrix read the last valid
 // one instead -- in bounds, and only ever multiplied into accumulators whose
 // C element is outside the matrix -- and those elements are not stored.
-template <int BM, int BN>
-using TileAcc = floatx16[BM / 64][BN / 64];
-
+//
 // The K tiles [kt0, kt1) of the output tile at (m0, n0), accumulated into
 // acc (zeroed here); ends with a barrier, so a following call may refill
 // the LDS stages.
@@ -340,74 +396,89 @@ template <int BM, int BN, bool BNK, typename BT, bool EDGE>
 __device__ __forceinline__ void dma_tile(const float* __restrict__ A, const BT* __restrict__ B,
                                          int M, int N, int K, int m0, int n0, int kt0, int kt1,
                                          TileAcc<BM, BN>& acc) {
+  using C = TileCfg<BM, BN>;
   constexpr bool HB = std::is_same<BT, _Float16>::value;
   constexpr int BV = 16 / static_cast<int>(sizeof(BT));  // B elements per 16-byte chunk
-  constexpr int WM = BM / 2;
-  constexpr int WN = BN / 2;
-  constexpr int MB = WM / 32;
-  constexpr int NB = WN / 32;
-  constexpr int A_CH = BM * BK / 4;        // 16-byte chunks of an A tile
+  constexpr int S = C::S;
+  constexpr int MB = C::MB;
+  constexpr int NB = C::NB;
+  constexpr int A_CH = BM * BK / 4;  // 16-byte chunks of an A tile
   constexpr int B_CH = BN * BK / BV;
-  constexpr int A_INST = A_CH / kThreads;  // chunk loads per thread (= per wave instruction count)
-  constexpr int B_INST = B_CH / kThreads;
-  constexpr int BROW = BN / BV;            // chunks per [K x N] B row
-  static_assert(A_CH % kThreads == 0 && B_CH % kThreads == 0, "tile shape");
+  constexpr int A_INST = A_CH / C::kThreads;  // chunk loads per thread (= per wave instruction count)
+  constexpr int B_INST = B_CH / C::kThreads;
+  constexpr int kLoads = A_INST + B_INST;     // direct loads per thread per K tile
+  constexpr int BROW = BN / BV;               // chunks per [K x N] B row
+  static_assert(A_CH % C::kThreads == 0 && B_CH % C::kThreads == 0, "tile shape");
+  static_assert(S == 2 || S == 3, "stages");
   __shared__ __attribute__((aligned(1024))) float As0[BM * BK];
   __shared__ __attribute__((aligned(1024))) float As1[BM * BK];
+  __shared__ __attribute__((aligned(1024))) float As2[S > 2 ? BM * BK : 1];
   __shared__ __attribute__((aligned(1024))) BT Bs0[BN * BK];
   __shared__ __attribute__((aligned(1024))) BT Bs1[BN * BK];
+  __shared__ __attribute__((aligned(1024))) BT Bs2[S > 2 ? BN * BK : 1];
+  auto a_stage = [&](auto st) -> float* {
+    if constexpr (decltype(st)::value == 0) return As0;
+    else if constexpr (decltype(st)::value == 1) return As1;
+    else return As2;
+  };
+  auto b_stage = [&](auto st) -> BT* {
+    if constexpr (decltype(st)::value == 0) return Bs0;
+    else if constexpr (decltype(st)::value == 1) return Bs1;
+    else return Bs2;
+  };
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int li = lane & 31;
   const int lg = lane >> 5;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave / C::WGN;
+  const int wn = wave % C::WGN;
 
-  // Issue the direct loads of K tile kt into one stage. Wave w's j-th
-  // instruction fills chunk slots (4 j + w) * 64 + lane.
+  // Direct loads of K tile kt into one stage. Wave w's j-th instruction fills
+  // chunk slots (waves j + w) * 64 + lane. Each lane's byte offset from the
+  // tile's corner is the same for every K tile (a_off, b_off); only the
+  // descriptor's base moves, by BK columns of A and BK rows (or columns) of B.
+  unsigned a_off[A_INST];
+  unsigned b_off[B_INST];
+#pragma unroll
+  for (int j = 0; j < A_INST; ++j) {
+    const int slot = (C::kWaves * j + wave) * 64 + lane;
+    const int r = slot >> 3;
+    const int c = (slot & 7) ^ swz_rows(r);
+    const int row = EDGE ? min(m0 + r, M - 1) - m0 : r;
+    a_off[j] = static_cast<unsigned>(row * K + 4 * c) * 4u;
+  }
+#pragma unroll
+  for (int j = 0; j < B_INST; ++j) {
+    const int slot = (C::kWaves * j + wave) * 64 + lane;
+    if constexpr (BNK) {
+      const int r = HB ? slot >> 2 : slot >> 3;
+      const int c = HB ? (slot & 3) ^ swz_rows_h(r) : (slot & 7) ^ swz_rows(r);
+      const int row = EDGE ? min(n0 + r, N - 1) - n0 : r;
+      b_off[j] = static_cast<unsigned>(row * K + BV * c) * static_cast<unsigned>(sizeof(BT));
+    } else {
+      const int k = slot / BROW;
+      const int c = (slot % BROW) ^ (HB ? swz_kn_h(k) : swz_kn(k));
+      // N % BV == 0: a chunk is inside the row or wholly past it.
+      const int col = EDGE ? min(n0 + BV * c, N - BV) - n0 : BV * c;
+      b_off[j] = static_cast<unsigned>(k * N + col) * static_cast<unsigned>(sizeof(BT));
+    }
+  }
+  const long long a_len = static_cast<long long>(M) * K;
+  const long long b_len = static_cast<long long>(N) * K;
   auto fetch = [&](float* as, BT* bs, int kt) {
     const int k0 = kt * BK;
+    const long long a0 = static_cast<long long>(m0) * K + k0;
+    const long long b0 = BNK ? static_cast<long long>(n0) * K + k0 : static_cast<long long>(k0) * N + n0;
+    const unsigned a_bytes = bytes_left<float>(a_len, a0);
+    const unsigned b_bytes = bytes_left<BT>(b_len, b0);
 #pragma unroll
-    for (int j = 0; j < A_INST; ++j) {
-      const int slot0 = (4 * j + wave) * 64;
-      const int slot = slot0 + lane;
-      const int r = slot >> 3;
-      const int c = (slot & 7) ^ swz_rows(r);
-      const float* src;
-      if constexpr (EDGE) {
-        src = A + static_cast<long long>(min(m0 + r, M - 1)) * K + k0 + 4 * c;
-      } else {
-        src = A + static_cast<long long>(m0 + r) * K + k0 + 4 * c;
-      }
-      lds_dma16(src, as + 4 * slot0);
-    }
+    for (int j = 0; j < A_INST; ++j)
+      lds_buf16(A + a0, a_bytes, a_off[j], as + 4 * (C::kWaves * j + wave) * 64);
 #pragma unroll
-    for (int j = 0; j < B_INST; ++j) {
-      const int slot0 = (4 * j + wave) * 64;
-      const int slot = slot0 + lane;
-      const BT* src;
-      if constexpr (BNK) {
-        const int r = HB ? slot >> 2 : slot >> 3;
-        const int c = HB ? (slot & 3) ^ swz_rows_h(r) : (slot & 7) ^ swz_rows(r);
-        if constexpr (EDGE) {
-          src = B + static_cast<long long>(min(n0 + r, N - 1)) * K + k0 + BV * c;
-        } else {
-          src = B + static_cast<long long>(n0 + r) * K + k0 + BV * c;
-        }
-      } else {
-        const int k = slot / BROW;
-        const int c = (slot % BROW) ^ (HB ? swz_kn_h(k) : swz_kn(k));
-        if constexpr (EDGE) {
-          // N % BV == 0: a chunk is inside the row or wholly past it.
-          src = B + static_cast<long long>(k0 + k) * N + min(n0 + BV * c, N - BV);
-        } else {
-          src = B + static_cast<long long>(k0 + k) * N + n0 + BV * c;
-        }
-      }
-      lds_dma16(src, bs + BV * slot0);
-    }
+    for (int j = 0; j < B_INST; ++j)
+      lds_buf16(B + b0, b_bytes, b_off[j], bs + BV * (C::kWaves * j + wave) * 64);
   };
 
 #pragma unroll
@@ -417,84 +488,124 @@ __device__ __forceinline__ void dma_tile(const float* __restrict__ A, const BT* 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
 
-  // One K step on a resident stage: fragment reads and 16 MFMA k-slices.
-  // The A fragment of lane (li, lg) holds k = 16 lg + 4 q + e.
-  auto compute = [&](const float* as, const BT* bs) {
-    floatx4 af[MB][4];
+  // Fragments of one quarter of a K tile (MFMA k-slices s = 4 q .. 4 q + 3):
+  // lane (li, lg) holds A[row][16 lg + s] and B[16 lg + s][col].
+  struct Quarter {
+    floatx4 a[MB];
+    float b[NB][4];
+  };
+  auto read_q = [&](const float* as, const BT* bs, int q, Quarter& f) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int r = wm * WM + mb * 32 + li;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = (lg * 4 + q) ^ swz_rows(r);
-        af[mb][q] = *reinterpret_cast<const floatx4*>(as + 4 * (r * 8 + c));
-      }
+      const int r = wm * C::WM + mb * 32 + li;
+      const int c = (lg * 4 + q) ^ swz_rows(r);
+      f.a[mb] = *reinterpret_cast<const floatx4*>(as + 4 * (r * 8 + c));
     }
-    float bf[NB][16];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       if constexpr (BNK && !HB) {
-        const int r = wn * WN + nb * 32 + li;
+        const int r = wn * C::WN + nb * 32 + li;
+        const int c = (lg * 4 + q) ^ swz_rows(r);
+        const floatx4 v = *reinterpret_cast<const floatx4*>(bs + 4 * (r * 8 + c));
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int c = (lg * 4 + q) ^ swz_rows(r);
-          const floatx4 v = *reinterpret_cast<const floatx4*>(bs + 4 * (r * 8 + c));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bf[nb][4 * q + e] = v[e];
-        }
+        for (int e = 0; e < 4; ++e) f.b[nb][e] = v[e];
       } else if constexpr (BNK) {
-        // Row r holds k = 0..31 as 4 chunks; this lane's k = 16 lg + s are
-        // chunks 2 lg and 2 lg + 1.
-        const int r = wn * WN + nb * 32 + li;
+        // Row r holds k = 0..31 as 4 chunks of 8; this lane's k = 16 lg + 4 q + e
+        // are halves 4 (q & 1) .. 4 (q & 1) + 3 of chunk 2 lg + q / 2.
+        const int r = wn * C::WN + nb * 32 + li;
+        const int c = (lg * 2 + (q >> 1)) ^ swz_rows_h(r);
+        const _Float16* p = bs + 8 * (r * 4 + c) + 4 * (q & 1);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int c = (lg * 2 + q) ^ swz_rows_h(r);
-          const halfx8 v = *reinterpret_cast<const halfx8*>(bs + 8 * (r * 4 + c));
-#pragma unroll
-          for (int e = 0; e < 8; ++e) bf[nb][8 * q + e] = static_cast<float>(v[e]);
-        }
+        for (int e = 0; e < 4; ++e) f.b[nb][e] = static_cast<float>(p[e]);
       } else {
-        const int n = wn * WN + nb * 32 + li;
+        const int n = wn * C::WN + nb * 32 + li;
 #pragma unroll
-        for (int s = 0; s < 16; ++s) {
-          const int k = lg * 16 + s;
+        for (int e = 0; e < 4; ++e) {
+          const int k = lg * 16 + 4 * q + e;
           if constexpr (HB) {
             const int c = (n >> 3) ^ swz_kn_h(k);
-            bf[nb][s] = static_cast<float>(bs[8 * (k * BROW + c) + (n & 7)]);
+            f.b[nb][e] = static_cast<float>(bs[8 * (k * BROW + c) + (n & 7)]);
           } else {
             const int c = (n >> 2) ^ swz_kn(k);
-            bf[nb][s] = bs[4 * (k * BROW + c) + (n & 3)];
+            f.b[nb][e] = bs[4 * (k * BROW + c) + (n & 3)];
           }
         }
       }
     }
+  };
+  auto mma_q = [&](const Quarter& f) {
 #pragma unroll
-    for (int s = 0; s < 16; ++s) {
+    for (int e = 0; e < 4; ++e) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const float a = af[mb][s >> 2][s & 3];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, bf[nb][s], acc[mb][nb], 0, 0, 0);
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x2f32(f.a[mb][e], f.b[nb][e], acc[mb][nb], 0, 0, 0);
       }
     }
   };
 
+  // Software pipeline over quarters: each quarter's fragments are read while
+  // the previous quarter's MFMAs run. The stage hand-over sits before a K
+  // tile's last quarter: it waits for the direct loads of the next tile (S - 2
+  // later tiles may stay in flight), makes every wave's loads of it visible
+  // (so that tile's first quarter can be read during this tile's last), and
+  // ends every wave's reads of the current stage, which the fetch after it
+  // refills with the tile S steps ahead. That fetch and the read after the
+  // barrier are unconditional so that nothing splits the block: near the end
+  // the fetch loads tile kt1 - 1 again into a finished stage and the read
+  // takes a stale quarter that is never used. Scheduling barriers keep each
+  // quarter's reads ahead of the previous quarter's MFMAs.
+  auto pin = [] {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_group_barrier(0x020, 16, 0);  // VMEM reads (the fetch)
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  };
+  Quarter x, y;
+  auto tile = [&](auto st, int kt) {
+    constexpr int cur = decltype(st)::value;
+    using Next = std::integral_constant<int, (cur + 1) % S>;
+    const float* as = a_stage(st);
+    const BT* bs = b_stage(st);
+    read_q(as, bs, 1, y);
+    mma_q(x);
+    pin();
+    read_q(as, bs, 2, x);
+    mma_q(y);
+    pin();
+    read_q(as, bs, 3, y);
+    mma_q(x);
+    pin();
+    stage_barrier<(S - 2) * kLoads>();
+    fetch(a_stage(st), b_stage(st), min(kt + S, kt1 - 1));
+    read_q(a_stage(Next{}), b_stage(Next{}), 0, x);
+    mma_q(y);
+    pin();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
   fetch(As0, Bs0, kt0);
+  fetch(As1, Bs1, min(kt0 + 1, kt1 - 1));
+  if constexpr (S > 2) fetch(As2, Bs2, min(kt0 + 2, kt1 - 1));
+  stage_barrier<(S - 1) * kLoads>();
+  read_q(As0, Bs0, 0, x);
+  int kt = kt0;
+  for (; kt + S - 1 < kt1; kt += S) {
+    tile(I0{}, kt);
+    tile(I1{}, kt + 1);
+    if constexpr (S > 2) tile(I2{}, kt + 2);
+  }
+  if (kt < kt1) tile(I0{}, kt);
+  if constexpr (S > 2) {
+    if (kt + 1 < kt1) tile(I1{}, kt + 1);
+  }
   wait_all_memory();
   __syncthreads();
-  for (int kt = kt0; kt < kt1; kt += 2) {
-    if (kt + 1 < kt1) fetch(As1, Bs1, kt + 1);
-    compute(As0, Bs0);
-    wait_all_memory();  // this wave's loads of the next tile have landed
-    __syncthreads();
-    if (kt + 1 < kt1) {
-      if (kt + 2 < kt1) fetch(As0, Bs0, kt + 2);
-      compute(As1, Bs1);
-      wait_all_memory();
-      __syncthreads();
-    }
-  }
 }
 
 // Stores a tile's accumulators: element (r, c) of the tile to out[r * ld + c]
@@ -503,22 +614,21 @@ __device__ __forceinline__ void dma_tile(const float* __restrict__ A, const BT* 
 template <int BM, int BN, bool EDGE>
 __device__ __forceinline__ void store_acc(const TileAcc<BM, BN>& acc, float* __restrict__ out,
                                           long long ld, int rows_left, int cols_left) {
-  constexpr int WM = BM / 2;
-  constexpr int WN = BN / 2;
+  using C = TileCfg<BM, BN>;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 31;
   const int lg = lane >> 5;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
+  const int wm = wave / C::WGN;
+  const int wn = wave % C::WGN;
 #pragma unroll
-  for (int mb = 0; mb < BM / 64; ++mb) {
+  for (int mb = 0; mb < C::MB; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < BN / 64; ++nb) {
-      const int col = wn * WN + nb * 32 + li;
+    for (int nb = 0; nb < C::NB; ++nb) {
+      const int col = wn * C::WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int row = wm * WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        const int row = wm * C::WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
         if (!EDGE || (row < rows_left && col < cols_left)) out[row * ld + col] = acc[mb][nb][v];
       }
     }
@@ -526,9 +636,9 @@ __device__ __forceinline__ void store_acc(const TileAcc<BM, BN>& acc, float* __r
 }
 
 template <int BM, int BN, bool BNK, typename BT = float, bool EDGE = false>
-__global__ __launch_bounds__(kThreads, 2) void gemm_f32_mfma_dma_kernel(
-    const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C, int M, int N,
-    int K, int tiles_m, int tiles_n) {
+__global__ __launch_bounds__((TileCfg<BM, BN>::kThreads), (TileCfg<BM, BN>::kMinBlocks)) void
+gemm_f32_mfma_dma_kernel(const float* __restrict__ A, const BT* __restrict__ B,
+                         float* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * BM;
@@ -574,26 +684,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_sk_kernel(
     const float* __restrict__ A, const BT* __restrict__ B, float* __restrict__ C,
     float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n, SkPlan plan) {
   TileAcc<BM, BN> acc;
+  // One loop for both kinds of workgroup (a single inlined copy of the tile
+  // loop): a data-parallel workgroup g covers iterations [0, nk) of tile g; a
+  // stream-K workgroup its share of the tail, whose tile t is tile dp + t.
   const int g = blockIdx.x;
-  if (g < plan.dp) {
-    int tm, tn;
-    tile_of(g, tiles_m, tiles_n, tm, tn);
-    const int m0 = tm * BM;
-    const int n0 = tn * BN;
-    dma_tile<BM, BN, BNK, BT, false>(A, B, M, N, K, m0, n0, 0, plan.nk, acc);
-    store_acc<BM, BN, false>(acc, C + static_cast<long long>(m0) * N + n0, N, BM, BN);
-    return;
-  }
-  const long long s = g - plan.dp;
-  const long long i0 = sk_begin(s, plan);
-  const long long i1 = sk_begin(s + 1, plan);
+  const bool dp = g < plan.dp;
+  const long long s = dp ? 0 : g - plan.dp;
+  const long long i0 = dp ? 0 : sk_begin(s, plan);
+  const long long i1 = dp ? plan.nk : sk_begin(s + 1, plan);
+  const int first_tile = dp ? g : plan.dp;
   for (long long it = i0; it < i1;) {
-    const long long t = it / plan.nk;  // tail tile
+    const long long t = it / plan.nk;
     const int ka = static_cast<int>(it - t * plan.nk);
     const long long tend = (t + 1) * plan.nk;
     const int kb = static_cast<int>((i1 < tend ? i1 : tend) - t * plan.nk);
     int tm, tn;
-    tile_of(plan.dp + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
+    tile_of(first_tile + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
     dma_tile<BM, BN, BNK, BT, false>(A, B, M, N, K, m0, n0, ka, kb, acc);
@@ -646,6 +752,31 @@ bool dma_enabled() {
   return on;
 }
 
+// Direct loads need K % BK == 0, 16-byte aligned operands and 16-byte
+// aligned B rows ([K x N] rows of N elements; [N x K] rows of K), and every
+// lane's byte offset from a tile's corner (up to BM rows of A, BN rows of an
+// [N x K] B or BK rows of a [K x N] B) must fit the 31 bits of a buffer
+// load's offset.
+template <int BM, int BN, typename BT, bool BNK>
+bool direct_ok(const GemmArgs& a) {
+  constexpr long long kBVec = 16 / static_cast<long long>(sizeof(BT));
+  constexpr long long kLim = 0x7fffffffLL;
+  const long long b_span = BNK ? static_cast<long long>(BN) * a.K : static_cast<long long>(BK) * a.N;
+  return dma_enabled() && a.K % BK == 0 && aligned_to(a.A, 16) && aligned_to(a.B, 16) &&
+         (BNK || a.N % kBVec == 0) && static_cast<long long>(BM) * a.K * 4 <= kLim &&
+         b_span * static_cast<long long>(sizeof(BT)) <= kLim;
+}
+
+// The 256 x 128 tile can be switched off (ENGINE_GEMM_NO_BIG=1) to compare
+// it with 128 x 128 on the same shapes.
+bool big_tile_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_NO_BIG");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
 template <int BM, int BN, typename BT, bool BNK>
 void run_gemm(const GemmArgs& a, hipStream_t stream) {
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
@@ -661,38 +792,38 @@ void run_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
   const dim3 grid(static_cast<unsigned>(ntiles));
   const BT* B = static_cast<const BT*>(a.B);
-  {
-    // Direct loads need K % BK == 0, 16-byte aligned operands and 16-byte
-    // aligned B rows ([K x N] rows of N elements; [N x K] rows of K). Whole
-    // tiles take the plain kernel, ragged M / N its EDGE form.
-    const bool direct = K % BK == 0 && aligned_to(a.A, 16) && aligned_to(a.B, 16) &&
-                        (BNK || N % kBVec == 0);
-    if (direct && dma_enabled()) {
-      if (M % BM == 0 && N % BN == 0) {
-        gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, false><<<grid, kThreads, 0, stream>>>(
-            a.A, B, a.C, M, N, K, tiles_m, tiles_n);
-      } else {
-        gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, true><<<grid, kThreads, 0, stream>>>(
-            a.A, B, a.C, M, N, K, tiles_m, tiles_n);
-      }
-      ENG_LAUNCH_CHECK();
-      return;
+  if (direct_ok<BM, BN, BT, BNK>(a)) {
+    // Whole tiles take the plain kernel, ragged M / N its EDGE form.
+    constexpr int kDmaThreads = TileCfg<BM, BN>::kThreads;
+    if (M % BM == 0 && N % BN == 0) {
+      gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, false><<<grid, kDmaThreads, 0, stream>>>(
+          a.A, B, a.C, M, N, K, tiles_m, tiles_n);
+    } else {
+      gemm_f32_mfma_dma_kernel<BM, BN, BNK, BT, true><<<grid, kDmaThreads, 0, stream>>>(
+          a.A, B, a.C, M, N, K, tiles_m, tiles_n);
     }
+    ENG_LAUNCH_CHECK();
+    return;
   }
-#define ENG_GEMM_LAUNCH(VA_, VB_)                                                  \
-  gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_><<<grid, kThreads, 0, stream>>>(  \
-      a.A, B, a.C, M, N, K, tiles_m, tiles_n)
-  if (va && vb) {
-    ENG_GEMM_LAUNCH(true, true);
-  } else if (va) {
-    ENG_GEMM_LAUNCH(true, false);
-  } else if (vb) {
-    ENG_GEMM_LAUNCH(false, true);
+  if constexpr (TileCfg<BM, BN>::kBig) {
+    // big_tile() only picks 256 x 128 when the direct loads apply
+    ENG_CHECK(false, "matmul: 256-row tiles need the direct-load kernel");
   } else {
-    ENG_GEMM_LAUNCH(false, false);
-  }
+#define ENG_GEMM_LAUNCH(VA_, VB_)                                                    \
+    gemm_f32_mfma_kernel<BM, BN, BT, BNK, VA_, VB_><<<grid, kThreads, 0, stream>>>( \
+        a.A, B, a.C, M, N, K, tiles_m, tiles_n)
+    if (va && vb) {
+      ENG_GEMM_LAUNCH(true, true);
+    } else if (va) {
+      ENG_GEMM_LAUNCH(true, false);
+    } else if (vb) {
+      ENG_GEMM_LAUNCH(false, true);
+    } else {
+      ENG_GEMM_LAUNCH(false, false);
+    }
 #undef ENG_GEMM_LAUNCH
-  ENG_LAUNCH_CHECK();
+    ENG_LAUNCH_CHECK();
+  }
 }
 
 // Tile shape: the largest of 128 x 128, 128 x 64, 64 x 64 whose makespan (rounds
@@ -737,9 +868,8 @@ template <typename BT, bool BNK>
 bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
   constexpr int BM = 128, BN = 128;
   constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
-  if (!sk_enabled() || !dma_enabled()) return false;
-  if (a.M % BM != 0 || a.N % BN != 0 || a.K % BK != 0 || a.K / BK < 8) return false;
-  if (!aligned_to(a.A, 16) || !aligned_to(a.B, 16) || (!BNK && a.N % kBVec != 0)) return false;
+  if (!sk_enabled() || !direct_ok<BM, BN, BT, BNK>(a)) return false;
+  if (a.M % BM != 0 || a.N % BN != 0 || a.K / BK < 8) return false;
   const long long cus = device_cu_count();
   const int tiles_m = static_cast<int>(a.M / BM);
   const int tiles_n = static_cast<int>(a.N / BN);
@@ -763,9 +893,28 @@ bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
   return true;
 }
 
+// 256 x 128 tiles where choose_tile's model takes 128 x 128 and gives the
+// larger tile no longer a makespan (rounds of one tile per CU, times the
+// tile's area: 4096^3 has 512 such tiles against 1024, two rounds of twice
+// the work against four), and the direct loads apply.
+template <typename BT, bool BNK>
+bool big_tile(const GemmArgs& a) {
+  if (!big_tile_enabled() || !direct_ok<256, 128, BT, BNK>(a)) return false;
+  if (choose_tile(a.M, a.N) != Tile::T128x128) return false;
+  const long long cus = device_cu_count();
+  auto rounds = [&](long long bm, long long bn) {
+    return (((a.M + bm - 1) / bm) * ((a.N + bn - 1) / bn) + cus - 1) / cus;
+  };
+  return 2 * rounds(256, 128) <= rounds(128, 128);
+}
+
 template <typename BT, bool BNK>
 void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
   if (run_gemm_sk<BT, BNK>(a, stream)) return;
+  if (big_tile<BT, BNK>(a)) {
+    run_gemm<256, 128, BT, BNK>(a, stream);
+    return;
+  }
   switch (choose_tile(a.M, a.N)) {
     case Tile::T128x128:
       run_gemm<128, 128, BT, BNK>(a, stream);

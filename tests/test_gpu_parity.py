@@ -237,6 +237,53 @@ def test_matmul_ragged_tiles_take_direct_loads(gpu, orc, M, N, K):
     check_dot(got[rows], y, helpers.absdot(A[rows], B) + np.abs(y), K, f"matmul {M}x{N}x{K}")
 
 
+def big_tile_rows(M, rng):
+    # every 64-row wave band of the first two 256-row tiles, a middle and the
+    # last tile, and a few random rows
+    fixed = [0, 63, 64, 127, 128, 191, 192, 255, 256, 319, 320, 383, 384, 447, 448, 511, M // 2, M - 1]
+    return np.unique(np.concatenate([fixed, rng.integers(0, M, 4)]))
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 32), (2048, 4096, 64), (2048, 4096, 96),
+                                   (2048, 4096, 288), (2000, 4000, 256)])
+def test_matmul_256_row_tiles(gpu, orc, M, N, K):
+    # 2048 x 4096 (and 4096^3) take 256 x 128 tiles: 8 waves, three LDS
+    # stages, the K loop unrolled by three. 1, 2, 3 and 9 K tiles cover the
+    # loop's remainders and a ring that wraps; 2000 x 4000 is the ragged form.
+    rng = np.random.default_rng(M + N + K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    rows = big_tile_rows(M, rng)
+    y = orc.matmul(A[rows], B).astype(np.float64)
+    check_dot(got[rows], y, helpers.absdot(A[rows], B) + np.abs(y), K, f"matmul {M}x{N}x{K} rows {rows}")
+    colsum = got.astype(np.float64).sum(axis=0)
+    ref = A.astype(np.float64).sum(axis=0) @ B.astype(np.float64)
+    bound = (K + M) * helpers.U32 * (np.abs(A).astype(np.float64).sum(axis=0) @ np.abs(B).astype(np.float64))
+    helpers.assert_within(colsum, ref, bound, f"matmul {M}x{N}x{K} column sums")
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 4096, 256), (2000, 4000, 160)])
+@pytest.mark.parametrize("wdtype", ["f32", "f16"])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_rmsnorm_linear_256_row_tiles(gpu, orc, M, N, K, wdtype, layout):
+    # The 256 x 128 tile with B given [N x K] and with fp16 B (converted as
+    # fragments are read), whole and ragged.
+    rng = np.random.default_rng(5 * M + N + K + (layout == "nk") + 2 * (wdtype == "f16"))
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float32)
+    if wdtype == "f16":
+        W = W.astype(np.float16).view(np.uint16)
+    if layout == "kn":
+        got = gpu_rmsnorm_linear(gpu, x, g, W)
+    else:
+        got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    rows = big_tile_rows(M, rng)
+    y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear {wdtype} {layout} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K", [(100, 11008, 4096), (77, 200, 512), (3, 136, 64)])
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 def test_rmsnorm_linear_f16w_ragged_tiles(gpu, orc, M, N, K, layout):
