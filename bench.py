@@ -946,6 +946,35 @@ def bench_llama_stack(eng, timer, nk=False, fused_glu=False, graph=False, fused_
     return row
 
 
+def vendor_gemm() -> int:
+    """torch.matmul in fp32 (TF32 off) on the GEMM shapes of BASELINE configs 1
+    and 4: the vendor library's figure beside eng_matmul_f32's. HIP events around
+    10 back-to-back calls, median of 7 such windows, after 5 warm-up calls."""
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    for M, N, K in ((512, 512, 512), (4096, 4096, 4096), (512, 11008, 4096), (512, 4096, 11008)):
+        a = torch.rand(M, K, device="cuda") * 2 - 1
+        b = torch.rand(K, N, device="cuda") * 2 - 1
+        for _ in range(5):
+            a @ b
+        torch.cuda.synchronize()
+        ms = []
+        for _ in range(7):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                a @ b
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1) / 10)
+        med = sorted(ms)[3]
+        print(json.dumps({"name": f"torch.matmul fp32 {M}x{N}x{K}", "ms_per_call": round(med, 4),
+                          "TFLOP/s": round(2.0 * M * N * K / (med * 1e-3) / 1e12, 2),
+                          "frac_fp32_mfma_peak": round(2.0 * M * N * K / (med * 1e-3) / 1e12
+                                                       / FP32_MFMA_PEAK_TFLOPS, 4)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -958,7 +987,13 @@ def main() -> int:
     ap.add_argument("--only", default="", help="comma-separated secondary groups to run: "
                     + ", ".join(GROUPS) + " (default: all but the profiling groups "
                     + ", ".join(PROFILING_GROUPS) + ", which repeat or sweep single rows)")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="time torch.matmul (hipBLASLt) in fp32 on the config-1/4 GEMM shapes and exit; "
+                    "a comparison point only, run without loading the engine (a process that has "
+                    "initialised HIP through the engine library does not see the GPU through torch)")
     args = ap.parse_args()
+    if args.vendor_gemm:
+        return vendor_gemm()
 
     global NO_GRAPHS
     NO_GRAPHS = args.no_graphs
@@ -1077,7 +1112,7 @@ def result_line(*, steps, warmup, ms, nbytes, head_clocks, head_hold, spread, ge
     return line
 
 
-HEADLINE_GEMM_KERNEL = "eng::gemm_f32_mfma_dma_kernel<128, 128, false>"
+HEADLINE_GEMM_KERNEL = "eng::gemm_f32_mfma_dma_kernel<256, 128, false>"
 GEMM_PROFILE = os.path.join("profiles", "gemm_f32_mfma_configs1_4.md")
 
 
