@@ -18,9 +18,10 @@
 // -- across the key lanes of a wave by shuffles, across the 4 waves through
 // LDS, and across splits in a merge kernel, always in a fixed order. Splits
 // write fp32 (o, m, l) partials to the stream's scratch arena (reused in
-// stream order: no allocation or event per call). D = 64 GQA groups on
-// aligned caches take flash_decode_gqa_wave_kernel instead: the matrix cores,
-// K / V loaded straight into MFMA operand registers, 1 to 8 waves per split.
+// stream order: no allocation or event per call). GQA groups on aligned
+// caches (D = 64 or 128) take flash_decode_gqa_wave_kernel instead: the matrix
+// cores, K / V loaded straight into MFMA operand registers, 1 to 8 waves per
+// split.
 #include "gemv_kernels.hpp"
 #include "launch.hpp"
 
@@ -689,14 +690,14 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
   }
 }
 
-// GQA decode at D = 64 for G <= 16 query heads of one KV head: NW waves (1, 2,
-// 4 or 8), each owning 32-key blocks (block b of the split goes to wave b % NW) that it
+// GQA decode at D = 64 or 128 for G <= 16 query heads of one KV head: NW
+// waves (1, 2, 4 or 8), each owning 32-key blocks (block b of the split goes to wave b % NW) that it
 // loads straight into the registers the matrix cores read them from -- no LDS
 // staging, no workgroup barrier until the final merge -- with P blocks in
 // flight per wave. Per block, on the matrix cores:
-//   scores  S^T[32 keys x 16 heads] = K . q^T  (two v_mfma_f32_16x16x32_f16 per
-//           16 keys; fp16 products are exact in fp32, summed in fp32),
-//   values  O^T[64 dims x 16 heads] += V^T . P^T over the 32 keys, on
+//   scores  S^T[32 keys x 16 heads] = K . q^T  (D / 32 v_mfma_f32_16x16x32_f16
+//           per 16 keys; fp16 products are exact in fp32, summed in fp32),
+//   values  O^T[D dims x 16 heads] += V^T . P^T over the 32 keys, on
 //           v_mfma_f32_16x16x32_f16 with the fp32 softmax weights split into two
 //           fp16 terms p = hi + lo (hi = fp16(p), lo = fp16(p - hi): 22
 //           significant bits, each product exact in fp32), two MFMAs per
@@ -713,24 +714,28 @@ __global__ __launch_bounds__(kThreads) void flash_decode_gqa_dma_kernel(
 // 16 h + i / 4 + 4 (i % 4)), so lane group g holds the weights of keys
 // {16 h + g + 4 e}; the value step's k index 8 g + e is key
 // 16 (e / 4) + g + 4 (e % 4) -- the lane's own weights, in order -- and its A
-// operand (V^T, row i = dim 4 i + mb of block mb) is one 8-byte load of dims
-// 4 i .. 4 i + 3 per key, the four lane groups reading four consecutive V rows
-// (512 contiguous bytes per load). A block is 128 bytes per lane: four 16-byte
-// K loads, eight 8-byte V loads. The waves' states merge through LDS in wave
-// order: the output, or an fp32 partial state per split.
-template <int G, int NW, int P, bool RING, bool PARTIAL>
+// operand (V^T, row i = dim VW i + mb of block mb, VW = D / 16) is one load of
+// dims VW i .. VW i + VW - 1 per key (8 bytes at D = 64, 16 at D = 128),
+// transposed in registers into the D / 16 value blocks, the four lane groups
+// reading four consecutive V rows (4 D contiguous bytes per load). A block is
+// 2 D bytes per lane: 2 D / 32 16-byte K loads and eight V loads. The waves'
+// states merge through LDS in wave order: the output, or an fp32 partial state
+// per split.
+template <int D, int G, int NW, int P, bool RING, bool PARTIAL>
 __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
     const _Float16* __restrict__ q, const _Float16* k, const _Float16* v,
     _Float16* __restrict__ out, float* __restrict__ part_o,
     float* __restrict__ part_ml, long long kv_len, long long group_size,
     long long kv_head_stride, float scale, int nsplit) {
+  static_assert(D == 64 || D == 128, "head_dim 64 or 128");
   static_assert(G >= 2 && G <= 16, "2 to 16 heads per workgroup");
   static_assert(NW == 1 || NW == 2 || NW == 4 || NW == 8, "1, 2, 4 or 8 waves");
   static_assert(P >= 1 && P <= 4, "1 to 4 blocks in flight per wave");
   typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-  typedef _Float16 half4 __attribute__((ext_vector_type(4)));
   typedef float float4v __attribute__((ext_vector_type(4)));
-  constexpr int D = 64;
+  constexpr int KS = D / 32;                 // 32-dim steps of a score
+  constexpr int VW = D / 16;                 // value blocks = dims per lane per key
+  typedef _Float16 halfvw __attribute__((ext_vector_type(VW)));
   constexpr int KB = 32;                     // keys per block
   constexpr int WS = 16 * D + 32;            // floats of one wave's state in LDS
   __shared__ __attribute__((aligned(16))) float s_state[NW > 1 ? NW * WS : 4];
@@ -753,10 +758,10 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   // q^T as the score B operand (head col, dims 32 ks + 8 grp + j). Columns
   // past G repeat head G - 1 (no load is conditional): they compute its state
   // again, vote as it does in the rescale test, and are never written.
-  half8 qb[2];
+  half8 qb[KS];
   const _Float16* qh = q + (hg0 + min(col, G - 1)) * D + 8 * grp;
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
+  for (int ks = 0; ks < KS; ++ks) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) qb[ks][j] = qh[32 * ks + j];
   }
@@ -764,10 +769,10 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   const _Float16* kb = k + kvh * kv_head_stride + j0 * D;
   const _Float16* vb = v + kvh * kv_head_stride + j0 * D;
   struct Block {
-    half8 k[2][2];                           // [half-block][32-dim step]
-    half4 v[8];                              // [k element]
+    half8 k[2][KS];                          // [half-block][32-dim step]
+    halfvw v[8];                             // [k element]
   };
-  // Every call issues the same 12 loads, so the compiler's waits count
+  // Every call issues the same 2 KS + 8 loads, so the compiler's waits count
   // exactly P - 1 blocks in flight behind the one a compute needs. Rows past
   // the split's end load its last key (in bounds; masked below), so a block
   // past this wave's last one is the last key for every lane: one K and one
@@ -778,7 +783,7 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
     for (int h = 0; h < 2; ++h) {
       const int kk = min(key0 + 16 * h + (col >> 2) + 4 * (col & 3), nkeys - 1);
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < KS; ++s)
         b.k[h][s] = __builtin_nontemporal_load(
             reinterpret_cast<const half8*>(kb + static_cast<long long>(kk) * D + 32 * s + 8 * grp));
     }
@@ -786,7 +791,7 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
     for (int e = 0; e < 8; ++e) {
       const int kk = min(key0 + 16 * (e >> 2) + grp + 4 * (e & 3), nkeys - 1);
       b.v[e] = __builtin_nontemporal_load(
-          reinterpret_cast<const half4*>(vb + static_cast<long long>(kk) * D + 4 * col));
+          reinterpret_cast<const halfvw*>(vb + static_cast<long long>(kk) * D + VW * col));
     }
   };
 
@@ -814,16 +819,18 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   constexpr float kWeightShift = 7.0f;
   float m = kNegInf;
   float lsum = 0.0f;
-  float4v o[4];
+  float4v o[VW];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb) o[mb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int mb = 0; mb < VW; ++mb) o[mb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](const Block& b, int t) __attribute__((always_inline)) {
     float4v sc[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[h][0], qb[0], float4v{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-      sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[h][1], qb[1], sc[h], 0, 0, 0);
+#pragma unroll
+      for (int ks = 1; ks < KS; ++ks)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(b.k[h][ks], qb[ks], sc[h], 0, 0, 0);
     }
     const int kbase = (wave + NW * t) * KB + grp;
     float sv[8];
@@ -840,7 +847,7 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
       m = mn;
       lsum *= alpha;
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) o[mb] *= alpha;
+      for (int mb = 0; mb < VW; ++mb) o[mb] *= alpha;
     }
     half8 ph, pl;
 #pragma unroll
@@ -850,16 +857,16 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
       ph[e] = static_cast<_Float16>(p);
       pl[e] = static_cast<_Float16>(p - static_cast<float>(ph[e]));
     }
-    half8 av[4];
+    half8 av[VW];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < VW; ++mb) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) av[mb][e] = b.v[e][mb];
     }
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], ph, o[mb], 0, 0, 0);
+    for (int mb = 0; mb < VW; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], ph, o[mb], 0, 0, 0);
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], pl, o[mb], 0, 0, 0);
+    for (int mb = 0; mb < VW; ++mb) o[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mb], pl, o[mb], 0, 0, 0);
   };
 
   // Ring of P blocks: block t lives in buf[t % P], every buffer named
@@ -893,7 +900,8 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
     }
   }
 
-  // Lane (col, grp) holds dims 16 grp + 4 r + mb of head col in o[mb][r].
+  // Lane (col, grp) holds dims VW (4 grp + r) + mb of head col in o[mb][r]:
+  // VW consecutive dims per r.
   const float lt = group_sum(lsum);
   if constexpr (NW == 1) {
     // One wave: its state is the workgroup's, written from registers.
@@ -902,9 +910,12 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
       if constexpr (PARTIAL) {
         const long long slot = h * nsplit + split;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          *reinterpret_cast<float4v*>(part_o + slot * D + 16 * grp + 4 * r) =
-              float4v{o[0][r], o[1][r], o[2][r], o[3][r]};
+        for (int r = 0; r < 4; ++r) {
+#pragma unroll
+          for (int c = 0; c < VW; c += 4)
+            *reinterpret_cast<float4v*>(part_o + slot * D + VW * (4 * grp + r) + c) =
+                float4v{o[c][r], o[c + 1][r], o[c + 2][r], o[c + 3][r]};
+        }
         if (grp == 0) {
           part_ml[2 * slot] = m;
           part_ml[2 * slot + 1] = lt;
@@ -913,8 +924,8 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb)  // out is only 2-byte aligned
-            out[h * D + 16 * grp + 4 * r + mb] = static_cast<_Float16>(lt > 0.0f ? o[mb][r] / lt : 0.0f);
+          for (int mb = 0; mb < VW; ++mb)  // out is only 2-byte aligned
+            out[h * D + VW * (4 * grp + r) + mb] = static_cast<_Float16>(lt > 0.0f ? o[mb][r] / lt : 0.0f);
         }
       }
     }
@@ -925,9 +936,12 @@ __global__ __launch_bounds__(64 * NW) void flash_decode_gqa_wave_kernel(
   float* const ws = s_state + wave * WS;
   if (col < G) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<float4v*>(ws + col * D + 16 * grp + 4 * r) =
-          float4v{o[0][r], o[1][r], o[2][r], o[3][r]};
+    for (int r = 0; r < 4; ++r) {
+#pragma unroll
+      for (int c = 0; c < VW; c += 4)
+        *reinterpret_cast<float4v*>(ws + col * D + VW * (4 * grp + r) + c) =
+            float4v{o[c][r], o[c + 1][r], o[c + 2][r], o[c + 3][r]};
+    }
     if (grp == 0) {
       ws[16 * D + col] = m;
       ws[16 * D + 16 + col] = lt;
@@ -1369,11 +1383,11 @@ struct DecodeArgs {
   int splits;
 };
 
-// 16-byte aligned caches: D = 64 GQA groups on flash_decode_gqa_wave_kernel
-// (matrix cores, K / V straight into registers), one head per workgroup (MHA,
-// or GQA sharing switched off) on flash_decode_mha_wave_kernel (VALU, K / V
-// straight into registers), D = 128 GQA groups and long D = 64 single-head
-// splits on the direct-to-LDS pipelined kernel. Unaligned caches: one query
+// 16-byte aligned caches: GQA groups on flash_decode_gqa_wave_kernel (matrix
+// cores, K / V straight into registers), one head per workgroup (MHA, or GQA
+// sharing switched off) on flash_decode_mha_wave_kernel (VALU, K / V straight
+// into registers), long D = 64 single-head splits on the direct-to-LDS
+// pipelined kernel. Unaligned caches: one query
 // head per workgroup on the register kernel with 8 key steps in flight per
 // lane; GQA groups on the register-staged LDS-tile kernel.
 
@@ -1381,8 +1395,11 @@ struct DecodeArgs {
 // blocks: up to 8 blocks, one wave per block (1, 2, 4 or 8 waves, so a
 // one-block split is one wave with no LDS merge); more, 8 waves with every
 // block in flight at once (2 or 4 per wave) or a ring of 4.
-template <int G, bool PARTIAL>
+template <int D, int G, bool PARTIAL>
 void launch_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, hipStream_t s) {
+  // A block is 2 D bytes per lane in registers: up to 4 in flight at D = 64,
+  // 2 at D = 128.
+  constexpr int PMAX = D == 64 ? 4 : 2;
   const long long keys = (a.kv_len + a.splits - 1) / a.splits;
   const long long blocks = (keys + 31) / 32;
   auto go = [&](auto kernel, int waves) {
@@ -1390,25 +1407,22 @@ void launch_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, 
                                        a.group_size, a.kv_head_stride, a.scale, a.splits);
   };
   if (blocks <= 1) {
-    go(flash_decode_gqa_wave_kernel<G, 1, 1, false, PARTIAL>, 1);
+    go(flash_decode_gqa_wave_kernel<D, G, 1, 1, false, PARTIAL>, 1);
   } else if (blocks <= 2) {
-    go(flash_decode_gqa_wave_kernel<G, 2, 1, false, PARTIAL>, 2);
+    go(flash_decode_gqa_wave_kernel<D, G, 2, 1, false, PARTIAL>, 2);
   } else if (blocks <= 4) {
-    go(flash_decode_gqa_wave_kernel<G, 4, 1, false, PARTIAL>, 4);
+    go(flash_decode_gqa_wave_kernel<D, G, 4, 1, false, PARTIAL>, 4);
   } else if (blocks <= 8) {
-    go(flash_decode_gqa_wave_kernel<G, 8, 1, false, PARTIAL>, 8);
+    go(flash_decode_gqa_wave_kernel<D, G, 8, 1, false, PARTIAL>, 8);
   } else if (blocks <= 16) {
-    go(flash_decode_gqa_wave_kernel<G, 8, 2, false, PARTIAL>, 8);
-  } else if (blocks <= 32) {
-    go(flash_decode_gqa_wave_kernel<G, 8, 4, false, PARTIAL>, 8);
+    go(flash_decode_gqa_wave_kernel<D, G, 8, 2, false, PARTIAL>, 8);
+  } else if (PMAX == 4 && blocks <= 32) {
+    go(flash_decode_gqa_wave_kernel<D, G, 8, PMAX, false, PARTIAL>, 8);
   } else {
-    go(flash_decode_gqa_wave_kernel<G, 8, 4, true, PARTIAL>, 8);
+    go(flash_decode_gqa_wave_kernel<D, G, 8, PMAX, true, PARTIAL>, 8);
   }
 }
 
-// flash_decode_mha_wave_kernel's shape, as launch_wave's: one wave per
-// 32-key block up to 8 blocks, then 8 waves with 2 (or, at D = 64, 4) blocks
-// in flight, then a ring.
 template <int D, bool PARTIAL>
 void launch_mha_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 grid, hipStream_t s) {
   const long long keys = (a.kv_len + a.splits - 1) / a.splits;
@@ -1438,8 +1452,8 @@ void launch_mha_wave(const DecodeArgs& a, float* part_o, float* part_ml, dim3 gr
 template <int D, int G, bool VEC, bool PARTIAL>
 void launch_split(const DecodeArgs& a, float* part_o, float* part_ml, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(a.n_heads / G), static_cast<unsigned>(a.splits));
-  if constexpr (VEC && D == 64 && G >= 2) {
-    launch_wave<G, PARTIAL>(a, part_o, part_ml, grid, s);
+  if constexpr (VEC && G >= 2) {
+    launch_wave<D, G, PARTIAL>(a, part_o, part_ml, grid, s);
   } else if constexpr (VEC) {
     // One head per workgroup: the register-fed kernel, except at D = 64 for
     // splits past 8 waves x 4 blocks (its ring streamed a TinyLlama head without
@@ -1553,7 +1567,7 @@ void attention_decode_any(const eng_half* q, const eng_half* k, const eng_half* 
   // 256 (more splits only add partial states to merge); the result does not
   // depend on the split count beyond rounding.
   const bool vec = aligned_to(k, 16) && aligned_to(v, 16) && kv_head_stride % 8 == 0;
-  const bool wave_kernel = vec && head_dim == 64 && G >= 2;
+  const bool wave_kernel = vec && G >= 2;
   const int req = split_kv == 0 ? auto_splits(kv_len, n_heads / G, wave_kernel) : split_kv;
   a.splits = static_cast<int>(std::max<long long>(1, std::min<long long>({req, kv_len, 256})));
   if (head_dim == 64) {

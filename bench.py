@@ -732,14 +732,16 @@ def rows_ffn(eng, timer) -> list:
 
 
 ATTENTION_CASES = [(512, 32, 4, 64), (2048, 32, 4, 64), (8192, 32, 4, 64), (16384, 32, 4, 64),
-                   (32768, 32, 4, 64), (512, 32, 32, 128), (2048, 32, 32, 128), (8192, 32, 32, 128)]
+                   (32768, 32, 4, 64), (512, 32, 32, 128), (2048, 32, 32, 128), (8192, 32, 32, 128),
+                   (8192, 32, 8, 128), (32768, 32, 8, 128)]
 
 
 def rows_attention(eng, timer, cases=ATTENTION_CASES, extra_variants=True) -> list:
     """Decode attention at the reference's benchmark shapes (bench_kernels.cu:
     1079-1092): TinyLlama 32/4 heads at D = 64 and Llama-2-7B 32/32 at D = 128,
-    cold KV caches (about 1 GiB of rotating copies). Bytes: K and V once plus
-    q and out, 2 (2 H_kv L D + 2 H D)."""
+    plus GQA at D = 128 (32/8 heads, the Llama-3-8B layout, which the reference's
+    kernel also takes), cold KV caches (about 1 GiB of rotating copies). Bytes:
+    K and V once plus q and out, 2 (2 H_kv L D + 2 H D)."""
     rows = []
     rng = np.random.default_rng(11)
     f = eng.lib.eng_attention_decode_with_mode_f16
@@ -752,7 +754,7 @@ def rows_attention(eng, timer, cases=ATTENTION_CASES, extra_variants=True) -> li
         do = eng.empty(H * D, np.uint16)
         sc = 1.0 / np.sqrt(D)
         nbytes = 2 * (2 * Hkv * L * D + 2 * H * D)
-        arch = "TinyLlama" if Hkv == 4 else "Llama-2-7B"
+        arch = "TinyLlama" if Hkv == 4 else ("Llama-2-7B" if Hkv == H else "GQA-8 (Llama-3-8B layout)")
         variants = [("auto splits", 0, 1)]
         if extra_variants and L >= 8192:
             variants.append(("split_kv=1", 1, 1))

@@ -11,7 +11,7 @@ Two tolerances are checked everywhere:
   hardware exp2 rounding once each (<= 4 u max_j |s_j| + 8 u relative), so the
   weights carry at most 2 max_j e_j + 4 u max_j |s_j| + 8 u relative error;
   the fp32 sums of p_j v_j and p_j add (s_kv + 24) u relative to
-  sum_j w_j |v_j|; the matrix-core kernel (D = 64 GQA) multiplies V by each
+  sum_j w_j |v_j|; the matrix-core kernel (GQA groups) multiplies V by each
   weight as two fp16 terms (hi + lo, scaled by 2^7), which adds 4 u relative
   and at most 2^-32 absolute per weight (the max key's weight is >= 1, so
   s_kv 2^-32 max_j |v_j| in all); the output adds half rounding 2^-11 |y| + 2^-25:
@@ -262,6 +262,26 @@ def test_attention_decode_single_head_every_shape(gpu, orc, D):
         check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"single head D={D} L={L} split={split}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_attention_decode_gqa_every_shape(gpu, orc, D):
+    """GQA groups (4 query heads per KV head; also 2 and 8) on the matrix-core
+    kernel, one split, lengths of 1 to 70 32-key blocks: 1, 2, 4 and 8 waves,
+    1, 2 and (D = 64) 4 blocks in flight per wave, and the ring (D = 128 past 16
+    blocks, D = 64 past 32); ragged last blocks and splits, against the oracle."""
+    rng = np.random.default_rng(500 + D)
+    sc = 1.0 / np.sqrt(D)
+    cases = [(8, 2, L, split) for L, split in ((1, 1), (31, 1), (33, 1), (64, 1), (100, 1), (250, 1),
+                                                (256, 1), (290, 1), (512, 1), (530, 1), (1000, 1),
+                                                (1024, 1), (1060, 1), (2240, 1), (1111, 2), (777, 3))]
+    cases += [(16, 2, 530, 1), (16, 2, 2240, 0), (4, 2, 290, 1), (4, 2, 1060, 2)]
+    for H, Hkv, L, split in cases:
+        q = rand_half(orc, rng, (H, D))
+        k = rand_half(orc, rng, (Hkv, L, D))
+        v = rand_half(orc, rng, (Hkv, L, D))
+        got = gpu_decode(gpu, q, k, v, L, H, Hkv, D, L * D, sc, split)
+        check_decode(got, q, k, v, H, Hkv, D, L, L * D, sc, orc, f"GQA H={H}/{Hkv} D={D} L={L} split={split}")
+
+
 def test_attention_decode_unaligned_cache_takes_scalar_loads(gpu, orc):
     """K / V not 16-byte aligned, and a head stride that is not a multiple of 8."""
     rng = np.random.default_rng(41)
@@ -280,12 +300,13 @@ def test_attention_decode_unaligned_cache_takes_scalar_loads(gpu, orc):
     check_decode(got, q, k[1:], v[1:], H, Hkv, D, L, stride, sc, orc, "unaligned cache")
 
 
-@pytest.mark.parametrize("L", [8192, 32768])
-def test_attention_decode_long_sequence(gpu, orc, L):
-    """Reference attention_decode_long_sequence: GQA 8:1, D = 64, a strided
-    KV cache padded with NaN past kv_len (never read), O(1) outputs."""
-    rng = np.random.default_rng(L)
-    H, Hkv, D = 8, 1, 64
+@pytest.mark.parametrize("L,D", [(8192, 64), (32768, 64), (8192, 128), (32768, 128)])
+def test_attention_decode_long_sequence(gpu, orc, L, D):
+    """Reference attention_decode_long_sequence: GQA 8:1, D = 64 (and the same
+    at D = 128), a strided KV cache padded with NaN past kv_len (never read),
+    O(1) outputs."""
+    rng = np.random.default_rng(L + D)
+    H, Hkv = 8, 1
     stride = (L + 17) * D
     nan16 = np.uint16(0x7E00)
     sc = 1.0 / np.sqrt(D)
