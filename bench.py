@@ -573,27 +573,38 @@ def rows_few_rows(eng, timer) -> list:
 
 
 def rows_reference_api(eng, timer) -> list:
+    """The reference's published decode rows through the reference-layout API
+    (W [K x N]): fp32 gemv, half-I/O gemv_fp16 and fp32-weight rmsnorm_linear
+    at 1 x 4096 x 4096 and 1 x 12288 x 4096 (README / results.json rows), cold
+    weights (rotating copies past the 256 MB Infinity Cache)."""
     rows = []
     rng = np.random.default_rng(8)
-    # Reference-API GEMVs: fp32 gemv and half-I/O gemv_fp16, 4096x4096, cold.
-    K = N = 4096
-    R = 16
-    Wf = rotating(eng, (0.02 * rng.standard_normal((K, N), dtype=np.float32)), R)
-    dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
-    dy = eng.empty(N, np.float32)
-    f = eng.lib.eng_gemv_f32
-    st = timer.sampled(lambda i, s: f(Wf[i % R].ptr, dx.ptr, dy.ptr, N, K, s))
-    rows.append(hbm_row("gemv (fp32 W) 4096x4096 cold", st, 4 * K * N + 8 * K))
-    for w in Wf:
-        w.free()
-    Wh = rotating(eng, rand_f16(rng, (K, N)), 32)
-    dxh = eng.upload(rng.standard_normal(K, dtype=np.float32).astype(np.float16).view(np.uint16))
-    dyh = eng.empty(N, np.uint16)
-    f = eng.lib.eng_gemv_f16
-    st = timer.sampled(lambda i, s: f(Wh[i % 32].ptr, dxh.ptr, dyh.ptr, N, K, s))
-    rows.append(hbm_row("gemv_fp16 (half x/out) 4096x4096 cold", st, 2 * K * N + 4 * K))
-    for w in Wh:
-        w.free()
+    K = 4096
+    for N in (4096, 12288):
+        Wf32 = (0.02 * rng.standard_normal((K, N), dtype=np.float32))
+        R = max(2, (1 << 30) // Wf32.nbytes + 1)
+        Wf = rotating(eng, Wf32, R)
+        dx = eng.upload(rng.standard_normal(K, dtype=np.float32))
+        dg = eng.upload((1 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+        dy = eng.empty(N, np.float32)
+        f = eng.lib.eng_gemv_f32
+        st = timer.sampled(lambda i, s: f(Wf[i % R].ptr, dx.ptr, dy.ptr, N, K, s))
+        rows.append(hbm_row(f"gemv (fp32 W) {K}x{N} cold", st, 4 * K * N + 4 * K + 4 * N))
+        f = eng.lib.eng_rmsnorm_linear_f32
+        st = timer.sampled(lambda i, s: f(dx.ptr, dg.ptr, Wf[i % R].ptr, dy.ptr, 1, N, K, 1e-5, s))
+        rows.append(hbm_row(f"rmsnorm_linear (fp32 W) 1x{N}x{K} cold", st, 4 * K * N + 8 * K + 4 * N))
+        for d in Wf + [dx, dg, dy]:
+            d.free()
+        Wf16 = rand_f16(rng, (K, N))
+        R = max(2, (1 << 30) // Wf16.nbytes + 1)
+        Wh = rotating(eng, Wf16, R)
+        dxh = eng.upload(rng.standard_normal(K, dtype=np.float32).astype(np.float16).view(np.uint16))
+        dyh = eng.empty(N, np.uint16)
+        f = eng.lib.eng_gemv_f16
+        st = timer.sampled(lambda i, s: f(Wh[i % R].ptr, dxh.ptr, dyh.ptr, N, K, s))
+        rows.append(hbm_row(f"gemv_fp16 (half x/out) {K}x{N} cold", st, 2 * K * N + 2 * K + 2 * N))
+        for d in Wh + [dxh, dyh]:
+            d.free()
     return rows
 
 
@@ -603,13 +614,15 @@ def rows_gemm(eng, timer) -> list:
     # configs 1 and 4: FP32 GEMMs on MFMA.
     f = eng.lib.eng_matmul_f32
     for cfg, M, N, K, seed in ((1, 512, 512, 512, 0), (4, 4096, 4096, 4096, 3), (4, 512, 11008, 4096, 3),
-                               (4, 512, 4096, 11008, 3)):
+                               (4, 512, 4096, 11008, 3), (0, 1024, 1024, 1024, 3), (0, 2048, 2048, 2048, 3)):
         r3 = np.random.default_rng(seed)
         dA = eng.upload(r3.uniform(-1, 1, (M, K)).astype(np.float32))
         dB = eng.upload(r3.uniform(-1, 1, (K, N)).astype(np.float32))
         dC = eng.empty((M, N), np.float32)
         st = timer.sampled(lambda i, s: f(dA.ptr, dB.ptr, dC.ptr, M, N, K, s))
-        rows.append(gemm_row(f"matmul_f32 {M}x{N}x{K} (config {cfg})", st, M, N, K))
+        # config 0: the reference's other published matmul_register_tiled sizes
+        tag = f"(config {cfg})" if cfg else "(reference README size)"
+        rows.append(gemm_row(f"matmul_f32 {M}x{N}x{K} {tag}", st, M, N, K))
         dA.free(), dB.free(), dC.free()
 
     # Reference bench shape: rmsnorm_linear (fp32 W) at M = 512, 4096 x 4096.
@@ -1195,12 +1208,19 @@ SUMMARY_ROWS = (
     ("cfg4_gemm_4096_frac", "matmul_f32 4096x4096x4096 (config 4)", "frac_fp32_mfma_peak"),
     ("cfg4_gemm_512x11008x4096_tflops", "matmul_f32 512x11008x4096 (config 4)", "TFLOP/s"),
     ("cfg4_gemm_512x4096x11008_tflops", "matmul_f32 512x4096x11008 (config 4)", "TFLOP/s"),
+    ("gemm_1024_tflops", "matmul_f32 1024x1024x1024", "TFLOP/s"),
+    ("gemm_2048_tflops", "matmul_f32 2048x2048x2048", "TFLOP/s"),
     ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
+    ("gemv_fp32_12288_us", "gemv (fp32 W) 4096x12288 cold", "us_per_call"),
     ("gemv_fp16_halfio_4096_us", "gemv_fp16 (half x/out) 4096x4096 cold", "us_per_call"),
+    ("gemv_fp16_halfio_12288_us", "gemv_fp16 (half x/out) 4096x12288 cold", "us_per_call"),
+    ("rmsnorm_linear_f32_4096_us", "rmsnorm_linear (fp32 W) 1x4096x4096 cold", "us_per_call"),
     ("attn_tinyllama_512_us", "attention_decode TinyLlama L=512 H=32/4 D=64 cold, auto splits", "us_per_call"),
     ("attn_tinyllama_2048_us", "attention_decode TinyLlama L=2048 H=32/4 D=64 cold, auto splits", "us_per_call"),
     ("attn_tinyllama_32768_us", "attention_decode TinyLlama L=32768 H=32/4 D=64 cold, auto splits", "us_per_call"),
     ("attn_llama7b_8192_us", "attention_decode Llama-2-7B L=8192 H=32/32 D=128 cold, auto splits", "us_per_call"),
+    ("attn_gqa_d128_8192_us", "attention_decode GQA-8 (Llama-3-8B layout) L=8192 H=32/8 D=128 cold, auto splits",
+     "us_per_call"),
 )
 
 
