@@ -3,7 +3,10 @@
 Index arithmetic past 32 bits is exercised where it matters for the decode
 path: an output-major fp16 GEMV with W [N x K] of 2^31 + 2^18 elements, the
 transpose of that W into the reference layout, and the reference-layout
-split-K GEMV over it. W repeats every 64 rows (built on the device by
+split-K GEMV over it; and for the MFMA GEMM, whose direct loads address each
+tile through a buffer descriptor (a 64-bit base and a 32-bit range clamped at
+4 GiB): fp16 B [N x K] of the same size through rmsnorm_linear_f16w_nk at 128
+rows, and an fp32 A [M x 4096] of 4 GiB + 1 MiB through matmul. W repeats every 64 rows (built on the device by
 doubling copies of one 64-row block), so every output equals the output of
 its row modulo 64, bit for bit (the kernels compute each row / column with
 the same arithmetic in the same order); the first 64 outputs are checked
@@ -25,11 +28,11 @@ N = (1 << 19) + PERIOD  # N * K = 2^31 + 2^18 elements (4 GiB + 512 KiB of fp16)
 
 
 def tiled_rows(eng, block, rows):
-    """Device [rows x K] fp16 matrix repeating `block` ([PERIOD x K]) by rows."""
-    d = eng.empty((rows, block.shape[1]), np.uint16)
+    """Device [rows x cols] matrix repeating `block` ([PERIOD x cols]) by rows."""
+    d = eng.empty((rows, block.shape[1]), block.dtype)
     eng.call("eng_memcpy_h2d", d.ptr, block.ctypes.data, block.nbytes)
     have = block.shape[0]
-    row_bytes = block.shape[1] * 2
+    row_bytes = block.shape[1] * block.itemsize
     while have < rows:
         n = min(have, rows - have)
         eng.call("eng_memcpy_d2d", d.ptr + have * row_bytes, d.ptr, n * row_bytes)
@@ -82,3 +85,47 @@ def test_gemv_past_2_31_elements_both_layouts(gpu, orc):
     helpers.assert_within(block_kn, y64, derived, "reference-layout gemv block 0 [derived bound]")
     helpers.assert_within(block_kn, y64, stat, "reference-layout gemv block 0 [statistical bound]")
     A.free()
+
+
+def test_gemm_operands_past_4_gib(gpu, orc):
+    rng = np.random.default_rng(32)
+    # fp16 B [N x K] (4 GiB + 512 KiB) at M = 128: the GEMM path of rmsnorm_linear
+    M = 128
+    W0 = (0.02 * rng.standard_normal((PERIOD, K), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = tiled_rows(gpu, W0, N)
+    dx, dg = gpu.upload(x), gpu.upload(g)
+    out = gpu.empty((M, N), np.float32)
+    print(f"large: rmsnorm_linear_f16w_nk M={M} N={N} K={K}", flush=True)
+    gpu.call("eng_rmsnorm_linear_f16w_nk", dx.ptr, dg.ptr, W.ptr, out.ptr, M, N, K, 1e-5, None)
+    gpu.sync()
+    got = out.download().reshape(M, N // PERIOD, PERIOD)
+    W.free()
+    out.free()
+    assert np.array_equal(got, np.broadcast_to(got[:, :1, :], got.shape)), "columns not periodic"
+    rows = np.array([0, 1, 63, 64, M - 1])
+    Wt = np.ascontiguousarray(W0.T)  # [K x PERIOD]
+    y64 = orc.rmsnorm_linear(x[rows], g, Wt, 1e-5).astype(np.float64)
+    derived, stat = helpers.rmsnorm_linear_bounds(x[rows], g, Wt, y64, K)
+    helpers.assert_within(got[rows, 0, :], y64, derived, "rmsnorm_linear_f16w_nk [derived bound]")
+    helpers.assert_within(got[rows, 0, :], y64, stat, "rmsnorm_linear_f16w_nk [statistical bound]")
+
+    # fp32 A [M x K] of 4 GiB + 1 MiB, B [K x 128]
+    MA, NB = (1 << 18) + PERIOD, 128
+    A0 = rng.uniform(-1, 1, (PERIOD, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, NB)).astype(np.float32)
+    A = tiled_rows(gpu, A0, MA)
+    dB = gpu.upload(B)
+    C = gpu.empty((MA, NB), np.float32)
+    print(f"large: matmul_f32 M={MA} N={NB} K={K}", flush=True)
+    gpu.call("eng_matmul_f32", A.ptr, dB.ptr, C.ptr, MA, NB, K, None)
+    gpu.sync()
+    got = C.download().reshape(MA // PERIOD, PERIOD, NB)
+    A.free()
+    C.free()
+    assert np.array_equal(got, np.broadcast_to(got[:1], got.shape)), "rows not periodic"
+    y64 = orc.matmul(A0, B).astype(np.float64)
+    derived, stat = helpers.dot_bounds(helpers.absdot(A0, B) + np.abs(y64), y64, K)
+    helpers.assert_within(got[0], y64, derived, "matmul block 0 [derived bound]")
+    helpers.assert_within(got[0], y64, stat, "matmul block 0 [statistical bound]")
