@@ -734,9 +734,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_sk_kernel(
 // Split tail tiles: C = the tile's records added in workgroup order. One
 // block per (tail tile, 1024 elements); tiles one workgroup covered whole are
 // skipped (already stored).
-template <int BM, int BN>
+template <int BM, int BN, bool EDGE = false>
 __global__ __launch_bounds__(256) void gemm_sk_fixup_kernel(const float* __restrict__ rec,
-                                                            float* __restrict__ C, int N,
+                                                            float* __restrict__ C, int M, int N,
                                                             int tiles_m, int tiles_n,
                                                             SkPlan plan) {
   const long long t = blockIdx.x;
@@ -754,9 +754,16 @@ __global__ __launch_bounds__(256) void gemm_sk_fixup_kernel(const float* __restr
   }
   int tm, tn;
   tile_of(plan.dp + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
-  const int row = e / BN;
-  const int col = e % BN;
-  *reinterpret_cast<floatx4*>(C + static_cast<long long>(tm * BM + row) * N + tn * BN + col) = v;
+  const int row = tm * BM + e / BN;
+  const int col = tn * BN + e % BN;
+  float* dst = C + static_cast<long long>(row) * N + col;
+  if constexpr (!EDGE) {
+    *reinterpret_cast<floatx4*>(dst) = v;
+  } else if (row < M) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (col + q < N) dst[q] = v[q];
+  }
 }
 
 // The direct-load kernel can be switched off (ENGINE_GEMM_NO_DMA=1) to
@@ -905,7 +912,7 @@ bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
       a.A, B, a.C, rec, M, N, K, tiles_m, tiles_n, plan);
   ENG_LAUNCH_CHECK();
   gemm_sk_fixup_kernel<BM, BN><<<dim3(static_cast<unsigned>(T - cus), BM * BN / 1024), 256, 0,
-                                 stream>>>(rec, a.C, N, tiles_m, tiles_n, plan);
+                                 stream>>>(rec, a.C, M, N, tiles_m, tiles_n, plan);
   ENG_LAUNCH_CHECK();
   return true;
 }
@@ -945,7 +952,395 @@ void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp16 weights on the fp16 matrix cores: C[M x N] = diag(rscale) (P0 + P1 +
+// P2) . B^T for B fp16 [N x K] (output-major weights) and the three fp16
+// planes P of the scaled activation rows (launch_rmsnorm_split3). Every
+// product of an fp16 plane value and an fp16 weight is exact in fp32 and the
+// planes sum to the scaled row (to 2^-39 of its largest value), so this is
+// the FP32 GEMM's arithmetic on v_mfma_f32_32x32x16_f16, which runs 16 times
+// the FP32 instruction's rate: three of them (one per plane) per 32 x 32 x 16
+// block against eight v_mfma_f32_32x32x2_f32.
+//
+// Tiles of 128 x 128, 8 waves (4 x 2) of 32 x 64 each (two 32 x 32 blocks:
+// per 16-deep slice three plane fragments and two B fragments feed six
+// MFMAs), K step 32 (two slices), four LDS stages of 32 KiB (the three plane
+// tiles and the B tile) and one workgroup per CU. The planes are K-blocked
+// (launch_rmsnorm_split3), so a plane tile of one K step is 8 KiB in one
+// piece and every load instruction reads whole cache lines; with the planes
+// row-major each instruction touched 16 rows of 64 bytes, half of each
+// 128-byte line, and the vector memory path, not the MFMAs, set the pace.
+// Operand layout of the instruction (checked on the device): A[i][k] in lane
+// i + 32 (k / 8) element k % 8, B[k][j] in lane j + 32 (k / 8) element k %
+// 8, the accumulator as for the FP32 instruction. Each lane's fragment is one
+// 16-byte LDS read of its row (plane or B^T row); tiles are rows of 4
+// 16-byte chunks, chunk c of row r at c ^ swz_rows_h(r). Direct loads, the
+// slice read-ahead, the stage hand-over and the interleaved fetch follow the
+// FP32 kernel. Tile counts past one round of one tile per CU take the
+// stream-K split of gemm_sk_kernel (gemm_h3_sk_kernel).
+namespace h3 {
+constexpr int BM = 128;
+constexpr int BN = 128;
+constexpr int WAVES = 8;
+constexpr int THREADS = 64 * WAVES;
+constexpr int PT = BM * BK;                   // halves of one plane tile
+constexpr int A_INST = 3 * PT / 8 / THREADS;  // direct loads per thread per K step (A planes)
+constexpr int B_INST = BN * BK / 8 / THREADS; // (B)
+constexpr int LOADS = A_INST + B_INST;
+static_assert(A_INST == 3 && B_INST == 1, "tile shape");
+
+// WGN waves along N, WAVES / WGN along M; each wave a WM x WN block of the
+// tile as MB x NB 32 x 32 MFMA blocks.
+template <int WGN>
+struct Shape {
+  static constexpr int WM = BM / (WAVES / WGN);
+  static constexpr int WN = BN / WGN;
+  static constexpr int MB = WM / 32;
+  static constexpr int NB = WN / 32;
+};
+template <int WGN>
+using Acc = floatx16[Shape<WGN>::MB][Shape<WGN>::NB];
+}  // namespace h3
+
+// K tiles [kt0, kt1) of the 128 x 128 tile at (m0, n0) into acc (zeroed
+// here); ends with a barrier, so a following call may refill the stages.
+template <int S, int WGN, bool EDGE>
+__device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
+                                        const _Float16* __restrict__ B, int M, int N, int K,
+                                        int m0, int n0, int kt0, int kt1, h3::Acc<WGN>& acc) {
+  using namespace h3;
+  static_assert(S >= 3 && S <= 4, "stages");
+  constexpr int WM = Shape<WGN>::WM;
+  constexpr int WN = Shape<WGN>::WN;
+  constexpr int MB = Shape<WGN>::MB;
+  constexpr int NB = Shape<WGN>::NB;
+  typedef _Float16 halfx8v __attribute__((ext_vector_type(8)));
+  __shared__ __attribute__((aligned(1024))) _Float16 As0[3 * PT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As1[3 * PT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As2[3 * PT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As3[S > 3 ? 3 * PT : 8];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs0[BN * BK];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs1[BN * BK];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs2[BN * BK];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs3[S > 3 ? BN * BK : 8];
+  auto a_stage = [&](auto st) -> _Float16* {
+    if constexpr (decltype(st)::value == 0) return As0;
+    else if constexpr (decltype(st)::value == 1) return As1;
+    else if constexpr (decltype(st)::value == 2) return As2;
+    else return As3;
+  };
+  auto b_stage = [&](auto st) -> _Float16* {
+    if constexpr (decltype(st)::value == 0) return Bs0;
+    else if constexpr (decltype(st)::value == 1) return Bs1;
+    else if constexpr (decltype(st)::value == 2) return Bs2;
+    else return Bs3;
+  };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 31;
+  const int lg = lane >> 5;
+  const int wm = wave / WGN;
+  const int wn = wave % WGN;
+
+  // Direct loads: instruction j of wave w fills 16-byte slots (8 j + w) * 64 +
+  // lane of the stage; A slots 512 p .. 512 p + 511 are plane p's tile (so
+  // instruction j loads plane j), B's 512 slots its tile. Slot q of a tile is
+  // row q / 4, position q % 4, holding chunk (q % 4) ^ swz_rows_h(row).
+  // The planes are K-blocked ([K / 32][M][32] each): the tile's rows of one
+  // K step are a contiguous slab of 64-byte rows, so a load instruction
+  // covers 1 KiB in one piece (whole cache lines).
+  unsigned a_off[A_INST];
+  unsigned b_off;
+#pragma unroll
+  for (int j = 0; j < A_INST; ++j) {
+    const int q = wave * 64 + lane;  // slot within plane j's tile
+    const int r = q >> 2;
+    const int c = (q & 3) ^ swz_rows_h(r);
+    const int row = EDGE ? min(m0 + r, M - 1) - m0 : r;
+    a_off[j] = static_cast<unsigned>(row * BK + 8 * c) * 2u;
+  }
+  {
+    const int q = wave * 64 + lane;
+    const int r = q >> 2;
+    const int c = (q & 3) ^ swz_rows_h(r);
+    const int row = EDGE ? min(n0 + r, N - 1) - n0 : r;
+    b_off = static_cast<unsigned>(row * K + 8 * c) * 2u;
+  }
+  const long long plane = static_cast<long long>(M) * K;
+  const long long b_len = static_cast<long long>(N) * K;
+  auto fetch = [&](_Float16* as, _Float16* bs, int kt) {
+    const int k0 = kt * BK;
+    const long long a0 = (static_cast<long long>(kt) * M + m0) * BK;
+    const long long b0 = static_cast<long long>(n0) * K + k0;
+    const unsigned a_bytes = bytes_left<_Float16>(plane, a0);
+#pragma unroll
+    for (int j = 0; j < A_INST; ++j)
+      lds_buf16(P + j * plane + a0, a_bytes, a_off[j], as + j * PT + 8 * wave * 64);
+    lds_buf16(B + b0, bytes_left<_Float16>(b_len, b0), b_off, bs + 8 * wave * 64);
+  };
+
+  struct Slice {
+    halfx8v a[3][MB];
+    halfx8v b[NB];
+  };
+  auto read_s = [&](const _Float16* as, const _Float16* bs, int sl, Slice& f) {
+    const int cq = 2 * sl + lg;  // this lane's chunk: k = 16 sl + 8 lg .. + 7
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int r = wm * WM + mb * 32 + li;
+        f.a[p][mb] = *reinterpret_cast<const halfx8v*>(as + p * PT + r * BK + 8 * (cq ^ swz_rows_h(r)));
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int r = wn * WN + nb * 32 + li;
+      f.b[nb] = *reinterpret_cast<const halfx8v*>(bs + r * BK + 8 * (cq ^ swz_rows_h(r)));
+    }
+  };
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
+  auto mma_s = [&](const Slice& f) {
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[p][mb], f.b[nb], acc[mb][nb], 0,
+                                                               0, 0);
+    }
+  };
+  auto pin = [] {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  };
+  // After the stage barrier: one MFMA, the next slice's fragment reads
+  // (six MFMAs ahead of their use: a slice has only six per wave, so reads
+  // placed after the fetch would leave one MFMA to cover their latency),
+  // then the fetch's loads one per MFMA.
+  auto pin_after_barrier = [] {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+  };
+
+  // As the FP32 kernel: the hand-over before a K step's last slice waits for
+  // the next tile (S - 2 later tiles stay in flight) and refills the current
+  // stage with the tile S steps ahead (clamped to the last tile: a duplicate
+  // load into a finished stage); the read after it takes the next tile's
+  // first slice (stale past the last tile, never used).
+  Slice x, y;
+  auto tile = [&](auto st, int kt) {
+    constexpr int cur = decltype(st)::value;
+    using Next = std::integral_constant<int, (cur + 1) % S>;
+    read_s(a_stage(st), b_stage(st), 1, y);
+    mma_s(x);
+    pin();
+    stage_barrier<(S - 2) * LOADS>();
+    fetch(a_stage(st), b_stage(st), min(kt + S, kt1 - 1));
+    read_s(a_stage(Next{}), b_stage(Next{}), 0, x);
+    mma_s(y);
+    pin_after_barrier();
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  fetch(As0, Bs0, kt0);
+  fetch(As1, Bs1, min(kt0 + 1, kt1 - 1));
+  fetch(As2, Bs2, min(kt0 + 2, kt1 - 1));
+  if constexpr (S > 3) fetch(As3, Bs3, min(kt0 + 3, kt1 - 1));
+  stage_barrier<(S - 1) * LOADS>();
+  read_s(As0, Bs0, 0, x);
+  int kt = kt0;
+  for (; kt + S - 1 < kt1; kt += S) {
+    tile(I0{}, kt);
+    tile(I1{}, kt + 1);
+    tile(I2{}, kt + 2);
+    if constexpr (S > 3) tile(I3{}, kt + 3);
+  }
+  if (kt < kt1) tile(I0{}, kt);
+  if (kt + 1 < kt1) tile(I1{}, kt + 1);
+  if constexpr (S > 3) {
+    if (kt + 2 < kt1) tile(I2{}, kt + 2);
+  }
+  wait_all_memory();
+  __syncthreads();
+}
+
+// acc times the row's 2^-e into dst (row r, column c of the tile at dst[r ld
+// + c]); GUARD keeps rows < rows_left and columns < cols_left. Rows past M
+// (an edge tile's clamped rows) take row M - 1's scale.
+template <int WGN, bool GUARD>
+__device__ __forceinline__ void h3_store(const h3::Acc<WGN>& acc, const float* __restrict__ rscale,
+                                         int M, int m0, float* __restrict__ dst, long long ld,
+                                         int rows_left, int cols_left) {
+  using namespace h3;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 31;
+  const int lg = lane >> 5;
+  const int wm = wave / WGN;
+  const int wn = wave % WGN;
+
+  // Accumulator element v of lane (li, lg): row 8 (v / 4) + 4 lg + v % 4 of
+  // the block, column li.
+#pragma unroll
+  for (int mb = 0; mb < Shape<WGN>::MB; ++mb) {
+#pragma unroll
+    for (int nb = 0; nb < Shape<WGN>::NB; ++nb) {
+      const int col = wn * Shape<WGN>::WN + nb * 32 + li;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = wm * Shape<WGN>::WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        if (!GUARD || (r < rows_left && col < cols_left))
+          dst[r * ld + col] = acc[mb][nb][v] * rscale[min(m0 + r, M - 1)];
+      }
+    }
+  }
+}
+
+template <int S, int WGN, bool EDGE>
+__global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
+    const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
+    float* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
+  int tm, tn;
+  tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * h3::BM;
+  const int n0 = tn * h3::BN;
+  h3::Acc<WGN> acc;
+  h3_tile<S, WGN, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
+  h3_store<WGN, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+                      N - n0);
+}
+
+// Stream-K form (the plan of gemm_sk_kernel): workgroups 0 .. dp - 1 compute
+// tiles 0 .. dp - 1 whole (whole rounds of one tile per CU), and the rest
+// split the remaining tiles' K tiles evenly, one workgroup per CU after its
+// data-parallel tiles; a split tile leaves one record per workgroup (scaled
+// rows, slot 0 its first tile, slot 1 its last) for gemm_sk_fixup_kernel.
+template <int S, int WGN, bool EDGE>
+__global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
+    const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
+    float* __restrict__ C, float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n,
+    SkPlan plan) {
+  constexpr int BM = h3::BM, BN = h3::BN;
+  h3::Acc<WGN> acc;
+  const int g = blockIdx.x;
+  const bool dp = g < plan.dp;
+  const long long s = dp ? 0 : g - plan.dp;
+  const long long i0 = dp ? 0 : sk_begin(s, plan);
+  const long long i1 = dp ? plan.nk : sk_begin(s + 1, plan);
+  const int first_tile = dp ? g : plan.dp;
+  for (long long it = i0; it < i1;) {
+    const long long t = it / plan.nk;
+    const int ka = static_cast<int>(it - t * plan.nk);
+    const long long tend = (t + 1) * plan.nk;
+    const int kb = static_cast<int>((i1 < tend ? i1 : tend) - t * plan.nk);
+    int tm, tn;
+    tile_of(first_tile + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM;
+    const int n0 = tn * BN;
+    h3_tile<S, WGN, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
+    if (ka == 0 && kb == plan.nk) {
+      h3_store<WGN, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+                          N - n0);
+    } else {
+      const int slot = it == i0 ? 0 : 1;
+      h3_store<WGN, false>(acc, rscale, M, m0,
+                           rec + (s * 2 + slot) * static_cast<long long>(BM * BN), BN, BM, BN);
+    }
+    it = t * plan.nk + kb;
+  }
+}
+
+// The fp16-MFMA form of the fp16-weight GEMM can be switched off
+// (ENGINE_GEMM_NO_H3=1) to compare it with the FP32 MFMA on converted weights.
+bool h3_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_NO_H3");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
 }  // namespace
+
+bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B) {
+  constexpr long long kLim = 0x7fffffffLL;
+  // K % 32 == 0, 16-byte aligned B rows, every lane's byte offset from a
+  // tile's corner (up to 128 rows of K halves) within a buffer load's 31 bits
+  return h3_enabled() && M > 0 && N > 0 && K > 0 && K % BK == 0 && M <= kLim && N <= kLim &&
+         K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM) * K * 2 <= kLim;
+}
+
+void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
+  ENG_CHECK(gemm_h3_applies(a.M, a.N, a.K, a.B) && aligned_to(a.P, 16) && a.rscale != nullptr,
+            "matmul (fp16 weights): shape or alignment not supported");
+  const int M = static_cast<int>(a.M), N = static_cast<int>(a.N), K = static_cast<int>(a.K);
+  const int tiles_m = (M + h3::BM - 1) / h3::BM;
+  const int tiles_n = (N + h3::BN - 1) / h3::BN;
+  const long long ntiles = static_cast<long long>(tiles_m) * tiles_n;
+  ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
+  const bool whole = M % h3::BM == 0 && N % h3::BN == 0;
+  // Stream-K when the last round of one tile per CU is at most half full
+  // (512 x 11008: 88 of 256, 148.7 -> 138.3 us; at 176 of 256 the records
+  // and the fix-up pass cost more than the split saves), with at least 8 K
+  // tiles per tile.
+  const long long cus = device_cu_count();
+  const long long tail = ntiles % cus;
+  const int nk = K / BK;
+  const bool split = sk_enabled() && ntiles > cus && tail != 0 && 2 * tail <= cus && nk >= 8;
+  SkPlan plan;
+  plan.dp = static_cast<int>(ntiles - tail);
+  plan.nk = nk;
+  plan.I = tail * nk;
+  plan.nsk = static_cast<int>(std::min<long long>(cus, plan.I));
+  auto go = [&](auto edge) {
+    constexpr bool E = decltype(edge)::value;
+    constexpr int S = 4, G = 2;  // four stages, waves 4 (M) x 2 (N) of 32 x 64
+    if (!split) {
+      gemm_h3_kernel<S, G, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
+          a.P, a.rscale, a.B, a.C, M, N, K, tiles_m, tiles_n);
+      ENG_LAUNCH_CHECK();
+      return;
+    }
+    StreamScratch records(
+        stream, static_cast<std::size_t>(plan.nsk) * 2 * h3::BM * h3::BN * sizeof(float), 2);
+    float* rec = static_cast<float*>(records.get());
+    gemm_h3_sk_kernel<S, G, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS, 0,
+                                 stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K, tiles_m, tiles_n,
+                                           plan);
+    ENG_LAUNCH_CHECK();
+    gemm_sk_fixup_kernel<h3::BM, h3::BN, E>
+        <<<dim3(static_cast<unsigned>(tail), h3::BM * h3::BN / 1024), 256, 0, stream>>>(
+            rec, a.C, M, N, tiles_m, tiles_n, plan);
+    ENG_LAUNCH_CHECK();
+  };
+  if (whole)
+    go(std::integral_constant<bool, false>{});
+  else
+    go(std::integral_constant<bool, true>{});
+}
 
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {
   ENG_CHECK(a.M <= 0x7fffffffLL && a.N <= 0x7fffffffLL && a.K <= 0x7fffffffLL,

@@ -156,6 +156,30 @@ void launch_gemm(const GemmArgs& a, hipStream_t stream);
 void launch_rmsnorm(const float* in, const float* weight, float* out, long long rows,
                     long long cols, float eps, hipStream_t stream);
 
+// The same rows scaled by 2^e_r (largest |value| of each row in [2^14, 2^15))
+// as three fp16 planes, p = 0..2, that sum to the scaled value; rscale[r] =
+// 2^-e_r. Each plane is K-blocked, [cols / 32][rows][32]: value (r, c) at
+// planes[p rows cols + ((c / 32) rows + r) 32 + c % 32]. Needs cols % 32 == 0
+// and 16-byte aligned in and planes.
+void launch_rmsnorm_split3(const float* in, const float* weight, _Float16* planes, float* rscale,
+                           long long rows, long long cols, float eps, hipStream_t stream);
+
+// C[M x N] = diag(rscale) (P[0] + P[1] + P[2]) . B^T on fp16 MFMA, B fp16
+// [N x K] (output-major weights), P the K-blocked planes of
+// launch_rmsnorm_split3.
+// Needs K % 32 == 0 and 16-byte aligned P and B.
+struct GemmH3Args {
+  const _Float16* P = nullptr;
+  const float* rscale = nullptr;
+  const _Float16* B = nullptr;
+  float* C = nullptr;
+  std::int64_t M = 0;
+  std::int64_t N = 0;
+  std::int64_t K = 0;
+};
+bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B);
+void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream);
+
 // out[i] = SiLU(g[i]) * u[i] in fp32.
 void launch_swiglu_f32(const float* g, const float* u, float* out, long long n,
                        hipStream_t stream);

@@ -302,6 +302,69 @@ def test_rmsnorm_linear_f16w_ragged_tiles(gpu, orc, M, N, K, layout):
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(65, 128, 32), (128, 128, 64), (200, 136, 96), (256, 256, 128),
+                                   (130, 300, 160), (1000, 257, 224)])
+@pytest.mark.parametrize("with_gamma", [True, False])
+def test_rmsnorm_linear_f16w_nk_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma):
+    # M > 64, fp16 output-major W, K % 32 == 0: the rows are split into three
+    # K-blocked fp16 planes and multiplied on the fp16 matrix cores. K = 32 ..
+    # 224 is 1 to 7 K steps (every remainder of the four-stage ring), M and N
+    # whole and ragged; every row is checked.
+    rng = np.random.default_rng(13 * M + N + K + with_gamma)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w nk {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 12760, 256), (384, 11008, 256), (1000, 4100, 384),
+                                   (1000, 9000, 256)])
+def test_rmsnorm_linear_f16w_nk_fp16_mfma_stream_k(gpu, orc, M, N, K):
+    # Tile counts past one round of one 128 x 128 tile per CU (256 on MI355X:
+    # 300, 258 and 264 tiles): whole rounds data-parallel, the last round's
+    # tiles split over the CUs by K tile and added by the fix-up pass (ragged
+    # M and N on the first and third shapes; on the second, 2 tail tiles split
+    # into single K tiles). 1000 x 9000 (568 tiles, a last round of 56) splits
+    # after two whole rounds. Eight rows of every 128-row tile (its edges and
+    # random ones) against every column, so every tile is checked.
+    rng = np.random.default_rng(17 * M + N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    rows = []
+    for m0 in range(0, M, 128):
+        last = min(m0 + 127, M - 1)
+        rows += [m0, m0 + 1, min(m0 + 63, last), min(m0 + 64, last), last]
+        rows += list(rng.integers(m0, last + 1, 3))
+    rows = np.unique(rows)
+    y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w nk stream-K {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("gscale", [1e-30, 1e-3, 1.0, 1e25])
+def test_rmsnorm_linear_f16w_nk_fp16_mfma_row_scales(gpu, orc, gscale):
+    # The planes hold each row times its own power of two (row maximum moved
+    # into [2^14, 2^15)): gamma far below and above fp16's range keeps the
+    # FP32 bound, rows of very different size share a tile, and an all-zero
+    # row stays exactly zero.
+    M, N, K = 96, 160, 256
+    rng = np.random.default_rng(int(np.log10(gscale)) + 40)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    x[::7] *= np.float32(1e-6)   # eps-dominated: normalised rows ~3e-4 of the others
+    x[3::7] *= np.float32(1e15)
+    x[5] = 0.0
+    x[40] = 0.0
+    g = (gscale * (1 + 0.1 * rng.standard_normal(K))).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    assert np.all(got[5] == 0.0) and np.all(got[40] == 0.0)
+    y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w nk row scales, gamma x {gscale:g}")
+
+
 @pytest.mark.parametrize("N,K,dtype", [(127, 31, "f32"), (73, 125, "f16w"), (4100, 4096, "f16w"),
                                        (11008, 4096, "f32"), (8, 20000, "f16w"), (1, 1, "f32"),
                                        (3000, 7, "f16"), (64, 1, "f16w")])
