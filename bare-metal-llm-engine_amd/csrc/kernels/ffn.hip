@@ -19,7 +19,9 @@
 //     takes five, and the same bits.
 //   * Otherwise gate and up are computed separately into the stream's scratch
 //     arena -- single-row GEMVs, small-batch passes over W, or (more rows)
-//     RMSNorm once and the MFMA GEMM -- and the SwiGLU kernel finishes.
+//     RMSNorm once and the MFMA GEMM: with output-major fp16 weights the rows
+//     are split once into three fp16 planes and gate and up each run the
+//     fp16-MFMA GEMM (launch_gemm_h3) -- and the SwiGLU kernel finishes.
 // Preconditions and messages follow rmsnorm_linear; any zero dimension
 // writes nothing.
 #include "gemv_kernels.hpp"
@@ -180,10 +182,25 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
   const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
+  // Rows past the few-row kernels go to a GEMM. With output-major fp16 Wg and
+  // Wu (both aligned) that is the fp16-MFMA GEMM on the rows' three fp16
+  // planes, split once for gate and up; else the rows normalised in fp32.
+  const bool h3 = elem == Elem::F16 && nk && aligned_to(in, 16) &&
+                  gemm_h3_applies(M, N, K, Wg) && gemm_h3_applies(M, N, K, Wu);
+  // The leading region holds the normalised rows (4 mk bytes) or the planes
+  // and row scales (6 mk + 4 M bytes); gate and up follow, 256-byte aligned.
+  const std::size_t plane_bytes = 3 * mk * sizeof(_Float16);
+  const std::size_t lead =
+      M > 1 ? (std::max(mk * sizeof(float), plane_bytes + static_cast<std::size_t>(M) * sizeof(float)) +
+               255) & ~static_cast<std::size_t>(255)
+            : 0;
   // Level 1: the GEMV launches below may lease split-K partials (level 0).
-  StreamScratch scratch(s, (mk + 2 * mn) * sizeof(float), 1);
-  float* xn = static_cast<float*>(scratch.get());  // first: the GEMM wants it 16-byte aligned
-  float* gate = xn + mk;
+  StreamScratch scratch(s, lead + 2 * mn * sizeof(float), 1);
+  char* base = static_cast<char*>(scratch.get());
+  float* xn = reinterpret_cast<float*>(base);  // first: the GEMMs want it 16-byte aligned
+  _Float16* planes = reinterpret_cast<_Float16*>(base);
+  float* rscale = reinterpret_cast<float*>(base + plane_bytes);
+  float* gate = reinterpret_cast<float*>(base + lead);
   float* up = gate + mn;
   bool normed = false;
   for (int half = 0; half < 2; ++half) {
@@ -204,6 +221,22 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
       launch_gemv(gv, s);
     } else if (!(nk ? launch_gemv_nk_rows(gv, M, s) : launch_gemv_kn_rows(gv, M, s))) {
       // more than a few rows: normalise once, then the MFMA GEMM
+      if (h3) {
+        if (!normed) {
+          launch_rmsnorm_split3(in, gamma, planes, rscale, M, K, eps, s);
+          normed = true;
+        }
+        GemmH3Args h;
+        h.P = planes;
+        h.rscale = rscale;
+        h.B = static_cast<const _Float16*>(W);
+        h.C = out;
+        h.M = M;
+        h.N = N;
+        h.K = K;
+        launch_gemm_h3(h, s);
+        continue;
+      }
       if (!normed) {
         launch_rmsnorm(in, gamma, xn, M, K, eps, s);
         normed = true;

@@ -741,6 +741,19 @@ def rows_ffn(eng, timer) -> list:
                         st, 2 * 2 * H * F + 4 * M * H + 4 * H + 4 * M * F))
     for d in Wg + Wu + [dx, dgm, dgate, dup, dact, dxm, dam]:
         d.free()
+    # Prefill at 512 tokens, output-major fp16 weights: the rows split once
+    # into fp16 planes, gate and up on the fp16-MFMA GEMM, then SwiGLU. FLOP:
+    # the two GEMMs, 2 x 2MNK.
+    M = 512
+    dWg, dWu = eng.upload(base), eng.upload(rand_f16(rng, (F, H)))
+    dxp = eng.upload(rng.standard_normal((M, H), dtype=np.float32))
+    dgp = eng.upload((1 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    dap = eng.empty((M, F), np.float32)
+    st = timer.sampled(lambda i, s: glu(dxp.ptr, dgp.ptr, dWg.ptr, dWu.ptr, dap.ptr, M, F, H, 1e-5, s))
+    rows.append(gemm_row(f"FFN gate/up + SwiGLU {M}x11008x4096 fp16-W prefill (both GEMMs' FLOP)",
+                         st, M, 2 * F, H))
+    for d in (dWg, dWu, dxp, dgp, dap):
+        d.free()
     return rows
 
 
@@ -1210,6 +1223,9 @@ SUMMARY_ROWS = (
     ("cfg4_gemm_512x4096x11008_tflops", "matmul_f32 512x4096x11008 (config 4)", "TFLOP/s"),
     ("gemm_1024_tflops", "matmul_f32 1024x1024x1024", "TFLOP/s"),
     ("gemm_2048_tflops", "matmul_f32 2048x2048x2048", "TFLOP/s"),
+    ("prefill_f16w_nk_512x11008_ms", "rmsnorm_linear_f16w 512x11008x4096 prefill, fp16 W output-major",
+     "ms_per_call"),
+    ("ffn_prefill_512_ms", "FFN gate/up + SwiGLU 512x11008x4096 fp16-W prefill", "ms_per_call"),
     ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
     ("gemv_fp32_12288_us", "gemv (fp32 W) 4096x12288 cold", "us_per_call"),
     ("gemv_fp16_halfio_4096_us", "gemv_fp16 (half x/out) 4096x4096 cold", "us_per_call"),

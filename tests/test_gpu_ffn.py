@@ -284,7 +284,9 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (40, 200, 512, "f16", True),     # few rows (three m-blocks) + SwiGLU kernel
     (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
     (64, 256, 512, "f16", False),    # 64 rows: the few-row kernel's largest batch
-    (65, 256, 512, "f16", True),     # past it: rmsnorm + MFMA GEMMs + SwiGLU kernel
+    (65, 256, 512, "f16", True),     # past it: rows split into fp16 planes + fp16-MFMA GEMMs
+    (65, 256, 500, "f16", True),     # K % 32 != 0: rmsnorm + FP32 MFMA GEMMs on fp16 B
+    (130, 300, 200, "f32", True),    # fp32 weights past the few-row kernel: FP32 MFMA GEMMs
 ])
 def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma):
     rng = np.random.default_rng(M + N + K)
@@ -299,6 +301,30 @@ def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma
     act64, bd, bs = glu_reference(x, g, Wg_kn, Wu_kn)
     check_glu(got, orc.rmsnorm_linear_swiglu(x, g, Wg_kn, Wu_kn, EPS), act64, bd, bs,
               f"rmsnorm_linear_swiglu nk {M}x{N}x{K} {dtype}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1000, 2816, 1024), (300, 11008, 512)])
+def test_rmsnorm_linear_swiglu_nk_prefill_fp16_mfma(gpu, orc, M, N, K):
+    # Prefill with output-major fp16 weights: the rows split once into three
+    # fp16 planes, gate and up on the fp16-MFMA GEMM (ragged M and N on the
+    # first shape; 258 tiles and the stream-K split on the second). Eight rows
+    # of every 128-row tile against every column.
+    rng = np.random.default_rng(M + 3 * N + K)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Wg = orc.f32_to_f16((rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32))
+    Wu = orc.f32_to_f16((rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32))
+    got = gpu_glu_nk(gpu, x, g, Wg, Wu)
+    rows = []
+    for m0 in range(0, M, 128):
+        last = min(m0 + 127, M - 1)
+        rows += [m0, m0 + 1, min(m0 + 63, last), min(m0 + 64, last), last]
+        rows += list(rng.integers(m0, last + 1, 3))
+    rows = np.unique(rows)
+    Wg_kn, Wu_kn = np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T)
+    act64, bd, bs = glu_reference(x[rows], g, Wg_kn, Wu_kn)
+    check_glu(got[rows], orc.rmsnorm_linear_swiglu(x[rows], g, Wg_kn, Wu_kn, EPS), act64, bd, bs,
+              f"rmsnorm_linear_swiglu nk prefill {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("M,N,K,dtype", [(2, 11008, 4096, "f16"), (3, 1000, 2048, "f16"),
