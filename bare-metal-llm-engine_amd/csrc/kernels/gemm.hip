@@ -292,7 +292,7 @@ __device__ __forceinline__ int swz_rows(int r) { return (r >> 1) & 7; }
 // unlike global_load_lds, are not FLAT instructions: the compiler then counts
 // the in-flight direct loads on vmcnt only and keeps the LDS fragment reads'
 // waits partial instead of draining them with lgkmcnt(0).
-constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw dword access)
+[[maybe_unused]] constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer descriptor word 3 (raw dword access)
 
 template <typename T>
 __device__ __forceinline__ void lds_buf16(const T* base, unsigned bytes, unsigned off, T* lds) {
@@ -891,7 +891,6 @@ bool sk_enabled() {
 template <typename BT, bool BNK>
 bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
   constexpr int BM = 128, BN = 128;
-  constexpr int kBVec = 16 / static_cast<int>(sizeof(BT));
   if (!sk_enabled() || !direct_ok<BM, BN, BT, BNK>(a)) return false;
   if (a.M % BM != 0 || a.N % BN != 0 || a.K / BK < 8) return false;
   const long long cus = device_cu_count();
@@ -1014,15 +1013,17 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   constexpr int WN = Shape<WGN>::WN;
   constexpr int MB = Shape<WGN>::MB;
   constexpr int NB = Shape<WGN>::NB;
+  constexpr int AT = 3 * PT;   // halves of a stage's plane tiles
+  constexpr int BTL = BN * BK; // halves of a stage's B tile
   typedef _Float16 halfx8v __attribute__((ext_vector_type(8)));
-  __shared__ __attribute__((aligned(1024))) _Float16 As0[3 * PT];
-  __shared__ __attribute__((aligned(1024))) _Float16 As1[3 * PT];
-  __shared__ __attribute__((aligned(1024))) _Float16 As2[3 * PT];
-  __shared__ __attribute__((aligned(1024))) _Float16 As3[S > 3 ? 3 * PT : 8];
-  __shared__ __attribute__((aligned(1024))) _Float16 Bs0[BN * BK];
-  __shared__ __attribute__((aligned(1024))) _Float16 Bs1[BN * BK];
-  __shared__ __attribute__((aligned(1024))) _Float16 Bs2[BN * BK];
-  __shared__ __attribute__((aligned(1024))) _Float16 Bs3[S > 3 ? BN * BK : 8];
+  __shared__ __attribute__((aligned(1024))) _Float16 As0[AT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As1[AT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As2[AT];
+  __shared__ __attribute__((aligned(1024))) _Float16 As3[S > 3 ? AT : 8];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs0[BTL];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs1[BTL];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs2[BTL];
+  __shared__ __attribute__((aligned(1024))) _Float16 Bs3[S > 3 ? BTL : 8];
   auto a_stage = [&](auto st) -> _Float16* {
     if constexpr (decltype(st)::value == 0) return As0;
     else if constexpr (decltype(st)::value == 1) return As1;
@@ -1043,41 +1044,55 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   const int wm = wave / WGN;
   const int wn = wave % WGN;
 
-  // Direct loads: instruction j of wave w fills 16-byte slots (8 j + w) * 64 +
-  // lane of the stage; A slots 512 p .. 512 p + 511 are plane p's tile (so
-  // instruction j loads plane j), B's 512 slots its tile. Slot q of a tile is
-  // row q / 4, position q % 4, holding chunk (q % 4) ^ swz_rows_h(row).
-  // The planes are K-blocked ([K / 32][M][32] each): the tile's rows of one
-  // K step are a contiguous slab of 64-byte rows, so a load instruction
-  // covers 1 KiB in one piece (whole cache lines).
-  unsigned a_off[A_INST];
-  unsigned b_off;
-#pragma unroll
-  for (int j = 0; j < A_INST; ++j) {
-    const int q = wave * 64 + lane;  // slot within plane j's tile
-    const int r = q >> 2;
-    const int c = (q & 3) ^ swz_rows_h(r);
-    const int row = EDGE ? min(m0 + r, M - 1) - m0 : r;
-    a_off[j] = static_cast<unsigned>(row * BK + 8 * c) * 2u;
-  }
+  // Direct loads: load j of wave w fills 16-byte slots 64 w + lane of a
+  // 512-slot tile (plane j's for j < 3, then B's); slot q of a tile is row q
+  // / 4, position q % 4, holding chunk (q % 4) ^ swz_rows_h(row). The planes
+  // are K-blocked ([K / 32][M][32] each): a plane tile is a contiguous run of
+  // 64-byte rows, so a load instruction covers 1 KiB in one piece (whole
+  // cache lines).
+  [[maybe_unused]] unsigned a_off;  // (read by device code only)
+  [[maybe_unused]] unsigned b_off;
   {
     const int q = wave * 64 + lane;
     const int r = q >> 2;
     const int c = (q & 3) ^ swz_rows_h(r);
-    const int row = EDGE ? min(n0 + r, N - 1) - n0 : r;
-    b_off = static_cast<unsigned>(row * K + 8 * c) * 2u;
+    const int ra = EDGE ? min(m0 + r, M - 1) - m0 : r;
+    const int rb = EDGE ? min(n0 + r, N - 1) - n0 : r;
+    a_off = static_cast<unsigned>(ra * BK + 8 * c) * 2u;
+    b_off = static_cast<unsigned>(rb * K + 8 * c) * 2u;
   }
-  const long long plane = static_cast<long long>(M) * K;
-  const long long b_len = static_cast<long long>(N) * K;
+  // One buffer descriptor per plane (its whole extent) and one for the
+  // tile's B rows (from row n0 to the end of B, capped at 4 GiB), made once;
+  // a K step moves only the scalar offset: (kt M + m0) 64 bytes into a plane
+  // (under 2^31: M K 2 bytes is), kt 64 bytes along B's rows.
+  // Rebuilding the descriptors per K step (64-bit adds, the range clamp)
+  // took some 40 scalar instructions per wave and K step, issue slots the
+  // MFMAs then waited behind.
+  [[maybe_unused]] const long long plane = static_cast<long long>(M) * K;
+  [[maybe_unused]] const long long b_first = static_cast<long long>(n0) * K;
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto ra0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(P), 0,
+                                                     static_cast<int>(plane * 2), kRsrcWord3);
+  const auto ra1 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(P + plane), 0,
+                                                     static_cast<int>(plane * 2), kRsrcWord3);
+  const auto ra2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(P + 2 * plane), 0,
+                                                     static_cast<int>(plane * 2), kRsrcWord3);
+  const auto rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(B + b_first), 0,
+      static_cast<int>(bytes_left<_Float16>(static_cast<long long>(N) * K, b_first)), kRsrcWord3);
+#endif
   auto fetch = [&](_Float16* as, _Float16* bs, int kt) {
-    const int k0 = kt * BK;
-    const long long a0 = (static_cast<long long>(kt) * M + m0) * BK;
-    const long long b0 = static_cast<long long>(n0) * K + k0;
-    const unsigned a_bytes = bytes_left<_Float16>(plane, a0);
-#pragma unroll
-    for (int j = 0; j < A_INST; ++j)
-      lds_buf16(P + j * plane + a0, a_bytes, a_off[j], as + j * PT + 8 * wave * 64);
-    lds_buf16(B + b0, bytes_left<_Float16>(b_len, b0), b_off, bs + 8 * wave * 64);
+#if defined(__HIP_DEVICE_COMPILE__)
+    const int soff = (kt * M + m0) * (BK * 2);
+    _Float16* dst = as + 8 * wave * 64;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra0, dst, 16, static_cast<int>(a_off), soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra1, dst + PT, 16, static_cast<int>(a_off), soff, 0,
+                                             0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra2, dst + 2 * PT, 16, static_cast<int>(a_off), soff,
+                                             0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * wave * 64, 16, static_cast<int>(b_off),
+                                             kt * (BK * 2), 0, 0);
+#endif
   };
 
   struct Slice {
@@ -1289,8 +1304,10 @@ bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void*
   constexpr long long kLim = 0x7fffffffLL;
   // K % 32 == 0, 16-byte aligned B rows, every lane's byte offset from a
   // tile's corner (up to 128 rows of K halves) within a buffer load's 31 bits
+  // and each activation plane (M K halves) within 31 bits of byte offset
   return h3_enabled() && M > 0 && N > 0 && K > 0 && K % BK == 0 && M <= kLim && N <= kLim &&
-         K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM) * K * 2 <= kLim;
+         K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM) * K * 2 <= kLim &&
+         M * K * 2 <= kLim;
 }
 
 void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
@@ -1305,7 +1322,7 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
   // Stream-K when the last round of one tile per CU is at most half full
   // (512 x 11008: 88 of 256, 148.7 -> 138.3 us; at 176 of 256 the records
   // and the fix-up pass cost more than the split saves), with at least 8 K
-  // tiles per tile.
+  // tiles per tile; the tail's workgroups run after the whole rounds.
   const long long cus = device_cu_count();
   const long long tail = ntiles % cus;
   const int nk = K / BK;
