@@ -979,42 +979,46 @@ void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
 // stream-K split of gemm_sk_kernel (gemm_h3_sk_kernel).
 namespace h3 {
 constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int WAVES = 8;
 constexpr int THREADS = 64 * WAVES;
 constexpr int PT = BM * BK;                   // halves of one plane tile
 constexpr int A_INST = 3 * PT / 8 / THREADS;  // direct loads per thread per K step (A planes)
-constexpr int B_INST = BN * BK / 8 / THREADS; // (B)
-constexpr int LOADS = A_INST + B_INST;
-static_assert(A_INST == 3 && B_INST == 1, "tile shape");
+static_assert(A_INST == 3, "tile shape");
 
-// WGN waves along N, WAVES / WGN along M; each wave a WM x WN block of the
-// tile as MB x NB 32 x 32 MFMA blocks.
-template <int WGN>
+// Tiles of 128 x BNT (BNT 128 or 256): BNT / 64 waves along N and the rest
+// of the 8 along M, each wave a WM x 64 block as MB x 2 32 x 32 MFMA blocks.
+template <int BNT>
 struct Shape {
+  static_assert(BNT == 128 || BNT == 256, "tile width");
+  static constexpr int WGN = BNT / 64;
   static constexpr int WM = BM / (WAVES / WGN);
-  static constexpr int WN = BN / WGN;
+  static constexpr int WN = 64;
   static constexpr int MB = WM / 32;
   static constexpr int NB = WN / 32;
+  static constexpr int B_INST = BNT * BK / 8 / THREADS;  // direct loads per thread per K step (B)
+  static constexpr int LOADS = A_INST + B_INST;
 };
-template <int WGN>
-using Acc = floatx16[Shape<WGN>::MB][Shape<WGN>::NB];
+template <int BNT>
+using Acc = floatx16[Shape<BNT>::MB][Shape<BNT>::NB];
 }  // namespace h3
 
-// K tiles [kt0, kt1) of the 128 x 128 tile at (m0, n0) into acc (zeroed
+// K tiles [kt0, kt1) of the 128 x BNT tile at (m0, n0) into acc (zeroed
 // here); ends with a barrier, so a following call may refill the stages.
-template <int S, int WGN, bool EDGE>
+template <int S, int BNT, bool EDGE>
 __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
                                         const _Float16* __restrict__ B, int M, int N, int K,
-                                        int m0, int n0, int kt0, int kt1, h3::Acc<WGN>& acc) {
+                                        int m0, int n0, int kt0, int kt1, h3::Acc<BNT>& acc) {
   using namespace h3;
   static_assert(S >= 3 && S <= 4, "stages");
-  constexpr int WM = Shape<WGN>::WM;
-  constexpr int WN = Shape<WGN>::WN;
-  constexpr int MB = Shape<WGN>::MB;
-  constexpr int NB = Shape<WGN>::NB;
-  constexpr int AT = 3 * PT;   // halves of a stage's plane tiles
-  constexpr int BTL = BN * BK; // halves of a stage's B tile
+  constexpr int WGN = Shape<BNT>::WGN;
+  constexpr int WM = Shape<BNT>::WM;
+  constexpr int WN = Shape<BNT>::WN;
+  constexpr int MB = Shape<BNT>::MB;
+  constexpr int NB = Shape<BNT>::NB;
+  constexpr int B_INST = Shape<BNT>::B_INST;
+  constexpr int LOADS = Shape<BNT>::LOADS;
+  constexpr int AT = 3 * PT;    // halves of a stage's plane tiles
+  constexpr int BTL = BNT * BK; // halves of a stage's B tile
   typedef _Float16 halfx8v __attribute__((ext_vector_type(8)));
   __shared__ __attribute__((aligned(1024))) _Float16 As0[AT];
   __shared__ __attribute__((aligned(1024))) _Float16 As1[AT];
@@ -1044,22 +1048,29 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   const int wm = wave / WGN;
   const int wn = wave % WGN;
 
-  // Direct loads: load j of wave w fills 16-byte slots 64 w + lane of a
-  // 512-slot tile (plane j's for j < 3, then B's); slot q of a tile is row q
-  // / 4, position q % 4, holding chunk (q % 4) ^ swz_rows_h(row). The planes
-  // are K-blocked ([K / 32][M][32] each): a plane tile is a contiguous run of
+  // Direct loads: each load of wave w fills 16-byte slots 64 w + lane of a
+  // 512-slot part of a tile (the three plane tiles; the B tile's BNT / 128
+  // parts, part i holding slots 512 i ..); slot q of a tile is row q / 4,
+  // position q % 4, holding chunk (q % 4) ^ swz_rows_h(row). The planes are
+  // K-blocked ([K / 32][M][32] each): a plane tile is a contiguous run of
   // 64-byte rows, so a load instruction covers 1 KiB in one piece (whole
   // cache lines).
   [[maybe_unused]] unsigned a_off;  // (read by device code only)
-  [[maybe_unused]] unsigned b_off;
+  [[maybe_unused]] unsigned b_off[B_INST];
   {
     const int q = wave * 64 + lane;
     const int r = q >> 2;
     const int c = (q & 3) ^ swz_rows_h(r);
     const int ra = EDGE ? min(m0 + r, M - 1) - m0 : r;
-    const int rb = EDGE ? min(n0 + r, N - 1) - n0 : r;
     a_off = static_cast<unsigned>(ra * BK + 8 * c) * 2u;
-    b_off = static_cast<unsigned>(rb * K + 8 * c) * 2u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_INST; ++i) {
+    const int q = i * 512 + wave * 64 + lane;
+    const int r = q >> 2;
+    const int c = (q & 3) ^ swz_rows_h(r);
+    const int rb = EDGE ? min(n0 + r, N - 1) - n0 : r;
+    b_off[i] = static_cast<unsigned>(rb * K + 8 * c) * 2u;
   }
   // One buffer descriptor per plane (its whole extent) and one for the
   // tile's B rows (from row n0 to the end of B, capped at 4 GiB), made once;
@@ -1090,8 +1101,10 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
                                              0);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(ra2, dst + 2 * PT, 16, static_cast<int>(a_off), soff,
                                              0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * wave * 64, 16, static_cast<int>(b_off),
-                                             kt * (BK * 2), 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_INST; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * (i * 512 + wave * 64), 16,
+                                               static_cast<int>(b_off[i]), kt * (BK * 2), 0, 0);
 #endif
   };
 
@@ -1205,8 +1218,8 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
 // acc times the row's 2^-e into dst (row r, column c of the tile at dst[r ld
 // + c]); GUARD keeps rows < rows_left and columns < cols_left. Rows past M
 // (an edge tile's clamped rows) take row M - 1's scale.
-template <int WGN, bool GUARD>
-__device__ __forceinline__ void h3_store(const h3::Acc<WGN>& acc, const float* __restrict__ rscale,
+template <int BNT, bool GUARD>
+__device__ __forceinline__ void h3_store(const h3::Acc<BNT>& acc, const float* __restrict__ rscale,
                                          int M, int m0, float* __restrict__ dst, long long ld,
                                          int rows_left, int cols_left) {
   using namespace h3;
@@ -1214,19 +1227,26 @@ __device__ __forceinline__ void h3_store(const h3::Acc<WGN>& acc, const float* _
   const int wave = threadIdx.x >> 6;
   const int li = lane & 31;
   const int lg = lane >> 5;
-  const int wm = wave / WGN;
-  const int wn = wave % WGN;
+  using Sh = Shape<BNT>;
+  const int wm = wave / Sh::WGN;
+  const int wn = wave % Sh::WGN;
+#if defined(__HIP_DEVICE_COMPILE__)
+  // In the stream-K kernel's tile loop the per-element offsets r ld + col
+  // are loop-invariant, and hoisted they held 32-64 registers for the whole
+  // K loop (spilling the 128 x 256 form); an opaque ld keeps them here.
+  asm volatile("" : "+s"(ld));
+#endif
 
   // Accumulator element v of lane (li, lg): row 8 (v / 4) + 4 lg + v % 4 of
   // the block, column li.
 #pragma unroll
-  for (int mb = 0; mb < Shape<WGN>::MB; ++mb) {
+  for (int mb = 0; mb < Sh::MB; ++mb) {
 #pragma unroll
-    for (int nb = 0; nb < Shape<WGN>::NB; ++nb) {
-      const int col = wn * Shape<WGN>::WN + nb * 32 + li;
+    for (int nb = 0; nb < Sh::NB; ++nb) {
+      const int col = wn * Sh::WN + nb * 32 + li;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int r = wm * Shape<WGN>::WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
+        const int r = wm * Sh::WM + mb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
         if (!GUARD || (r < rows_left && col < cols_left))
           dst[r * ld + col] = acc[mb][nb][v] * rscale[min(m0 + r, M - 1)];
       }
@@ -1234,17 +1254,17 @@ __device__ __forceinline__ void h3_store(const h3::Acc<WGN>& acc, const float* _
   }
 }
 
-template <int S, int WGN, bool EDGE>
+template <int S, int BNT, bool EDGE>
 __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * h3::BM;
-  const int n0 = tn * h3::BN;
-  h3::Acc<WGN> acc;
-  h3_tile<S, WGN, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
-  h3_store<WGN, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+  const int n0 = tn * BNT;
+  h3::Acc<BNT> acc;
+  h3_tile<S, BNT, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
+  h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                       N - n0);
 }
 
@@ -1253,13 +1273,13 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
 // split the remaining tiles' K tiles evenly, one workgroup per CU after its
 // data-parallel tiles; a split tile leaves one record per workgroup (scaled
 // rows, slot 0 its first tile, slot 1 its last) for gemm_sk_fixup_kernel.
-template <int S, int WGN, bool EDGE>
+template <int S, int BNT, bool EDGE>
 __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n,
     SkPlan plan) {
-  constexpr int BM = h3::BM, BN = h3::BN;
-  h3::Acc<WGN> acc;
+  constexpr int BM = h3::BM, BN = BNT;
+  h3::Acc<BNT> acc;
   const int g = blockIdx.x;
   const bool dp = g < plan.dp;
   const long long s = dp ? 0 : g - plan.dp;
@@ -1275,13 +1295,13 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
     tile_of(first_tile + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
-    h3_tile<S, WGN, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
+    h3_tile<S, BNT, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
     if (ka == 0 && kb == plan.nk) {
-      h3_store<WGN, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+      h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                           N - n0);
     } else {
       const int slot = it == i0 ? 0 : 1;
-      h3_store<WGN, false>(acc, rscale, M, m0,
+      h3_store<BNT, false>(acc, rscale, M, m0,
                            rec + (s * 2 + slot) * static_cast<long long>(BM * BN), BN, BM, BN);
     }
     it = t * plan.nk + kb;
@@ -1290,6 +1310,15 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
 
 // The fp16-MFMA form of the fp16-weight GEMM can be switched off
 // (ENGINE_GEMM_NO_H3=1) to compare it with the FP32 MFMA on converted weights.
+// The 128 x 256 tiles can be switched off (ENGINE_GEMM_H3_NO_WIDE=1).
+bool h3_wide_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_H3_NO_WIDE");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
 bool h3_enabled() {
   static const bool on = [] {
     const char* v = std::getenv("ENGINE_GEMM_NO_H3");
@@ -1314,49 +1343,64 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
   ENG_CHECK(gemm_h3_applies(a.M, a.N, a.K, a.B) && aligned_to(a.P, 16) && a.rscale != nullptr,
             "matmul (fp16 weights): shape or alignment not supported");
   const int M = static_cast<int>(a.M), N = static_cast<int>(a.N), K = static_cast<int>(a.K);
-  const int tiles_m = (M + h3::BM - 1) / h3::BM;
-  const int tiles_n = (N + h3::BN - 1) / h3::BN;
-  const long long ntiles = static_cast<long long>(tiles_m) * tiles_n;
-  ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
-  const bool whole = M % h3::BM == 0 && N % h3::BN == 0;
-  // Stream-K when the last round of one tile per CU is at most half full
-  // (512 x 11008: 88 of 256, 148.7 -> 138.3 us; at 176 of 256 the records
-  // and the fix-up pass cost more than the split saves), with at least 8 K
-  // tiles per tile; the tail's workgroups run after the whole rounds.
   const long long cus = device_cu_count();
-  const long long tail = ntiles % cus;
-  const int nk = K / BK;
-  const bool split = sk_enabled() && ntiles > cus && tail != 0 && 2 * tail <= cus && nk >= 8;
-  SkPlan plan;
-  plan.dp = static_cast<int>(ntiles - tail);
-  plan.nk = nk;
-  plan.I = tail * nk;
-  plan.nsk = static_cast<int>(std::min<long long>(cus, plan.I));
-  auto go = [&](auto edge) {
-    constexpr bool E = decltype(edge)::value;
-    constexpr int S = 4, G = 2;  // four stages, waves 4 (M) x 2 (N) of 32 x 64
-    if (!split) {
-      gemm_h3_kernel<S, G, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
-          a.P, a.rscale, a.B, a.C, M, N, K, tiles_m, tiles_n);
+  const int tiles_m = (M + h3::BM - 1) / h3::BM;
+  auto run = [&](auto bnt, auto stages) {
+    constexpr int BNT = decltype(bnt)::value;
+    constexpr int S = decltype(stages)::value;
+    const int tiles_n = (N + BNT - 1) / BNT;
+    const long long ntiles = static_cast<long long>(tiles_m) * tiles_n;
+    ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
+    const bool whole = M % h3::BM == 0 && N % BNT == 0;
+    // Stream-K when the last round of one tile per CU is at most half full
+    // (512 x 11008 on 128 x 128 tiles: 88 of 256, 148.7 -> 138.3 us; at 176 of
+    // 256 the records and the fix-up pass cost more than the split saves),
+    // with at least 8 K tiles per tile; the tail's workgroups run after the
+    // whole rounds.
+    const long long tail = ntiles % cus;
+    const int nk = K / BK;
+    const bool split = sk_enabled() && ntiles > cus && tail != 0 && 2 * tail <= cus && nk >= 8;
+    SkPlan plan;
+    plan.dp = static_cast<int>(ntiles - tail);
+    plan.nk = nk;
+    plan.I = tail * nk;
+    plan.nsk = static_cast<int>(std::min<long long>(cus, plan.I));
+    auto go = [&](auto edge) {
+      constexpr bool E = decltype(edge)::value;
+      if (!split) {
+        gemm_h3_kernel<S, BNT, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
+            a.P, a.rscale, a.B, a.C, M, N, K, tiles_m, tiles_n);
+        ENG_LAUNCH_CHECK();
+        return;
+      }
+      StreamScratch records(
+          stream, static_cast<std::size_t>(plan.nsk) * 2 * h3::BM * BNT * sizeof(float), 2);
+      float* rec = static_cast<float*>(records.get());
+      gemm_h3_sk_kernel<S, BNT, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS, 0,
+                                     stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K, tiles_m,
+                                               tiles_n, plan);
       ENG_LAUNCH_CHECK();
-      return;
-    }
-    StreamScratch records(
-        stream, static_cast<std::size_t>(plan.nsk) * 2 * h3::BM * h3::BN * sizeof(float), 2);
-    float* rec = static_cast<float*>(records.get());
-    gemm_h3_sk_kernel<S, G, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS, 0,
-                                 stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K, tiles_m, tiles_n,
-                                           plan);
-    ENG_LAUNCH_CHECK();
-    gemm_sk_fixup_kernel<h3::BM, h3::BN, E>
-        <<<dim3(static_cast<unsigned>(tail), h3::BM * h3::BN / 1024), 256, 0, stream>>>(
-            rec, a.C, M, N, tiles_m, tiles_n, plan);
-    ENG_LAUNCH_CHECK();
+      gemm_sk_fixup_kernel<h3::BM, BNT, E>
+          <<<dim3(static_cast<unsigned>(tail), h3::BM * BNT / 1024), 256, 0, stream>>>(
+              rec, a.C, M, N, tiles_m, tiles_n, plan);
+      ENG_LAUNCH_CHECK();
+    };
+    if (whole)
+      go(std::integral_constant<bool, false>{});
+    else
+      go(std::integral_constant<bool, true>{});
   };
-  if (whole)
-    go(std::integral_constant<bool, false>{});
+  // 128 x 256 tiles (waves of 64 x 64, three 40 KiB stages) once they fill at
+  // least two rounds of one tile per CU: each plane tile loaded feeds twice
+  // the MFMAs (2048 x 11008 x 4096: 500 -> 462 us); with fewer the last
+  // round's share of the time grows, and 1000 x 11008 (344 of them, split by
+  // K past the first round) ran no faster than on 688 narrow ones. Else 128 x
+  // 128 (waves of 32 x 64, four 32 KiB stages).
+  const long long wide_tiles = static_cast<long long>(tiles_m) * ((N + 255) / 256);
+  if (h3_wide_enabled() && wide_tiles >= 2 * cus)
+    run(std::integral_constant<int, 256>{}, std::integral_constant<int, 3>{});
   else
-    go(std::integral_constant<bool, true>{});
+    run(std::integral_constant<int, 128>{}, std::integral_constant<int, 4>{});
 }
 
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {

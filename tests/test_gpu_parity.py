@@ -320,15 +320,20 @@ def test_rmsnorm_linear_f16w_nk_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamm
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 12760, 256), (384, 11008, 256), (1000, 4100, 384),
-                                   (1000, 9000, 256)])
+                                   (1000, 9000, 256), (2000, 8300, 256), (2000, 8300, 96),
+                                   (2000, 8300, 64), (2048, 8448, 256), (2048, 8192, 64)])
 def test_rmsnorm_linear_f16w_nk_fp16_mfma_stream_k(gpu, orc, M, N, K):
-    # Tile counts past one round of one 128 x 128 tile per CU (256 on MI355X:
-    # 300, 258 and 264 tiles): whole rounds data-parallel, the last round's
-    # tiles split over the CUs by K tile and added by the fix-up pass (ragged
-    # M and N on the first and third shapes; on the second, 2 tail tiles split
-    # into single K tiles). 1000 x 9000 (568 tiles, a last round of 56) splits
-    # after two whole rounds. Eight rows of every 128-row tile (its edges and
-    # random ones) against every column, so every tile is checked.
+    # Tile counts past one round of one tile per CU (256 on MI355X): whole
+    # rounds data-parallel, the last round's tiles split over the CUs by K
+    # tile and added by the fix-up pass. 128 x 128 tiles: 300, 258, 264 and
+    # 568 (ragged M and N on the first, third and fourth shapes; on the
+    # second, 2 tail tiles split into single K tiles; 1000 x 9000 splits after
+    # two whole rounds). 128 x 256 tiles (at least two rounds of them): 2000 x
+    # 8300, 528 tiles ragged both ways, splits the last 16 at K = 256 and runs
+    # unsplit through the three-stage ring's remainders at 3 and 2 K steps;
+    # 2048 x 8448 and 2048 x 8192 are the whole-tile forms, split and not.
+    # Eight rows of every 128-row tile (its edges and random ones) against
+    # every column, so every tile is checked.
     rng = np.random.default_rng(17 * M + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
