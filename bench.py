@@ -660,6 +660,13 @@ def rows_gemm(eng, timer) -> list:
     st = timer.sampled(lambda i, s: fn(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
     rows.append(gemm_row(f"rmsnorm_linear_f16w {M}x{N}x{K} prefill (ragged M), fp16 W output-major W[NxK]",
                          st, M, N, K))
+    dA.free(), dC.free()
+    # A long prompt (4096 tokens): 128 x 256 tiles on the fp16 matrix cores.
+    M = 4096
+    dA = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
+    dC = eng.empty((M, N), np.float32)
+    st = timer.sampled(lambda i, s: fn(dA.ptr, dg.ptr, dW.ptr, dC.ptr, M, N, K, 1e-5, s))
+    rows.append(gemm_row(f"rmsnorm_linear_f16w {M}x{N}x{K} prefill, fp16 W output-major W[NxK]", st, M, N, K))
     dA.free(), dg.free(), dC.free(), dW.free()
     return rows
 
@@ -1226,6 +1233,7 @@ SUMMARY_ROWS = (
     ("prefill_f16w_nk_512x11008_ms", "rmsnorm_linear_f16w 512x11008x4096 prefill, fp16 W output-major",
      "ms_per_call"),
     ("ffn_prefill_512_ms", "FFN gate/up + SwiGLU 512x11008x4096 fp16-W prefill", "ms_per_call"),
+    ("prefill_f16w_nk_4096x11008_tflops", "rmsnorm_linear_f16w 4096x11008x4096 prefill", "TFLOP/s"),
     ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
     ("gemv_fp32_12288_us", "gemv (fp32 W) 4096x12288 cold", "us_per_call"),
     ("gemv_fp16_halfio_4096_us", "gemv_fp16 (half x/out) 4096x4096 cold", "us_per_call"),
