@@ -19,8 +19,8 @@
 //     takes five, and the same bits.
 //   * Otherwise gate and up are computed separately into the stream's scratch
 //     arena -- single-row GEMVs, small-batch passes over W, or (more rows)
-//     RMSNorm once and the MFMA GEMM: with output-major fp16 weights the rows
-//     are split once into three fp16 planes and gate and up each run the
+//     RMSNorm once and the MFMA GEMM: with fp16 weights (either layout) the
+//     rows are split once into three fp16 planes and gate and up each run the
 //     fp16-MFMA GEMM (launch_gemm_h3) -- and the SwiGLU kernel finishes.
 // Preconditions and messages follow rmsnorm_linear; any zero dimension
 // writes nothing.
@@ -182,11 +182,11 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
   const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
-  // Rows past the few-row kernels go to a GEMM. With output-major fp16 Wg and
-  // Wu (both aligned) that is the fp16-MFMA GEMM on the rows' three fp16
+  // Rows past the few-row kernels go to a GEMM. With fp16 Wg and Wu (either
+  // layout, both aligned) that is the fp16-MFMA GEMM on the rows' three fp16
   // planes, split once for gate and up; else the rows normalised in fp32.
-  const bool h3 = elem == Elem::F16 && nk && aligned_to(in, 16) &&
-                  gemm_h3_applies(M, N, K, Wg) && gemm_h3_applies(M, N, K, Wu);
+  const bool h3 = elem == Elem::F16 && aligned_to(in, 16) &&
+                  gemm_h3_applies(M, N, K, Wg, !nk) && gemm_h3_applies(M, N, K, Wu, !nk);
   // The leading region holds the normalised rows (4 mk bytes) or the planes
   // and row scales (6 mk + 4 M bytes); gate and up follow, 256-byte aligned.
   const std::size_t plane_bytes = 3 * mk * sizeof(_Float16);
@@ -234,6 +234,7 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
         h.M = M;
         h.N = N;
         h.K = K;
+        h.b_kn = !nk;
         launch_gemm_h3(h, s);
         continue;
       }

@@ -1002,9 +1002,17 @@ template <int BNT>
 using Acc = floatx16[Shape<BNT>::MB][Shape<BNT>::NB];
 }  // namespace h3
 
+// Reference-layout B tiles ([K x N] rows of BNT halves, 16-byte chunks):
+// chunk c of row k sits at c ^ swz_h3_kn(k). A transposing read touches 8 rows
+// (4 consecutive, and the 4 eight rows on) x 64 bytes (4 chunks from a
+// multiple of 4); the swizzle puts 4 consecutive rows' chunk groups on 4
+// distinct 64-byte bank slots.
+__device__ __forceinline__ int swz_h3_kn(int k) { return 4 * (k & 3); }
+
 // K tiles [kt0, kt1) of the 128 x BNT tile at (m0, n0) into acc (zeroed
-// here); ends with a barrier, so a following call may refill the stages.
-template <int S, int BNT, bool EDGE>
+// here); ends with a barrier, so a following call may refill the stages. BKN:
+// B given [K x N] (the reference layout) instead of [N x K].
+template <int S, int BNT, bool BKN, bool EDGE>
 __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
                                         const _Float16* __restrict__ B, int M, int N, int K,
                                         int m0, int n0, int kt0, int kt1, h3::Acc<BNT>& acc) {
@@ -1020,6 +1028,8 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   constexpr int AT = 3 * PT;    // halves of a stage's plane tiles
   constexpr int BTL = BNT * BK; // halves of a stage's B tile
   typedef _Float16 halfx8v __attribute__((ext_vector_type(8)));
+  typedef _Float16 halfx4v __attribute__((ext_vector_type(4)));
+  typedef short shortx4v __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(1024))) _Float16 As0[AT];
   __shared__ __attribute__((aligned(1024))) _Float16 As1[AT];
   __shared__ __attribute__((aligned(1024))) _Float16 As2[AT];
@@ -1067,20 +1077,33 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
 #pragma unroll
   for (int i = 0; i < B_INST; ++i) {
     const int q = i * 512 + wave * 64 + lane;
-    const int r = q >> 2;
-    const int c = (q & 3) ^ swz_rows_h(r);
-    const int rb = EDGE ? min(n0 + r, N - 1) - n0 : r;
-    b_off[i] = static_cast<unsigned>(rb * K + 8 * c) * 2u;
+    if constexpr (BKN) {
+      // [K x N]: slot q is row q / CPR (one k), position q % CPR of its BNT / 8
+      // chunks, holding chunk (q % CPR) ^ swz_h3_kn(row); chunks past N read
+      // the tile's first (N % 8 == 0: a chunk is all in or all out).
+      constexpr int CPR = BNT / 8;
+      const int r = q / CPR;
+      const int c = (q % CPR) ^ swz_h3_kn(r);
+      const int cn = (!EDGE || n0 + 8 * c < N) ? 8 * c : 0;
+      b_off[i] = static_cast<unsigned>(r * N + cn) * 2u;
+    } else {
+      const int r = q >> 2;
+      const int c = (q & 3) ^ swz_rows_h(r);
+      const int rb = EDGE ? min(n0 + r, N - 1) - n0 : r;
+      b_off[i] = static_cast<unsigned>(rb * K + 8 * c) * 2u;
+    }
   }
   // One buffer descriptor per plane (its whole extent) and one for the
-  // tile's B rows (from row n0 to the end of B, capped at 4 GiB), made once;
-  // a K step moves only the scalar offset: (kt M + m0) 64 bytes into a plane
-  // (under 2^31: M K 2 bytes is), kt 64 bytes along B's rows.
+  // tile's B (from its first element to the end of B, capped at 4 GiB), made
+  // once; a K step moves only the scalar offset: (kt M + m0) 64 bytes into a
+  // plane (under 2^31: M K 2 bytes is), kt 64 bytes along B's rows ([N x K])
+  // or kt 32 N 2 bytes down them ([K x N]: under 2^31, K N 2 bytes is).
   // Rebuilding the descriptors per K step (64-bit adds, the range clamp)
   // took some 40 scalar instructions per wave and K step, issue slots the
   // MFMAs then waited behind.
   [[maybe_unused]] const long long plane = static_cast<long long>(M) * K;
-  [[maybe_unused]] const long long b_first = static_cast<long long>(n0) * K;
+  [[maybe_unused]] const long long b_first = BKN ? n0 : static_cast<long long>(n0) * K;
+  [[maybe_unused]] const int b_step = BKN ? BK * N * 2 : BK * 2;
 #if defined(__HIP_DEVICE_COMPILE__)
   const auto ra0 = __builtin_amdgcn_make_buffer_rsrc(const_cast<_Float16*>(P), 0,
                                                      static_cast<int>(plane * 2), kRsrcWord3);
@@ -1104,7 +1127,7 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
 #pragma unroll
     for (int i = 0; i < B_INST; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * (i * 512 + wave * 64), 16,
-                                               static_cast<int>(b_off[i]), kt * (BK * 2), 0, 0);
+                                               static_cast<int>(b_off[i]), kt * b_step, 0, 0);
 #endif
   };
 
@@ -1124,8 +1147,30 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const int r = wn * WN + nb * 32 + li;
-      f.b[nb] = *reinterpret_cast<const halfx8v*>(bs + r * BK + 8 * (cq ^ swz_rows_h(r)));
+      if constexpr (BKN) {
+        // Two transposing reads (ds_read_b64_tr_b16) per fragment: in each
+        // 16-lane group lane l names 8 bytes (row k0 + l / 4, columns cb + 4 (l
+        // % 4) .. + 3) and receives column cb + l of the 4 rows. Group G of the
+        // wave takes columns 16 (G % 2) .. + 15 of the block and k half G / 2,
+        // which is the B operand's lane j + 32 (k / 8), element k % 8.
+        const int l = lane & 15;
+        const int G = lane >> 4;
+        const int col = wn * WN + nb * 32 + 16 * (G & 1) + 4 * (l & 3);  // first of the lane's 4
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k = 16 * sl + 8 * (G >> 1) + 4 * h + (l >> 2);
+          const int off = k * (BNT * 2) + (((col >> 3) ^ swz_h3_kn(k)) << 4) + ((col & 7) << 1);
+          const halfx4v v = __builtin_bit_cast(
+              halfx4v, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                           (__attribute__((address_space(3))) shortx4v*)(
+                               (__attribute__((address_space(3))) char*)bs + off)));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) f.b[nb][4 * h + e] = v[e];
+        }
+      } else {
+        const int r = wn * WN + nb * 32 + li;
+        f.b[nb] = *reinterpret_cast<const halfx8v*>(bs + r * BK + 8 * (cq ^ swz_rows_h(r)));
+      }
     }
   };
 #pragma unroll
@@ -1254,7 +1299,7 @@ __device__ __forceinline__ void h3_store(const h3::Acc<BNT>& acc, const float* _
   }
 }
 
-template <int S, int BNT, bool EDGE>
+template <int S, int BNT, bool BKN, bool EDGE>
 __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
@@ -1263,7 +1308,7 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
   const int m0 = tm * h3::BM;
   const int n0 = tn * BNT;
   h3::Acc<BNT> acc;
-  h3_tile<S, BNT, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
+  h3_tile<S, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
   h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                       N - n0);
 }
@@ -1273,7 +1318,7 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
 // split the remaining tiles' K tiles evenly, one workgroup per CU after its
 // data-parallel tiles; a split tile leaves one record per workgroup (scaled
 // rows, slot 0 its first tile, slot 1 its last) for gemm_sk_fixup_kernel.
-template <int S, int BNT, bool EDGE>
+template <int S, int BNT, bool BKN, bool EDGE>
 __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n,
@@ -1295,7 +1340,7 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
     tile_of(first_tile + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
-    h3_tile<S, BNT, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
+    h3_tile<S, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
     if (ka == 0 && kb == plan.nk) {
       h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                           N - n0);
@@ -1329,18 +1374,18 @@ bool h3_enabled() {
 
 }  // namespace
 
-bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B) {
+bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B, bool b_kn) {
   constexpr long long kLim = 0x7fffffffLL;
   // K % 32 == 0, 16-byte aligned B rows, every lane's byte offset from a
   // tile's corner (up to 128 rows of K halves) within a buffer load's 31 bits
   // and each activation plane (M K halves) within 31 bits of byte offset
   return h3_enabled() && M > 0 && N > 0 && K > 0 && K % BK == 0 && M <= kLim && N <= kLim &&
          K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM) * K * 2 <= kLim &&
-         M * K * 2 <= kLim;
+         M * K * 2 <= kLim && (!b_kn || (N % 8 == 0 && K * N * 2 <= kLim));
 }
 
 void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
-  ENG_CHECK(gemm_h3_applies(a.M, a.N, a.K, a.B) && aligned_to(a.P, 16) && a.rscale != nullptr,
+  ENG_CHECK(gemm_h3_applies(a.M, a.N, a.K, a.B, a.b_kn) && aligned_to(a.P, 16) && a.rscale != nullptr,
             "matmul (fp16 weights): shape or alignment not supported");
   const int M = static_cast<int>(a.M), N = static_cast<int>(a.N), K = static_cast<int>(a.K);
   const long long cus = device_cu_count();
@@ -1365,10 +1410,11 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
     plan.nk = nk;
     plan.I = tail * nk;
     plan.nsk = static_cast<int>(std::min<long long>(cus, plan.I));
-    auto go = [&](auto edge) {
+    auto go = [&](auto kn, auto edge) {
+      constexpr bool KN = decltype(kn)::value;
       constexpr bool E = decltype(edge)::value;
       if (!split) {
-        gemm_h3_kernel<S, BNT, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
+        gemm_h3_kernel<S, BNT, KN, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
             a.P, a.rscale, a.B, a.C, M, N, K, tiles_m, tiles_n);
         ENG_LAUNCH_CHECK();
         return;
@@ -1376,19 +1422,27 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
       StreamScratch records(
           stream, static_cast<std::size_t>(plan.nsk) * 2 * h3::BM * BNT * sizeof(float), 2);
       float* rec = static_cast<float*>(records.get());
-      gemm_h3_sk_kernel<S, BNT, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS, 0,
-                                     stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K, tiles_m,
-                                               tiles_n, plan);
+      gemm_h3_sk_kernel<S, BNT, KN, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS,
+                                         0, stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K,
+                                                      tiles_m, tiles_n, plan);
       ENG_LAUNCH_CHECK();
       gemm_sk_fixup_kernel<h3::BM, BNT, E>
           <<<dim3(static_cast<unsigned>(tail), h3::BM * BNT / 1024), 256, 0, stream>>>(
               rec, a.C, M, N, tiles_m, tiles_n, plan);
       ENG_LAUNCH_CHECK();
     };
-    if (whole)
-      go(std::integral_constant<bool, false>{});
-    else
-      go(std::integral_constant<bool, true>{});
+    using std::integral_constant;
+    if (a.b_kn) {
+      if (whole)
+        go(integral_constant<bool, true>{}, integral_constant<bool, false>{});
+      else
+        go(integral_constant<bool, true>{}, integral_constant<bool, true>{});
+    } else {
+      if (whole)
+        go(integral_constant<bool, false>{}, integral_constant<bool, false>{});
+      else
+        go(integral_constant<bool, false>{}, integral_constant<bool, true>{});
+    }
   };
   // 128 x 256 tiles (waves of 64 x 64, three 40 KiB stages) once they fill at
   // least two rounds of one tile per CU: each plane tile loaded feeds twice

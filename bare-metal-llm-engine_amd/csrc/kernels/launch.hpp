@@ -165,9 +165,11 @@ void launch_rmsnorm_split3(const float* in, const float* weight, _Float16* plane
                            long long rows, long long cols, float eps, hipStream_t stream);
 
 // C[M x N] = diag(rscale) (P[0] + P[1] + P[2]) . B^T on fp16 MFMA, B fp16
-// [N x K] (output-major weights), P the K-blocked planes of
+// [N x K] (output-major weights), or C = diag(rscale) (P[0] + P[1] + P[2]) . B
+// with B fp16 [K x N] (the reference layout, b_kn); P the K-blocked planes of
 // launch_rmsnorm_split3.
-// Needs K % 32 == 0 and 16-byte aligned P and B.
+// Needs K % 32 == 0 and 16-byte aligned P and B; [K x N] B also N % 8 == 0
+// and at most 2^31 - 1 bytes.
 struct GemmH3Args {
   const _Float16* P = nullptr;
   const float* rscale = nullptr;
@@ -176,8 +178,9 @@ struct GemmH3Args {
   std::int64_t M = 0;
   std::int64_t N = 0;
   std::int64_t K = 0;
+  bool b_kn = false;
 };
-bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B);
+bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void* B, bool b_kn);
 void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream);
 
 // out[i] = SiLU(g[i]) * u[i] in fp32.

@@ -86,10 +86,10 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
   // 2 to 4 rows (small-batch decode, each row equal to its single-row call),
   // or rows the few-row kernel does not take: the rows share passes over W.
   if (nk ? launch_gemv_nk_rows(g1, M, s) : launch_gemv_kn_rows(g1, M, s)) return;
-  // Output-major fp16 W: the rows normalised into three fp16 planes, then the
-  // fp16-MFMA GEMM (the same arithmetic as the FP32 GEMM on converted
+  // fp16 W (either layout): the rows normalised into three fp16 planes, then
+  // the fp16-MFMA GEMM (the same arithmetic as the FP32 GEMM on converted
   // weights, 16x the matrix rate per instruction).
-  if (w_elem == Elem::F16 && nk && aligned_to(in, 16) && gemm_h3_applies(M, N, K, W)) {
+  if (w_elem == Elem::F16 && aligned_to(in, 16) && gemm_h3_applies(M, N, K, W, !nk)) {
     const std::size_t plane_bytes = 3 * static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * 2;
     StreamScratch ws(s, plane_bytes + static_cast<std::size_t>(M) * sizeof(float));
     GemmH3Args h;
@@ -100,6 +100,7 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     h.M = M;
     h.N = N;
     h.K = K;
+    h.b_kn = !nk;
     launch_rmsnorm_split3(in, rms_weight, static_cast<_Float16*>(ws.get()),
                           const_cast<float*>(h.rscale), M, K, eps, s);
     launch_gemm_h3(h, s);

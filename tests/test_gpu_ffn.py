@@ -304,27 +304,28 @@ def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma
 
 
 @pytest.mark.parametrize("M,N,K", [(1000, 2816, 1024), (300, 11008, 512)])
-def test_rmsnorm_linear_swiglu_nk_prefill_fp16_mfma(gpu, orc, M, N, K):
-    # Prefill with output-major fp16 weights: the rows split once into three
-    # fp16 planes, gate and up on the fp16-MFMA GEMM (ragged M and N on the
-    # first shape; 258 tiles and the stream-K split on the second). Eight rows
-    # of every 128-row tile against every column.
-    rng = np.random.default_rng(M + 3 * N + K)
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_swiglu_prefill_fp16_mfma(gpu, orc, M, N, K, layout):
+    # Prefill with fp16 weights in either layout: the rows split once into
+    # three fp16 planes, gate and up on the fp16-MFMA GEMM (ragged M and N on
+    # the first shape; 258 tiles and the stream-K split on the second). Eight
+    # rows of every 128-row tile against every column.
+    rng = np.random.default_rng(M + 3 * N + K + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     Wg = orc.f32_to_f16((rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32))
     Wu = orc.f32_to_f16((rng.standard_normal((N, K), dtype=np.float32) / np.sqrt(K)).astype(np.float32))
-    got = gpu_glu_nk(gpu, x, g, Wg, Wu)
+    Wg_kn, Wu_kn = np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T)
+    got = gpu_glu_nk(gpu, x, g, Wg, Wu) if layout == "nk" else gpu_glu_kn(gpu, x, g, Wg_kn, Wu_kn)
     rows = []
     for m0 in range(0, M, 128):
         last = min(m0 + 127, M - 1)
         rows += [m0, m0 + 1, min(m0 + 63, last), min(m0 + 64, last), last]
         rows += list(rng.integers(m0, last + 1, 3))
     rows = np.unique(rows)
-    Wg_kn, Wu_kn = np.ascontiguousarray(Wg.T), np.ascontiguousarray(Wu.T)
     act64, bd, bs = glu_reference(x[rows], g, Wg_kn, Wu_kn)
     check_glu(got[rows], orc.rmsnorm_linear_swiglu(x[rows], g, Wg_kn, Wu_kn, EPS), act64, bd, bs,
-              f"rmsnorm_linear_swiglu nk prefill {M}x{N}x{K}")
+              f"rmsnorm_linear_swiglu {layout} prefill {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("M,N,K,dtype", [(2, 11008, 4096, "f16"), (3, 1000, 2048, "f16"),

@@ -302,43 +302,55 @@ def test_rmsnorm_linear_f16w_ragged_tiles(gpu, orc, M, N, K, layout):
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
 
 
+def gpu_rmsnorm_linear_f16w(eng, x, g, W, layout):
+    """fp16 W given [K x N]: through the reference-layout entry point, or
+    transposed through the output-major one."""
+    if layout == "kn":
+        return gpu_rmsnorm_linear(eng, x, g, W)
+    return gpu_rmsnorm_linear_nk(eng, x, g, np.ascontiguousarray(W.T))
+
+
 @pytest.mark.parametrize("M,N,K", [(65, 128, 32), (128, 128, 64), (200, 136, 96), (256, 256, 128),
-                                   (130, 300, 160), (1000, 257, 224)])
+                                   (130, 304, 160), (1000, 264, 224), (130, 300, 160)])
 @pytest.mark.parametrize("with_gamma", [True, False])
-def test_rmsnorm_linear_f16w_nk_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma):
-    # M > 64, fp16 output-major W, K % 32 == 0: the rows are split into three
-    # K-blocked fp16 planes and multiplied on the fp16 matrix cores. K = 32 ..
-    # 224 is 1 to 7 K steps (every remainder of the four-stage ring), M and N
-    # whole and ragged; every row is checked.
-    rng = np.random.default_rng(13 * M + N + K + with_gamma)
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_f16w_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma, layout):
+    # M > 64, fp16 W in either layout, K % 32 == 0: the rows are split into
+    # three K-blocked fp16 planes and multiplied on the fp16 matrix cores
+    # ([K x N] weights through transposing LDS reads; N % 8 == 0 there, so
+    # N = 300 takes the FP32 GEMM in that layout). K = 32 .. 224 is 1 to 7 K
+    # steps (every remainder of the four-stage ring), M and N whole and
+    # ragged; every row is checked.
+    rng = np.random.default_rng(13 * M + N + K + with_gamma + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
     W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
-    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    got = gpu_rmsnorm_linear_f16w(gpu, x, g, W, layout)
     y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
-    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w nk {M}x{N}x{K}")
+    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 12760, 256), (384, 11008, 256), (1000, 4100, 384),
-                                   (1000, 9000, 256), (2000, 8300, 256), (2000, 8300, 96),
-                                   (2000, 8300, 64), (2048, 8448, 256), (2048, 8192, 64)])
-def test_rmsnorm_linear_f16w_nk_fp16_mfma_stream_k(gpu, orc, M, N, K):
+@pytest.mark.parametrize("M,N,K", [(300, 12760, 256), (384, 11008, 256), (1000, 4104, 384),
+                                   (1000, 9000, 256), (2000, 8296, 256), (2000, 8296, 96),
+                                   (2000, 8296, 64), (2048, 8448, 256), (2048, 8192, 64)])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_f16w_fp16_mfma_stream_k(gpu, orc, M, N, K, layout):
     # Tile counts past one round of one tile per CU (256 on MI355X): whole
     # rounds data-parallel, the last round's tiles split over the CUs by K
     # tile and added by the fix-up pass. 128 x 128 tiles: 300, 258, 264 and
     # 568 (ragged M and N on the first, third and fourth shapes; on the
     # second, 2 tail tiles split into single K tiles; 1000 x 9000 splits after
     # two whole rounds). 128 x 256 tiles (at least two rounds of them): 2000 x
-    # 8300, 528 tiles ragged both ways, splits the last 16 at K = 256 and runs
+    # 8296, 528 tiles ragged both ways, splits the last 16 at K = 256 and runs
     # unsplit through the three-stage ring's remainders at 3 and 2 K steps;
     # 2048 x 8448 and 2048 x 8192 are the whole-tile forms, split and not.
-    # Eight rows of every 128-row tile (its edges and random ones) against
-    # every column, so every tile is checked.
-    rng = np.random.default_rng(17 * M + N + K)
+    # Both weight layouts. Eight rows of every 128-row tile (its edges and
+    # random ones) against every column, so every tile is checked.
+    rng = np.random.default_rng(17 * M + N + K + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
     W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
-    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    got = gpu_rmsnorm_linear_f16w(gpu, x, g, W, layout)
     rows = []
     for m0 in range(0, M, 128):
         last = min(m0 + 127, M - 1)
@@ -346,11 +358,12 @@ def test_rmsnorm_linear_f16w_nk_fp16_mfma_stream_k(gpu, orc, M, N, K):
         rows += list(rng.integers(m0, last + 1, 3))
     rows = np.unique(rows)
     y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
-    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w nk stream-K {M}x{N}x{K}")
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} stream-K {M}x{N}x{K}")
 
 
 @pytest.mark.parametrize("gscale", [1e-30, 1e-3, 1.0, 1e25])
-def test_rmsnorm_linear_f16w_nk_fp16_mfma_row_scales(gpu, orc, gscale):
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_f16w_fp16_mfma_row_scales(gpu, orc, gscale, layout):
     # The planes hold each row times its own power of two (row maximum moved
     # into [2^14, 2^15)): gamma far below and above fp16's range keeps the
     # FP32 bound, rows of very different size share a tile, and an all-zero
@@ -364,10 +377,10 @@ def test_rmsnorm_linear_f16w_nk_fp16_mfma_row_scales(gpu, orc, gscale):
     x[40] = 0.0
     g = (gscale * (1 + 0.1 * rng.standard_normal(K))).astype(np.float32)
     W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
-    got = gpu_rmsnorm_linear_nk(gpu, x, g, np.ascontiguousarray(W.T))
+    got = gpu_rmsnorm_linear_f16w(gpu, x, g, W, layout)
     assert np.all(got[5] == 0.0) and np.all(got[40] == 0.0)
     y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
-    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w nk row scales, gamma x {gscale:g}")
+    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w {layout} row scales, gamma x {gscale:g}")
 
 
 @pytest.mark.parametrize("N,K,dtype", [(127, 31, "f32"), (73, 125, "f16w"), (4100, 4096, "f16w"),
