@@ -1232,6 +1232,8 @@ SUMMARY_ROWS = (
     ("gemm_2048_tflops", "matmul_f32 2048x2048x2048", "TFLOP/s"),
     ("prefill_f16w_nk_512x11008_ms", "rmsnorm_linear_f16w 512x11008x4096 prefill, fp16 W output-major",
      "ms_per_call"),
+    ("prefill_f16w_kn_512x11008_ms", "rmsnorm_linear_f16w 512x11008x4096 prefill, fp16 W reference layout",
+     "ms_per_call"),
     ("ffn_prefill_512_ms", "FFN gate/up + SwiGLU 512x11008x4096 fp16-W prefill", "ms_per_call"),
     ("prefill_f16w_nk_4096x11008_tflops", "rmsnorm_linear_f16w 4096x11008x4096 prefill", "TFLOP/s"),
     ("gemv_fp32_4096_us", "gemv (fp32 W) 4096x4096 cold", "us_per_call"),
