@@ -748,6 +748,9 @@ __global__ __launch_bounds__(256) void gemm_sk_fixup_kernel(const float* __restr
   const int slot_f = sk_begin(sf, plan) == t * plan.nk ? 0 : 1;
   const int e = 4 * (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x));
   floatx4 v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  // (unrolled so a group's loads are in flight together; the adds keep
+  // workgroup order)
+#pragma unroll 8
   for (long long s = sf; s <= sl; ++s) {
     const long long r = s * 2 + (s == sf ? slot_f : 0);
     v += *reinterpret_cast<const floatx4*>(rec + r * static_cast<long long>(BM * BN) + e);
@@ -1397,19 +1400,24 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
     const long long ntiles = static_cast<long long>(tiles_m) * tiles_n;
     ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
     const bool whole = M % h3::BM == 0 && N % BNT == 0;
-    // Stream-K when the last round of one tile per CU is at most half full
-    // (512 x 11008 on 128 x 128 tiles: 88 of 256, 148.7 -> 138.3 us; at 176 of
-    // 256 the records and the fix-up pass cost more than the split saves),
-    // with at least 8 K tiles per tile; the tail's workgroups run after the
-    // whole rounds.
-    const long long tail = ntiles % cus;
+    // Stream-K, with at least 8 K tiles per tile: past one round of one tile
+    // per CU when the last round is at most half full (512 x 11008 on 128 x
+    // 128 tiles: 88 of 256, 148.7 -> 138.3 us; at 176 of 256 the records and
+    // the fix-up pass cost more than the split saves), the tail's workgroups
+    // running after the whole rounds; below half a round every tile is split
+    // (65-128 x 11008, 86 tiles: 57-59 -> 45-52 us; at 172 tiles, 1.5 pieces
+    // a tile, 70-72 -> 78-84 us, so those run whole). Each split workgroup
+    // takes at least 8 K tiles, so a small tail is not spread one K tile per
+    // CU (384 x 11008, 2 tail tiles, 136.5 -> 102.7 us: the fix-up had summed
+    // 128 records per element).
     const int nk = K / BK;
-    const bool split = sk_enabled() && ntiles > cus && tail != 0 && 2 * tail <= cus && nk >= 8;
+    const long long tail = ntiles >= cus ? ntiles % cus : ntiles;
+    const bool split = sk_enabled() && nk >= 8 && tail != 0 && 2 * tail <= cus;
     SkPlan plan;
     plan.dp = static_cast<int>(ntiles - tail);
     plan.nk = nk;
     plan.I = tail * nk;
-    plan.nsk = static_cast<int>(std::min<long long>(cus, plan.I));
+    plan.nsk = static_cast<int>(std::max<long long>(1, std::min<long long>(cus, plan.I / 8)));
     auto go = [&](auto kn, auto edge) {
       constexpr bool KN = decltype(kn)::value;
       constexpr bool E = decltype(edge)::value;

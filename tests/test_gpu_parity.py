@@ -311,7 +311,8 @@ def gpu_rmsnorm_linear_f16w(eng, x, g, W, layout):
 
 
 @pytest.mark.parametrize("M,N,K", [(65, 128, 32), (128, 128, 64), (200, 136, 96), (256, 256, 128),
-                                   (130, 304, 160), (1000, 264, 224), (130, 300, 160)])
+                                   (130, 304, 160), (1000, 264, 224), (130, 300, 160),
+                                   (130, 1000, 512)])
 @pytest.mark.parametrize("with_gamma", [True, False])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_rmsnorm_linear_f16w_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma, layout):
@@ -320,7 +321,8 @@ def test_rmsnorm_linear_f16w_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma, 
     # ([K x N] weights through transposing LDS reads; N % 8 == 0 there, so
     # N = 300 takes the FP32 GEMM in that layout). K = 32 .. 224 is 1 to 7 K
     # steps (every remainder of the four-stage ring), M and N whole and
-    # ragged; every row is checked.
+    # ragged; 130 x 1000 x 512 (16 tiles, fewer than the CUs) splits every
+    # tile by K. Every row is checked.
     rng = np.random.default_rng(13 * M + N + K + with_gamma + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
