@@ -956,30 +956,33 @@ void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
 
 // ---------------------------------------------------------------------------
 // fp16 weights on the fp16 matrix cores: C[M x N] = diag(rscale) (P0 + P1 +
-// P2) . B^T for B fp16 [N x K] (output-major weights) and the three fp16
-// planes P of the scaled activation rows (launch_rmsnorm_split3). Every
-// product of an fp16 plane value and an fp16 weight is exact in fp32 and the
-// planes sum to the scaled row (to 2^-39 of its largest value), so this is
-// the FP32 GEMM's arithmetic on v_mfma_f32_32x32x16_f16, which runs 16 times
-// the FP32 instruction's rate: three of them (one per plane) per 32 x 32 x 16
-// block against eight v_mfma_f32_32x32x2_f32.
+// P2) . W for fp16 weights W, given [N x K] (output-major: the kernel reads
+// W^T) or [K x N] (the reference layout), and the three fp16 planes P of the
+// scaled activation rows (launch_rmsnorm_split3). Every product of an fp16
+// plane value and an fp16 weight is exact in fp32 and the planes sum to the
+// scaled row (to 2^-39 of its largest value), so this is the FP32 GEMM's
+// arithmetic on v_mfma_f32_32x32x16_f16, which runs 16 times the FP32
+// instruction's rate: three of them (one per plane) per 32 x 32 x 16 block
+// against eight v_mfma_f32_32x32x2_f32.
 //
-// Tiles of 128 x 128, 8 waves (4 x 2) of 32 x 64 each (two 32 x 32 blocks:
-// per 16-deep slice three plane fragments and two B fragments feed six
-// MFMAs), K step 32 (two slices), four LDS stages of 32 KiB (the three plane
-// tiles and the B tile) and one workgroup per CU. The planes are K-blocked
-// (launch_rmsnorm_split3), so a plane tile of one K step is 8 KiB in one
-// piece and every load instruction reads whole cache lines; with the planes
-// row-major each instruction touched 16 rows of 64 bytes, half of each
-// 128-byte line, and the vector memory path, not the MFMAs, set the pace.
-// Operand layout of the instruction (checked on the device): A[i][k] in lane
-// i + 32 (k / 8) element k % 8, B[k][j] in lane j + 32 (k / 8) element k %
-// 8, the accumulator as for the FP32 instruction. Each lane's fragment is one
-// 16-byte LDS read of its row (plane or B^T row); tiles are rows of 4
-// 16-byte chunks, chunk c of row r at c ^ swz_rows_h(r). Direct loads, the
-// slice read-ahead, the stage hand-over and the interleaved fetch follow the
-// FP32 kernel. Tile counts past one round of one tile per CU take the
-// stream-K split of gemm_sk_kernel (gemm_h3_sk_kernel).
+// Tiles of 128 x 128 (8 waves, 4 x 2, of 32 x 64: per 16-deep slice three
+// plane fragments and two weight fragments feed six MFMAs; four LDS stages
+// of 32 KiB) or, from two rounds of them up, 128 x 256 (8 waves, 2 x 4, of
+// 64 x 64; three stages of 40 KiB): K step 32 (two slices), one workgroup
+// per CU. The planes are K-blocked (launch_rmsnorm_split3), so a plane tile
+// of one K step is 8 KiB in one piece and every load instruction reads whole
+// cache lines; with the planes row-major each instruction touched 16 rows of
+// 64 bytes, half of each 128-byte line, and the vector memory path, not the
+// MFMAs, set the pace. Operand layout of the instruction (checked on the
+// device): A[i][k] in lane i + 32 (k / 8) element k % 8, B[k][j] in lane j +
+// 32 (k / 8) element k % 8, the accumulator as for the FP32 instruction.
+// Plane fragments, and [N x K] weight fragments, are one 16-byte LDS read of
+// their row (tiles are rows of 4 16-byte chunks, chunk c of row r at c ^
+// swz_rows_h(r)); [K x N] weight fragments are two transposing reads of the
+// k rows. Direct loads, the slice read-ahead, the stage hand-over and the
+// interleaved fetch follow the FP32 kernel. Past one round of tiles a last
+// round at most half full, and below half a round every tile, is split by K
+// (gemm_h3_sk_kernel, the plan of gemm_sk_kernel).
 namespace h3 {
 constexpr int BM = 128;
 constexpr int WAVES = 8;
