@@ -638,6 +638,12 @@ __device__ __forceinline__ void store_acc(const TileAcc<BM, BN>& acc, float* __r
   const int lg = lane >> 5;
   const int wm = wave / C::WGN;
   const int wn = wave % C::WGN;
+#if defined(__HIP_DEVICE_COMPILE__)
+  // In the stream-K kernel's tile loop the per-element offsets row ld + col
+  // are loop-invariant; hoisted they held registers through the K loop (36
+  // bytes of spills at 128 x 128). An opaque ld keeps them here.
+  asm volatile("" : "+s"(ld));
+#endif
 #pragma unroll
   for (int mb = 0; mb < C::MB; ++mb) {
 #pragma unroll
