@@ -889,6 +889,16 @@ Tile choose_tile(long long M, long long N) {
 // and two rounds of one tile per CU (CUs < T < 2 CUs; every other shape
 // keeps choose_tile's tiling): full tiles and the direct-load conditions
 // only. ENGINE_GEMM_NO_SK=1 switches it off.
+// The single-launch small-GEMM kernel can be switched off
+// (ENGINE_GEMM_NO_SMALL=1).
+bool small_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_NO_SMALL");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
 bool sk_enabled() {
   static const bool on = [] {
     const char* v = std::getenv("ENGINE_GEMM_NO_SK");
@@ -925,6 +935,96 @@ bool run_gemm_sk(const GemmArgs& a, hipStream_t stream) {
   return true;
 }
 
+// Small GEMMs in one launch: one 32 x 32 tile of C per workgroup, its four
+// waves each taking a quarter of K straight from global memory into the
+// v_mfma_f32_32x32x2_f32 operands, the four partial tiles summed through LDS
+// in wave order (512^3: 256 workgroups, every SIMD of the chip busy, where
+// 64 x 64 tiles keep a quarter of the CUs). MFMA step t of a lane group g
+// takes k = k8 + 4 g + t (k8 a multiple of 8): lane (r, g) loads A[row r][k8
+// + 4 g .. + 3] as one float4 and B[k8 + 4 g + t][column r] as four floats
+// (32 lanes read 128 consecutive bytes of a B row). Loads run DS iterations
+// of 8 k ahead in a register ring; two accumulators (even and odd t) per
+// wave, added before the wave sum. Needs M and N multiples of 32, K of 256,
+// A rows 16-byte aligned, B row-major [K x N].
+namespace small {
+constexpr int DS = 8;  // iterations (8 k each) in flight per wave
+}
+__global__ __launch_bounds__(256) void gemm_small_splitk_kernel(const float* __restrict__ A,
+                                                               const float* __restrict__ B,
+                                                               float* __restrict__ C, int M, int N,
+                                                               int K, int tiles_n) {
+  constexpr int D = small::DS;
+  __shared__ float red[4][16][64];
+  const int tm = blockIdx.x / tiles_n;
+  const int tn = blockIdx.x % tiles_n;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 31;
+  const int g = lane >> 5;
+  const int kq = K / 4;
+  const int iters = kq / 8;  // a multiple of D (K % 256 == 0)
+  const float* ap = A + static_cast<long long>(tm * 32 + r) * K + wave * kq + 4 * g;
+  const float* bp = B + static_cast<long long>(wave * kq + 4 * g) * N + tn * 32 + r;
+  const long long bstep = 8LL * N;
+  floatx4 a[D];
+  float b[D][4];
+  auto load = [&](int d, int it) {
+    a[d] = *reinterpret_cast<const floatx4*>(ap + 8 * it);
+    const float* q = bp + it * bstep;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[d][t] = q[static_cast<long long>(t) * N];
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, d);
+  floatx16 acc0, acc1;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc0[v] = acc1[v] = 0.0f;
+  for (int i = 0; i < iters; i += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d][0], b[d][0], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d][1], b[d][1], acc1, 0, 0, 0);
+      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d][2], b[d][2], acc0, 0, 0, 0);
+      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a[d][3], b[d][3], acc1, 0, 0, 0);
+      if (i + D + d < iters) load(d, i + D + d);
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < 16; ++v) red[wave][v][lane] = acc0[v] + acc1[v];
+  __syncthreads();
+  // Accumulator element v of lane l: C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int idx = threadIdx.x + 256 * q;
+    const int v = idx >> 6;
+    const int l = idx & 63;
+    const float sum = ((red[0][v][l] + red[1][v][l]) + red[2][v][l]) + red[3][v][l];
+    const int row = tm * 32 + 8 * (v >> 2) + 4 * (l >> 5) + (v & 3);
+    const int col = tn * 32 + (l & 31);
+    C[static_cast<long long>(row) * N + col] = sum;
+  }
+}
+
+template <typename BT, bool BNK>
+bool run_gemm_small(const GemmArgs& a, hipStream_t stream) {
+  if constexpr (BNK || !std::is_same<BT, float>::value) {
+    return false;
+  } else {
+    if (!small_enabled() || a.M % 32 != 0 || a.N % 32 != 0 || a.K % 256 != 0 ||
+        !aligned_to(a.A, 16))
+      return false;
+    const long long cus = device_cu_count();
+    if (2 * (a.M / 64) * (a.N / 64) > cus) return false;  // 64 x 64 tiles fill half the CUs
+    const long long tiles = (a.M / 32) * (a.N / 32);
+    ENG_CHECK(tiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
+    gemm_small_splitk_kernel<<<static_cast<unsigned>(tiles), 256, 0, stream>>>(
+        a.A, static_cast<const float*>(a.B), a.C, static_cast<int>(a.M), static_cast<int>(a.N),
+        static_cast<int>(a.K), static_cast<int>(a.N / 32));
+    ENG_LAUNCH_CHECK();
+    return true;
+  }
+}
+
 // 256 x 128 tiles where choose_tile's model takes 128 x 128 and gives the
 // larger tile no longer a makespan (rounds of one tile per CU, times the
 // tile's area: 4096^3 has 512 such tiles against 1024, two rounds of twice
@@ -943,6 +1043,7 @@ bool big_tile(const GemmArgs& a) {
 template <typename BT, bool BNK>
 void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
   if (run_gemm_sk<BT, BNK>(a, stream)) return;
+  if (run_gemm_small<BT, BNK>(a, stream)) return;
   if (big_tile<BT, BNK>(a)) {
     run_gemm<256, 128, BT, BNK>(a, stream);
     return;

@@ -171,6 +171,21 @@ def test_config3_rmsnorm_linear_f16w(gpu, orc):
     check_rmsnorm_linear(got, y, x, g, W, K, "config 3 rmsnorm_linear_f16w 4096x11008")
 
 
+@pytest.mark.parametrize("M,N,K", [(256, 512, 1024), (96, 320, 512), (512, 1024, 2048), (480, 480, 768)])
+def test_matmul_small_single_launch(gpu, orc, M, N, K):
+    # At most half a round of 64 x 64 tiles (config 1's 512^3 is another):
+    # one 32 x 32 tile per workgroup, its four waves splitting K and summing
+    # through LDS in wave order. Every row, and the same bits on a second
+    # call.
+    rng = np.random.default_rng(M + 3 * N + K)
+    A = rng.uniform(-1, 1, (M, K)).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    got = gpu_matmul(gpu, A, B)
+    y = orc.matmul(A, B).astype(np.float64)
+    check_dot(got, y, helpers.absdot(A, B) + np.abs(y), K, f"matmul {M}x{N}x{K}")
+    assert np.array_equal(got, gpu_matmul(gpu, A, B)), "same inputs, different bits"
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (512, 11008, 4096), (512, 4096, 11008)])
 def test_config4_matmul_sampled_rows(gpu, orc, M, N, K):
     rng = np.random.default_rng(3)
