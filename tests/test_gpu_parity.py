@@ -378,6 +378,30 @@ def test_rmsnorm_linear_f16w_fp16_mfma_stream_k(gpu, orc, M, N, K, layout):
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} stream-K {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_f16w_fp16_mfma_long_prompt(gpu, orc, layout):
+    # 4096 x 11008 x 4096 (a 4096-token prompt at the FFN width): 128 x 256
+    # tiles, 1376 of them, the last 96 split by K. Sampled rows of every
+    # 1024-row quarter against the oracle, and the column sums of all rows
+    # against float64: sum_r y[r] = (sum_r xn[r]) . W with xn the normalised
+    # rows.
+    M, N, K = 4096, 11008, 4096
+    rng = np.random.default_rng(4096 + (layout == "kn"))
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (0.02 * rng.standard_normal((K, N), dtype=np.float32)).astype(np.float16).view(np.uint16)
+    got = gpu_rmsnorm_linear_f16w(gpu, x, g, W, layout)
+    rows = np.unique(np.concatenate([[0, 128, 1023, 2048, M - 1], rng.integers(0, M, 2)]))
+    y = orc.rmsnorm_linear(x[rows], g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} {M}x{N}x{K}")
+    W64 = helpers.as_f64(W)
+    xn = helpers.rms_scale64(x) * helpers.as_f64(x) * helpers.as_f64(g)
+    colsum = got.astype(np.float64).sum(axis=0)
+    ref = xn.sum(axis=0) @ W64
+    bound = (K + M + 8) * helpers.U32 * (np.abs(xn).sum(axis=0) @ np.abs(W64))
+    helpers.assert_within(colsum, ref, bound, f"rmsnorm_linear f16w {layout} {M}x{N}x{K} column sums")
+
+
 @pytest.mark.parametrize("gscale", [1e-30, 1e-3, 1.0, 1e25])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_rmsnorm_linear_f16w_fp16_mfma_row_scales(gpu, orc, gscale, layout):
