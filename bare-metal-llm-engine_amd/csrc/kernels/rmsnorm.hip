@@ -142,7 +142,10 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 // block of any run of rows is one contiguous slab (a 128-row GEMM tile of one
 // K step is 8 KiB in one piece). Needs cols % 32 == 0 and 16-byte aligned in.
 // One workgroup per row (grid-stride); the row's first KPER float4 per thread
-// stay in registers between the three passes, the rest is read again.
+// and their gamma values are loaded together up front and stay in registers
+// between the three passes (gamma loaded only in the second pass cost a
+// second memory round trip behind the first reduction); the rest is read
+// again.
 template <int KPER>
 __global__ __launch_bounds__(kThreads) void rmsnorm_split3_kernel(
     const float* __restrict__ in, const float* __restrict__ weight, _Float16* __restrict__ planes,
@@ -154,11 +157,15 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_split3_kernel(
   const long long n4 = cols / 4;
   for (long long r = blockIdx.x; r < rows; r += gridDim.x) {
     const float4* src = reinterpret_cast<const float4*>(in + r * cols);
+    const float* wp = weight != nullptr ? weight : in;  // read and unused when null
     float4 keep[KPER];
+    float4 wk[KPER];
 #pragma unroll
     for (int j = 0; j < KPER; ++j) {
       const long long i = t + static_cast<long long>(j) * kThreads;
-      keep[j] = src[i < n4 ? i : 0];
+      const long long ic = i < n4 ? i : 0;
+      keep[j] = src[ic];
+      wk[j] = make_float4(wp[4 * ic], wp[4 * ic + 1], wp[4 * ic + 2], wp[4 * ic + 3]);
     }
     float ss = 0.0f;
     auto add_sq = [&](float4 v) {
@@ -173,18 +180,23 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_split3_kernel(
     for (long long i = t + static_cast<long long>(KPER) * kThreads; i < n4; i += kThreads)
       add_sq(src[i]);
     const float scale = 1.0f / sqrtf(block_sum(ss, red) / static_cast<float>(cols) + eps);
-    auto value = [&](float4 v, long long i) {
+    auto value = [&](float4 v, float4 gw) {
       v.x *= scale;
       v.y *= scale;
       v.z *= scale;
       v.w *= scale;
       if (weight != nullptr) {
-        v.x *= weight[4 * i];
-        v.y *= weight[4 * i + 1];
-        v.z *= weight[4 * i + 2];
-        v.w *= weight[4 * i + 3];
+        v.x *= gw.x;
+        v.y *= gw.y;
+        v.z *= gw.z;
+        v.w *= gw.w;
       }
       return v;
+    };
+    auto gamma_at = [&](long long i) {
+      return weight != nullptr ? make_float4(weight[4 * i], weight[4 * i + 1], weight[4 * i + 2],
+                                             weight[4 * i + 3])
+                               : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     };
     auto amax = [](float m, float4 v) {
       return fmaxf(fmaxf(fmaxf(m, fabsf(v.x)), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -194,12 +206,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_split3_kernel(
     for (int j = 0; j < KPER; ++j) {
       const long long i = t + static_cast<long long>(j) * kThreads;
       if (i < n4) {
-        keep[j] = value(keep[j], i);
+        keep[j] = value(keep[j], wk[j]);
         mx = amax(mx, keep[j]);
       }
     }
     for (long long i = t + static_cast<long long>(KPER) * kThreads; i < n4; i += kThreads)
-      mx = amax(mx, value(src[i], i));
+      mx = amax(mx, value(src[i], gamma_at(i)));
     mx = block_max(mx, red);
     int e = 0;
     if (mx > 0.0f && mx <= 3.4028235e38f) {
@@ -229,7 +241,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_split3_kernel(
       if (i < n4) put(i, keep[j]);
     }
     for (long long i = t + static_cast<long long>(KPER) * kThreads; i < n4; i += kThreads)
-      put(i, value(src[i], i));
+      put(i, value(src[i], gamma_at(i)));
     if (t == 0) rscale[r] = ldexpf(1.0f, -e);
   }
 }
