@@ -378,6 +378,32 @@ def test_rmsnorm_linear_f16w_fp16_mfma_stream_k(gpu, orc, M, N, K, layout):
     check_rmsnorm_linear(got[rows], y, x[rows], g, W, K, f"rmsnorm_linear f16w {layout} stream-K {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("case", ["k_not_32", "kn_n_not_8", "misaligned_x"])
+@pytest.mark.parametrize("layout", ["nk", "kn"])
+def test_rmsnorm_linear_f16w_prefill_fallbacks(gpu, orc, case, layout):
+    # Prefill calls the fp16-MFMA path does not take run RMSNorm into fp32
+    # scratch and the FP32 MFMA GEMM on converted weights: K % 32 != 0, a
+    # reference-layout N % 8 != 0, and activations not 16-byte aligned.
+    M, N, K = {"k_not_32": (100, 300, 200), "kn_n_not_8": (100, 302, 256),
+               "misaligned_x": (130, 256, 256)}[case]
+    rng = np.random.default_rng(M + N + K + (layout == "kn"))
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    W = (rng.standard_normal((K, N), dtype=np.float32) / np.sqrt(K)).astype(np.float16).view(np.uint16)
+    if case == "misaligned_x":
+        Wd = gpu.upload(W if layout == "kn" else np.ascontiguousarray(W.T))
+        dxb = gpu.upload(np.concatenate([[0.0], x.reshape(-1)]).astype(np.float32))
+        dg, dy = gpu.upload(g), gpu.empty((M, N), np.float32)
+        fn = "eng_rmsnorm_linear_f16w" if layout == "kn" else "eng_rmsnorm_linear_f16w_nk"
+        gpu.call(fn, dxb.ptr + 4, dg.ptr, Wd.ptr, dy.ptr, M, N, K, EPS, None)
+        gpu.sync()
+        got = dy.download()
+    else:
+        got = gpu_rmsnorm_linear_f16w(gpu, x, g, W, layout)
+    y = orc.rmsnorm_linear(x, g, W, EPS).astype(np.float64)
+    check_rmsnorm_linear(got, y, x, g, W, K, f"rmsnorm_linear f16w {layout} {case} {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_rmsnorm_linear_f16w_fp16_mfma_long_prompt(gpu, orc, layout):
     # 4096 x 11008 x 4096 (a 4096-token prompt at the FFN width): 128 x 256
