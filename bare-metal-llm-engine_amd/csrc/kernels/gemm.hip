@@ -1173,11 +1173,11 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
 
   // Direct loads: each load of wave w fills 16-byte slots 64 w + lane of a
   // 512-slot part of a tile (the three plane tiles; the B tile's BNT / 128
-  // parts, part i holding slots 512 i ..); slot q of a tile is row q / 4,
-  // position q % 4, holding chunk (q % 4) ^ swz_rows_h(row). The planes are
-  // K-blocked ([K / 32][M][32] each): a plane tile is a contiguous run of
-  // 64-byte rows, so a load instruction covers 1 KiB in one piece (whole
-  // cache lines).
+  // parts, part i holding slots 512 i ..). In plane tiles and [N x K] B
+  // tiles slot q is row q / 4, position q % 4, holding chunk (q % 4) ^
+  // swz_rows_h(row) ([K x N] B tiles below). The planes are K-blocked
+  // ([K / 32][M][32] each): a plane tile is a contiguous run of 64-byte rows,
+  // so a load instruction covers 1 KiB in one piece (whole cache lines).
   [[maybe_unused]] unsigned a_off;  // (read by device code only)
   [[maybe_unused]] unsigned b_off[B_INST];
   {
