@@ -1563,13 +1563,21 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
     }
   };
   // 128 x 256 tiles (waves of 64 x 64, three 40 KiB stages) once they fill at
-  // least two rounds of one tile per CU: each plane tile loaded feeds twice
-  // the MFMAs (2048 x 11008 x 4096: 500 -> 462 us); with fewer the last
-  // round's share of the time grows, and 1000 x 11008 (344 of them, split by
-  // K past the first round) ran no faster than on 688 narrow ones. Else 128 x
-  // 128 (waves of 32 x 64, four 32 KiB stages).
+  // least 60% of a round of one tile per CU: each plane tile loaded feeds
+  // twice the MFMAs (x 11008 x 4096: 512 rows 141 -> 128 us, one round of 172
+  // wide tiles against 344 narrow ones split past the first round; 1280 rows
+  // 332 -> 291; 2048 rows 489 -> 445; 512 x 12288: 148 -> 137). Below that
+  // the narrow tiles fill the CUs better (384 rows, 129 wide tiles: 106
+  // against 111 us; 256 rows 72 against 85), and so they do between one and
+  // two rounds of wide tiles when more than a quarter round would be split
+  // (1024 x 11008, 344 wide tiles, 88 split: 260 against 244 us on 688
+  // unsplit narrow ones). Else 128 x 128 (waves of 32 x 64, four 32 KiB
+  // stages).
   const long long wide_tiles = static_cast<long long>(tiles_m) * ((N + 255) / 256);
-  if (h3_wide_enabled() && wide_tiles >= 2 * cus)
+  const long long wide_tail = wide_tiles % cus;
+  const bool wide_split_heavy = wide_tiles > cus && wide_tiles < 2 * cus && 4 * wide_tail > cus &&
+                                2 * wide_tail <= cus;
+  if (h3_wide_enabled() && 5 * wide_tiles >= 3 * cus && !wide_split_heavy)
     run(std::integral_constant<int, 256>{}, std::integral_constant<int, 3>{});
   else
     run(std::integral_constant<int, 128>{}, std::integral_constant<int, 4>{});
