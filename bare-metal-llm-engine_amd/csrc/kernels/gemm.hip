@@ -1074,8 +1074,8 @@ void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
 //
 // Tiles of 128 x 128 (8 waves, 4 x 2, of 32 x 64: per 16-deep slice three
 // plane fragments and two weight fragments feed six MFMAs; four LDS stages
-// of 32 KiB) or, from two rounds of them up, 128 x 256 (8 waves, 2 x 4, of
-// 64 x 64; three stages of 40 KiB): K step 32 (two slices), one workgroup
+// of 32 KiB) or, from 60% of a round of them up, 128 x 256 (8 waves, 2 x 4,
+// of 64 x 64; three stages of 40 KiB): K step 32 (two slices), one workgroup
 // per CU. The planes are K-blocked (launch_rmsnorm_split3), so a plane tile
 // of one K step is 8 KiB in one piece and every load instruction reads whole
 // cache lines; with the planes row-major each instruction touched 16 rows of

@@ -354,13 +354,13 @@ def test_rmsnorm_linear_f16w_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma, 
 def test_rmsnorm_linear_f16w_fp16_mfma_stream_k(gpu, orc, M, N, K, layout):
     # Tile counts past one round of one tile per CU (256 on MI355X): whole
     # rounds data-parallel, the last round's tiles split over the CUs by K
-    # tile and added by the fix-up pass. 128 x 128 tiles: 300, 258, 264 and
-    # 568 (ragged M and N on the first, third and fourth shapes; on the
-    # second, 2 tail tiles split into single K tiles; 1000 x 9000 splits after
-    # two whole rounds). 128 x 256 tiles (at least two rounds of them): 2000 x
-    # 8296, 528 tiles ragged both ways, splits the last 16 at K = 256 and runs
-    # unsplit through the three-stage ring's remainders at 3 and 2 K steps;
-    # 2048 x 8448 and 2048 x 8192 are the whole-tile forms, split and not.
+    # tile and added by the fix-up pass. 128 x 128 tiles: 300, 258 and 264
+    # (ragged M and N on the first and third shapes; on the second, 2 tail
+    # tiles split into 8-K-tile pieces). 128 x 256 tiles: 1000 x 9000, 288 of
+    # them, the last 32 split; 2000 x 8296, 528 tiles ragged both ways, splits
+    # the last 16 after two whole rounds at K = 256 and runs unsplit through
+    # the three-stage ring's remainders at 3 and 2 K steps; 2048 x 8448 and
+    # 2048 x 8192 are the whole-tile forms, split and not.
     # Both weight layouts. Eight rows of every 128-row tile (its edges and
     # random ones) against every column, so every tile is checked.
     rng = np.random.default_rng(17 * M + N + K + (layout == "kn"))
