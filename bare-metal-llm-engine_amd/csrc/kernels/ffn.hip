@@ -49,9 +49,15 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
   constexpr long long kPiece = 64 * VEC;
   constexpr long long kMaxLds = sizeof(WT) == 2 ? kStagedLdsMax : 64 * 1024;
   const long long padded = (K + kPiece - 1) / kPiece * kPiece;
-  // 5 to 64 rows: gate and up each in one pass over its matrix on the matrix
-  // cores (skinny.hip), then SwiGLU.
-  {
+  // Rows past the few-row kernels go to a GEMM. With fp16 Wg and Wu (either
+  // layout, both aligned) that is the fp16-MFMA GEMM on the rows' three fp16
+  // planes, split once for gate and up; else the rows normalised in fp32.
+  // fp16 weights take it from kH3MinRows rows on.
+  const bool h3 = elem == Elem::F16 && aligned_to(in, 16) &&
+                  gemm_h3_applies(M, N, K, Wg, !nk) && gemm_h3_applies(M, N, K, Wu, !nk);
+  // 5 to 64 rows (fp16 weights: 5 to 32): gate and up each in one pass over
+  // its matrix on the matrix cores (skinny.hip), then SwiGLU.
+  if (!h3 || M < kH3MinRows) {
     SkinnyArgs sk;
     sk.W = Wg;
     sk.w = elem;
@@ -182,11 +188,6 @@ void rmsnorm_linear_swiglu(const float* in, const float* gamma, const WT* Wg, co
 
   const std::size_t mn = static_cast<std::size_t>(M) * static_cast<std::size_t>(N);
   const std::size_t mk = M > 1 ? static_cast<std::size_t>(M) * static_cast<std::size_t>(K) : 0;
-  // Rows past the few-row kernels go to a GEMM. With fp16 Wg and Wu (either
-  // layout, both aligned) that is the fp16-MFMA GEMM on the rows' three fp16
-  // planes, split once for gate and up; else the rows normalised in fp32.
-  const bool h3 = elem == Elem::F16 && aligned_to(in, 16) &&
-                  gemm_h3_applies(M, N, K, Wg, !nk) && gemm_h3_applies(M, N, K, Wu, !nk);
   // The leading region holds the normalised rows (4 mk bytes) or the planes
   // and row scales (6 mk + 4 M bytes); gate and up follow, 256-byte aligned.
   const std::size_t plane_bytes = 3 * mk * sizeof(_Float16);

@@ -1091,18 +1091,19 @@ void run_gemm_tiled(const GemmArgs& a, hipStream_t stream) {
 // round at most half full, and below half a round every tile, is split by K
 // (gemm_h3_sk_kernel, the plan of gemm_sk_kernel).
 namespace h3 {
-constexpr int BM = 128;
-constexpr int WAVES = 8;
-constexpr int THREADS = 64 * WAVES;
-constexpr int PT = BM * BK;                   // halves of one plane tile
-constexpr int A_INST = 3 * PT / 8 / THREADS;  // direct loads per thread per K step (A planes)
-static_assert(A_INST == 3, "tile shape");
-
-// Tiles of 128 x BNT (BNT 128 or 256): BNT / 64 waves along N and the rest
-// of the 8 along M, each wave a WM x 64 block as MB x 2 32 x 32 MFMA blocks.
-template <int BNT>
+// Tiles of BMT x BNT: 128 x 128 and 128 x 256 on 8 waves, 64 x 128 on 4 waves
+// (two workgroups per CU). BNT / 64 waves along N and the rest along M, each
+// wave a WM x 64 block as MB x 2 32 x 32 MFMA blocks; every shape loads its
+// three plane tiles with three direct loads per thread and K step.
+template <int BMT, int BNT>
 struct Shape {
-  static_assert(BNT == 128 || BNT == 256, "tile width");
+  static_assert((BMT == 128 && (BNT == 128 || BNT == 256)) || (BMT == 64 && BNT == 128),
+                "tile shape");
+  static constexpr int BM = BMT;
+  static constexpr int WAVES = BMT / 16;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int PT = BM * BK;                   // halves of one plane tile
+  static constexpr int A_INST = 3 * PT / 8 / THREADS;  // direct loads per thread per K step (A planes)
   static constexpr int WGN = BNT / 64;
   static constexpr int WM = BM / (WAVES / WGN);
   static constexpr int WN = 64;
@@ -1110,9 +1111,13 @@ struct Shape {
   static constexpr int NB = WN / 32;
   static constexpr int B_INST = BNT * BK / 8 / THREADS;  // direct loads per thread per K step (B)
   static constexpr int LOADS = A_INST + B_INST;
+  static constexpr int PER_CU = BMT == 64 ? 2 : 1;       // workgroups a CU runs at once
+  static_assert(A_INST == 3 && B_INST * THREADS * 8 == BNT * BK && MB >= 1, "tile shape");
+  static_assert(THREADS == 4 * BMT && PER_CU == (BMT == 64 ? 2 : 1), "the kernels' launch bounds");
 };
-template <int BNT>
-using Acc = floatx16[Shape<BNT>::MB][Shape<BNT>::NB];
+template <int BMT, int BNT>
+using Acc = floatx16[Shape<BMT, BNT>::MB][Shape<BMT, BNT>::NB];
+constexpr int BM_MAX = 128;  // tallest tile (the offset bounds of gemm_h3_applies)
 }  // namespace h3
 
 // Reference-layout B tiles ([K x N] rows of BNT halves, 16-byte chunks):
@@ -1122,22 +1127,25 @@ using Acc = floatx16[Shape<BNT>::MB][Shape<BNT>::NB];
 // distinct 64-byte bank slots.
 __device__ __forceinline__ int swz_h3_kn(int k) { return 4 * (k & 3); }
 
-// K tiles [kt0, kt1) of the 128 x BNT tile at (m0, n0) into acc (zeroed
+// K tiles [kt0, kt1) of the BMT x BNT tile at (m0, n0) into acc (zeroed
 // here); ends with a barrier, so a following call may refill the stages. BKN:
 // B given [K x N] (the reference layout) instead of [N x K].
-template <int S, int BNT, bool BKN, bool EDGE>
+template <int S, int BMT, int BNT, bool BKN, bool EDGE>
 __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
                                         const _Float16* __restrict__ B, int M, int N, int K,
-                                        int m0, int n0, int kt0, int kt1, h3::Acc<BNT>& acc) {
-  using namespace h3;
+                                        int m0, int n0, int kt0, int kt1,
+                                        h3::Acc<BMT, BNT>& acc) {
+  using Sh = h3::Shape<BMT, BNT>;
   static_assert(S >= 3 && S <= 4, "stages");
-  constexpr int WGN = Shape<BNT>::WGN;
-  constexpr int WM = Shape<BNT>::WM;
-  constexpr int WN = Shape<BNT>::WN;
-  constexpr int MB = Shape<BNT>::MB;
-  constexpr int NB = Shape<BNT>::NB;
-  constexpr int B_INST = Shape<BNT>::B_INST;
-  constexpr int LOADS = Shape<BNT>::LOADS;
+  constexpr int THREADS = Sh::THREADS;
+  constexpr int PT = Sh::PT;
+  constexpr int WGN = Sh::WGN;
+  constexpr int WM = Sh::WM;
+  constexpr int WN = Sh::WN;
+  constexpr int MB = Sh::MB;
+  constexpr int NB = Sh::NB;
+  constexpr int B_INST = Sh::B_INST;
+  constexpr int LOADS = Sh::LOADS;
   constexpr int AT = 3 * PT;    // halves of a stage's plane tiles
   constexpr int BTL = BNT * BK; // halves of a stage's B tile
   typedef _Float16 halfx8v __attribute__((ext_vector_type(8)));
@@ -1172,8 +1180,8 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   const int wn = wave % WGN;
 
   // Direct loads: each load of wave w fills 16-byte slots 64 w + lane of a
-  // 512-slot part of a tile (the three plane tiles; the B tile's BNT / 128
-  // parts, part i holding slots 512 i ..). In plane tiles and [N x K] B
+  // THREADS-slot part of a tile (the three plane tiles, one part each; the B
+  // tile's B_INST parts, part i holding slots THREADS i ..). In plane tiles and [N x K] B
   // tiles slot q is row q / 4, position q % 4, holding chunk (q % 4) ^
   // swz_rows_h(row) ([K x N] B tiles below). The planes are K-blocked
   // ([K / 32][M][32] each): a plane tile is a contiguous run of 64-byte rows,
@@ -1189,7 +1197,7 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
   }
 #pragma unroll
   for (int i = 0; i < B_INST; ++i) {
-    const int q = i * 512 + wave * 64 + lane;
+    const int q = i * THREADS + wave * 64 + lane;
     if constexpr (BKN) {
       // [K x N]: slot q is row q / CPR (one k), position q % CPR of its BNT / 8
       // chunks, holding chunk (q % CPR) ^ swz_h3_kn(row); chunks past N read
@@ -1239,7 +1247,7 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
                                              0, 0);
 #pragma unroll
     for (int i = 0; i < B_INST; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * (i * 512 + wave * 64), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, bs + 8 * (i * THREADS + wave * 64), 16,
                                                static_cast<int>(b_off[i]), kt * b_step, 0, 0);
 #endif
   };
@@ -1376,16 +1384,15 @@ __device__ __forceinline__ void h3_tile(const _Float16* __restrict__ P,
 // acc times the row's 2^-e into dst (row r, column c of the tile at dst[r ld
 // + c]); GUARD keeps rows < rows_left and columns < cols_left. Rows past M
 // (an edge tile's clamped rows) take row M - 1's scale.
-template <int BNT, bool GUARD>
-__device__ __forceinline__ void h3_store(const h3::Acc<BNT>& acc, const float* __restrict__ rscale,
+template <int BMT, int BNT, bool GUARD>
+__device__ __forceinline__ void h3_store(const h3::Acc<BMT, BNT>& acc, const float* __restrict__ rscale,
                                          int M, int m0, float* __restrict__ dst, long long ld,
                                          int rows_left, int cols_left) {
-  using namespace h3;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int li = lane & 31;
   const int lg = lane >> 5;
-  using Sh = Shape<BNT>;
+  using Sh = h3::Shape<BMT, BNT>;
   const int wm = wave / Sh::WGN;
   const int wn = wave % Sh::WGN;
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -1412,17 +1419,17 @@ __device__ __forceinline__ void h3_store(const h3::Acc<BNT>& acc, const float* _
   }
 }
 
-template <int S, int BNT, bool BKN, bool EDGE>
-__global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
+template <int S, int BMT, int BNT, bool BKN, bool EDGE>
+__global__ __launch_bounds__(4 * BMT, BMT == 64 ? 2 : 1) void gemm_h3_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, int M, int N, int K, int tiles_m, int tiles_n) {
   int tm, tn;
   tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
-  const int m0 = tm * h3::BM;
+  const int m0 = tm * BMT;
   const int n0 = tn * BNT;
-  h3::Acc<BNT> acc;
-  h3_tile<S, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
-  h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+  h3::Acc<BMT, BNT> acc;
+  h3_tile<S, BMT, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, 0, K / BK, acc);
+  h3_store<BMT, BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                       N - n0);
 }
 
@@ -1431,13 +1438,13 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_kernel(
 // split the remaining tiles' K tiles evenly, one workgroup per CU after its
 // data-parallel tiles; a split tile leaves one record per workgroup (scaled
 // rows, slot 0 its first tile, slot 1 its last) for gemm_sk_fixup_kernel.
-template <int S, int BNT, bool BKN, bool EDGE>
-__global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
+template <int S, int BMT, int BNT, bool BKN, bool EDGE>
+__global__ __launch_bounds__(4 * BMT, BMT == 64 ? 2 : 1) void gemm_h3_sk_kernel(
     const _Float16* __restrict__ P, const float* __restrict__ rscale, const _Float16* __restrict__ B,
     float* __restrict__ C, float* __restrict__ rec, int M, int N, int K, int tiles_m, int tiles_n,
     SkPlan plan) {
-  constexpr int BM = h3::BM, BN = BNT;
-  h3::Acc<BNT> acc;
+  constexpr int BM = BMT, BN = BNT;
+  h3::Acc<BMT, BNT> acc;
   const int g = blockIdx.x;
   const bool dp = g < plan.dp;
   const long long s = dp ? 0 : g - plan.dp;
@@ -1453,13 +1460,13 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
     tile_of(first_tile + static_cast<int>(t), tiles_m, tiles_n, tm, tn);
     const int m0 = tm * BM;
     const int n0 = tn * BN;
-    h3_tile<S, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
+    h3_tile<S, BMT, BNT, BKN, EDGE>(P, B, M, N, K, m0, n0, ka, kb, acc);
     if (ka == 0 && kb == plan.nk) {
-      h3_store<BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
+      h3_store<BMT, BNT, EDGE>(acc, rscale, M, m0, C + static_cast<long long>(m0) * N + n0, N, M - m0,
                           N - n0);
     } else {
       const int slot = it == i0 ? 0 : 1;
-      h3_store<BNT, false>(acc, rscale, M, m0,
+      h3_store<BMT, BNT, false>(acc, rscale, M, m0,
                            rec + (s * 2 + slot) * static_cast<long long>(BM * BN), BN, BM, BN);
     }
     it = t * plan.nk + kb;
@@ -1472,6 +1479,15 @@ __global__ __launch_bounds__(h3::THREADS, 1) void gemm_h3_sk_kernel(
 bool h3_wide_enabled() {
   static const bool on = [] {
     const char* v = std::getenv("ENGINE_GEMM_H3_NO_WIDE");
+    return !(v != nullptr && v[0] == '1');
+  }();
+  return on;
+}
+
+// The 64 x 128 tiles for M <= 64 can be switched off (ENGINE_GEMM_H3_NO_SHORT=1).
+bool h3_short_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("ENGINE_GEMM_H3_NO_SHORT");
     return !(v != nullptr && v[0] == '1');
   }();
   return on;
@@ -1493,7 +1509,7 @@ bool gemm_h3_applies(std::int64_t M, std::int64_t N, std::int64_t K, const void*
   // tile's corner (up to 128 rows of K halves) within a buffer load's 31 bits
   // and each activation plane (M K halves) within 31 bits of byte offset
   return h3_enabled() && M > 0 && N > 0 && K > 0 && K % BK == 0 && M <= kLim && N <= kLim &&
-         K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM) * K * 2 <= kLim &&
+         K <= kLim && aligned_to(B, 16) && static_cast<long long>(h3::BM_MAX) * K * 2 <= kLim &&
          M * K * 2 <= kLim && (!b_kn || (N % 8 == 0 && K * N * 2 <= kLim));
 }
 
@@ -1502,16 +1518,20 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
             "matmul (fp16 weights): shape or alignment not supported");
   const int M = static_cast<int>(a.M), N = static_cast<int>(a.N), K = static_cast<int>(a.K);
   const long long cus = device_cu_count();
-  const int tiles_m = (M + h3::BM - 1) / h3::BM;
-  auto run = [&](auto bnt, auto stages) {
+  auto run = [&](auto bmt, auto bnt, auto stages) {
+    constexpr int BMT = decltype(bmt)::value;
     constexpr int BNT = decltype(bnt)::value;
     constexpr int S = decltype(stages)::value;
+    using Sh = h3::Shape<BMT, BNT>;
+    const long long slots = cus * Sh::PER_CU;  // workgroups resident at once
+    const int tiles_m = (M + BMT - 1) / BMT;
     const int tiles_n = (N + BNT - 1) / BNT;
     const long long ntiles = static_cast<long long>(tiles_m) * tiles_n;
     ENG_CHECK(ntiles <= 0x7fffffffLL, "matmul: too many tiles for one launch");
-    const bool whole = M % h3::BM == 0 && N % BNT == 0;
-    // Stream-K, with at least 8 K tiles per tile: past one round of one tile
-    // per CU when the last round is at most half full (512 x 11008 on 128 x
+    const bool whole = M % BMT == 0 && N % BNT == 0;
+    // Stream-K, with at least 8 K tiles per tile (a round: one tile per
+    // resident workgroup, Sh::PER_CU per CU): past one round when the last
+    // round is at most half full (512 x 11008 on 128 x
     // 128 tiles: 88 of 256, 148.7 -> 138.3 us; at 176 of 256 the records and
     // the fix-up pass cost more than the split saves), the tail's workgroups
     // running after the whole rounds; below half a round every tile is split
@@ -1521,31 +1541,31 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
     // CU (384 x 11008, 2 tail tiles, 136.5 -> 102.7 us: the fix-up had summed
     // 128 records per element).
     const int nk = K / BK;
-    const long long tail = ntiles >= cus ? ntiles % cus : ntiles;
-    const bool split = sk_enabled() && nk >= 8 && tail != 0 && 2 * tail <= cus;
+    const long long tail = ntiles >= slots ? ntiles % slots : ntiles;
+    const bool split = sk_enabled() && nk >= 8 && tail != 0 && 2 * tail <= slots;
     SkPlan plan;
     plan.dp = static_cast<int>(ntiles - tail);
     plan.nk = nk;
     plan.I = tail * nk;
-    plan.nsk = static_cast<int>(std::max<long long>(1, std::min<long long>(cus, plan.I / 8)));
+    plan.nsk = static_cast<int>(std::max<long long>(1, std::min<long long>(slots, plan.I / 8)));
     auto go = [&](auto kn, auto edge) {
       constexpr bool KN = decltype(kn)::value;
       constexpr bool E = decltype(edge)::value;
       if (!split) {
-        gemm_h3_kernel<S, BNT, KN, E><<<static_cast<unsigned>(ntiles), h3::THREADS, 0, stream>>>(
+        gemm_h3_kernel<S, BMT, BNT, KN, E><<<static_cast<unsigned>(ntiles), Sh::THREADS, 0, stream>>>(
             a.P, a.rscale, a.B, a.C, M, N, K, tiles_m, tiles_n);
         ENG_LAUNCH_CHECK();
         return;
       }
       StreamScratch records(
-          stream, static_cast<std::size_t>(plan.nsk) * 2 * h3::BM * BNT * sizeof(float), 2);
+          stream, static_cast<std::size_t>(plan.nsk) * 2 * BMT * BNT * sizeof(float), 2);
       float* rec = static_cast<float*>(records.get());
-      gemm_h3_sk_kernel<S, BNT, KN, E><<<static_cast<unsigned>(plan.dp + plan.nsk), h3::THREADS,
+      gemm_h3_sk_kernel<S, BMT, BNT, KN, E><<<static_cast<unsigned>(plan.dp + plan.nsk), Sh::THREADS,
                                          0, stream>>>(a.P, a.rscale, a.B, a.C, rec, M, N, K,
                                                       tiles_m, tiles_n, plan);
       ENG_LAUNCH_CHECK();
-      gemm_sk_fixup_kernel<h3::BM, BNT, E>
-          <<<dim3(static_cast<unsigned>(tail), h3::BM * BNT / 1024), 256, 0, stream>>>(
+      gemm_sk_fixup_kernel<BMT, BNT, E>
+          <<<dim3(static_cast<unsigned>(tail), BMT * BNT / 1024), 256, 0, stream>>>(
               rec, a.C, M, N, tiles_m, tiles_n, plan);
       ENG_LAUNCH_CHECK();
     };
@@ -1573,14 +1593,22 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
   // (1024 x 11008, 344 wide tiles, 88 split: 260 against 244 us on 688
   // unsplit narrow ones). Else 128 x 128 (waves of 32 x 64, four 32 KiB
   // stages).
-  const long long wide_tiles = static_cast<long long>(tiles_m) * ((N + 255) / 256);
+  const long long wide_tiles = static_cast<long long>((M + 127) / 128) * ((N + 255) / 256);
   const long long wide_tail = wide_tiles % cus;
   const bool wide_split_heavy = wide_tiles > cus && wide_tiles < 2 * cus && 4 * wide_tail > cus &&
                                 2 * wide_tail <= cus;
-  if (h3_wide_enabled() && 5 * wide_tiles >= 3 * cus && !wide_split_heavy)
-    run(std::integral_constant<int, 256>{}, std::integral_constant<int, 3>{});
+  using std::integral_constant;
+  // Up to 64 rows: 64 x 128 tiles (4 waves of 32 x 64, two workgroups per
+  // CU, three 20 KiB stages): no MFMA work on padding rows past M. 33-64 x
+  // 11008 x 4096: 47 -> 34-38 us (4096 x 4096: 28 -> 22-23.5); four stages
+  // measured 0.5-1 us slower. From 65 rows the 128-row tiles are faster
+  // (65 x 11008: 43.3 against 51.1 us).
+  if (M <= 64 && h3_short_enabled())
+    run(integral_constant<int, 64>{}, integral_constant<int, 128>{}, integral_constant<int, 3>{});
+  else if (h3_wide_enabled() && 5 * wide_tiles >= 3 * cus && !wide_split_heavy)
+    run(integral_constant<int, 128>{}, integral_constant<int, 256>{}, integral_constant<int, 3>{});
   else
-    run(std::integral_constant<int, 128>{}, std::integral_constant<int, 4>{});
+    run(integral_constant<int, 128>{}, integral_constant<int, 128>{}, integral_constant<int, 4>{});
 }
 
 void launch_gemm(const GemmArgs& a, hipStream_t stream) {

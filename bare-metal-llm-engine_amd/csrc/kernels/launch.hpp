@@ -95,6 +95,12 @@ bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, std::int64_t M, hipSt
 // once for all rows. Rows of one call are independent of each other and of M.
 constexpr std::int64_t kSkinnyMinRows = 5;
 constexpr std::int64_t kSkinnyMaxRows = 64;
+// fp16 weights from this many rows take the fp16-MFMA GEMM on three fp16
+// planes (exact products, 64 x 128 tiles up to 64 rows) instead of the
+// few-row kernel, which takes 16-row blocks (33-64 x 11008 x 4096: 41-50 us
+// against 34-38); the few-row kernel keeps fp16 weights at 5-32 rows and
+// fp32 weights at 5-64.
+constexpr std::int64_t kH3MinRows = 33;
 struct SkinnyArgs {
   const void* W = nullptr;
   Elem w = Elem::F32;

@@ -77,19 +77,23 @@ void rmsnorm_linear_any(const float* in, const float* rms_weight, const void* W,
     launch_gemv(g1, s);
     return;
   }
-  // 5 to 64 rows: one pass over W on the matrix cores.
-  SkinnyArgs sk = skinny_args(g1, M);
-  if (skinny_applies(sk)) {
-    launch_skinny(sk, s);
-    return;
-  }
-  // 2 to 4 rows (small-batch decode, each row equal to its single-row call),
-  // or rows the few-row kernel does not take: the rows share passes over W.
-  if (nk ? launch_gemv_nk_rows(g1, M, s) : launch_gemv_kn_rows(g1, M, s)) return;
   // fp16 W (either layout): the rows normalised into three fp16 planes, then
   // the fp16-MFMA GEMM (the same arithmetic as the FP32 GEMM on converted
-  // weights, 16x the matrix rate per instruction).
-  if (w_elem == Elem::F16 && aligned_to(in, 16) && gemm_h3_applies(M, N, K, W, !nk)) {
+  // weights, 16x the matrix rate per instruction); from kH3MinRows rows, or
+  // below that for calls the few-row kernel and the row passes do not take.
+  const bool h3 = w_elem == Elem::F16 && aligned_to(in, 16) && gemm_h3_applies(M, N, K, W, !nk);
+  if (!h3 || M < kH3MinRows) {
+    // 5 to 64 rows (fp16 W: 5 to 32): one pass over W on the matrix cores.
+    SkinnyArgs sk = skinny_args(g1, M);
+    if (skinny_applies(sk)) {
+      launch_skinny(sk, s);
+      return;
+    }
+    // 2 to 4 rows (small-batch decode, each row equal to its single-row call),
+    // or rows the few-row kernel does not take: the rows share passes over W.
+    if (nk ? launch_gemv_nk_rows(g1, M, s) : launch_gemv_kn_rows(g1, M, s)) return;
+  }
+  if (h3) {
     const std::size_t plane_bytes = 3 * static_cast<std::size_t>(M) * static_cast<std::size_t>(K) * 2;
     StreamScratch ws(s, plane_bytes + static_cast<std::size_t>(M) * sizeof(float));
     GemmH3Args h;

@@ -517,10 +517,18 @@ def rows_config3(eng, timer) -> list:
     return rows
 
 
+def few_rows_arith(M: int) -> str:
+    """How fp16-weight RMSNorm + linear computes M rows (5 to 64)."""
+    if M < 33:
+        return "few rows, fp16 MFMA, activations as two fp16 terms = 22 significant bits"
+    return "33-64 rows: fp16-MFMA GEMM on three fp16 planes of the rows, exact products, 64-row tiles"
+
+
 def rows_few_rows(eng, timer) -> list:
-    """Few-row linear layers (5 to 64 activation rows, the MFMA kernel that
-    streams W once): RMSNorm + linear at config 3's shape in both layouts,
-    the down-projection shape, and a few-row FP32 matmul. Bytes: W once plus
+    """Few-row linear layers (5 to 64 activation rows): RMSNorm + linear at
+    config 3's shape in both layouts (fp16 weights: the few-row MFMA kernel
+    that streams W once up to 32 rows, the fp16-MFMA GEMM from 33), the
+    down-projection shape, and a few-row FP32 matmul. Bytes: W once plus
     the activation rows in and out; FLOPs 2 M N K."""
     rows = []
     rng = np.random.default_rng(9)
@@ -534,8 +542,7 @@ def rows_few_rows(eng, timer) -> list:
             dxm = eng.upload(rng.standard_normal((M, K), dtype=np.float32))
             dym = eng.empty((M, N), np.float32)
             st = timer.sampled(lambda i, s: f(dxm.ptr, dg.ptr, Ws[i % R].ptr, dym.ptr, M, N, K, 1e-5, s))
-            row = hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold (few rows, fp16 MFMA, activations "
-                          f"as two fp16 terms = 22 significant bits), {tag}", st,
+            row = hbm_row(f"rmsnorm_linear fp16-W {M}x11008x4096 cold ({few_rows_arith(M)}), {tag}", st,
                           2 * K * N + 4 * M * K + 4 * K + 4 * M * N)
             row["TFLOP/s"] = round(2.0 * M * N * K / (st["median_ms"] * 1e-3) / 1e12, 2)
             rows.append(row)
@@ -546,8 +553,7 @@ def rows_few_rows(eng, timer) -> list:
             dxd = eng.upload(rng.standard_normal((M, Kd), dtype=np.float32))
             dyd = eng.empty((M, Nd), np.float32)
             st = timer.sampled(lambda i, s: f(dxd.ptr, None, Ws[i % R].ptr, dyd.ptr, M, Nd, Kd, 1e-5, s))
-            rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold (few rows, fp16 MFMA, "
-                                "activations as two fp16 terms = 22 significant bits, "
+            rows.append(hbm_row(f"rmsnorm_linear fp16-W {M}x4096x11008 cold ({few_rows_arith(M)}, "
                                 "down-projection shape), output-major W[NxK]", st,
                                 2 * Kd * Nd + 4 * M * Kd + 4 * M * Nd))
             dxd.free(), dyd.free()

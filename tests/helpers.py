@@ -333,7 +333,8 @@ def peer_row(run, x, m):
     """Row m of run(x) recomputed in another call that must give the same bits:
     alone when x has at most 4 rows (small-batch GEMV passes: each row equals
     the single-row call), else inside a 5-row window of x (the few-row MFMA
-    kernel gives a row the same bits in any batch of 5 to 64 rows)."""
+    kernel gives a row the same bits in any batch of 5 to 32 rows of fp16
+    weights, 5 to 64 of fp32)."""
     M = x.shape[0]
     if M <= 4:
         return run(x[m:m + 1])[0]

@@ -281,10 +281,11 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (5, 200, 512, "f16", True),      # few rows: MFMA kernel for gate and up + SwiGLU kernel
     (4, 11008, 4096, "f16", True),   # small batch at the config 5 gate/up shape
     (3, 300, 1000, "f32", False),    # small batch, fp32 weights, null gain
-    (40, 200, 512, "f16", True),     # few rows (three m-blocks) + SwiGLU kernel
+    (40, 200, 512, "f16", True),     # 33-64 rows of fp16 W: fp16-MFMA GEMMs on 64-row tiles
+    (40, 200, 520, "f16", True),     # K % 32 != 0: few rows (three m-blocks) + SwiGLU kernel
     (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
-    (64, 256, 512, "f16", False),    # 64 rows: the few-row kernel's largest batch
-    (65, 256, 512, "f16", True),     # past it: rows split into fp16 planes + fp16-MFMA GEMMs
+    (64, 256, 512, "f16", False),    # 64 rows: the 64-row fp16-MFMA tiles' largest batch
+    (65, 256, 512, "f16", True),     # past it: 128-row fp16-MFMA tiles
     (65, 256, 500, "f16", True),     # K % 32 != 0: rmsnorm + FP32 MFMA GEMMs on fp16 B
     (130, 300, 200, "f32", True),    # fp32 weights past the few-row kernel: FP32 MFMA GEMMs
 ])
@@ -335,7 +336,7 @@ def test_rmsnorm_linear_swiglu_small_batch_rows_match_single_row_calls(gpu, orc,
     # Up to 4 rows share each pass over Wg and Wu (fused SwiGLU epilogue), each
     # row's act equal to the M = 1 fused call bit for bit; 5 or more take the
     # few-row MFMA kernel for gate and up, each row the same bits in any batch
-    # of 5 to 64 rows.
+    # of 5 to 32 rows (fp16 weights; 5 to 64 for fp32).
     rng = np.random.default_rng(M * 13 + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
@@ -400,7 +401,8 @@ def test_rmsnorm_linear_swiglu_kn_matches_golden(gpu, orc, stem):
     (16, 1024, 512, "f16", False),   # few rows: MFMA kernel for gate and up + SwiGLU kernel
     (6, 400, 256, "f32", True),      # few rows, fp32 weights
     (17, 256, 512, "f32", True),
-    (40, 200, 512, "f16", True),
+    (40, 200, 512, "f16", True),     # fp16-MFMA GEMMs on 64-row tiles
+    (40, 200, 520, "f16", True),     # K % 32 != 0: few rows (three m-blocks)
     (12, 36, 20, "f16", True),       # N % 8 != 0: GEMV passes of up to 4 rows + SwiGLU kernel
     (80, 200, 512, "f16", True),     # prefill: rmsnorm + MFMA GEMMs + SwiGLU kernel
 ])

@@ -327,17 +327,20 @@ def gpu_rmsnorm_linear_f16w(eng, x, g, W, layout):
 
 @pytest.mark.parametrize("M,N,K", [(65, 128, 32), (128, 128, 64), (200, 136, 96), (256, 256, 128),
                                    (130, 304, 160), (1000, 264, 224), (130, 300, 160),
-                                   (130, 1000, 512)])
+                                   (130, 1000, 512), (33, 128, 32), (64, 256, 96), (48, 136, 160),
+                                   (40, 300, 224), (64, 2048, 1024), (37, 1000, 512)])
 @pytest.mark.parametrize("with_gamma", [True, False])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_rmsnorm_linear_f16w_fp16_mfma_every_row(gpu, orc, M, N, K, with_gamma, layout):
-    # M > 64, fp16 W in either layout, K % 32 == 0: the rows are split into
+    # M >= 33, fp16 W in either layout, K % 32 == 0: the rows are split into
     # three K-blocked fp16 planes and multiplied on the fp16 matrix cores
     # ([K x N] weights through transposing LDS reads; N % 8 == 0 there, so
     # N = 300 takes the FP32 GEMM in that layout). K = 32 .. 224 is 1 to 7 K
-    # steps (every remainder of the four-stage ring), M and N whole and
-    # ragged; 130 x 1000 x 512 (16 tiles, fewer than the CUs) splits every
-    # tile by K. Every row is checked.
+    # steps (every remainder of the four-stage ring of the 128-row tiles and
+    # of the three-stage ring of the 64-row tiles that take 33-64 rows), M
+    # and N whole and ragged; 130 x 1000 x 512 (16 tiles, fewer than the
+    # CUs), 64 x 2048 x 1024 and 37 x 1000 x 512 split every tile by K.
+    # Every row is checked.
     rng = np.random.default_rng(13 * M + N + K + with_gamma + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None
@@ -884,8 +887,8 @@ def test_rmsnorm_linear_f16w_full_tiles_against_oracle(gpu, orc, M, N, K, layout
 @pytest.mark.parametrize("with_gamma", [True, False])
 def test_rmsnorm_linear_f16w_nk_small_batch_rows_match_single_row_calls(gpu, orc, M, N, K, with_gamma):
     # Small-batch decode: up to 4 rows share passes over W (multi-row kernel),
-    # each row the single-row call's bits; 5 or more take the few-row MFMA
-    # kernel, each row the same bits in any batch of 5 to 64 rows.
+    # each row the single-row call's bits; 5 to 32 take the few-row MFMA
+    # kernel, each row the same bits in any batch of 5 to 32 rows.
     rng = np.random.default_rng(M * 100 + N + K)
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32) if with_gamma else None

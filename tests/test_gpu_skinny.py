@@ -11,9 +11,15 @@ kernel's edge cases: a ragged last column tile, K % 32 != 0 (a partial last
 k-group), fp32 weights whose second 16-byte piece is past N, one K chunk
 (no partial sums, RMS scale applied in the kernel), K = 8.
 
+fp16 weights with K % 32 == 0 take the few-row kernel at 5 to 32 rows and
+the fp16-MFMA GEMM (exact products, 64-row tiles) at 33 to 64; the cases at
+33-64 rows with K % 32 != 0 keep the few-row kernel's three and four m-blocks
+of fp16 weights covered.
+
 Batch invariance: each row's result involves only its own activation row and
 the chunking of K depends on N, K and the CU count only, so a row computed in
-a call of any M from 5 to 64 has the same bits.
+a call of any M within one path (fp16 weights: 5 to 32 rows, 33 to 64 rows;
+fp32 weights: 5 to 64) has the same bits.
 """
 
 from __future__ import annotations
@@ -73,9 +79,13 @@ def check_rows(orc, got, x, g, W_kn, rows, what):
     (5, 11008, 4096, "f16", "kn", True),    # config 3 shape, the smallest few-row batch
     (16, 11008, 4096, "f16", "kn", True),
     (16, 11008, 4096, "f16", "nk", True),
-    (64, 11008, 4096, "f16", "nk", False),  # four m-blocks, null gain
+    # 33-64 rows of fp16 W with K % 32 == 0 take the fp16-MFMA GEMM (64-row tiles)
+    (64, 11008, 4096, "f16", "nk", False),  # null gain
     (64, 11008, 4096, "f16", "kn", True),
-    (33, 4096, 11008, "f16", "nk", True),   # down-projection shape, three m-blocks
+    (33, 4096, 11008, "f16", "nk", True),   # down-projection shape
+    # ... and the few-row kernel's three and four m-blocks with K % 32 = 8
+    (64, 11008, 4104, "f16", "nk", False),
+    (49, 4096, 4104, "f16", "kn", True),
     (17, 4096, 11008, "f16", "kn", True),
     (8, 1000, 776, "f16", "kn", True),      # ragged last column tile, K % 32 = 8 (partial k-group)
     (20, 300, 1000, "f16", "nk", True),     # rows of W past N read row N - 1, K % 32 = 8
@@ -87,7 +97,7 @@ def check_rows(orc, got, x, g, W_kn, rows, what):
     (9, 64, 8, "f16", "kn", True),          # K = 8: a single partial k-group
     (9, 1000, 776, "f16", "nk", True),      # one m-block, weights through LDS: ragged tile and unit
     (36, 1000, 776, "f16", "kn", False),    # three m-blocks, one X' buffer: ragged tile and unit
-    (50, 11008, 4096, "f16", "kn", True),   # four m-blocks at the config-3 shape
+    (50, 11008, 4096, "f16", "kn", True),   # config-3 shape (fp16-MFMA GEMM)
 ])
 def test_rmsnorm_linear_few_rows_against_oracle(gpu, orc, M, N, K, dtype, layout, gamma):
     rng = np.random.default_rng(M * 1000 + N + K)
@@ -101,17 +111,28 @@ def test_rmsnorm_linear_few_rows_against_oracle(gpu, orc, M, N, K, dtype, layout
 
 @pytest.mark.parametrize("layout", ["kn", "nk"])
 def test_few_row_results_do_not_depend_on_the_batch(gpu, orc, layout):
+    # A row's bits do not depend on the other rows of the call within each
+    # path: 5-32 rows of fp16 W (the few-row kernel) and 33-64 rows (the
+    # fp16-MFMA GEMM on one row of 64-row tiles, whose split plan depends on
+    # N and K only).
     rng = np.random.default_rng(71)
     N, K = 11008, 4096
     x = rng.standard_normal((64, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
-    _, W = make_weights(orc, rng, N, K, "f16", layout)
+    W_kn, W = make_weights(orc, rng, N, K, "f16", layout)
     full = run_rmsnorm_linear(gpu, x, g, W, layout)
-    for lo, hi in ((0, 5), (40, 57), (59, 64), (16, 48)):
+    for lo, hi in ((0, 33), (20, 64), (31, 64)):
         part = run_rmsnorm_linear(gpu, x[lo:hi], g, W, layout)
         assert np.array_equal(part, full[lo:hi]), f"rows {lo}:{hi} of a {hi - lo}-row call"
     again = run_rmsnorm_linear(gpu, x, g, W, layout)
     assert np.array_equal(again, full), "deterministic"
+    few = run_rmsnorm_linear(gpu, x[:32], g, W, layout)
+    for lo, hi in ((0, 5), (8, 25), (27, 32), (16, 32)):
+        part = run_rmsnorm_linear(gpu, x[lo:hi], g, W, layout)
+        assert np.array_equal(part, few[lo:hi]), f"rows {lo}:{hi} of a {hi - lo}-row call"
+    rows = np.array([0, 17, 31])
+    check_rows(orc, few, x[:32], g, W_kn, rows, f"few-row rmsnorm_linear {layout} 32x{N}x{K}")
+    check_rows(orc, full, x, g, W_kn, np.array([0, 40, 63]), f"rmsnorm_linear {layout} 64x{N}x{K}")
 
 
 @pytest.mark.parametrize("M,N,K", [(5, 4096, 4096), (24, 11008, 4096), (64, 1000, 1000),
