@@ -1434,8 +1434,9 @@ __global__ __launch_bounds__(4 * BMT, BMT == 64 ? 2 : 1) void gemm_h3_kernel(
 }
 
 // Stream-K form (the plan of gemm_sk_kernel): workgroups 0 .. dp - 1 compute
-// tiles 0 .. dp - 1 whole (whole rounds of one tile per CU), and the rest
-// split the remaining tiles' K tiles evenly, one workgroup per CU after its
+// tiles 0 .. dp - 1 whole (whole rounds of one tile per resident workgroup,
+// two per CU for 64-row tiles), and the rest split the remaining tiles' K
+// tiles evenly, at most one workgroup per CU after its
 // data-parallel tiles; a split tile leaves one record per workgroup (scaled
 // rows, slot 0 its first tile, slot 1 its last) for gemm_sk_fixup_kernel.
 template <int S, int BMT, int BNT, bool BKN, bool EDGE>
@@ -1547,7 +1548,10 @@ void launch_gemm_h3(const GemmH3Args& a, hipStream_t stream) {
     plan.dp = static_cast<int>(ntiles - tail);
     plan.nk = nk;
     plan.I = tail * nk;
-    plan.nsk = static_cast<int>(std::max<long long>(1, std::min<long long>(slots, plan.I / 8)));
+    // At most one split workgroup per CU, also for the 64-row tiles (two per
+    // CU: 64 x 11008 x 4096 44.8 against 40.9 us; 3/4 and 1/2 of the CUs 44.7
+    // and 53.7; 64 x 4096 x 4096 26.0 against 23.5).
+    plan.nsk = static_cast<int>(std::max<long long>(1, std::min<long long>(cus, plan.I / 8)));
     auto go = [&](auto kn, auto edge) {
       constexpr bool KN = decltype(kn)::value;
       constexpr bool E = decltype(edge)::value;
