@@ -94,13 +94,14 @@ bool launch_gemv_kn_glu(const GemvArgs& a, const void* Wu, std::int64_t M, hipSt
 // with row m scaled by 1/sqrt(mean_k x[m][k]^2 + eps) after the sum), W read
 // once for all rows. Rows of one call are independent of each other and of M.
 constexpr std::int64_t kSkinnyMinRows = 5;
-constexpr std::int64_t kSkinnyMaxRows = 64;
+constexpr std::int64_t kSkinnyMaxRows = 64;     // fp32 weights
+constexpr std::int64_t kSkinnyMaxRowsF16 = 32;  // fp16 weights
 // fp16 weights from this many rows take the fp16-MFMA GEMM on three fp16
 // planes (exact products, 64 x 128 tiles up to 64 rows) instead of the
 // few-row kernel, which takes 16-row blocks (33-64 x 11008 x 4096: 41-50 us
-// against 34-38); the few-row kernel keeps fp16 weights at 5-32 rows and
-// fp32 weights at 5-64.
-constexpr std::int64_t kH3MinRows = 33;
+// against 37.5-42 cold); the few-row kernel keeps fp16 weights at 5-32 rows
+// and fp32 weights at 5-64.
+constexpr std::int64_t kH3MinRows = kSkinnyMaxRowsF16 + 1;
 struct SkinnyArgs {
   const void* W = nullptr;
   Elem w = Elem::F32;
@@ -119,7 +120,7 @@ struct SkinnyArgs {
   std::size_t scratch_bytes = 0;
 };
 // Whether the few-row kernel takes this call: kSkinnyMinRows <= M <=
-// kSkinnyMaxRows, K % 8 == 0, N a multiple of the 16-byte vector in the
+// kSkinnyMaxRows (fp16 W: kSkinnyMaxRowsF16), K % 8 == 0, N a multiple of the 16-byte vector in the
 // reference layout, and 16-byte aligned W, x and gamma.
 bool skinny_applies(const SkinnyArgs& a);
 // Scratch bytes launch_skinny takes (0 when K is not split).

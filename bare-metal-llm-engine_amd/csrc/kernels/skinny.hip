@@ -482,15 +482,17 @@ struct WVec<float> {
 //
 // fp16 weights: v_mfma_f32_16x16x32_f16 takes a load as it arrives (lane
 // (j, s) holds A[j][8 s .. 8 s + 7] of the 32 values of k of load i). The
-// activations enter as two fp16 planes: per unit and row, t = x' 2^e with
-// the power of two 2^e putting max |t| in [2^14, 2^15), hi = fp16(t) and
-// lo = fp16((t - hi) 2^11) -- t - hi is exact in fp32 and lo keeps its top
-// 11 bits, so hi + lo 2^-11 carries 22 significant bits of each x' and the
-// products hi w, lo w are exact in fp32. Two MFMAs per load and m-block
-// (hi and lo accumulators); after each unit the row's partial
-// (acc_hi + acc_lo 2^-11) 2^-e is added to its running sum. That is 4x fewer
-// matrix cycles than fp32 MFMA on the same data, within 2^-22 relative of
-// each x' (fp32 products round at 2^-24).
+// activations enter as three fp16 planes: per unit and row, t = x' 2^e with
+// the power of two 2^e putting max |t| in [2^14, 2^15), hi = fp16(t), lo =
+// fp16((t - hi) 2^11) and lo2 = fp16(((t - hi) 2^11 - lo) 2^11) -- each
+// difference is exact in fp32 and each term keeps the next 11 bits, so hi +
+// lo 2^-11 + lo2 2^-22 is t exactly (every x' whose bits reach no lower than
+// 2^-39 of the unit's largest) and the products hi w, lo w, lo2 w are exact
+// in fp32. Three MFMAs per load and m-block (one accumulator per plane);
+// after each unit the row's partial (acc_hi + (acc_lo + acc_lo2 2^-11)
+// 2^-11) 2^-e is added to its running sum: the fp32 arithmetic, exact
+// products and fp32 sums, in 3/8 of the matrix cycles of fp32 MFMA on the
+// same data.
 // fp32 weights: v_mfma_f32_16x16x4_f32, 8 MFMAs per load (step t takes
 // element t, k slot s), X' in fp32 planes.
 // Both: D[i][j] (lane j + 16 (i / 4), element i % 4) is weight row 16 w + i
@@ -533,17 +535,21 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   constexpr int SPT = ROWS * CPR / THREADS;                // staged chunks per thread
   constexpr int HCR = static_cast<int>(kUnitK) / 8;        // 8-value chunks per fp16 plane row
   static_assert(SPT * THREADS == ROWS * CPR, "staging covers the unit");
-  // One LDS buffer: fp32 X' (ROWS x 32 16-byte chunks), or the fp16 hi and
-  // lo planes (ROWS x 16 chunks each) and the rows' descale factors 2^-e.
+  // One LDS buffer: fp32 X' (ROWS x 32 16-byte chunks), or the fp16 hi, lo
+  // and lo2 planes (ROWS x 16 chunks each) and the rows' descale factors 2^-e.
   struct XBuf {
     floatx4 f[H ? 1 : ROWS * CPR];
     halfx8 hi[H ? ROWS * HCR : 1];
     halfx8 lo[H ? ROWS * HCR : 1];
+    halfx8 lo2[H ? ROWS * HCR : 1];
     float ds[H ? ROWS : 1];
   };
-  // Staged weights: one X buffer past 32 rows (LDS for two workgroups per CU), read and
-  // rewritten between two barriers per unit.
-  constexpr int XB = (STAGED && MB > 2) ? 1 : 2;
+  // Two X buffers where they fit beside the weight stages and the RMS sums
+  // in half the LDS (two workgroups per CU), else one (staged weights, read
+  // and rewritten between two barriers per unit): the reference layout at
+  // 17-32 rows with the three fp16 planes.
+  constexpr int XB =
+      (STAGED && 2 * sizeof(XBuf) + 2 * 128 * 8 * sizeof(halfx8) + 4 * ROWS > 80 * 1024) ? 1 : 2;
   __shared__ XBuf xbuf[XB];
   __shared__ float ssc[RMS ? ROWS : 1];
   // Staged weights: two stages of a unit's 16 KiB block of W (KN: 128 rows
@@ -614,16 +620,19 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
         int ex = 0;
         (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1) (ex = 0 for 0, inf, nan)
         const int e = min(15 - ex, 126);
-        halfx4 h, l;
+        halfx4 h, l, l2;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const float t = ldexpf(xv[q], e);
           h[q] = static_cast<_Float16>(t);
-          l[q] = static_cast<_Float16>((t - static_cast<float>(h[q])) * 2048.0f);
+          const float r1 = (t - static_cast<float>(h[q])) * 2048.0f;
+          l[q] = static_cast<_Float16>(r1);
+          l2[q] = static_cast<_Float16>((r1 - static_cast<float>(l[q])) * 2048.0f);
         }
         const int pos = m * HCR + ((qc >> 1) ^ (m & 15));
         reinterpret_cast<halfx4*>(&xb.hi[pos])[qc & 1] = h;
         reinterpret_cast<halfx4*>(&xb.lo[pos])[qc & 1] = l;
+        reinterpret_cast<halfx4*>(&xb.lo2[pos])[qc & 1] = l2;
         if (qc == 0) xb.ds[m] = ldexpf(1.0f, -e);
       } else {
         xb.f[m * CPR + (qc ^ (m & 7))] = xv;
@@ -663,14 +672,14 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
   };
 
   // acc: the running sums (fp32 path: the MFMA accumulators themselves);
-  // acl: the fp16 path's lo accumulators (acc_hi is ach).
-  floatx4 acc[MB], ach[H ? MB : 1], acl[H ? MB : 1];
+  // ach, acl, acm: the fp16 path's hi, lo and lo2 accumulators of a unit.
+  floatx4 acc[MB], ach[H ? MB : 1], acl[H ? MB : 1], acm[H ? MB : 1];
   auto zero4 = [] { return floatx4{0.0f, 0.0f, 0.0f, 0.0f}; };
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = zero4();
   if constexpr (H) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) ach[mb] = acl[mb] = zero4();
+    for (int mb = 0; mb < MB; ++mb) ach[mb] = acl[mb] = acm[mb] = zero4();
   }
 
   // The LPU loads of the unit at cur against buffer xb; load i of w is
@@ -686,12 +695,13 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
       const bool kok = cur.ku * kUnitK + 4 * E * i + E * s < K;
       if constexpr (H) {
         const halfx8 wi = kok ? w[i] : halfx8{};
-        halfx8 bh[MB], bl[MB];
+        halfx8 bh[MB], bl[MB], bm[MB];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
           const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 15));
           bh[mb] = xb.hi[pos];
           bl[mb] = xb.lo[pos];
+          bm[mb] = xb.lo2[pos];
         }
         __builtin_amdgcn_sched_barrier(0);
         w[i] = __builtin_nontemporal_load(w_src(next, i));
@@ -700,6 +710,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
         for (int mb = 0; mb < MB; ++mb) {
           ach[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bh[mb], ach[mb], 0, 0, 0);
           acl[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bl[mb], acl[mb], 0, 0, 0);
+          acm[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bm[mb], acm[mb], 0, 0, 0);
         }
       } else {
         const WV wi = kok ? w[i] : WV{};
@@ -723,9 +734,9 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const float d = xb.ds[16 * mb + j];
-        const floatx4 p = ach[mb] + acl[mb] * (1.0f / 2048.0f);
+        const floatx4 p = ach[mb] + (acl[mb] + acm[mb] * (1.0f / 2048.0f)) * (1.0f / 2048.0f);
         acc[mb] += p * d;
-        ach[mb] = acl[mb] = zero4();
+        ach[mb] = acl[mb] = acm[mb] = zero4();
       }
     }
   };
@@ -802,25 +813,27 @@ __global__ __launch_bounds__(kWaves * 64, 2) void skinny_nk_kernel(
         wv = wst[st * 1024 + (16 * wave + j) * 16 + ((4 * i + s) ^ j)];
       }
       const halfx8 wi = kok ? wv : halfx8{};
-      halfx8 bh[MB], bl[MB];
+      halfx8 bh[MB], bl[MB], bm[MB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const int pos = (16 * mb + j) * HCR + ((4 * i + s) ^ (j & 15));
         bh[mb] = xb.hi[pos];
         bl[mb] = xb.lo[pos];
+        bm[mb] = xb.lo2[pos];
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         ach[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bh[mb], ach[mb], 0, 0, 0);
         acl[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bl[mb], acl[mb], 0, 0, 0);
+        acm[mb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wi, bm[mb], acm[mb], 0, 0, 0);
       }
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
       const float d = xb.ds[16 * mb + j];
-      const floatx4 p = ach[mb] + acl[mb] * (1.0f / 2048.0f);
+      const floatx4 p = ach[mb] + (acl[mb] + acm[mb] * (1.0f / 2048.0f)) * (1.0f / 2048.0f);
       acc[mb] += p * d;
-      ach[mb] = acl[mb] = zero4();
+      ach[mb] = acl[mb] = acm[mb] = zero4();
     }
   };
 
@@ -1044,11 +1057,18 @@ void run_skinny(const SkinnyArgs& a, hipStream_t stream) {
 
 template <typename WT, bool NK, bool RMS>
 void dispatch_mb(const SkinnyArgs& a, hipStream_t stream) {
-  switch ((a.M + 15) / 16) {
-    case 1: run_skinny<WT, NK, 1, RMS>(a, stream); break;
-    case 2: run_skinny<WT, NK, 2, RMS>(a, stream); break;
-    case 3: run_skinny<WT, NK, 3, RMS>(a, stream); break;
-    default: run_skinny<WT, NK, 4, RMS>(a, stream); break;
+  if constexpr (std::is_same<WT, _Float16>::value) {  // at most 32 rows
+    if (a.M <= 16)
+      run_skinny<WT, NK, 1, RMS>(a, stream);
+    else
+      run_skinny<WT, NK, 2, RMS>(a, stream);
+  } else {
+    switch ((a.M + 15) / 16) {
+      case 1: run_skinny<WT, NK, 1, RMS>(a, stream); break;
+      case 2: run_skinny<WT, NK, 2, RMS>(a, stream); break;
+      case 3: run_skinny<WT, NK, 3, RMS>(a, stream); break;
+      default: run_skinny<WT, NK, 4, RMS>(a, stream); break;
+    }
   }
 }
 
@@ -1064,7 +1084,8 @@ void dispatch_rms(const SkinnyArgs& a, hipStream_t stream) {
 }  // namespace
 
 bool skinny_applies(const SkinnyArgs& a) {
-  if (a.M < kSkinnyMinRows || a.M > kSkinnyMaxRows) return false;
+  if (a.M < kSkinnyMinRows || a.M > (a.w == Elem::F16 ? kSkinnyMaxRowsF16 : kSkinnyMaxRows))
+    return false;
   const long long vpw = a.w == Elem::F16 ? 8 : 4;
   if (a.K % 8 != 0) return false;
   if (!a.w_nk && a.N % vpw != 0) return false;

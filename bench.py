@@ -520,7 +520,7 @@ def rows_config3(eng, timer) -> list:
 def few_rows_arith(M: int) -> str:
     """How fp16-weight RMSNorm + linear computes M rows (5 to 64)."""
     if M < 33:
-        return "few rows, fp16 MFMA, activations as two fp16 terms = 22 significant bits"
+        return "few rows, fp16 MFMA, activations as three fp16 terms, exact products"
     return "33-64 rows: fp16-MFMA GEMM on three fp16 planes of the rows, exact products, 64-row tiles"
 
 

@@ -282,7 +282,7 @@ def test_rmsnorm_linear_swiglu_nk_matches_golden(gpu, orc, stem):
     (4, 11008, 4096, "f16", True),   # small batch at the config 5 gate/up shape
     (3, 300, 1000, "f32", False),    # small batch, fp32 weights, null gain
     (40, 200, 512, "f16", True),     # 33-64 rows of fp16 W: fp16-MFMA GEMMs on 64-row tiles
-    (40, 200, 520, "f16", True),     # K % 32 != 0: few rows (three m-blocks) + SwiGLU kernel
+    (40, 200, 520, "f16", True),     # K % 32 != 0 past 32 rows: rmsnorm + FP32 MFMA GEMMs
     (128, 512, 256, "f16", True),    # prefill, whole tiles: direct-to-LDS GEMM with fp16 B
     (64, 256, 512, "f16", False),    # 64 rows: the 64-row fp16-MFMA tiles' largest batch
     (65, 256, 512, "f16", True),     # past it: 128-row fp16-MFMA tiles
@@ -402,7 +402,8 @@ def test_rmsnorm_linear_swiglu_kn_matches_golden(gpu, orc, stem):
     (6, 400, 256, "f32", True),      # few rows, fp32 weights
     (17, 256, 512, "f32", True),
     (40, 200, 512, "f16", True),     # fp16-MFMA GEMMs on 64-row tiles
-    (40, 200, 520, "f16", True),     # K % 32 != 0: few rows (three m-blocks)
+    (40, 200, 520, "f16", True),     # K % 32 != 0 past 32 rows: rmsnorm + FP32 MFMA GEMMs
+    (24, 200, 520, "f16", True),     # few rows (two m-blocks), K % 32 != 0
     (12, 36, 20, "f16", True),       # N % 8 != 0: GEMV passes of up to 4 rows + SwiGLU kernel
     (80, 200, 512, "f16", True),     # prefill: rmsnorm + MFMA GEMMs + SwiGLU kernel
 ])

@@ -11,10 +11,11 @@ kernel's edge cases: a ragged last column tile, K % 32 != 0 (a partial last
 k-group), fp32 weights whose second 16-byte piece is past N, one K chunk
 (no partial sums, RMS scale applied in the kernel), K = 8.
 
-fp16 weights with K % 32 == 0 take the few-row kernel at 5 to 32 rows and
-the fp16-MFMA GEMM (exact products, 64-row tiles) at 33 to 64; the cases at
-33-64 rows with K % 32 != 0 keep the few-row kernel's three and four m-blocks
-of fp16 weights covered.
+fp16 weights take the few-row kernel at 5 to 32 rows (activations as three
+fp16 terms that add up to them exactly) and, from 33 rows, the fp16-MFMA GEMM
+(64-row tiles up to 64 rows) or, with K % 32 != 0, rmsnorm and the FP32 GEMM.
+test_fp16_weight_paths_keep_every_activation_bit pins the exactness of both
+fp16 paths bit for bit.
 
 Batch invariance: each row's result involves only its own activation row and
 the chunking of K depends on N, K and the CU count only, so a row computed in
@@ -83,7 +84,7 @@ def check_rows(orc, got, x, g, W_kn, rows, what):
     (64, 11008, 4096, "f16", "nk", False),  # null gain
     (64, 11008, 4096, "f16", "kn", True),
     (33, 4096, 11008, "f16", "nk", True),   # down-projection shape
-    # ... and the few-row kernel's three and four m-blocks with K % 32 = 8
+    # ... and with K % 32 = 8 rmsnorm and the FP32 GEMM on the fp16 weights
     (64, 11008, 4104, "f16", "nk", False),
     (49, 4096, 4104, "f16", "kn", True),
     (17, 4096, 11008, "f16", "kn", True),
@@ -96,7 +97,9 @@ def check_rows(orc, got, x, g, W_kn, rows, what):
     (7, 40000, 256, "f16", "nk", True),
     (9, 64, 8, "f16", "kn", True),          # K = 8: a single partial k-group
     (9, 1000, 776, "f16", "nk", True),      # one m-block, weights through LDS: ragged tile and unit
-    (36, 1000, 776, "f16", "kn", False),    # three m-blocks, one X' buffer: ragged tile and unit
+    (36, 1000, 776, "f16", "kn", False),    # K % 32 != 0 past 32 rows: the FP32 GEMM
+    (32, 1000, 776, "f16", "kn", True),     # two m-blocks, one X' buffer: ragged tile and unit
+    (17, 1000, 776, "f16", "nk", False),    # two m-blocks, weights in registers: ragged
     (50, 11008, 4096, "f16", "kn", True),   # config-3 shape (fp16-MFMA GEMM)
 ])
 def test_rmsnorm_linear_few_rows_against_oracle(gpu, orc, M, N, K, dtype, layout, gamma):
@@ -107,6 +110,40 @@ def test_rmsnorm_linear_few_rows_against_oracle(gpu, orc, M, N, K, dtype, layout
     got = run_rmsnorm_linear(gpu, x, g, W, layout)
     rows = np.array(sorted({0, M // 2, M - 1}))
     check_rows(orc, got, x, g, W_kn, rows, f"few-row rmsnorm_linear {layout} {dtype} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M", [5, 16, 17, 32, 33, 64, 130])
+@pytest.mark.parametrize("layout", ["kn", "nk"])
+def test_fp16_weight_paths_keep_every_activation_bit(gpu, M, layout):
+    # Both fp16-weight paths for M > 4 carry every fp32 activation into the
+    # fp16 matrix instruction as three fp16 terms that add up to it exactly
+    # (the few-row kernel per unit of 128 values of k, the fp16-MFMA GEMM per
+    # row), with exact products. With a weight matrix that selects one
+    # activation per output (a single 1.0 per column) the output is that
+    # activation times the row's RMS factor s, rounded once:
+    # y[m][n] = fp32(x[m][k_n] s_m). Column 64 t of each 64-column tile selects
+    # x[m][0] = 1.0, which reads back the s_m that tile applied. Two fp16
+    # terms (22 bits) would round most of these activations.
+    rng = np.random.default_rng(500 + M + (layout == "nk"))
+    K, N = 4096, 512
+    mag = rng.uniform(0.5, 1.0, (M, K)) * 2.0 ** rng.integers(-8, 1, (M, K))
+    x = (mag * rng.choice([-1.0, 1.0], (M, K))).astype(np.float32)  # full 24-bit significands
+    x[:, 0] = 1.0
+    sel = rng.integers(1, K, N)
+    sel[::64] = 0
+    W_kn = np.zeros((K, N), np.float16)
+    W_kn[sel, np.arange(N)] = 1.0
+    W = W_kn.view(np.uint16) if layout == "kn" else np.ascontiguousarray(W_kn.T).view(np.uint16)
+    got = run_rmsnorm_linear(gpu, x, None, W, layout)
+    for t in range(N // 64):
+        cols = np.arange(64 * t, 64 * t + 64)
+        s = got[:, 64 * t]
+        want = x[:, sel[cols]] * s[:, None]  # float32 x float32: one rounding
+        assert want.dtype == np.float32
+        bad = np.argwhere(got[:, cols] != want)
+        assert bad.size == 0, (f"{layout} M={M}: tile {t}, {len(bad)} outputs differ, first "
+                               f"(row, col) {tuple(bad[0])}: {got[:, cols][tuple(bad[0])]!r} "
+                               f"!= {want[tuple(bad[0])]!r}")
 
 
 @pytest.mark.parametrize("layout", ["kn", "nk"])
