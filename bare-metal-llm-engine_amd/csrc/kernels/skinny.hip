@@ -1,5 +1,6 @@
-// skinny.hip -- linear layers over a few activation rows (5 <= M <= 64) on
-// the matrix cores, streaming the weights once.
+// skinny.hip -- linear layers over a few activation rows (5 <= M <= 64; fp16
+// weights up to 32, past that the fp16-MFMA GEMM) on the matrix cores,
+// streaming the weights once.
 //
 // Y[M x N] = X'[M x K] . W with X' = X (matmul) or X * gamma (rmsnorm_linear,
 // whose row scale s_m = 1/sqrt(mean_k X[m][k]^2 + eps) is applied after the
@@ -21,14 +22,14 @@
 // per workgroup, added by skinny_reduce_kernel in workgroup order. The split
 // points depend on N, K and the CU count only -- never on M -- and each
 // output's arithmetic involves only its own row of X, so a row's result is
-// the same bits whichever M (5..64) it is computed in.
+// the same bits whichever M (5..64; fp16 W 5..32) it is computed in.
 //
 // skinny_nk_kernel covers a unit the same way for output-major W (its
 // weights straight into registers, or at one m-block of fp16 W through LDS
 // stages) and for reference-layout fp16 W (through LDS stages, read
 // transposed); skinny_mfma_kernel takes reference-layout fp32 W. At 11008 x
-// 4096 fp16 W [K x N] the staged form takes 25.5 us at M = 16 and 54.6 us at
-// M = 64, against 31.1 and 88.5 us for skinny_mfma_kernel (fp32 MFMA on
+// 4096 fp16 W [K x N] the staged form took 25.5 us at M = 16 (27.6 with the
+// third activation term) against 31.1 us for skinny_mfma_kernel (fp32 MFMA on
 // converted weights).
 #include "device_sync.hpp"
 #include "launch.hpp"
