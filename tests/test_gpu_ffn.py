@@ -304,13 +304,17 @@ def test_rmsnorm_linear_swiglu_nk_against_oracle(gpu, orc, M, N, K, dtype, gamma
               f"rmsnorm_linear_swiglu nk {M}x{N}x{K} {dtype}")
 
 
-@pytest.mark.parametrize("M,N,K", [(1000, 2816, 1024), (300, 11008, 512)])
+@pytest.mark.parametrize("M,N,K", [(1000, 2816, 1024), (300, 11008, 512), (33, 11008, 1024),
+                                   (64, 2816, 512), (48, 1004, 512)])
 @pytest.mark.parametrize("layout", ["nk", "kn"])
 def test_rmsnorm_linear_swiglu_prefill_fp16_mfma(gpu, orc, M, N, K, layout):
-    # Prefill with fp16 weights in either layout: the rows split once into
-    # three fp16 planes, gate and up on the fp16-MFMA GEMM (ragged M and N on
-    # the first shape; 258 tiles and the stream-K split on the second). Eight
-    # rows of every 128-row tile against every column.
+    # Prefill and batches past 32 rows with fp16 weights in either layout: the
+    # rows split once into three fp16 planes, gate and up on the fp16-MFMA
+    # GEMM (ragged M and N on the first shape; 258 tiles and the stream-K
+    # split on the second; 64-row tiles, every tile split by K, on the 33- and
+    # 64-row shapes; N = 1004 in the reference layout, N % 8 != 0, takes
+    # rmsnorm and the FP32 GEMM). Eight rows of every 128-row tile against
+    # every column.
     rng = np.random.default_rng(M + 3 * N + K + (layout == "kn"))
     x = rng.standard_normal((M, K), dtype=np.float32)
     g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
